@@ -1,0 +1,199 @@
+"""Paged-attention decode benchmark on one MI355X.
+
+Workload (default): Llama-3-8B-shaped GQA decode, bf16 -- 256 sequences,
+32 query / 8 KV heads, head_dim 128, block size 16, contexts
+clip(round(lognormal(ln 1024, 1.0)), 32, 8192), random non-contiguous block
+tables, N(0,1) synthetic values.  A "step" is one decode pass of one layer
+over the batch (the HIP split-K partition kernel + its merge kernel), with
+the batch already packed and resident in HBM.
+
+value   = algorithmic KV-read GB/s = decode bytes / mean step time, where
+          decode bytes = sum_i ctx_i * 2 * H_kv * D * 2 (K+V read once per
+          KV head) + q and out rows + block-table entries + context lengths;
+tokens/s = sequences / mean step time (one token per sequence per layer).
+Also reported: the roofline fraction against 8 TB/s, the full step time
+(GPU packing + K/V write of the step's 256 tokens + decode), and the
+reference CPU kernel timed on a bounded sample of the same workload on this
+host's cores.
+
+python bench.py [--steps K] [--warmup W] [--config 3|4|5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+PACKAGE = "low-latency-distributed-llm-serving-infrastructure-custom-k8s-control-plane_amd"
+METRIC = "paged-attn decode KV-read GB/s (% HBM peak) + decode tokens/s, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def pkg(sub):
+    return importlib.import_module(PACKAGE + "." + sub)
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w, t, budget_s: float):
+    """Reference kernel (oracle/_ref) per sequence on fp32 up-casts, until
+    ~budget_s seconds of kernel time; returns the baseline dict."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as oa
+
+    kind = "reference" if oa.reference_available() else "port"
+    q_all = t.query[0].transpose(0, 1)
+    done_seqs, done_bytes, spent = 0, 0, 0.0
+    e = 2 if w.dtype == torch.bfloat16 else 4
+    for i in range(w.num_seqs):
+        blocks = torch.tensor(w.block_lists[i], dtype=torch.long, device=t.key_cache.device)
+        k = t.key_cache[:, blocks].float().cpu().numpy()
+        v = t.value_cache[:, blocks].float().cpu().numpy()
+        ctx = w.context_lens[i]
+        slots = np.arange(len(w.block_lists[i]) * w.block_size, dtype=np.int64)[:ctx]
+        q = q_all[i : i + 1].float().cpu().numpy().transpose(1, 0, 2)
+        _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [w.start_positions[i]], [1], slots, w.scaling,
+                                                  kind=kind)
+        spent += secs
+        done_seqs += 1
+        done_bytes += ctx * 2 * w.num_kv_heads * w.head_dim * e + w.num_query_heads * w.head_dim * 2 * e
+        if spent >= budget_s:
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": done_bytes / spent / 1e9,
+        "unit": "GB/s",
+        "tokens_per_s": done_seqs / spent,
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"first {done_seqs} of {w.num_seqs} sequences, one call per sequence (T=1, all-ones mask, "
+                   f"OpenMP over T*H_q={w.num_query_heads} rows), fp32 up-casts of the bf16 values, "
+                   f"{spent:.1f} s kernel time; host {cpu_model()}, nproc {os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=4, choices=[3, 4, 5])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this path has no multi-GPU sharding "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    pkg("_native").load_library()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+
+    w = wl.CONFIGS[args.config](seed=args.seed)
+    t = wl.make_tensors(w, device, seed=args.seed)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile)
+    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def decode_step():
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+
+    def full_step():
+        s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile)
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps  # ms
+
+    ms = timed(decode_step, args.steps, args.warmup)
+    full_ms = timed(full_step, max(5, args.steps // 5), 2)
+
+    kv_bytes = wl.decode_bytes(w)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    tokens_per_s = w.num_query_tokens / (ms * 1e-3)
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) K/V/Q, random non-contiguous block tables)",
+        "config": {
+            "workload": w.name,
+            "num_seqs": w.num_seqs,
+            "num_query_heads": w.num_query_heads,
+            "num_kv_heads": w.num_kv_heads,
+            "head_dim": w.head_dim,
+            "block_size": w.block_size,
+            "context_tokens": w.num_context_tokens,
+            "query_tokens": w.num_query_tokens,
+            "partition": step.partition_size,
+        },
+        "tokens_per_s": round(tokens_per_s, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "full_step_ms": round(full_ms, 5),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if args.config == 5:
+        pf = wl.prefill_flops(w)
+        result["prefill_gflop"] = round(pf / 1e9, 2)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, t, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

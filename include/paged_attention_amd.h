@@ -1,0 +1,224 @@
+/*
+ * paged_attention_amd.h -- C ABI of the MI355X (gfx950) paged-attention path.
+ *
+ * Every pointer argument is a DEVICE pointer (HBM) unless stated otherwise;
+ * `stream` is a hipStream_t passed as void* (NULL = the null stream).  No
+ * entry point allocates, frees or synchronises: outputs and workspaces are
+ * caller-owned, every launch is asynchronous on `stream`, and the library
+ * keeps no device-side state between calls (reentrant).
+ *
+ * Entry points returning int return 0 (PA_OK) on success or a PA_ERR_* code;
+ * pa_error_string() turns a code into text and pa_last_error_message()
+ * returns the detailed message of the calling thread's last failure.
+ *
+ * Cache layout (fixed by the reference, app/memory/strategies.py:73-97):
+ *   key_cache / value_cache : (num_layers, total_blocks, block_size,
+ *                              num_kv_heads, head_dim), contiguous
+ *   slot s of layer l, kv head h  ->  element
+ *       ((l * total_blocks * block_size) + s) * num_kv_heads * head_dim
+ *       + h * head_dim
+ */
+#ifndef PAGED_ATTENTION_AMD_H
+#define PAGED_ATTENTION_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+    PA_OK = 0,
+    PA_ERR_INVALID_ARGUMENT = 1, /* shape / stride / dtype rejected        */
+    PA_ERR_UNSUPPORTED = 2,      /* valid but not implemented on this path */
+    PA_ERR_WORKSPACE = 3,        /* workspace missing or too small         */
+    PA_ERR_LAUNCH = 4            /* the HIP runtime refused a launch       */
+};
+
+/* Element type tags for K/V/query/output buffers. */
+enum { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1, PA_DTYPE_F16 = 2 };
+
+/* Default split-K partition of the decode kernel, in context tokens. */
+#define PA_DECODE_PARTITION 512
+
+/* ---- (0) reference ABI, device pointers -------------------------------- */
+
+/* Same fields, same order as the reference's PagedAttentionDims
+ * (csrc/include/paged_kernels.h:11-20). */
+typedef struct {
+    int32_t num_query_heads;
+    int32_t num_query_tokens;
+    int32_t head_dim;
+    int32_t num_layers;
+    int32_t total_blocks;
+    int32_t block_size;
+    int32_t num_kv_heads;
+    int32_t num_context_tokens;
+} PagedAttentionDims;
+
+/*
+ * Replaces: paged_attention(), csrc/include/paged_kernels.h:22-34 and
+ * csrc/src/paged_kernels.cpp:7-105 (bound by csrc/src/bindings.cpp:56-71).
+ * Same signature and semantics, fp32, over device pointers:
+ *   query  [1, H_q, T, D] head-major, caches as above (fp32),
+ *   gather_slots int32 [C], attention_mask uint8 [T, C] (nonzero = attend),
+ *   output [T, H_q, D]; a fully masked row and C == 0 give zeros.
+ * `scratch` is accepted for ABI compatibility and not touched (may be NULL).
+ * The reference returns void; so does this.  Failures are latched per
+ * thread: read them with pa_last_error().
+ */
+void paged_attention(const float *query, const float *key_cache,
+                     const float *value_cache, int32_t layer_idx,
+                     PagedAttentionDims dims, const int32_t *gather_slots,
+                     const uint8_t *attention_mask, float scaling,
+                     float *output, float *scratch, void *stream);
+
+/* Status of the calling thread's last paged_attention() call. */
+int pa_last_error(void);
+
+/* ---- shared step description ------------------------------------------ */
+
+/*
+ * One engine step over the flattened ragged batch (the layout of
+ * app/model/paged_attention.py:37-118): B sequences, sequence i owns query
+ * tokens [cu_seqlens[i], cu_seqlens[i+1]) of the flat buffer, its new tokens
+ * sit at positions [start_i, start_i + count_i), and its context is
+ * positions [0, context_lens[i]) with context_lens[i] = start_i + count_i.
+ * The query token at position start_i + j attends context positions
+ * [0, start_i + j] of its own sequence only (paged_attention.py:101-117).
+ */
+typedef struct {
+    int32_t num_seqs;           /* B                                        */
+    int32_t num_query_tokens;   /* T = sum of new-token counts              */
+    int32_t num_query_heads;    /* H_q                                      */
+    int32_t num_kv_heads;       /* H_kv (H_q % H_kv == 0)                   */
+    int32_t head_dim;           /* D                                        */
+    int32_t block_size;         /* bs, tokens per KV block                  */
+    int32_t total_blocks;       /* N, blocks per layer in the pool          */
+    int32_t num_layers;         /* L                                        */
+    int32_t max_blocks_per_seq; /* row stride of block_tables (elements)    */
+    int32_t partition_size;     /* decode split-K partition, tokens         */
+    int32_t dtype;              /* PA_DTYPE_* of query, caches and output   */
+    int32_t reserved;
+    int64_t q_token_stride;     /* query element stride between tokens      */
+    int64_t q_head_stride;      /* query element stride between heads       */
+} PaStepDims;
+
+/* ---- (a) ragged-batch packing ------------------------------------------ */
+
+typedef struct {
+    int32_t num_seqs;           /* B                                        */
+    int32_t block_size;         /* bs                                       */
+    int32_t max_blocks_per_seq; /* row stride of block_tables               */
+    int32_t partition_size;     /* decode split-K partition, tokens         */
+    int32_t prefill_tile;       /* query tokens per prefill work item       */
+    int32_t reserved;
+    int64_t max_query_tokens;   /* capacity of scatter_slots / position_ids */
+    int64_t max_context_tokens; /* capacity of gather_slots                 */
+    int64_t max_decode_items;   /* capacity of decode_items (pairs)         */
+    int64_t max_prefill_items;  /* capacity of prefill_items (pairs)        */
+} PaPackDims;
+
+/*
+ * Replaces, on the GPU: _cumulative_offsets (app/model/paged_attention.py:
+ * 121-125), PagedKVCacheManager.build_slot_mapping / _sequence_slots
+ * (app/memory/manager.py:104-128, 301-333) for both the scatter slots and
+ * the gather slots (paged_attention.py:64-69), and PagedStepContext.
+ * position_ids (paged_attention.py:81-90).
+ *
+ * Inputs: block_tables int32 [B, max_blocks_per_seq] (-1 padded, the layout
+ * of manager.py:236-271), start_positions / new_token_counts int64 [B].
+ * Outputs (all int64 unless noted, bit-exact with the reference):
+ *   cu_seqlens [B+1], cu_context_offsets [B+1], context_lens int32 [B],
+ *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
+ *   decode_items int32 pairs (seq, partition) for every sequence with one
+ *   new token, ordered by sequence then partition (may be NULL),
+ *   prefill_items int32 pairs (seq, query tile) for every sequence with more
+ *   than one new token (may be NULL).
+ * Writes past a capacity in PaPackDims are dropped, never performed.
+ * A block-table entry that is negative or past its row yields slot -1.
+ */
+int pa_pack(const int32_t *block_tables, const int64_t *start_positions,
+            const int64_t *new_token_counts, PaPackDims dims,
+            int64_t *cu_seqlens, int64_t *cu_context_offsets,
+            int32_t *context_lens, int64_t *scatter_slots,
+            int64_t *position_ids, int64_t *gather_slots,
+            int32_t *decode_items, int32_t *prefill_items, void *stream);
+
+/* ---- (b) K/V cache write ------------------------------------------------ */
+
+/*
+ * Replaces: PagedKVCacheManager.scatter_layer_kv (app/memory/manager.py:
+ * 150-168), i.e. key_cache[layer].view(N*bs, H_kv, D)[slot_mapping] = key,
+ * and the same for value, called from paged_attention.py:152-154.
+ * key / value: [num_tokens, H_kv, D] with arbitrary token / head strides
+ * (elements) and unit stride along D, so the model's transposed
+ * [1, H_kv, T, D] projections are consumed without a copy.
+ * slot_mapping int64 [num_tokens].  Slots outside [0, N*bs) are skipped
+ * (never written).  A bit-exact copy: no arithmetic on the values.
+ */
+int pa_reshape_and_cache(const void *key, const void *value,
+                         int64_t key_token_stride, int64_t key_head_stride,
+                         int64_t value_token_stride, int64_t value_head_stride,
+                         void *key_cache, void *value_cache,
+                         const int64_t *slot_mapping, int32_t num_tokens,
+                         int32_t num_kv_heads, int32_t head_dim,
+                         int32_t block_size, int32_t total_blocks,
+                         int32_t num_layers, int32_t layer_idx, int32_t dtype,
+                         void *stream);
+
+/* ---- (c) paged-attention decode (split-K) ------------------------------ */
+
+/* Bytes of workspace pa_decode needs for `num_decode_items` work items. */
+size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
+
+/*
+ * Replaces: NativePagedBackend.attend for decode steps
+ * (app/model/attention_backends.py:88-117) and the paged_attention kernel
+ * it calls, over block tables instead of a dense mask.
+ * Runs every (sequence, partition) item of `decode_items` (from pa_pack) for
+ * every KV head, then merges the split-K partials.  The single query token
+ * of decode sequence i is flat token cu_seqlens[i]; it attends positions
+ * [0, context_lens[i]).  query: [T, H_q, D] through PaStepDims strides;
+ * output: [T, H_q, D] contiguous, dtype of the caches; rows of tokens that
+ * are not decode tokens are not written.
+ */
+int pa_decode(const void *query, const void *key_cache,
+              const void *value_cache, int32_t layer_idx, PaStepDims dims,
+              const int32_t *block_tables, const int32_t *context_lens,
+              const int64_t *cu_seqlens, const int32_t *decode_items,
+              int64_t num_decode_items, float scaling, void *output,
+              void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- (d) causal chunked prefill ----------------------------------------- */
+
+/*
+ * Replaces: the SDPA path for multi-token steps (paged_attention.py:165-180,
+ * attention_backends.py:55-78) over the block-diagonal causal mask.
+ * Runs every (sequence, query tile) item of `prefill_items` (from pa_pack):
+ * query token j of sequence i (flat index cu_seqlens[i] + j, position
+ * context_lens[i] - count_i + j) attends positions [0, that position].
+ * K/V are read from the paged cache, so the new tokens must already have
+ * been written with pa_reshape_and_cache.
+ */
+int pa_prefill(const void *query, const void *key_cache,
+               const void *value_cache, int32_t layer_idx, PaStepDims dims,
+               const int32_t *block_tables, const int32_t *context_lens,
+               const int64_t *cu_seqlens, const int32_t *prefill_items,
+               int64_t num_prefill_items, int32_t prefill_tile, float scaling,
+               void *output, void *stream);
+
+/* ---- utilities ------------------------------------------------------------ */
+
+const char *pa_error_string(int code);
+const char *pa_last_error_message(void);
+/* ABI version: bumped whenever a signature or a struct above changes. */
+int pa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_ATTENTION_AMD_H */

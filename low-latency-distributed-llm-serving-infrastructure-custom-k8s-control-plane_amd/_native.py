@@ -1,0 +1,161 @@
+"""ctypes binding of libpaged_attention_amd.so (the C ABI in
+include/paged_attention_amd.h).
+
+The library is built in-tree by ``csrc/build.py`` and loaded from this
+package directory only.  There is no fallback: if the library is missing or
+does not export the expected symbols, :func:`load_library` raises, and every
+GPU operation of the package raises with it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
+ABI_VERSION = 1
+
+PA_OK = 0
+PA_ERR_INVALID_ARGUMENT = 1
+PA_ERR_UNSUPPORTED = 2
+PA_ERR_WORKSPACE = 3
+PA_ERR_LAUNCH = 4
+
+PA_DTYPE_F32 = 0
+PA_DTYPE_BF16 = 1
+PA_DTYPE_F16 = 2
+
+PA_DECODE_PARTITION = 512
+
+#: Every symbol the header declares; tests check the library exports them all.
+EXPORTED_SYMBOLS = (
+    "paged_attention",
+    "pa_last_error",
+    "pa_pack",
+    "pa_reshape_and_cache",
+    "pa_decode_workspace_size",
+    "pa_decode",
+    "pa_prefill",
+    "pa_error_string",
+    "pa_last_error_message",
+    "pa_abi_version",
+)
+
+
+class PagedAttentionDims(ctypes.Structure):
+    """Mirror of the reference PagedAttentionDims (csrc/include/paged_kernels.h:11-20)."""
+
+    _fields_ = [
+        ("num_query_heads", ctypes.c_int32),
+        ("num_query_tokens", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("num_layers", ctypes.c_int32),
+        ("total_blocks", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("num_context_tokens", ctypes.c_int32),
+    ]
+
+
+class PaStepDims(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_query_tokens", ctypes.c_int32),
+        ("num_query_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("total_blocks", ctypes.c_int32),
+        ("num_layers", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("partition_size", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("q_token_stride", ctypes.c_int64),
+        ("q_head_stride", ctypes.c_int64),
+    ]
+
+
+class PaPackDims(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("partition_size", ctypes.c_int32),
+        ("prefill_tile", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("max_query_tokens", ctypes.c_int64),
+        ("max_context_tokens", ctypes.c_int64),
+        ("max_decode_items", ctypes.c_int64),
+        ("max_prefill_items", ctypes.c_int64),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGNATURES = {
+    "paged_attention": (None, [_vp, _vp, _vp, _i32, PagedAttentionDims, _vp, _vp, _f32, _vp, _vp, _vp]),
+    "pa_last_error": (ctypes.c_int, []),
+    "pa_pack": (ctypes.c_int, [_vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pa_reshape_and_cache": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
+    "pa_decode": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
+    ),
+    "pa_prefill": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
+    ),
+    "pa_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "pa_last_error_message": (ctypes.c_char_p, []),
+    "pa_abi_version": (ctypes.c_int, []),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_built() -> bool:
+    return LIBRARY_PATH.exists()
+
+
+def load_library():
+    """Open the in-tree HIP library (once) and type its entry points."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(
+                f"HIP extension {LIBRARY_PATH.name} is not built; run __graft_entry__.build() "
+                "(or csrc/build.py) before using the GPU paged-attention path"
+            )
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.pa_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY_PATH.name} has ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError for a non-zero status returned by the library."""
+    if status == PA_OK:
+        return
+    lib = load_library()
+    detail = lib.pa_last_error_message().decode(errors="replace")
+    kind = lib.pa_error_string(status).decode(errors="replace")
+    raise RuntimeError(f"{what} failed ({kind}): {detail}")

@@ -1,0 +1,370 @@
+// extern "C" entry points of libpaged_attention_amd.so (declared in
+// include/paged_attention_amd.h).  Validation lives here; the kernels trust
+// what passes it.  Nothing in this file allocates, frees or synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pa_common.hpp"
+#include "pa_launch.hpp"
+
+namespace {
+
+thread_local char g_msg[512] = "";
+thread_local int g_ref_abi_status = PA_OK;
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return PA_OK;
+  if (e == hipErrorNotSupported) return fail(PA_ERR_UNSUPPORTED, "%s: shape not supported", what);
+  return fail(PA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+int elem_bytes(int dtype) {
+  switch (dtype) {
+    case PA_DTYPE_F32: return 4;
+    case PA_DTYPE_BF16: return 2;
+    case PA_DTYPE_F16: return 2;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int log2_exact(int v) {
+  int r = 0;
+  while ((1 << r) < v) ++r;
+  return (1 << r) == v ? r : -1;
+}
+
+int check_step(const PaStepDims& d, const char* who) {
+  if (elem_bytes(d.dtype) == 0) return fail(PA_ERR_INVALID_ARGUMENT, "%s: unknown dtype %d", who, d.dtype);
+  if (d.num_seqs < 0 || d.num_query_tokens < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: negative batch size", who);
+  if (d.num_query_heads <= 0 || d.num_kv_heads <= 0 || d.head_dim <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: heads and head_dim must be positive", who);
+  if (d.num_query_heads % d.num_kv_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "%s: num_query_heads must be a multiple of num_kv_heads for GQA", who);
+  if (d.block_size <= 0 || d.total_blocks <= 0 || d.num_layers <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: cache geometry must be positive", who);
+  if (d.max_blocks_per_seq < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: negative block-table stride", who);
+  return PA_OK;
+}
+
+const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx) {
+  const int64_t span = static_cast<int64_t>(d.total_blocks) * d.block_size * d.num_kv_heads *
+                       d.head_dim * elem_bytes(d.dtype);
+  return reinterpret_cast<const char*>(cache) + span * layer_idx;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_abi_version(void) { return 1; }
+
+const char* pa_error_string(int code) {
+  switch (code) {
+    case PA_OK: return "ok";
+    case PA_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case PA_ERR_UNSUPPORTED: return "unsupported shape";
+    case PA_ERR_WORKSPACE: return "workspace missing or too small";
+    case PA_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+const char* pa_last_error_message(void) { return g_msg; }
+
+int pa_last_error(void) { return g_ref_abi_status; }
+
+void paged_attention(const float* query, const float* key_cache, const float* value_cache,
+                     int32_t layer_idx, PagedAttentionDims dims, const int32_t* gather_slots,
+                     const uint8_t* attention_mask, float scaling, float* output, float* scratch,
+                     void* stream) {
+  (void)scratch;
+  g_ref_abi_status = PA_OK;
+  // Checks of csrc/src/bindings.cpp:25-48.
+  if (dims.num_kv_heads <= 0 || dims.num_query_heads % dims.num_kv_heads != 0) {
+    g_ref_abi_status = fail(PA_ERR_INVALID_ARGUMENT,
+                            "num_query_heads must be a multiple of num_kv_heads for GQA");
+    return;
+  }
+  if (layer_idx < 0 || layer_idx >= dims.num_layers) {
+    g_ref_abi_status = fail(PA_ERR_INVALID_ARGUMENT, "layer_idx out of range");
+    return;
+  }
+  if (dims.num_query_tokens < 0 || dims.num_context_tokens < 0 || dims.head_dim <= 0 ||
+      dims.block_size <= 0 || dims.total_blocks < 0) {
+    g_ref_abi_status = fail(PA_ERR_INVALID_ARGUMENT, "negative dimension");
+    return;
+  }
+  if (!pa::generic_supported(PA_DTYPE_F32, dims.head_dim)) {
+    g_ref_abi_status = fail(PA_ERR_UNSUPPORTED, "head_dim %d not supported", dims.head_dim);
+    return;
+  }
+  pa::GenericArgs a{};
+  a.query = query;
+  a.q_token_stride = dims.head_dim;
+  a.q_head_stride = static_cast<int64_t>(dims.num_query_tokens) * dims.head_dim;
+  const int64_t span = static_cast<int64_t>(dims.total_blocks) * dims.block_size *
+                       dims.num_kv_heads * dims.head_dim;
+  a.key_cache = key_cache + span * layer_idx;
+  a.value_cache = value_cache + span * layer_idx;
+  a.gather_slots = gather_slots;
+  a.mask = attention_mask;
+  a.total_blocks = dims.total_blocks;  // out-of-pool slots are skipped
+  a.block_size = dims.block_size;
+  a.num_context_tokens = dims.num_context_tokens;
+  a.output = output;
+  a.num_query_tokens = dims.num_query_tokens;
+  a.num_query_heads = dims.num_query_heads;
+  a.num_kv_heads = dims.num_kv_heads;
+  a.head_dim = dims.head_dim;
+  a.scale_log2e = scaling * pa::kLog2e;
+  g_ref_abi_status = from_hip(
+      pa::launch_generic(a, PA_DTYPE_F32, true, static_cast<hipStream_t>(stream)), "paged_attention");
+}
+
+int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
+            const int64_t* new_token_counts, PaPackDims dims, int64_t* cu_seqlens,
+            int64_t* cu_context_offsets, int32_t* context_lens, int64_t* scatter_slots,
+            int64_t* position_ids, int64_t* gather_slots, int32_t* decode_items,
+            int32_t* prefill_items, void* stream) {
+  if (dims.num_seqs < 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative num_seqs");
+  if (dims.block_size <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: block_size must be positive");
+  if (dims.max_blocks_per_seq < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative block-table stride");
+  if (dims.partition_size <= 0 || dims.prefill_tile <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: partition and prefill tile must be positive");
+  if (cu_seqlens == nullptr || cu_context_offsets == nullptr)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: cu_seqlens and cu_context_offsets are required");
+  if (dims.num_seqs > 0 &&
+      (start_positions == nullptr || new_token_counts == nullptr || context_lens == nullptr ||
+       scatter_slots == nullptr || position_ids == nullptr ||
+       (block_tables == nullptr && dims.max_blocks_per_seq > 0)))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: missing input or output buffer");
+  pa::PackArgs a{};
+  a.block_tables = block_tables;
+  a.start_positions = start_positions;
+  a.new_token_counts = new_token_counts;
+  a.cu_seqlens = cu_seqlens;
+  a.cu_context_offsets = cu_context_offsets;
+  a.context_lens = context_lens;
+  a.scatter_slots = scatter_slots;
+  a.position_ids = position_ids;
+  a.gather_slots = gather_slots;
+  a.decode_items = decode_items;
+  a.prefill_items = prefill_items;
+  a.num_seqs = dims.num_seqs;
+  a.block_size = dims.block_size;
+  a.block_table_stride = dims.max_blocks_per_seq;
+  a.partition = dims.partition_size;
+  a.prefill_tile = dims.prefill_tile;
+  a.max_query_tokens = dims.max_query_tokens;
+  a.max_context_tokens = gather_slots ? dims.max_context_tokens : 0;
+  a.max_decode_items = decode_items ? dims.max_decode_items : 0;
+  a.max_prefill_items = prefill_items ? dims.max_prefill_items : 0;
+  return from_hip(pa::launch_pack(a, static_cast<hipStream_t>(stream)), "pa_pack");
+}
+
+int pa_reshape_and_cache(const void* key, const void* value, int64_t key_token_stride,
+                         int64_t key_head_stride, int64_t value_token_stride,
+                         int64_t value_head_stride, void* key_cache, void* value_cache,
+                         const int64_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_size, int32_t total_blocks,
+                         int32_t num_layers, int32_t layer_idx, int32_t dtype, void* stream) {
+  const int eb = elem_bytes(dtype);
+  if (eb == 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_reshape_and_cache: unknown dtype %d", dtype);
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || total_blocks < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_reshape_and_cache: bad geometry");
+  if (layer_idx < 0 || layer_idx >= num_layers)
+    return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
+                num_layers);
+  if (num_tokens == 0) return PA_OK;
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_reshape_and_cache: null buffer");
+  pa::CacheWriteArgs a{};
+  const int64_t span = static_cast<int64_t>(total_blocks) * block_size * num_kv_heads * head_dim * eb;
+  a.key = key;
+  a.value = value;
+  a.key_token_stride = key_token_stride;
+  a.key_head_stride = key_head_stride;
+  a.value_token_stride = value_token_stride;
+  a.value_head_stride = value_head_stride;
+  a.key_cache = reinterpret_cast<char*>(key_cache) + span * layer_idx;
+  a.value_cache = reinterpret_cast<char*>(value_cache) + span * layer_idx;
+  a.slot_mapping = slot_mapping;
+  a.num_slots = static_cast<int64_t>(total_blocks) * block_size;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  return from_hip(pa::launch_cache_write(a, dtype, static_cast<hipStream_t>(stream)),
+                  "pa_reshape_and_cache");
+}
+
+size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items) {
+  if (num_decode_items <= 0 || dims.num_query_heads <= 0 || dims.head_dim <= 0) return 0;
+  // part_acc [items, H_q, D] fp32 followed by part_ml [items, H_q, 2] fp32,
+  // each rounded up to 256 bytes.
+  const size_t rows = static_cast<size_t>(num_decode_items) * dims.num_query_heads;
+  const size_t acc = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
+  const size_t ml = (rows * 2 * sizeof(float) + 255) & ~size_t(255);
+  return acc + ml;
+}
+
+int pa_decode(const void* query, const void* key_cache, const void* value_cache,
+              int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
+              const int32_t* context_lens, const int64_t* cu_seqlens,
+              const int32_t* decode_items, int64_t num_decode_items, float scaling,
+              void* output, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_step(dims, "pa_decode");
+  if (rc != PA_OK) return rc;
+  if (layer_idx < 0 || layer_idx >= dims.num_layers)
+    return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
+                dims.num_layers);
+  if (num_decode_items <= 0 || dims.num_seqs == 0) return PA_OK;
+  if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) > 0x7fffffffLL)
+    return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int group = dims.num_query_heads / dims.num_kv_heads;
+  const int eb = elem_bytes(dims.dtype);
+  const int log2_bs = log2_exact(dims.block_size);
+  const bool fast =
+      pa::decode_fast_path_supported(dims.dtype, dims.head_dim, group, dims.block_size,
+                                     dims.partition_size) &&
+      aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&
+      (dims.q_token_stride * eb) % 16 == 0 && (dims.q_head_stride * eb) % 16 == 0;
+  if (fast) {
+    const size_t need = pa_decode_workspace_size(dims, num_decode_items);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(PA_ERR_WORKSPACE, "pa_decode: workspace of %zu bytes needed, %zu given", need,
+                  workspace_bytes);
+    const size_t rows = static_cast<size_t>(num_decode_items) * dims.num_query_heads;
+    const size_t acc_bytes = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
+    pa::DecodeArgs a{};
+    a.query = query;
+    a.q_token_stride = dims.q_token_stride;
+    a.q_head_stride = dims.q_head_stride;
+    a.key_cache = layer_base(key_cache, dims, layer_idx);
+    a.value_cache = layer_base(value_cache, dims, layer_idx);
+    a.block_tables = block_tables;
+    a.context_lens = context_lens;
+    a.cu_seqlens = cu_seqlens;
+    a.items = decode_items;
+    a.num_items = num_decode_items;
+    a.output = output;
+    a.part_acc = reinterpret_cast<float*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + acc_bytes);
+    a.block_table_stride = dims.max_blocks_per_seq;
+    a.num_kv_heads = dims.num_kv_heads;
+    a.total_blocks = dims.total_blocks;
+    a.log2_block_size = log2_bs;
+    a.partition = dims.partition_size;
+    a.scale_log2e = scaling * pa::kLog2e;
+    return from_hip(pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, s),
+                    "pa_decode");
+  }
+  if (!pa::generic_supported(dims.dtype, dims.head_dim))
+    return fail(PA_ERR_UNSUPPORTED, "pa_decode: head_dim %d / dtype %d not supported",
+                dims.head_dim, dims.dtype);
+  pa::GenericArgs a{};
+  a.query = query;
+  a.q_token_stride = dims.q_token_stride;
+  a.q_head_stride = dims.q_head_stride;
+  a.key_cache = layer_base(key_cache, dims, layer_idx);
+  a.value_cache = layer_base(value_cache, dims, layer_idx);
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.cu_seqlens = cu_seqlens;
+  a.num_seqs = dims.num_seqs;
+  a.block_table_stride = dims.max_blocks_per_seq;
+  a.block_size = dims.block_size;
+  a.total_blocks = dims.total_blocks;
+  a.filter = 1;
+  a.output = output;
+  a.num_query_tokens = dims.num_query_tokens;
+  a.num_query_heads = dims.num_query_heads;
+  a.num_kv_heads = dims.num_kv_heads;
+  a.head_dim = dims.head_dim;
+  a.scale_log2e = scaling * pa::kLog2e;
+  return from_hip(pa::launch_generic(a, dims.dtype, false, s), "pa_decode");
+}
+
+int pa_prefill(const void* query, const void* key_cache, const void* value_cache,
+               int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
+               const int32_t* context_lens, const int64_t* cu_seqlens,
+               const int32_t* prefill_items, int64_t num_prefill_items, int32_t prefill_tile,
+               float scaling, void* output, void* stream) {
+  int rc = check_step(dims, "pa_prefill");
+  if (rc != PA_OK) return rc;
+  if (layer_idx < 0 || layer_idx >= dims.num_layers)
+    return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
+                dims.num_layers);
+  if (num_prefill_items <= 0 || dims.num_seqs == 0) return PA_OK;
+  if (num_prefill_items * static_cast<int64_t>(dims.num_kv_heads) > 0x7fffffffLL)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: too many work items");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int group = dims.num_query_heads / dims.num_kv_heads;
+  const int eb = elem_bytes(dims.dtype);
+  const bool fast =
+      pa::prefill_fast_path_supported(dims.dtype, dims.head_dim, group, dims.block_size) &&
+      prefill_tile == pa::prefill_tile_for(group) && aligned16(query) && aligned16(key_cache) &&
+      aligned16(value_cache) && aligned16(output) && (dims.q_token_stride * eb) % 16 == 0 &&
+      (dims.q_head_stride * eb) % 16 == 0;
+  if (fast) {
+    pa::PrefillArgs a{};
+    a.query = query;
+    a.q_token_stride = dims.q_token_stride;
+    a.q_head_stride = dims.q_head_stride;
+    a.key_cache = layer_base(key_cache, dims, layer_idx);
+    a.value_cache = layer_base(value_cache, dims, layer_idx);
+    a.block_tables = block_tables;
+    a.context_lens = context_lens;
+    a.cu_seqlens = cu_seqlens;
+    a.items = prefill_items;
+    a.output = output;
+    a.block_table_stride = dims.max_blocks_per_seq;
+    a.num_kv_heads = dims.num_kv_heads;
+    a.total_blocks = dims.total_blocks;
+    a.log2_block_size = log2_exact(dims.block_size);
+    a.scale_log2e = scaling * pa::kLog2e;
+    return from_hip(
+        pa::launch_prefill(a, dims.dtype, dims.head_dim, group, num_prefill_items, s),
+        "pa_prefill");
+  }
+  if (!pa::generic_supported(dims.dtype, dims.head_dim))
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: head_dim %d / dtype %d not supported",
+                dims.head_dim, dims.dtype);
+  pa::GenericArgs a{};
+  a.query = query;
+  a.q_token_stride = dims.q_token_stride;
+  a.q_head_stride = dims.q_head_stride;
+  a.key_cache = layer_base(key_cache, dims, layer_idx);
+  a.value_cache = layer_base(value_cache, dims, layer_idx);
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.cu_seqlens = cu_seqlens;
+  a.num_seqs = dims.num_seqs;
+  a.block_table_stride = dims.max_blocks_per_seq;
+  a.block_size = dims.block_size;
+  a.total_blocks = dims.total_blocks;
+  a.filter = 2;
+  a.output = output;
+  a.num_query_tokens = dims.num_query_tokens;
+  a.num_query_heads = dims.num_query_heads;
+  a.num_kv_heads = dims.num_kv_heads;
+  a.head_dim = dims.head_dim;
+  a.scale_log2e = scaling * pa::kLog2e;
+  return from_hip(pa::launch_generic(a, dims.dtype, false, s), "pa_prefill");
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// Shared device helpers for the gfx950 paged-attention kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wavefront = 64 lanes; workgroups are 256 threads (4 waves) unless a
+//    kernel says otherwise;
+//  * bf16 values travel as raw uint16 pairs packed in uint32 and are widened
+//    to fp32 with shifts (exact); fp32 -> bf16 rounds to nearest even;
+//  * all accumulation is fp32;
+//  * softmax runs in base 2: scores are pre-multiplied by scale*log2(e) and
+//    exponentiated with the hardware exp2 (v_exp_f32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "paged_attention_amd.h"
+
+namespace pa {
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+// Finite floor used as the initial running maximum: exp2(s - floor) of a
+// masked score (-inf) is exactly 0 and no (-inf) - (-inf) NaN can appear.
+constexpr float kScoreFloor = -3.402823466e+38f;
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static constexpr int kBytes = 4;
+  static constexpr int kDtype = PA_DTYPE_F32;
+};
+template <>
+struct Elem<bf16_t> {
+  static constexpr int kBytes = 2;
+  static constexpr int kDtype = PA_DTYPE_BF16;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) |
+         (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ float load_scalar(const T* p);
+template <>
+__device__ __forceinline__ float load_scalar<float>(const float* p) {
+  return *p;
+}
+template <>
+__device__ __forceinline__ float load_scalar<bf16_t>(const bf16_t* p) {
+  return bf16_to_f32(p->bits);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_scalar(T* p, float v);
+template <>
+__device__ __forceinline__ void store_scalar<float>(float* p, float v) {
+  *p = v;
+}
+template <>
+__device__ __forceinline__ void store_scalar<bf16_t>(bf16_t* p, float v) {
+  p->bits = f32_to_bf16(v);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+// ---- cross-lane helpers -----------------------------------------------
+// DPP controls (gfx9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7-i within 8
+constexpr int kDppRowMirror = 0x140;      // lane i <- lane 15-i within 16
+constexpr int kDppRowRor8 = 0x128;        // lane i <- lane (i+8)%16 within 16
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), Ctrl, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of L consecutive lanes (L in {1,2,4,8,16}); every
+// lane of the group ends with the group total.
+template <int L>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (L >= 2) x += dpp<kDppQuadXor1>(x);
+  if constexpr (L >= 4) x += dpp<kDppQuadXor2>(x);
+  if constexpr (L >= 8) x += dpp<kDppRowHalfMirror>(x);
+  if constexpr (L >= 16) x += dpp<kDppRowMirror>(x);
+  static_assert(L <= 16, "group_sum supports groups of at most 16 lanes");
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+// 16-byte global load / store.
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, uint4 v) {
+  *reinterpret_cast<uint4*>(p) = v;
+}
+
+}  // namespace pa

@@ -1,0 +1,140 @@
+// Kernel argument blocks and host-side launchers shared between the kernel
+// sources and the C-ABI layer (abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pa {
+
+// Decode (split-K) over block tables.
+struct DecodeArgs {
+  const void* query;
+  int64_t q_token_stride;
+  int64_t q_head_stride;
+  const void* key_cache;    // base of the layer
+  const void* value_cache;  // base of the layer
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  const int64_t* cu_seqlens;
+  const int32_t* items;     // (seq, partition) pairs
+  int64_t num_items;
+  void* output;             // [T, H_q, D]
+  float* part_acc;          // [items, H_q, D]
+  float* part_ml;           // [items, H_q, 2]
+  int32_t block_table_stride;
+  int32_t num_kv_heads;
+  int32_t total_blocks;
+  int32_t log2_block_size;
+  int32_t partition;
+  float scale_log2e;
+};
+
+// Generic one-wave-per-(query token, head) attention: any head_dim <= 256,
+// any GQA ratio, any block size.  Two context sources:
+//   masked = 0: block tables + causal limit (flat ragged batch),
+//   masked = 1: the reference ABI's flat gather list + dense uint8 mask.
+struct GenericArgs {
+  const void* query;
+  int64_t q_token_stride;
+  int64_t q_head_stride;
+  const void* key_cache;   // base of the layer
+  const void* value_cache;
+  // block-table source
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  const int64_t* cu_seqlens;
+  int32_t num_seqs;
+  int32_t block_table_stride;
+  int32_t block_size;
+  int32_t total_blocks;
+  int32_t filter;  // 0 = every token, 1 = decode sequences only, 2 = multi-token only
+  // gather/mask source
+  const int32_t* gather_slots;
+  const uint8_t* mask;
+  int32_t num_context_tokens;
+  // common
+  void* output;  // [T, H_q, D] contiguous
+  int32_t num_query_tokens;
+  int32_t num_query_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  float scale_log2e;
+};
+
+struct PackArgs {
+  const int32_t* block_tables;
+  const int64_t* start_positions;
+  const int64_t* new_token_counts;
+  int64_t* cu_seqlens;
+  int64_t* cu_context_offsets;
+  int32_t* context_lens;
+  int64_t* scatter_slots;
+  int64_t* position_ids;
+  int64_t* gather_slots;
+  int32_t* decode_items;
+  int32_t* prefill_items;
+  int32_t num_seqs;
+  int32_t block_size;
+  int32_t block_table_stride;
+  int32_t partition;
+  int32_t prefill_tile;
+  int64_t max_query_tokens;
+  int64_t max_context_tokens;
+  int64_t max_decode_items;
+  int64_t max_prefill_items;
+};
+
+struct CacheWriteArgs {
+  const void* key;
+  const void* value;
+  int64_t key_token_stride;
+  int64_t key_head_stride;
+  int64_t value_token_stride;
+  int64_t value_head_stride;
+  void* key_cache;    // base of the layer
+  void* value_cache;  // base of the layer
+  const int64_t* slot_mapping;
+  int64_t num_slots;  // total_blocks * block_size
+  int32_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+};
+
+// Causal chunked prefill over block tables (MFMA tiles).
+struct PrefillArgs {
+  const void* query;
+  int64_t q_token_stride;
+  int64_t q_head_stride;
+  const void* key_cache;
+  const void* value_cache;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  const int64_t* cu_seqlens;
+  const int32_t* items;  // (seq, query tile) pairs
+  void* output;
+  int32_t block_table_stride;
+  int32_t num_kv_heads;
+  int32_t total_blocks;
+  int32_t log2_block_size;
+  float scale_log2e;
+};
+
+bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
+                                int partition);
+hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
+                         int64_t num_items, hipStream_t stream);
+
+bool generic_supported(int dtype, int head_dim);
+hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStream_t stream);
+
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
+
+hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t stream);
+
+bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size);
+int prefill_tile_for(int group);
+hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
+                          int64_t num_items, hipStream_t stream);
+
+}  // namespace pa

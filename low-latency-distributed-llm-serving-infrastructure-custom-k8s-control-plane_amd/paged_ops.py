@@ -1,0 +1,520 @@
+"""Torch-facing wrappers of the HIP paged-attention kernels.
+
+Every function here takes device tensors, launches on the current HIP stream
+of that device (``torch.cuda.current_stream()``) and never synchronises.
+They fail loudly: a missing library, a CPU tensor or a shape the kernels
+reject raises instead of falling back to another implementation.
+
+The four jobs of the path:
+  (a) :func:`pack_step`          ragged-batch packing (cu_seqlens, slots, work lists)
+  (b) :func:`reshape_and_cache`  new K/V rows -> paged cache
+  (c) :func:`decode`             split-K paged decode
+  (d) :func:`prefill`            causal chunked prefill (MFMA)
+plus :func:`attention` (decode + prefill of one flattened step) and
+:func:`paged_attention_flat`, the reference C-ABI call over device tensors.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _native
+from ._native import PA_DECODE_PARTITION
+
+_DTYPES = {
+    torch.float32: _native.PA_DTYPE_F32,
+    torch.bfloat16: _native.PA_DTYPE_BF16,
+    torch.float16: _native.PA_DTYPE_F16,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError as exc:
+        raise ValueError(f"unsupported dtype for the HIP path: {dtype}") from exc
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"HIP paged-attention kernels need device tensors, got a tensor on {t.device}"
+            )
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError(f"tensors on different devices: {device} and {t.device}")
+    if device is None:
+        raise RuntimeError("no device tensor given")
+    return device
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def prefill_tile_for(num_query_heads: int, num_kv_heads: int) -> int:
+    """Query tokens per prefill work item (128 query rows per workgroup)."""
+    group = num_query_heads // num_kv_heads
+    return max(1, 128 // group) if group in (1, 2, 4, 8) else 128
+
+
+# ---------------------------------------------------------------------------
+# (a) packing
+
+
+@dataclass
+class PackedStep:
+    """Device-side description of one flattened ragged step (output of pa_pack).
+
+    Host-side counts are derived from the host lists the scheduler already
+    holds, so no device->host synchronisation is needed to size the grids.
+    """
+
+    block_tables: torch.Tensor  # int32 [B, max_blocks]
+    start_positions: torch.Tensor  # int64 [B]
+    new_token_counts: torch.Tensor  # int64 [B]
+    cu_seqlens: torch.Tensor  # int64 [B+1]
+    cu_context_offsets: torch.Tensor  # int64 [B+1]
+    context_lens: torch.Tensor  # int32 [B]
+    scatter_slots: torch.Tensor  # int64 [T]
+    position_ids: torch.Tensor  # int64 [T]
+    decode_items: torch.Tensor  # int32 [num_decode_items, 2]
+    prefill_items: torch.Tensor  # int32 [num_prefill_items, 2]
+    block_size: int
+    partition_size: int
+    prefill_tile: int
+    num_query_tokens: int
+    num_context_tokens: int
+    num_decode_items: int
+    num_prefill_items: int
+    num_decode_seqs: int
+    num_prefill_seqs: int
+    _gather_slots: Optional[torch.Tensor] = field(default=None, repr=False)
+    _workspace: Optional[torch.Tensor] = field(default=None, repr=False)
+
+    @property
+    def num_seqs(self) -> int:
+        return int(self.block_tables.shape[0])
+
+    @property
+    def gather_slots(self) -> torch.Tensor:
+        """int64 [C] slots of every context token (built on first use)."""
+        if self._gather_slots is None:
+            self._gather_slots = _run_pack(self, with_gather=True)
+        return self._gather_slots
+
+    def workspace(self, num_query_heads: int, head_dim: int, device: torch.device) -> torch.Tensor:
+        need = decode_workspace_bytes(self.num_decode_items, num_query_heads, head_dim)
+        ws = self._workspace
+        if ws is None or ws.numel() < need or ws.device != device:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+            self._workspace = ws
+        return ws
+
+
+def work_counts(
+    start_positions: Sequence[int],
+    new_token_counts: Sequence[int],
+    partition_size: int,
+    prefill_tile: int,
+):
+    """Host-side sizes of a step: (T, C, decode items, prefill items, #decode, #prefill)."""
+    t = c = ditems = pitems = ndec = npre = 0
+    for start, count in zip(start_positions, new_token_counts):
+        ctx = start + count
+        t += count
+        c += ctx
+        if count == 1:
+            ditems += -(-ctx // partition_size)
+            ndec += 1
+        elif count > 1:
+            pitems += -(-count // prefill_tile)
+            npre += 1
+    return t, c, ditems, pitems, ndec, npre
+
+
+def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Tensor]:
+    lib = _native.load_library()
+    device = _require_device(step.block_tables)
+    gather = None
+    if with_gather:
+        gather = torch.empty(step.num_context_tokens, dtype=torch.int64, device=device)
+    dims = _native.PaPackDims(
+        num_seqs=step.num_seqs,
+        block_size=step.block_size,
+        max_blocks_per_seq=int(step.block_tables.shape[1]) if step.block_tables.dim() == 2 else 0,
+        partition_size=step.partition_size,
+        prefill_tile=step.prefill_tile,
+        max_query_tokens=step.num_query_tokens,
+        max_context_tokens=step.num_context_tokens,
+        max_decode_items=step.num_decode_items,
+        max_prefill_items=step.num_prefill_items,
+    )
+    status = lib.pa_pack(
+        _ptr(step.block_tables),
+        _ptr(step.start_positions),
+        _ptr(step.new_token_counts),
+        dims,
+        _ptr(step.cu_seqlens),
+        _ptr(step.cu_context_offsets),
+        _ptr(step.context_lens),
+        _ptr(step.scatter_slots),
+        _ptr(step.position_ids),
+        _ptr(gather),
+        _ptr(step.decode_items),
+        _ptr(step.prefill_items),
+        _stream(device),
+    )
+    _native.check(status, "pa_pack")
+    return gather
+
+
+def pack_step(
+    block_tables: torch.Tensor,
+    start_positions: Sequence[int],
+    new_token_counts: Sequence[int],
+    block_size: int,
+    *,
+    prefill_tile: int = 32,
+    partition_size: int = PA_DECODE_PARTITION,
+    with_gather: bool = False,
+    start_positions_dev: Optional[torch.Tensor] = None,
+    new_token_counts_dev: Optional[torch.Tensor] = None,
+) -> PackedStep:
+    """Run the GPU packing kernel for one step.
+
+    ``block_tables``: int32 [B, max_blocks] device tensor (-1 padded).
+    ``start_positions`` / ``new_token_counts``: the host lists of the step
+    (also uploaded unless device copies are passed in).
+    """
+    device = _require_device(block_tables)
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
+        raise ValueError("block_tables must be an int32 [B, max_blocks] tensor")
+    if not block_tables.is_contiguous():
+        block_tables = block_tables.contiguous()
+    b = int(block_tables.shape[0])
+    if len(start_positions) != b or len(new_token_counts) != b:
+        raise ValueError("start_positions / new_token_counts must have one entry per block-table row")
+    if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
+        raise ValueError("start positions and token counts must be non-negative")
+    t, c, ditems, pitems, ndec, npre = work_counts(start_positions, new_token_counts, partition_size, prefill_tile)
+    if start_positions_dev is None:
+        start_positions_dev = torch.tensor(list(start_positions), dtype=torch.int64).to(device, non_blocking=True)
+    if new_token_counts_dev is None:
+        new_token_counts_dev = torch.tensor(list(new_token_counts), dtype=torch.int64).to(device, non_blocking=True)
+    step = PackedStep(
+        block_tables=block_tables,
+        start_positions=start_positions_dev,
+        new_token_counts=new_token_counts_dev,
+        cu_seqlens=torch.empty(b + 1, dtype=torch.int64, device=device),
+        cu_context_offsets=torch.empty(b + 1, dtype=torch.int64, device=device),
+        context_lens=torch.empty(b, dtype=torch.int32, device=device),
+        scatter_slots=torch.empty(t, dtype=torch.int64, device=device),
+        position_ids=torch.empty(t, dtype=torch.int64, device=device),
+        decode_items=torch.empty((ditems, 2), dtype=torch.int32, device=device),
+        prefill_items=torch.empty((pitems, 2), dtype=torch.int32, device=device),
+        block_size=int(block_size),
+        partition_size=int(partition_size),
+        prefill_tile=int(prefill_tile),
+        num_query_tokens=t,
+        num_context_tokens=c,
+        num_decode_items=ditems,
+        num_prefill_items=pitems,
+        num_decode_seqs=ndec,
+        num_prefill_seqs=npre,
+    )
+    step._gather_slots = _run_pack(step, with_gather=with_gather)
+    return step
+
+
+# ---------------------------------------------------------------------------
+# (b) cache write
+
+
+def reshape_and_cache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    layer_idx: int,
+) -> None:
+    """key_cache[layer].view(-1, H_kv, D)[slot_mapping] = key (and value), on the GPU.
+
+    ``key`` / ``value``: [T, H_kv, D] (any token / head strides, unit stride on D);
+    caches: (L, N, bs, H_kv, D) contiguous; ``slot_mapping``: int64 [T].
+    """
+    device = _require_device(key, value, key_cache, value_cache, slot_mapping)
+    if key_cache.dim() != 5 or value_cache.shape != key_cache.shape:
+        raise ValueError("caches must be 5-D (layers, blocks, block_size, heads, dim) and alike")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    num_layers, total_blocks, block_size, num_kv_heads, head_dim = key_cache.shape
+    if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (num_kv_heads, head_dim):
+        raise ValueError(f"Expected keys shape (T, {num_kv_heads}, {head_dim}), got {tuple(key.shape)}")
+    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype:
+        raise ValueError("key/value dtype must match the cache dtype")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != key.shape[0]:
+        raise ValueError("slot_mapping must be int64 with one entry per token")
+    if key.stride(2) != 1:
+        key = key.contiguous()
+    if value.stride(2) != 1:
+        value = value.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    lib = _native.load_library()
+    status = lib.pa_reshape_and_cache(
+        key.data_ptr(),
+        value.data_ptr(),
+        key.stride(0),
+        key.stride(1),
+        value.stride(0),
+        value.stride(1),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        slot_mapping.data_ptr(),
+        int(key.shape[0]),
+        num_kv_heads,
+        head_dim,
+        block_size,
+        total_blocks,
+        num_layers,
+        int(layer_idx),
+        dtype_code(key_cache.dtype),
+        _stream(device),
+    )
+    _native.check(status, "pa_reshape_and_cache")
+
+
+# ---------------------------------------------------------------------------
+# (c)/(d) attention
+
+
+def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
+    if num_decode_items <= 0:
+        return 0
+    rows = num_decode_items * num_query_heads
+    acc = (rows * head_dim * 4 + 255) & ~255
+    ml = (rows * 2 * 4 + 255) & ~255
+    return acc + ml
+
+
+def _step_dims(query_t: torch.Tensor, key_cache: torch.Tensor, step: PackedStep) -> _native.PaStepDims:
+    """query_t is the [T, H_q, D] view of the query."""
+    num_layers, total_blocks, block_size, num_kv_heads, head_dim = key_cache.shape
+    return _native.PaStepDims(
+        num_seqs=step.num_seqs,
+        num_query_tokens=int(query_t.shape[0]),
+        num_query_heads=int(query_t.shape[1]),
+        num_kv_heads=int(num_kv_heads),
+        head_dim=int(head_dim),
+        block_size=int(block_size),
+        total_blocks=int(total_blocks),
+        num_layers=int(num_layers),
+        max_blocks_per_seq=int(step.block_tables.shape[1]),
+        partition_size=step.partition_size,
+        dtype=dtype_code(key_cache.dtype),
+        q_token_stride=query_t.stride(0),
+        q_head_stride=query_t.stride(1),
+    )
+
+
+def _query_view(query: torch.Tensor) -> torch.Tensor:
+    """Accept [1, H_q, T, D] (reference layout) or [T, H_q, D]; return a [T, H_q, D] view."""
+    if query.dim() == 4:
+        if query.shape[0] != 1:
+            raise ValueError("query must be (1, heads, tokens, dim)")
+        q = query[0].transpose(0, 1)
+    elif query.dim() == 3:
+        q = query
+    else:
+        raise ValueError("query must be (1, H_q, T, D) or (T, H_q, D)")
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    return q
+
+
+def _check_attention_inputs(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, step: PackedStep):
+    if key_cache.dim() != 5 or value_cache.shape != key_cache.shape:
+        raise ValueError("caches must be 5-D (layers, blocks, block_size, heads, dim) and alike")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if q.dtype != key_cache.dtype:
+        raise ValueError(f"query dtype {q.dtype} differs from cache dtype {key_cache.dtype}")
+    num_kv_heads, head_dim = key_cache.shape[3], key_cache.shape[4]
+    if q.shape[2] != head_dim:
+        raise ValueError("query head_dim differs from the cache head_dim")
+    if q.shape[1] % num_kv_heads != 0:
+        raise RuntimeError("num_query_heads must be a multiple of num_kv_heads for GQA")
+    if q.shape[0] != step.num_query_tokens:
+        raise ValueError(f"query has {q.shape[0]} tokens, the step has {step.num_query_tokens}")
+
+
+def decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer_idx: int,
+    step: PackedStep,
+    scaling: float,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Split-K paged decode for the single-token sequences of ``step``.
+
+    Returns (or fills) ``out`` [T, H_q, D]; rows of other tokens are untouched.
+    """
+    q = _query_view(query)
+    device = _require_device(q, key_cache, value_cache, step.block_tables)
+    _check_attention_inputs(q, key_cache, value_cache, step)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    dims = _step_dims(q, key_cache, step)
+    ws = step.workspace(int(q.shape[1]), int(q.shape[2]), device)
+    lib = _native.load_library()
+    status = lib.pa_decode(
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        step.block_tables.data_ptr(),
+        step.context_lens.data_ptr(),
+        step.cu_seqlens.data_ptr(),
+        _ptr(step.decode_items),
+        step.num_decode_items,
+        float(scaling),
+        out.data_ptr(),
+        ws.data_ptr(),
+        ws.numel(),
+        _stream(device),
+    )
+    _native.check(status, "pa_decode")
+    return out
+
+
+def prefill(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer_idx: int,
+    step: PackedStep,
+    scaling: float,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal chunked prefill for the multi-token sequences of ``step``."""
+    q = _query_view(query)
+    device = _require_device(q, key_cache, value_cache, step.block_tables)
+    _check_attention_inputs(q, key_cache, value_cache, step)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    dims = _step_dims(q, key_cache, step)
+    lib = _native.load_library()
+    status = lib.pa_prefill(
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        step.block_tables.data_ptr(),
+        step.context_lens.data_ptr(),
+        step.cu_seqlens.data_ptr(),
+        _ptr(step.prefill_items),
+        step.num_prefill_items,
+        step.prefill_tile,
+        float(scaling),
+        out.data_ptr(),
+        _stream(device),
+    )
+    _native.check(status, "pa_prefill")
+    return out
+
+
+def attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer_idx: int,
+    step: PackedStep,
+    scaling: float,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D]."""
+    q = _query_view(query)
+    device = _require_device(q)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    if step.num_prefill_items > 0:
+        prefill(q, key_cache, value_cache, layer_idx, step, scaling, out=out)
+    if step.num_decode_items > 0:
+        decode(q, key_cache, value_cache, layer_idx, step, scaling, out=out)
+    if step.num_query_tokens > 0 and step.num_decode_items == 0 and step.num_prefill_items == 0:
+        out.zero_()
+    return out
+
+
+def paged_attention_flat(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    layer_idx: int,
+    gather_slots: torch.Tensor,
+    attention_mask: torch.Tensor,
+    scaling: float,
+) -> torch.Tensor:
+    """The reference's ``llm_allocator_cpp.paged_attention`` (csrc/src/bindings.cpp:10-76)
+    over device tensors: fp32, query [1, H_q, T, D], caches (L, N, bs, H_kv, D),
+    gather_slots int32 [C], mask uint8 [1, 1, T, C]; returns [1, T, H_q, D]."""
+    device = _require_device(query, key_cache, value_cache, gather_slots, attention_mask)
+    if query.dim() != 4:
+        raise RuntimeError("query must be 4-D (1, heads, seq, dim)")
+    if key_cache.dim() != 5:
+        raise RuntimeError("key_cache must be 5-D (layers, blocks, block_size, heads, dim)")
+    if gather_slots.dim() != 1:
+        raise RuntimeError("gather_slots must be 1-D")
+    if attention_mask.dim() != 4:
+        raise RuntimeError("attention_mask must be 4-D (1, 1, query, context)")
+    query = query.to(torch.float32).contiguous()
+    key_cache = key_cache.to(torch.float32).contiguous()
+    value_cache = value_cache.to(torch.float32).contiguous()
+    gather_slots = gather_slots.to(torch.int32).contiguous()
+    attention_mask = attention_mask.to(torch.uint8).contiguous()
+    dims = _native.PagedAttentionDims(
+        num_query_heads=int(query.shape[1]),
+        num_query_tokens=int(query.shape[2]),
+        head_dim=int(query.shape[3]),
+        num_layers=int(key_cache.shape[0]),
+        total_blocks=int(key_cache.shape[1]),
+        block_size=int(key_cache.shape[2]),
+        num_kv_heads=int(key_cache.shape[3]),
+        num_context_tokens=int(gather_slots.shape[0]),
+    )
+    out = torch.empty((1, dims.num_query_tokens, dims.num_query_heads, dims.head_dim), dtype=torch.float32, device=device)
+    lib = _native.load_library()
+    lib.paged_attention(
+        query.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        gather_slots.data_ptr(),
+        attention_mask.data_ptr(),
+        float(scaling),
+        out.data_ptr(),
+        None,
+        _stream(device),
+    )
+    status = lib.pa_last_error()
+    if status != _native.PA_OK:
+        raise RuntimeError(lib.pa_last_error_message().decode(errors="replace"))
+    return out

@@ -1,0 +1,98 @@
+"""The C-ABI library loads and exports every entry point the header declares.
+
+No kernel is launched here (no GPU needed): only symbol presence, the ABI
+version and argument checks that return before any HIP call."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from helpers import pkg
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "paged_attention_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "while", "sizeof")))
+
+
+def test_header_declarations_match_binding_table():
+    native = pkg("_native")
+    assert declared_functions() == sorted(native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    native = pkg("_native")
+    lib = native.load_library()
+    raw = ctypes.CDLL(str(native.LIBRARY_PATH))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+    assert lib.pa_abi_version() == native.ABI_VERSION
+
+
+def test_struct_layouts():
+    native = pkg("_native")
+    assert ctypes.sizeof(native.PagedAttentionDims) == 32
+    assert ctypes.sizeof(native.PaStepDims) == 12 * 4 + 2 * 8
+    assert ctypes.sizeof(native.PaPackDims) == 6 * 4 + 4 * 8
+
+
+def test_error_strings():
+    lib = pkg("_native").load_library()
+    assert lib.pa_error_string(0) == b"ok"
+    assert lib.pa_error_string(3) == b"workspace missing or too small"
+
+
+def test_invalid_arguments_rejected_before_launch():
+    native = pkg("_native")
+    lib = native.load_library()
+    dims = native.PaStepDims(num_seqs=1, num_query_tokens=1, num_query_heads=6, num_kv_heads=4, head_dim=64,
+                             block_size=16, total_blocks=8, num_layers=1, max_blocks_per_seq=1,
+                             partition_size=512, dtype=native.PA_DTYPE_BF16, q_token_stride=384, q_head_stride=64)
+    rc = lib.pa_decode(None, None, None, 0, dims, None, None, None, None, 1, 1.0, None, None, 0, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    assert b"multiple of num_kv_heads" in lib.pa_last_error_message()
+    dims.num_query_heads = 8
+    rc = lib.pa_prefill(None, None, None, 3, dims, None, None, None, None, 1, 32, 1.0, None, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    assert b"Layer index 3 out of range" in lib.pa_last_error_message()
+    rc = lib.pa_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 2, 8, 4, 4, 1, 0, 7, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
+    rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+
+
+def test_reference_abi_latches_errors():
+    native = pkg("_native")
+    lib = native.load_library()
+    dims = native.PagedAttentionDims(num_query_heads=3, num_query_tokens=1, head_dim=8, num_layers=1,
+                                     total_blocks=1, block_size=4, num_kv_heads=2, num_context_tokens=1)
+    lib.paged_attention(None, None, None, 0, dims, None, None, 1.0, None, None, None)
+    assert lib.pa_last_error() == native.PA_ERR_INVALID_ARGUMENT
+    dims.num_query_heads = 4
+    lib.paged_attention(None, None, None, 1, dims, None, None, 1.0, None, None, None)
+    assert lib.pa_last_error() == native.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_last_error_message() == b"layer_idx out of range"
+
+
+def test_workspace_size():
+    native = pkg("_native")
+    lib = native.load_library()
+    ops = pkg("paged_ops")
+    dims = native.PaStepDims(num_query_heads=32, head_dim=128)
+    assert lib.pa_decode_workspace_size(dims, 925) == ops.decode_workspace_bytes(925, 32, 128)
+    assert lib.pa_decode_workspace_size(dims, 0) == 0
+
+
+def test_product_path_fails_loudly_without_library(monkeypatch, tmp_path):
+    native = pkg("_native")
+    monkeypatch.setattr(native, "LIBRARY_PATH", tmp_path / "missing.so")
+    monkeypatch.setattr(native, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        native.load_library()

@@ -1,0 +1,357 @@
+"""GPU parity of the HIP path against the oracle and the reference's golden vectors.
+
+Integer work (packing, cache write) must be bit-exact.  Attention: fp32
+max-abs-err <= 1e-4 against the reference kernel; bf16 inputs against the
+reference kernel run on exact fp32 up-casts of the same values, with
+max|g - r| / max|r| <= 2e-2 and |g - r| <= 2e-2 |r| + 2e-2 rms(r)
+elementwise (helpers.bf16_close).  Full-size workloads are checked on a
+subset of sequences (the oracle runs per sequence on the CPU) plus
+size-independent properties on the whole batch.
+"""
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_close, load_golden, pkg, sha256
+from oracle import attention as oa
+from oracle import packing as op
+
+sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+import make_golden  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+ops = pkg("paged_ops")
+wl = pkg("workloads")
+
+FP32_TOL = 1e-4
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# helpers
+
+
+def pack_workload(w, device, prefill_tile=None, with_gather=False):
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    tile = prefill_tile or ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
+    return ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         prefill_tile=tile, with_gather=with_gather)
+
+
+def oracle_rows(w, t, seqs):
+    """Oracle output rows ([n_i, H_q, D] fp32 per sequence) for `seqs`, on
+    fp32 copies of exactly the values the GPU read."""
+    cu = op.cumulative_offsets(w.new_token_counts)
+    q_all = t.query[0].transpose(0, 1)  # [T, H_q, D]
+    out = {}
+    for i in seqs:
+        blocks = torch.tensor(w.block_lists[i], dtype=torch.long, device=t.key_cache.device)
+        k = t.key_cache[:, blocks].float().cpu().numpy()  # [1, nb, bs, H_kv, D]
+        v = t.value_cache[:, blocks].float().cpu().numpy()
+        nb = len(w.block_lists[i])
+        ctx = w.context_lens[i]
+        slots = np.arange(nb * w.block_size, dtype=np.int64)[:ctx]
+        q = q_all[cu[i] : cu[i + 1]].float().cpu().numpy().transpose(1, 0, 2)  # [H_q, n, D]
+        o, _ = oa.paged_attention_per_sequence(q, k, v, 0, [w.start_positions[i]], [w.new_token_counts[i]],
+                                               slots, w.scaling)
+        out[i] = o
+    return out
+
+
+def check_rows(w, got, ref_rows, fp32):
+    cu = op.cumulative_offsets(w.new_token_counts)
+    g = got.float().cpu().numpy()
+    for i, ref in ref_rows.items():
+        rows = g[cu[i] : cu[i + 1]]
+        if fp32:
+            err = np.max(np.abs(rows - ref))
+            assert err <= FP32_TOL, f"seq {i}: max abs err {err}"
+        else:
+            ok, worst = bf16_close(rows, ref)
+            assert ok, f"seq {i}: bf16 relative error {worst}"
+
+
+def golden_case(name):
+    g = load_golden(name)
+    if "query" not in g:
+        case = make_golden.fp32_mha_decode_case(0)
+        assert sha256(case["query"], case["key_cache"], case["value_cache"]) == str(g["input_sha256"])
+        g.update({k: case[k] for k in ("query", "key_cache", "value_cache", "gather_slots", "mask")})
+    return g
+
+
+# ---------------------------------------------------------------------------
+# (a) packing
+
+
+def _pack_expect(starts, counts, lists, bs, partition, tile):
+    ctx = [s + c for s, c in zip(starts, counts)]
+    dec, pre = op.work_items(starts, counts, partition, tile)
+    return dict(
+        cu_seqlens=op.cumulative_offsets(counts),
+        cu_context_offsets=op.cumulative_offsets(ctx),
+        context_lens=np.asarray(ctx, dtype=np.int32),
+        scatter_slots=op.build_slot_mapping(lists, ctx, bs, starts, counts),
+        position_ids=op.position_ids(starts, counts)[0],
+        gather_slots=op.build_slot_mapping(lists, ctx, bs, [0] * len(ctx), ctx),
+        decode_items=dec,
+        prefill_items=pre,
+    )
+
+
+def _check_pack(step, exp):
+    for name in ("cu_seqlens", "cu_context_offsets", "context_lens", "scatter_slots", "position_ids",
+                 "decode_items", "prefill_items"):
+        got = getattr(step, name).cpu().numpy()
+        assert got.dtype == exp[name].dtype, name
+        assert np.array_equal(got.reshape(exp[name].shape), exp[name]), name
+    g = step.gather_slots.cpu().numpy()
+    assert g.dtype == np.int64 and np.array_equal(g, exp["gather_slots"])
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 5])
+def test_pack_matches_oracle_on_workloads(device, cfg):
+    w = wl.CONFIGS[cfg](seed=cfg)
+    log(f"pack cfg{cfg}: B={w.num_seqs} T={w.num_query_tokens} C={w.num_context_tokens}")
+    tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
+    step = pack_workload(w, device, with_gather=True)
+    exp = _pack_expect(w.start_positions, w.new_token_counts, w.block_lists, w.block_size, 512, tile)
+    _check_pack(step, exp)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_pack_matches_oracle_on_ragged_edges(device, seed):
+    rng = np.random.default_rng(seed)
+    bs = int(rng.choice([1, 4, 16, 32]))
+    b = int(rng.integers(1, 40))
+    starts = [int(x) for x in rng.integers(0, 700, size=b)]
+    counts = [int(rng.choice([0, 1, 1, 2, int(rng.integers(3, 90))])) for _ in range(b)]
+    lists, off = [], 0
+    perm = rng.permutation(100000)
+    for s, c in zip(starts, counts):
+        n = -(-(s + c) // bs)
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    table = torch.from_numpy(op.build_block_tables(lists, [s + c for s, c in zip(starts, counts)])[0]).to(device)
+    step = ops.pack_step(table, starts, counts, bs, prefill_tile=16, with_gather=True)
+    _check_pack(step, _pack_expect(starts, counts, lists, bs, 512, 16))
+
+
+def test_pack_empty_batch(device):
+    table = torch.empty((0, 1), dtype=torch.int32, device=device)
+    step = ops.pack_step(table, [], [], 16, with_gather=True)
+    assert step.cu_seqlens.cpu().tolist() == [0]
+    assert step.cu_context_offsets.cpu().tolist() == [0]
+    assert step.scatter_slots.numel() == 0 and step.gather_slots.numel() == 0
+
+
+# ---------------------------------------------------------------------------
+# (b) cache write
+
+
+def test_reshape_and_cache_bit_exact_kv_write_pack(device):
+    w = wl.kv_write_pack(seed=2)
+    t = wl.make_tensors(w, device, seed=7)
+    step = pack_workload(w, device)
+    before_k = t.key_cache.view(torch.int16).cpu().numpy().view(np.uint16).copy()
+    before_v = t.value_cache.view(torch.int16).cpu().numpy().view(np.uint16).copy()
+    # the model's projections arrive as [1, H_kv, T, D]; the hook passes a
+    # transposed [T, H_kv, D] view
+    k_hf = t.new_keys.transpose(0, 1).contiguous().unsqueeze(0)
+    v_hf = t.new_values.transpose(0, 1).contiguous().unsqueeze(0)
+    ops.reshape_and_cache(k_hf[0].transpose(0, 1), v_hf[0].transpose(0, 1), t.key_cache, t.value_cache,
+                          step.scatter_slots, 0)
+    torch.cuda.synchronize()
+    slots = op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size, w.start_positions,
+                                  w.new_token_counts)
+    op.scatter_layer_kv(before_k, 0, t.new_keys.view(torch.int16).cpu().numpy().view(np.uint16), slots)
+    op.scatter_layer_kv(before_v, 0, t.new_values.view(torch.int16).cpu().numpy().view(np.uint16), slots)
+    assert np.array_equal(t.key_cache.view(torch.int16).cpu().numpy().view(np.uint16), before_k)
+    assert np.array_equal(t.value_cache.view(torch.int16).cpu().numpy().view(np.uint16), before_v)
+
+
+@pytest.mark.parametrize("dtype,head_dim", [(torch.float32, 6), (torch.float32, 8), (torch.bfloat16, 12)])
+def test_reshape_and_cache_bit_exact_odd_shapes(device, dtype, head_dim):
+    gen = torch.Generator(device=device)
+    gen.manual_seed(3)
+    L, N, bs, H = 3, 5, 4, 2
+    kc = torch.randn((L, N, bs, H, head_dim), generator=gen, device=device).to(dtype)
+    vc = torch.randn((L, N, bs, H, head_dim), generator=gen, device=device).to(dtype)
+    keys = torch.randn((7, H, head_dim), generator=gen, device=device).to(dtype)
+    vals = torch.randn((7, H, head_dim), generator=gen, device=device).to(dtype)
+    slots = torch.tensor([0, 5, 19, 3, 8, -1, 100], dtype=torch.int64, device=device)  # last two skipped
+    ek, ev = kc.clone(), vc.clone()
+    ek[1].view(-1, H, head_dim)[slots[:5]] = keys[:5]
+    ev[1].view(-1, H, head_dim)[slots[:5]] = vals[:5]
+    ops.reshape_and_cache(keys, vals, kc, vc, slots, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.uint8), ek.view(torch.uint8))
+    assert torch.equal(vc.view(torch.uint8), ev.view(torch.uint8))
+
+
+# ---------------------------------------------------------------------------
+# reference ABI and golden vectors
+
+
+@pytest.mark.parametrize("name", ["fp32_mha_decode", "gqa_prefill", "gqa_decode", "mixed_small", "masked_rows",
+                                  "empty_context"])
+def test_reference_abi_matches_golden(device, name):
+    g = golden_case(name)
+    log(f"reference ABI on {name}")
+    out = ops.paged_attention_flat(
+        torch.from_numpy(g["query"]).to(device), torch.from_numpy(g["key_cache"]).to(device),
+        torch.from_numpy(g["value_cache"]).to(device), 0,
+        torch.from_numpy(g["gather_slots"].astype(np.int32)).to(device),
+        torch.from_numpy(g["mask"].astype(np.uint8)).to(device), float(g["scale"]))
+    err = np.max(np.abs(out.cpu().numpy() - g["expected"]), initial=0.0)
+    assert err <= FP32_TOL, err
+
+
+@pytest.mark.parametrize("name", ["fp32_mha_decode", "gqa_prefill", "gqa_decode", "mixed_small"])
+def test_block_table_path_matches_golden(device, name):
+    g = golden_case(name)
+    starts, counts = [int(x) for x in g["starts"]], [int(x) for x in g["counts"]]
+    table = torch.from_numpy(g["block_table"]).to(device)
+    hq, hkv = int(g["hq"]), int(g["hkv"])
+    step = ops.pack_step(table, starts, counts, int(g["bs"]), prefill_tile=ops.prefill_tile_for(hq, hkv))
+    q = torch.from_numpy(g["query"]).to(device)
+    out = ops.attention(q, torch.from_numpy(g["key_cache"]).to(device),
+                        torch.from_numpy(g["value_cache"]).to(device), 0, step, float(g["scale"]))
+    err = np.max(np.abs(out.cpu().numpy() - g["expected"][0]))
+    assert err <= FP32_TOL, err
+
+
+# ---------------------------------------------------------------------------
+# (c) decode at full size
+
+
+@pytest.mark.parametrize("cfg,subset", [(3, [0, 1, 17, 33, 63]), (4, [0, 5, 100, 200, 255])])
+def test_decode_bf16_full_size(device, cfg, subset):
+    w = wl.CONFIGS[cfg](seed=cfg)
+    longest = int(np.argmax(w.context_lens))
+    shortest = int(np.argmin(w.context_lens))
+    seqs = sorted(set(subset + [longest, shortest]))
+    log(f"decode cfg{cfg}: B={w.num_seqs} C={w.num_context_tokens} checking seqs {seqs}")
+    t = wl.make_tensors(w, device, seed=cfg)
+    step = pack_workload(w, device)
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    check_rows(w, out, oracle_rows(w, t, seqs), fp32=False)
+
+
+def test_decode_fp32_matches_oracle(device):
+    w = wl.fp32_mha_decode(seed=11)
+    t = wl.make_tensors(w, device, seed=11)
+    step = pack_workload(w, device)
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=True)
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (16, 16, 64, torch.bfloat16),
+                                            (16, 2, 64, torch.float32), (8, 4, 128, torch.float32),
+                                            (12, 4, 32, torch.bfloat16)])
+def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
+    rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
+    ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
+    need = [-(-c // 16) for c in ctx]
+    perm = rng.permutation(sum(need))
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    w = wl.StepWorkload("decode_edges", hq, hkv, d, 16, dtype, 1.0, [c - 1 for c in ctx], [1] * len(ctx),
+                        lists, sum(need))
+    t = wl.make_tensors(w, device, seed=5)
+    step = pack_workload(w, device)
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=dtype == torch.float32)
+
+
+def test_decode_properties_full_size(device):
+    """Size-independent properties on the whole GQA batch: the output depends
+    only on logical context (moving blocks + table gives identical bits) and
+    not on the other sequences of the batch."""
+    w = wl.llama3_8b_gqa_decode(seed=4)
+    t = wl.make_tensors(w, device, seed=4)
+    step = pack_workload(w, device)
+    base = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    # relocate every block through a permutation of the pool
+    gen = torch.Generator()
+    gen.manual_seed(1)
+    perm = torch.randperm(w.total_blocks, generator=gen)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(w.total_blocks)
+    kc = torch.empty_like(t.key_cache)
+    vc = torch.empty_like(t.value_cache)
+    kc[:, perm.to(device)] = t.key_cache
+    vc[:, perm.to(device)] = t.value_cache
+    lists = [[int(perm[b]) for b in blocks] for blocks in w.block_lists]
+    w2 = wl.StepWorkload(w.name, w.num_query_heads, w.num_kv_heads, w.head_dim, w.block_size, w.dtype, 1.0,
+                         w.start_positions, w.new_token_counts, lists, w.total_blocks)
+    moved = ops.decode(t.query, kc, vc, 0, pack_workload(w2, device), w.scaling)
+    assert torch.equal(base.view(torch.int16), moved.view(torch.int16))
+    # batch independence: sequences 10..19 alone
+    sub = list(range(10, 20))
+    w3 = wl.StepWorkload(w.name, w.num_query_heads, w.num_kv_heads, w.head_dim, w.block_size, w.dtype, 1.0,
+                         [w.start_positions[i] for i in sub], [1] * len(sub), [w.block_lists[i] for i in sub],
+                         w.total_blocks)
+    q_sub = t.query[:, :, 10:20]
+    alone = ops.decode(q_sub, t.key_cache, t.value_cache, 0, pack_workload(w3, device), w.scaling)
+    assert torch.equal(alone.view(torch.int16), base[10:20].view(torch.int16))
+
+
+# ---------------------------------------------------------------------------
+# (d) prefill
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 2, 64), (8, 1, 64)])
+def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
+    starts = [0, 0, 37, 512, 100]
+    counts = [1, 200, 64, 300, 7]
+    rng = np.random.Generator(np.random.PCG64(hq + d))
+    ctx = [s + c for s, c in zip(starts, counts)]
+    need = [-(-c // 16) for c in ctx]
+    perm = rng.permutation(sum(need) + 3)
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    w = wl.StepWorkload("prefill_edges", hq, hkv, d, 16, torch.bfloat16, 1.0, starts, counts, lists, sum(need) + 3)
+    t = wl.make_tensors(w, device, seed=9)
+    step = pack_workload(w, device)
+    log(f"prefill hq={hq} hkv={hkv} d={d} items={step.num_prefill_items} tile={step.prefill_tile}")
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
+
+
+# ---------------------------------------------------------------------------
+# mixed continuous-batching step
+
+
+def test_mixed_step_end_to_end(device):
+    """4 x 512-token prefill chunks + 128 long-context decodes: pack, write the
+    step's K/V, attend -- all on the GPU -- then check the cache bytes and a
+    subset of rows against the oracle."""
+    w = wl.mixed_step(seed=5)
+    t = wl.make_tensors(w, device, seed=5)
+    step = pack_workload(w, device)
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    slots = torch.from_numpy(op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size,
+                                                   w.start_positions, w.new_token_counts)).to(device)
+    got_k = t.key_cache[0].view(-1, w.num_kv_heads, w.head_dim)[slots]
+    assert torch.equal(got_k.view(torch.int16), t.new_keys.view(torch.int16))
+    seqs = [0, 3, 4, 50, 131]
+    log(f"mixed step: checking rows of seqs {seqs}")
+    check_rows(w, out, oracle_rows(w, t, seqs), fp32=False)
