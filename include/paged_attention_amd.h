@@ -118,6 +118,7 @@ typedef struct {
     int64_t max_query_tokens;   /* capacity of scatter_slots / position_ids */
     int64_t max_context_tokens; /* capacity of gather_slots                 */
     int64_t max_decode_items;   /* capacity of decode_items (pairs)         */
+    int64_t max_merge_items;    /* capacity of merge_items                  */
     int64_t max_prefill_items;  /* capacity of prefill_items (pairs)        */
 } PaPackDims;
 
@@ -135,6 +136,9 @@ typedef struct {
  *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
  *   decode_items int32 pairs (seq, partition) for every sequence with one
  *   new token, ordered by sequence then partition (may be NULL),
+ *   merge_items int32: index in decode_items of the first item of every
+ *   single-token sequence whose context spans more than one partition,
+ *   ordered by sequence (may be NULL),
  *   prefill_items int32 pairs (seq, query tile) for every sequence with more
  *   than one new token (may be NULL).
  * Writes past a capacity in PaPackDims are dropped, never performed.
@@ -145,7 +149,8 @@ int pa_pack(const int32_t *block_tables, const int64_t *start_positions,
             int64_t *cu_seqlens, int64_t *cu_context_offsets,
             int32_t *context_lens, int64_t *scatter_slots,
             int64_t *position_ids, int64_t *gather_slots,
-            int32_t *decode_items, int32_t *prefill_items, void *stream);
+            int32_t *decode_items, int32_t *merge_items,
+            int32_t *prefill_items, void *stream);
 
 /* ---- (b) K/V cache write ------------------------------------------------ */
 
@@ -171,7 +176,8 @@ int pa_reshape_and_cache(const void *key, const void *value,
 
 /* ---- (c) paged-attention decode (split-K) ------------------------------ */
 
-/* Bytes of workspace pa_decode needs for `num_decode_items` work items. */
+/* Bytes of workspace pa_decode needs for `num_decode_items` work items (the
+ * split-K partials).  Calls that share a workspace must not overlap in time. */
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
 
 /*
@@ -179,7 +185,9 @@ size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
  * (app/model/attention_backends.py:88-117) and the paged_attention kernel
  * it calls, over block tables instead of a dense mask.
  * Runs every (sequence, partition) item of `decode_items` (from pa_pack) for
- * every KV head, then merges the split-K partials.  The single query token
+ * every KV head, then a merge kernel over `merge_items` (from pa_pack)
+ * combines the split-K partials of the multi-partition sequences;
+ * merge_items may be NULL only when num_merge_items is 0.  The single query token
  * of decode sequence i is flat token cu_seqlens[i]; it attends positions
  * [0, context_lens[i]).  query: [T, H_q, D] through PaStepDims strides;
  * output: [T, H_q, D] contiguous, dtype of the caches; rows of tokens that
@@ -189,7 +197,8 @@ int pa_decode(const void *query, const void *key_cache,
               const void *value_cache, int32_t layer_idx, PaStepDims dims,
               const int32_t *block_tables, const int32_t *context_lens,
               const int64_t *cu_seqlens, const int32_t *decode_items,
-              int64_t num_decode_items, float scaling, void *output,
+              int64_t num_decode_items, const int32_t *merge_items,
+              int64_t num_merge_items, float scaling, void *output,
               void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- (d) causal chunked prefill ----------------------------------------- */

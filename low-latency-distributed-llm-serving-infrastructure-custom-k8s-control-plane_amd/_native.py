@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -88,6 +88,7 @@ class PaPackDims(ctypes.Structure):
         ("max_query_tokens", ctypes.c_int64),
         ("max_context_tokens", ctypes.c_int64),
         ("max_decode_items", ctypes.c_int64),
+        ("max_merge_items", ctypes.c_int64),
         ("max_prefill_items", ctypes.c_int64),
     ]
 
@@ -101,7 +102,7 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "paged_attention": (None, [_vp, _vp, _vp, _i32, PagedAttentionDims, _vp, _vp, _f32, _vp, _vp, _vp]),
     "pa_last_error": (ctypes.c_int, []),
-    "pa_pack": (ctypes.c_int, [_vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pa_pack": (ctypes.c_int, [_vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pa_reshape_and_cache": (
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
@@ -109,7 +110,7 @@ _SIGNATURES = {
     "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
     "pa_decode": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
+        [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
     ),
     "pa_prefill": (
         ctypes.c_int,

@@ -69,7 +69,7 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 extern "C" {
 
-int pa_abi_version(void) { return 1; }
+int pa_abi_version(void) { return 2; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -138,7 +138,7 @@ int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
             const int64_t* new_token_counts, PaPackDims dims, int64_t* cu_seqlens,
             int64_t* cu_context_offsets, int32_t* context_lens, int64_t* scatter_slots,
             int64_t* position_ids, int64_t* gather_slots, int32_t* decode_items,
-            int32_t* prefill_items, void* stream) {
+            int32_t* merge_items, int32_t* prefill_items, void* stream) {
   if (dims.num_seqs < 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative num_seqs");
   if (dims.block_size <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: block_size must be positive");
   if (dims.max_blocks_per_seq < 0)
@@ -163,6 +163,7 @@ int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
   a.position_ids = position_ids;
   a.gather_slots = gather_slots;
   a.decode_items = decode_items;
+  a.merge_items = merge_items;
   a.prefill_items = prefill_items;
   a.num_seqs = dims.num_seqs;
   a.block_size = dims.block_size;
@@ -172,6 +173,7 @@ int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
   a.max_query_tokens = dims.max_query_tokens;
   a.max_context_tokens = gather_slots ? dims.max_context_tokens : 0;
   a.max_decode_items = decode_items ? dims.max_decode_items : 0;
+  a.max_merge_items = merge_items ? dims.max_merge_items : 0;
   a.max_prefill_items = prefill_items ? dims.max_prefill_items : 0;
   return from_hip(pa::launch_pack(a, static_cast<hipStream_t>(stream)), "pa_pack");
 }
@@ -211,20 +213,32 @@ int pa_reshape_and_cache(const void* key, const void* value, int64_t key_token_s
                   "pa_reshape_and_cache");
 }
 
+namespace {
+struct DecodeWorkspaceLayout {
+  size_t acc, ml, total;
+};
+// part_acc [items, H_q, D] fp32 | part_ml [items, H_q, 2] fp32, each
+// rounded up to 256 bytes.
+DecodeWorkspaceLayout decode_workspace_layout(const PaStepDims& dims, int64_t items) {
+  DecodeWorkspaceLayout w{0, 0, 0};
+  if (items <= 0 || dims.num_query_heads <= 0 || dims.head_dim <= 0) return w;
+  const size_t rows = static_cast<size_t>(items) * dims.num_query_heads;
+  w.acc = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
+  w.ml = (rows * 2 * sizeof(float) + 255) & ~size_t(255);
+  w.total = w.acc + w.ml;
+  return w;
+}
+}  // namespace
+
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items) {
-  if (num_decode_items <= 0 || dims.num_query_heads <= 0 || dims.head_dim <= 0) return 0;
-  // part_acc [items, H_q, D] fp32 followed by part_ml [items, H_q, 2] fp32,
-  // each rounded up to 256 bytes.
-  const size_t rows = static_cast<size_t>(num_decode_items) * dims.num_query_heads;
-  const size_t acc = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
-  const size_t ml = (rows * 2 * sizeof(float) + 255) & ~size_t(255);
-  return acc + ml;
+  return decode_workspace_layout(dims, num_decode_items).total;
 }
 
 int pa_decode(const void* query, const void* key_cache, const void* value_cache,
               int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
               const int32_t* context_lens, const int64_t* cu_seqlens,
-              const int32_t* decode_items, int64_t num_decode_items, float scaling,
+              const int32_t* decode_items, int64_t num_decode_items,
+              const int32_t* merge_items, int64_t num_merge_items, float scaling,
               void* output, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_step(dims, "pa_decode");
   if (rc != PA_OK) return rc;
@@ -234,6 +248,8 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
   if (num_decode_items <= 0 || dims.num_seqs == 0) return PA_OK;
   if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
+  if (num_merge_items < 0 || (num_merge_items > 0 && merge_items == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items is required when num_merge_items > 0");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = dims.num_query_heads / dims.num_kv_heads;
   const int eb = elem_bytes(dims.dtype);
@@ -248,8 +264,7 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
     if (workspace == nullptr || workspace_bytes < need)
       return fail(PA_ERR_WORKSPACE, "pa_decode: workspace of %zu bytes needed, %zu given", need,
                   workspace_bytes);
-    const size_t rows = static_cast<size_t>(num_decode_items) * dims.num_query_heads;
-    const size_t acc_bytes = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
+    const DecodeWorkspaceLayout wl = decode_workspace_layout(dims, num_decode_items);
     pa::DecodeArgs a{};
     a.query = query;
     a.q_token_stride = dims.q_token_stride;
@@ -263,7 +278,9 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
     a.num_items = num_decode_items;
     a.output = output;
     a.part_acc = reinterpret_cast<float*>(workspace);
-    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + acc_bytes);
+    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + wl.acc);
+    a.merge_items = merge_items;
+    a.num_merge = merge_items != nullptr ? num_merge_items : 0;
     a.block_table_stride = dims.max_blocks_per_seq;
     a.num_kv_heads = dims.num_kv_heads;
     a.total_blocks = dims.total_blocks;

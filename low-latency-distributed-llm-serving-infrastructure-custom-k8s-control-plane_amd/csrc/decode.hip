@@ -1,24 +1,33 @@
 // Paged-attention decode for gfx950: one workgroup per
 // (sequence, 512-token context partition, KV head), split-K merge after.
 //
-// Work per workgroup (256 threads = 4 waves), for the H_q/H_kv = G query
-// heads that share one KV head, so every K/V row is read from HBM once:
+// The workgroup (4 waves) serves the G = H_q / H_kv query heads that share
+// one KV head, so every K/V row of the partition is read from HBM once.
+// The partition is cut into 32-token tiles dealt round-robin to the waves;
+// each wave runs flash-style online softmax over its tiles with no
+// workgroup barrier inside the loop:
 //
-//  phase 1 (QK)  tokens are spread over "row groups" of kQkLanes lanes; each
-//                lane reads two 16-byte pieces of the token's K row (the two
-//                loads of a group cover the row contiguously), dots them with
-//                its slice of the G query rows (v_dot2_f32_bf16 for bf16),
-//                and a DPP butterfly sums the group.  Scores (log2 domain)
-//                go to LDS.
-//  phase 2       workgroup max per head, p = exp2(s - max) in place, sums.
-//  phase 3 (PV)  each wave streams whole V rows (one row per wave load for
-//                256-byte rows), every lane owning a fixed slice of the head
-//                dimension for all G heads; waves then add their partial
-//                outputs through LDS.
+//  K (QK layout)  a "row group" of kL lanes holds one token's K row, each
+//                 lane two 16-byte pieces (the group's loads cover the row
+//                 contiguously); a wave covers 64 / kL tokens per load.
+//                 Dots with the G query slices use v_dot2_f32_bf16 (bf16)
+//                 and a DPP butterfly sums each group.
+//  V (PV layout)  one wave load covers whole V rows (one 256-byte row for
+//                 bf16 D=128, 4 bytes per lane), so the row address of a
+//                 load is wave-uniform and is formed in scalar registers
+//                 from the block id fetched with v_readlane.  Every lane
+//                 owns a fixed slice of the head dimension for all G heads.
+//  softmax        per tile: wave-wide max per head (DPP + shuffles), rescale
+//                 of the running sum / accumulator only when the max moved,
+//                 p = exp2(s - max) staged in LDS.  For bf16 the p of two
+//                 tokens are packed as a bf16 pair and the PV product uses
+//                 v_dot2_f32_bf16 on the matching V pair (one v_perm_b32 per
+//                 two elements); fp32 keeps fp32 FMAs throughout.
 //
-// A sequence whose context fits one partition gets its normalised output
-// written directly; otherwise (max, sum, unnormalised acc) partials go to
-// the workspace and decode_merge_kernel combines them.
+// At the end the four waves combine (max, sum, acc) through LDS.  A sequence
+// whose context fits one partition gets its normalised output directly;
+// otherwise the partials go to the workspace and decode_merge_kernel
+// combines them.
 //
 // The reference computes the same quantity with its CPU loop nest
 // (csrc/src/paged_kernels.cpp:49-104) over a flat gather list and dense mask.
@@ -29,122 +38,176 @@ namespace pa {
 
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeWaves = kDecodeThreads / kWave;
-constexpr int kMaxPartition = PA_DECODE_PARTITION;
+// Largest split-K partition (context tokens per workgroup) the kernel takes.
+constexpr int kMaxPartition = 2048;
+#ifndef PA_DECODE_TILE
+#define PA_DECODE_TILE 32  // context tokens per wave iteration (at least 2 rows per group)
+#endif
+#ifndef PA_DECODE_TILE_WIDE
+#define PA_DECODE_TILE_WIDE 16  // the same for groups of more than 4 query heads
+#endif
 
-template <typename T, int D>
-struct DecodeShape {
-  static constexpr int kE = Elem<T>::kBytes;
-  static constexpr int kRowBytes = D * kE;
-  static constexpr int kChunkElems = 16 / kE;           // elements per 16 B
-  static constexpr int kQkLanes = kRowBytes / 32;        // lanes per K row
-  static constexpr int kQkChunks = 2;                    // 16 B loads per lane
-  static constexpr int kQkElems = kQkChunks * kChunkElems;
-  static constexpr int kQkGroups = kDecodeThreads / kQkLanes;
-  static constexpr int kPvBytes = (kRowBytes / kWave) >= 4 ? (kRowBytes / kWave) : 4;
-  static constexpr int kPvLanes = kRowBytes / kPvBytes;  // lanes per V row
-  static constexpr int kPvElems = kPvBytes / kE;
-  static constexpr int kPvRows = kWave / kPvLanes;       // V rows per wave load
-  static_assert(kQkLanes >= 1 && kQkLanes <= 16, "row must be 32..512 bytes");
-  static_assert(kPvLanes <= kWave, "V row wider than a wave");
-};
+// Tuning switches (compile-time; the defaults are the shipped choice).
+#ifndef PA_DECODE_NT
+#define PA_DECODE_NT 1  // non-temporal K/V loads
+#endif
+#ifndef PA_DECODE_MIN_WAVES
+#define PA_DECODE_MIN_WAVES 4  // occupancy floor per SIMD (0 = compiler choice)
+#endif
+// Occupancy floor for a group of G query heads: the register budget of the
+// wider groups does not fit four waves per SIMD without spilling.
+#define PA_DECODE_OCCUPANCY(T, D, G) \
+  __attribute__((amdgpu_waves_per_eu(((G) <= 4 && (D) * sizeof(T) <= 256) ? PA_DECODE_MIN_WAVES : 2)))
 
-// Dot product of one lane's slice of a query row with the matching K slice.
-template <typename T, int N>
-__device__ __forceinline__ float slice_dot(const uint4 (&q)[N], const uint4 (&k)[N]);
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+// Streaming K/V loads (read once, never reused by this kernel).
+template <typename V>
+__device__ __forceinline__ V kv_load(const void* p);
+template <>
+__device__ __forceinline__ uint4 kv_load<uint4>(const void* p) {
+#if PA_DECODE_NT
+  const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+template <>
+__device__ __forceinline__ uint2 kv_load<uint2>(const void* p) {
+#if PA_DECODE_NT
+  const u32x2v v = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(p));
+  return make_uint2(v.x, v.y);
+#else
+  return *reinterpret_cast<const uint2*>(p);
+#endif
+}
+template <>
+__device__ __forceinline__ uint32_t kv_load<uint32_t>(const void* p) {
+#if PA_DECODE_NT
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+#else
+  return *reinterpret_cast<const uint32_t*>(p);
+#endif
+}
 
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a),
+                                         __builtin_bit_cast(bf16x2v, b), c, false);
+}
+
+template <typename T, int D, int TILE>
+struct DecodeShape {
+  static constexpr bool kBf16 = Elem<T>::kDtype == PA_DTYPE_BF16;
+  static constexpr int kE = Elem<T>::kBytes;
+  static constexpr int kRowBytes = D * kE;
+  // QK layout
+  static constexpr int kChunkElems = 16 / kE;  // elements per 16-byte piece
+  static constexpr int kL = kRowBytes / 32;    // lanes per K row
+  static constexpr int kGpw = kWave / kL;      // K rows per wave load
+  static constexpr int kTile = TILE >= 2 * kGpw ? TILE : 2 * kGpw;
+  static constexpr int kLog2Gpw = kGpw == 4 ? 2 : kGpw == 8 ? 3 : kGpw == 16 ? 4 : kGpw == 32 ? 5 : 6;
+  static constexpr int kTpg = kTile / kGpw;    // tile tokens per row group
+  // PV layout
+  static constexpr int kPvBytes = (kRowBytes / kWave) >= 4 ? (kRowBytes / kWave) : 4;
+  static constexpr int kLp = kRowBytes / kPvBytes;  // lanes per V row
+  static constexpr int kR = kWave / kLp;            // V rows per wave load
+  static constexpr int kPe = kPvBytes / kE;         // elements per lane
+  static constexpr int kRows = kTile / kR;          // V loads per lane per tile
+  static_assert(kL >= 1 && kL <= 16, "row must be 32..512 bytes");
+  static_assert(kTpg >= 2 && kTpg % 2 == 0, "token pairs need an even count per group");
+  static_assert(kGpw % kR == 0, "pair partner must sit in the same lane");
+};
+
+template <int NB>
+struct VRaw;
 template <>
-__device__ __forceinline__ float slice_dot<bf16_t, 2>(const uint4 (&q)[2], const uint4 (&k)[2]) {
+struct VRaw<4> {
+  using type = uint32_t;
+};
+template <>
+struct VRaw<8> {
+  using type = uint2;
+};
+
+// Dot product of one lane's K slice (two 16-byte pieces) with its q slice.
+template <typename T>
+__device__ __forceinline__ float slice_dot(const uint4 (&q)[2], const uint4 (&k)[2]) {
   float acc = 0.f;
+  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, q[c].x),
-                                          __builtin_bit_cast(bf16x2v, k[c].x), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, q[c].y),
-                                          __builtin_bit_cast(bf16x2v, k[c].y), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, q[c].z),
-                                          __builtin_bit_cast(bf16x2v, k[c].z), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, q[c].w),
-                                          __builtin_bit_cast(bf16x2v, k[c].w), acc, false);
+    for (int c = 0; c < 2; ++c) {
+      acc = dot2_bf16(q[c].x, k[c].x, acc);
+      acc = dot2_bf16(q[c].y, k[c].y, acc);
+      acc = dot2_bf16(q[c].z, k[c].z, acc);
+      acc = dot2_bf16(q[c].w, k[c].w, acc);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      acc = fmaf(__uint_as_float(q[c].x), __uint_as_float(k[c].x), acc);
+      acc = fmaf(__uint_as_float(q[c].y), __uint_as_float(k[c].y), acc);
+      acc = fmaf(__uint_as_float(q[c].z), __uint_as_float(k[c].z), acc);
+      acc = fmaf(__uint_as_float(q[c].w), __uint_as_float(k[c].w), acc);
+    }
   }
   return acc;
 }
 
-template <>
-__device__ __forceinline__ float slice_dot<float, 2>(const uint4 (&q)[2], const uint4 (&k)[2]) {
-  float acc = 0.f;
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    acc = fmaf(__uint_as_float(q[c].x), __uint_as_float(k[c].x), acc);
-    acc = fmaf(__uint_as_float(q[c].y), __uint_as_float(k[c].y), acc);
-    acc = fmaf(__uint_as_float(q[c].z), __uint_as_float(k[c].z), acc);
-    acc = fmaf(__uint_as_float(q[c].w), __uint_as_float(k[c].w), acc);
-  }
-  return acc;
+// Max over the lanes of a wave that share (lane % L): every row group.
+// gfx950 v_permlane16_swap / v_permlane32_swap with both operands = x:
+// element 0 holds rows {0,0,2,2} (halves {0,0}) and element 1 rows {1,1,3,3}
+// (halves {1,1}) of the 16-lane rows, so their max pairs rows (0,1),(2,3)
+// (resp. the two 32-lane halves).
+__device__ __forceinline__ float max_row_pairs(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Widen one lane's V slice (kPvBytes bytes) to fp32.
-template <typename T, int NB>
-struct PvSlice;
-template <>
-struct PvSlice<bf16_t, 4> {
-  using raw = uint32_t;
-  static constexpr int kElems = 2;
-  __device__ static raw load(const bf16_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
-  __device__ static void widen(raw r, float (&v)[2]) {
-    v[0] = bf16_lo(r);
-    v[1] = bf16_hi(r);
-  }
-};
-template <>
-struct PvSlice<bf16_t, 8> {
-  using raw = uint2;
-  static constexpr int kElems = 4;
-  __device__ static raw load(const bf16_t* p) { return *reinterpret_cast<const uint2*>(p); }
-  __device__ static void widen(raw r, float (&v)[4]) {
-    v[0] = bf16_lo(r.x);
-    v[1] = bf16_hi(r.x);
-    v[2] = bf16_lo(r.y);
-    v[3] = bf16_hi(r.y);
-  }
-};
-template <>
-struct PvSlice<float, 4> {
-  using raw = uint32_t;
-  static constexpr int kElems = 1;
-  __device__ static raw load(const float* p) { return *reinterpret_cast<const uint32_t*>(p); }
-  __device__ static void widen(raw r, float (&v)[1]) { v[0] = __uint_as_float(r); }
-};
-template <>
-struct PvSlice<float, 8> {
-  using raw = uint2;
-  static constexpr int kElems = 2;
-  __device__ static raw load(const float* p) { return *reinterpret_cast<const uint2*>(p); }
-  __device__ static void widen(raw r, float (&v)[2]) {
-    v[0] = __uint_as_float(r.x);
-    v[1] = __uint_as_float(r.y);
-  }
-};
+template <int L>
+__device__ __forceinline__ float across_groups_max(float x) {
+  if constexpr (L <= 8) x = fmaxf(x, dpp<kDppRowRor8>(x));
+  if constexpr (L <= 16) x = max_row_pairs(x);
+  x = max_halves(x);
+  if constexpr (L <= 4) x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  if constexpr (L <= 2) x = fmaxf(x, dpp<kDppQuadXor2>(x));
+  if constexpr (L <= 1) x = fmaxf(x, dpp<kDppQuadXor1>(x));
+  return x;
+}
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kDecodeThreads) void decode_partition_kernel(DecodeArgs a) {
-  using S = DecodeShape<T, D>;
-  using PV = PvSlice<T, S::kPvBytes>;
-  constexpr int L = S::kQkLanes;
-  constexpr int NG = S::kQkGroups;
+__global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void decode_partition_kernel(DecodeArgs a) {
+  using S = DecodeShape<T, D, (G > 4 ? PA_DECODE_TILE_WIDE : PA_DECODE_TILE)>;
+  using VR = typename VRaw<S::kPvBytes>::type;
+  constexpr int L = S::kL;
+  constexpr int GPW = S::kGpw;
+  constexpr int TPG = S::kTpg;
   constexpr int CE = S::kChunkElems;
-  constexpr int U = 4;   // K rows in flight per group
-  constexpr int U3 = 8;  // V loads in flight per wave
+  constexpr int PE = S::kPe;
+  constexpr int R = S::kR;
+  constexpr int ROWS = S::kRows;
+  constexpr bool BF16 = S::kBf16;
+  // p staging per wave: bf16 pairs [16 pairs][G] or fp32 [32 tokens][G]
+  constexpr int kTile = S::kTile;
+  constexpr int PWORDS = BF16 ? (kTile / 2) * G : kTile * G;
 
-  __shared__ float s_logit[kMaxPartition * G];
   __shared__ int s_blk[kMaxPartition + 2];
-  __shared__ float s_part[kDecodeWaves][G];
+  __shared__ uint4 s_q[G * D * S::kE / 16];
+  __shared__ uint32_t s_p[kDecodeWaves][PWORDS];
+  __shared__ float s_m[kDecodeWaves][G];
+  __shared__ float s_l[kDecodeWaves][G];
   __shared__ float s_acc[kDecodeWaves][G * D];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int hkv = a.num_kv_heads;
   const int64_t item = blockIdx.x / hkv;
   const int kvh = blockIdx.x - static_cast<int>(item) * hkv;
@@ -173,146 +236,297 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partition_kernel(Decode
     s_blk[i] = b;
   }
 
-  // Query slices for the G heads of this KV head.
-  const int lig = tid % L;
-  const int grp = tid / L;
-  uint4 qv[G][2];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
+  // The G query rows of this KV head -> LDS (read back per tile, one head
+  // at a time, so they do not occupy registers across the loop).
+  const int lig = lane % L;  // lane within its row group
+  const int gi = lane / L;   // row group within the wave
+  constexpr int QCHUNKS = G * D / CE;  // 16-byte pieces of the G query rows
+  for (int i = tid; i < QCHUNKS; i += kDecodeThreads) {
+    const int g = i / (D / CE);
+    const int c = i - g * (D / CE);
     const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                     static_cast<int64_t>(kvh * G + g) * a.q_head_stride;
-    qv[g][0] = ld16(qrow + lig * CE);
-    qv[g][1] = ld16(qrow + (L + lig) * CE);
+    s_q[i] = ld16(qrow + c * CE);
   }
   __syncthreads();
 
-  // ---- phase 1: scores ------------------------------------------------
-  float run_max[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) run_max[g] = kScoreFloor;
   const float scale = a.scale_log2e;
-
-  for (int t0 = 0; t0 < n; t0 += NG * U) {
-    uint4 kb[U][2];
-    bool ok[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * NG + grp;
-      int b = -1;
-      if (t < n) b = s_blk[((p0 + t) >> log2_bs) - first_blk];
-      ok[u] = b >= 0;
-      if (ok[u]) {
-        const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
-        const T* row = kbase + slot * row_stride;
-        kb[u][0] = ld16(row + lig * CE);
-        kb[u][1] = ld16(row + (L + lig) * CE);
-      } else {
-        kb[u][0] = make_uint4(0, 0, 0, 0);
-        kb[u][1] = make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * NG + grp;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float s = group_sum<L>(slice_dot<T, 2>(qv[g], kb[u])) * scale;
-        if (!ok[u]) s = -INFINITY;
-        run_max[g] = fmaxf(run_max[g], s);
-        if (lig == 0 && t < n) s_logit[t * G + g] = s;
-      }
-    }
-  }
-
-  // ---- phase 2: softmax over the partition --------------------------
+  const int sub = lane / S::kLp;  // V row of this lane within a wave load
+  const int lp = lane % S::kLp;   // head-dimension slice of this lane
+  float m[G], acc[G][PE];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float m = wave_max(run_max[g]);
-    if (lane == 0) s_part[wave][g] = m;
-  }
-  __syncthreads();
-  float pmax[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = s_part[0][g];
-#pragma unroll
-    for (int w = 1; w < kDecodeWaves; ++w) m = fmaxf(m, s_part[w][g]);
-    pmax[g] = m;
-  }
-  __syncthreads();  // s_part is reused for the sums below
-
-  // Thread tid always sees head tid % G (G divides the block size).
-  float psum = 0.f;
-  {
-    const int g = tid % G;
-    float m = pmax[0];
-#pragma unroll
-    for (int gg = 1; gg < G; ++gg)
-      if (g == gg) m = pmax[gg];
-    for (int i = tid; i < n * G; i += kDecodeThreads) {
-      const float p = fast_exp2(s_logit[i] - m);
-      s_logit[i] = p;
-      psum += p;
-    }
-  }
-#pragma unroll
-  for (int o = kWave / 2; o >= G; o >>= 1) psum += __shfl_xor(psum, o, kWave);
-  if (lane < G) s_part[wave][lane] = psum;
-  __syncthreads();
-  float lsum[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float l = 0.f;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) l += s_part[w][g];
-    lsum[g] = l;
-  }
-
-  // ---- phase 3: P x V -------------------------------------------------
-  constexpr int PE = S::kPvElems;
-  constexpr int R = S::kPvRows;
-  const int sub = lane / S::kPvLanes;   // V row within a wave load
-  const int lp = lane % S::kPvLanes;    // slice of the head dimension
-  float acc[G][PE];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
+    m[g] = kScoreFloor;
 #pragma unroll
     for (int e = 0; e < PE; ++e) acc[g][e] = 0.f;
+  }
 
-  for (int t0 = 0; t0 < n; t0 += kDecodeWaves * R * U3) {
-    typename PV::raw vb[U3];
-    bool ok[U3];
+  // ---- per-tile work ------------------------------------------------------
+  // Softmax exponentials are spread over the lanes of a row group: lane lig
+  // owns "combos" c = lig + L*r, each one (token pair, head) for bf16 or
+  // (token, head) for fp32, and computes, sums and stages only those.
+  constexpr int NC = (BF16 ? TPG / 2 : TPG) * G;  // combos per row group
+  constexpr int CPL = (NC + L - 1) / L;           // combos per lane
+  float lsum[G];  // this lane's share of the softmax denominators
 #pragma unroll
-    for (int u = 0; u < U3; ++u) {
-      const int t = t0 + (u * kDecodeWaves + wave) * R + sub;
-      int b = -1;
-      if (t < n) b = s_blk[((p0 + t) >> log2_bs) - first_blk];
-      ok[u] = b >= 0;
-      if (ok[u]) {
-        const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
-        vb[u] = PV::load(vbase + slot * row_stride + lp * PE);
+  for (int g = 0; g < G; ++g) lsum[g] = 0.f;
+
+  uint4 kb[TPG][2];
+  bool kok[TPG];
+  VR vb[ROWS];
+
+  auto tile_blocks = [&](int tile) {
+    const int t = tile * kTile + (lane & (kTile - 1));
+    return t < n ? s_blk[((p0 + t) >> log2_bs) - first_blk] : -1;
+  };
+  // Per-lane element offset of its K slice within a wave load: row group gi
+  // reads row gi of the load (GPW consecutive tokens).
+  const int64_t koff = static_cast<int64_t>(gi) * row_stride + lig * CE;
+  const bool k_uniform = log2_bs >= S::kLog2Gpw;  // a load's GPW tokens share a block
+  auto issue_k = [&](int tile, int blk_lane) {
+    const int t0 = tile * kTile;
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) {
+      const int t = t0 + gi + GPW * i;
+      if (k_uniform) {
+        // Block id and row base of the load are wave-uniform (scalar regs).
+        // Lanes past the end of the partition still read a row of the same
+        // (valid) block; their scores are masked.
+        const int b = __builtin_amdgcn_readlane(blk_lane, GPW * i);
+        kok[i] = t < n && b >= 0;
+        if (b >= 0) {
+          const int64_t slot0 =
+              (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + GPW * i) & bs_mask);
+          const T* row = kbase + slot0 * row_stride + koff;
+          kb[i][0] = kv_load<uint4>(row);
+          kb[i][1] = kv_load<uint4>(row + L * CE);
+        } else {
+          kb[i][0] = make_uint4(0, 0, 0, 0);
+          kb[i][1] = make_uint4(0, 0, 0, 0);
+        }
       } else {
-        vb[u] = typename PV::raw{};
+        int b = -1;
+        if (t < n) b = s_blk[((p0 + t) >> log2_bs) - first_blk];
+        kok[i] = b >= 0;
+        if (kok[i]) {
+          const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
+          const T* row = kbase + slot * row_stride;
+          kb[i][0] = kv_load<uint4>(row + lig * CE);
+          kb[i][1] = kv_load<uint4>(row + (L + lig) * CE);
+        } else {
+          kb[i][0] = make_uint4(0, 0, 0, 0);
+          kb[i][1] = make_uint4(0, 0, 0, 0);
+        }
       }
     }
+  };
+  // V rows.  Fast path (one V row per wave load, blocks of >= 16 tokens):
+  // rows come in runs of 16 consecutive tokens inside one block, so the
+  // block lookup and the 64-bit row address are formed once per run in
+  // scalar registers and each further row is one scalar pointer increment.
+  // Rows past the end of the partition are zeroed (p = 0 must not meet
+  // uninitialised cache contents).
+  constexpr int kRun = 16;
+  const bool v_runs = R == 1 && log2_bs >= 4;
+  auto issue_v = [&](int tile, int blk_lane, bool full) {
+    const int t0 = tile * kTile;
+    if (v_runs) {
 #pragma unroll
-    for (int u = 0; u < U3; ++u) {
-      const int t = t0 + (u * kDecodeWaves + wave) * R + sub;
-      if (ok[u]) {
-        float v[PE];
-        PV::widen(vb[u], v);
+      for (int run = 0; run < ROWS / kRun; ++run) {
+        const int b = __builtin_amdgcn_readlane(blk_lane, run * kRun);
+        if (b >= 0) {
+          const int64_t slot0 =
+              (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + run * kRun) & bs_mask);
+          const T* rowp = vbase + slot0 * row_stride + lp * PE;
+          if (full) {
+#pragma unroll
+            for (int r = 0; r < kRun; ++r) {
+              vb[run * kRun + r] = kv_load<VR>(rowp);
+              rowp += row_stride;
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < kRun; ++r) {
+              const int u = run * kRun + r;
+              vb[u] = t0 + u < n ? kv_load<VR>(rowp) : VR{};
+              rowp += row_stride;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < kRun; ++r) vb[run * kRun + r] = VR{};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < ROWS; ++u) {
+        int b;
+        int t;
+        if constexpr (R == 1) {
+          t = t0 + u;
+          b = __builtin_amdgcn_readlane(blk_lane, u);
+        } else {
+          t = t0 + R * u + sub;
+          b = __shfl(blk_lane, R * u + sub, kWave);
+        }
+        if (b >= 0) {
+          const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
+          vb[u] = kv_load<VR>(vbase + slot * row_stride + lp * PE);
+        } else {
+          vb[u] = VR{};
+        }
+      }
+    }
+  };
+
+  // Scores of the loaded K tile, online-softmax update, p -> LDS.
+  // Scores stay unscaled (the max commutes with the positive scale); the
+  // scale is applied inside the exponent: p = exp2(s * scale - max * scale).
+  auto qk_softmax = [&](bool full) {
+    float s[TPG][G];
+    float tmax[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) tmax[g] = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      uint4 qg[2];
+      qg[0] = s_q[g * (D / CE) + lig];
+      qg[1] = s_q[g * (D / CE) + L + lig];
+#pragma unroll
+      for (int i = 0; i < TPG; ++i) {
+        float v = group_sum<L>(slice_dot<T>(qg, kb[i]));
+        if (!full) v = kok[i] ? v : -INFINITY;
+        s[i][g] = v;
+        tmax[g] = fmaxf(tmax[g], v);
+      }
+    }
+    bool moved = false;
+    float m_new[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m_new[g] = __int_as_float(__builtin_amdgcn_readfirstlane(
+          __float_as_int(fmaxf(m[g], across_groups_max<L>(tmax[g])))));
+      moved |= m_new[g] != m[g];
+    }
+    if (moved) {  // wave-uniform
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float alpha = fast_exp2((m[g] - m_new[g]) * scale);
+        lsum[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < PE; ++e) acc[g][e] *= alpha;
+        m[g] = m_new[g];
+      }
+    }
+    float mneg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) mneg[g] = -m[g] * scale;
+    uint32_t* sp = s_p[wave];
+#pragma unroll
+    for (int r = 0; r < CPL; ++r) {
+      const int c = lig + L * r;
+      if (NC % L != 0 && c >= NC) break;
+      float sa = -INFINITY, sb = -INFINITY, mc = 0.f;  // mc: -max * scale of the head
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const bool mine = c == cc;
+        if constexpr (BF16) {
+          sa = mine ? s[2 * (cc / G)][cc % G] : sa;
+          sb = mine ? s[2 * (cc / G) + 1][cc % G] : sb;
+        } else {
+          sa = mine ? s[cc / G][cc % G] : sa;
+        }
+      }
+      const int g = c % G;
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) mc = g == gg ? mneg[gg] : mc;
+      if constexpr (BF16) {
+        const float pa = fast_exp2(fmaf(sa, scale, mc));
+        const float pb = fast_exp2(fmaf(sb, scale, mc));
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) lsum[gg] += g == gg ? pa + pb : 0.f;
+        sp[((c / G) * GPW + gi) * G + g] = pack_bf16x2(pa, pb);
+      } else {
+        const float pa = fast_exp2(fmaf(sa, scale, mc));
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) lsum[gg] += g == gg ? pa : 0.f;
+        sp[(gi + GPW * (c / G)) * G + g] = __float_as_uint(pa);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // Accumulate P x V of the loaded V tile.
+  auto pv = [&]() {
+    const uint32_t* sp = s_p[wave];
+    if constexpr (BF16) {
+      constexpr int PARTNER = GPW / R;  // V load holding token t + GPW
+#pragma unroll
+      for (int u = 0; u < ROWS; ++u) {
+        if (((R * u) % (2 * GPW)) >= GPW) continue;
+        const int t = R * u + sub;
+        const int pidx = (t / (2 * GPW)) * GPW + (t % GPW);
+        uint32_t pw[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pw[g] = sp[pidx * G + g];
+        const uint32_t va = vb[u], vbb = vb[u + PARTNER];
+        const uint32_t lo = __builtin_amdgcn_perm(vbb, va, 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(vbb, va, 0x07060302u);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float p = s_logit[t * G + g];
+          acc[g][0] = dot2_bf16(pw[g], lo, acc[g][0]);
+          acc[g][1] = dot2_bf16(pw[g], hi, acc[g][1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < ROWS; ++u) {
+        const int t = R * u + sub;
+        float v[PE];
+        if constexpr (PE == 1) {
+          v[0] = __uint_as_float(vb[u]);
+        } else {
+          v[0] = __uint_as_float(vb[u].x);
+          v[1] = __uint_as_float(vb[u].y);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float p = __uint_as_float(sp[t * G + g]);
 #pragma unroll
           for (int e = 0; e < PE; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e]);
         }
       }
     }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // Each wave walks its tiles: all K and V loads of a tile are issued at
+  // the top of the iteration (several waves per SIMD hide the latency; a
+  // pipeline carrying the next tile's loads across the loop did not fit the
+  // register budget).
+  const int ntiles = (n + kTile - 1) / kTile;
+  for (int tile = wave; tile < ntiles; tile += kDecodeWaves) {
+    const int blk_lane = tile_blocks(tile);
+    // Tile fully inside the partition with every block valid: no masking.
+    const bool full = (tile + 1) * kTile <= n && __ballot(lane < kTile && blk_lane < 0) == 0;
+    issue_k(tile, blk_lane);
+    issue_v(tile, blk_lane, full);
+    qk_softmax(full);
+    pv();
   }
-  // Rows of one wave load that hold different tokens -> add them up.
+
+  // ---- combine the waves -------------------------------------------------
+  // Each (token, head) exponential was summed by exactly one lane.
 #pragma unroll
-  for (int o = kWave / 2; o >= S::kPvLanes; o >>= 1)
+  for (int g = 0; g < G; ++g) {
+    float l = lsum[g];
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
+    lsum[g] = l;
+  }
+  // V rows of one wave load that hold different tokens -> add them up.
+#pragma unroll
+  for (int o = kWave / 2; o >= S::kLp; o >>= 1)
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -323,42 +537,41 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partition_kernel(Decode
 #pragma unroll
       for (int e = 0; e < PE; ++e) s_acc[wave][g * D + lp * PE + e] = acc[g][e];
   }
+  if (lane < G) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (lane == g) {
+        s_m[wave][g] = m[g] * scale;
+        s_l[wave][g] = lsum[g];
+      }
+  }
   __syncthreads();
 
   const int hq = hkv * G;
   const int nparts = (ctx + a.partition - 1) / a.partition;
-  if (nparts <= 1) {
-    T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * D;
-    for (int i = tid; i < G * D; i += kDecodeThreads) {
-      float o = 0.f;
+  float* pacc = a.part_acc + (item * hq + kvh * G) * D;
+  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * D;
+  for (int i = tid; i < G * D; i += kDecodeThreads) {
+    const int g = i / D;
+    float mx = s_m[0][g];
 #pragma unroll
-      for (int w = 0; w < kDecodeWaves; ++w) o += s_acc[w][i];
-      const int g = i / D;
-      float l = lsum[0];
+    for (int w = 1; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    float o = 0.f, l = 0.f;
 #pragma unroll
-      for (int gg = 1; gg < G; ++gg)
-        if (g == gg) l = lsum[gg];
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float f = fast_exp2(s_m[w][g] - mx);
+      o = fmaf(s_acc[w][i], f, o);
+      l = fmaf(s_l[w][g], f, l);
+    }
+    if (nparts <= 1) {
       store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
-    }
-  } else {
-    float* pacc = a.part_acc + (item * hq + kvh * G) * D;
-    for (int i = tid; i < G * D; i += kDecodeThreads) {
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < kDecodeWaves; ++w) o += s_acc[w][i];
+    } else {
       pacc[i] = o;
-    }
-    if (tid < G) {
-      float m = pmax[0], l = lsum[0];
-#pragma unroll
-      for (int gg = 1; gg < G; ++gg)
-        if (tid == gg) {
-          m = pmax[gg];
-          l = lsum[gg];
-        }
-      float* pml = a.part_ml + (item * hq + kvh * G + tid) * 2;
-      pml[0] = m;
-      pml[1] = l;
+      if (i % D == 0) {
+        float* pml = a.part_ml + (item * hq + kvh * G + g) * 2;
+        pml[0] = mx;
+        pml[1] = l;
+      }
     }
   }
 }
@@ -366,55 +579,95 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partition_kernel(Decode
 // Combines the split-K partials of every multi-partition sequence.  One
 // workgroup per (first work item of a sequence, KV head); the items of a
 // sequence are contiguous in `items` (pa_pack orders them that way).
+// Combines the split-K partials (max, sum, unnormalised acc) of one
+// multi-partition sequence for the G heads of one KV head.  One workgroup
+// per (entry of the merge list, KV head); the merge list holds the first
+// decode item of every sequence with more than one partition, and the
+// items of a sequence are contiguous (pa_pack orders them that way).
+//  phase A  wave w takes heads w, w+4, ...: lane p reads (max, sum) of
+//           partition p, the wave reduces them, and each lane writes its
+//           partition's weight exp2(max_p - max) / sum to LDS;
+//  phase B  every thread owns G*D/256 outputs and accumulates the weighted
+//           partials over the partitions.
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
+  constexpr int kMaxW = 4096;  // LDS weights: partitions x heads per pass
+  __shared__ float s_w[kMaxW];
   const int hkv = a.num_kv_heads;
-  const int64_t item = blockIdx.x / hkv;
-  const int kvh = blockIdx.x - static_cast<int>(item) * hkv;
-  if (a.items[2 * item + 1] != 0) return;
-  const int seq = a.items[2 * item];
-  const int ctx = a.context_lens[seq];
-  int nparts = (ctx + a.partition - 1) / a.partition;
+  const int64_t m = blockIdx.x / hkv;
+  const int kvh = blockIdx.x - static_cast<int>(m) * hkv;
+  const int64_t first = a.merge_items[m];
+  const int seq = a.items[2 * first];
+  int nparts = (a.context_lens[seq] + a.partition - 1) / a.partition;
+  if (first + nparts > a.num_items) nparts = static_cast<int>(a.num_items - first);
   if (nparts <= 1) return;
-  if (item + nparts > a.num_items) nparts = static_cast<int>(a.num_items - item);
   const int hq = hkv * G;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  const int chunk = kMaxW / G;
+  const int64_t stride = static_cast<int64_t>(hq) * D;
+  T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[seq] * hq + kvh * G) * D;
+  const float* acc_base = a.part_acc + (first * hq + kvh * G) * static_cast<int64_t>(D);
 
+  // Phase A over all partitions first: global max and normaliser per head.
   __shared__ float s_max[64];
   __shared__ float s_inv[64];
-  // Per-head global max and normaliser; wave w handles heads w, w+4, ...
   for (int g = wave; g < G; g += kDecodeWaves) {
     const int h = kvh * G + g;
-    float m = kScoreFloor;
-    for (int p = lane; p < nparts; p += kWave)
-      m = fmaxf(m, a.part_ml[((item + p) * hq + h) * 2]);
-    m = wave_max(m);
+    float mx = kScoreFloor;
+    for (int p = lane; p < nparts; p += kWave) mx = fmaxf(mx, a.part_ml[((first + p) * hq + h) * 2]);
+    mx = wave_max(mx);
     float l = 0.f;
     for (int p = lane; p < nparts; p += kWave) {
-      const float* ml = a.part_ml + ((item + p) * hq + h) * 2;
-      l += ml[1] * fast_exp2(ml[0] - m);
+      const float* ml = a.part_ml + ((first + p) * hq + h) * 2;
+      const float w = fast_exp2(ml[0] - mx);
+      l = fmaf(ml[1], w, l);
+      if (p < chunk) s_w[p * G + g] = w;
     }
     l = wave_sum(l);
     if (lane == 0) {
-      s_max[g] = m;
+      s_max[g] = mx;
       s_inv[g] = l > 0.f ? 1.f / l : 0.f;
     }
   }
-  __syncthreads();
-  const int64_t qtok = a.cu_seqlens[seq];
-  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * D;
-  for (int i = tid; i < G * D; i += kDecodeThreads) {
-    const int g = i / D;
-    const int h = kvh * G + g;
-    const float m = s_max[g];
-    float o = 0.f;
-    for (int p = 0; p < nparts; ++p) {
-      const float w = fast_exp2(a.part_ml[((item + p) * hq + h) * 2] - m);
-      o = fmaf(a.part_acc[((item + p) * hq + kvh * G) * D + i], w, o);
+  float o[8];  // up to 8 outputs per thread (G * D <= 2048)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = 0.f;
+  for (int c0 = 0; c0 < nparts; c0 += chunk) {
+    const int pn = min(chunk, nparts - c0);
+    if (c0 > 0) {  // weights of a further chunk (contexts past chunk*partition)
+      __syncthreads();
+      for (int i = tid; i < pn * G; i += kDecodeThreads) {
+        const int p = i / G, g = i - (i / G) * G;
+        s_w[i] = fast_exp2(a.part_ml[((first + c0 + p) * hq + kvh * G + g) * 2] - s_max[g]);
+      }
     }
-    store_scalar<T>(out + i, o * s_inv[g]);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = tid + j * kDecodeThreads;
+      if (i >= G * D) break;
+      const int g = i / D;
+      const float* src = acc_base + c0 * stride + i;
+      float acc = 0.f;
+      int p = 0;
+      for (; p + 4 <= pn; p += 4) {
+        const float x0 = src[(p + 0) * stride], x1 = src[(p + 1) * stride];
+        const float x2 = src[(p + 2) * stride], x3 = src[(p + 3) * stride];
+        acc = fmaf(x0, s_w[(p + 0) * G + g], acc);
+        acc = fmaf(x1, s_w[(p + 1) * G + g], acc);
+        acc = fmaf(x2, s_w[(p + 2) * G + g], acc);
+        acc = fmaf(x3, s_w[(p + 3) * G + g], acc);
+      }
+      for (; p < pn; ++p) acc = fmaf(src[p * stride], s_w[p * G + g], acc);
+      o[j] += acc;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = tid + j * kDecodeThreads;
+    if (i < G * D) store_scalar<T>(out + i, o[j] * s_inv[i / D]);
   }
 }
 
@@ -423,11 +676,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
 template <typename T, int D, int G>
 static hipError_t launch_decode_t(const DecodeArgs& a, int64_t num_items, hipStream_t stream) {
   const int64_t grid = num_items * a.num_kv_heads;
+  const int64_t merge_grid = a.num_merge * a.num_kv_heads;
   hipLaunchKernelGGL((decode_partition_kernel<T, D, G>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kDecodeThreads), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(static_cast<uint32_t>(grid)),
+  if (merge_grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(static_cast<uint32_t>(merge_grid)),
                      dim3(kDecodeThreads), 0, stream, a, G, D);
   return hipGetLastError();
 }
@@ -449,7 +704,7 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
   if (head_dim != 64 && head_dim != 128) return false;
   if (group != 1 && group != 2 && group != 4 && group != 8) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
-  if (partition <= 0 || partition > kMaxPartition) return false;
+  if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;
   return true;
 }
 

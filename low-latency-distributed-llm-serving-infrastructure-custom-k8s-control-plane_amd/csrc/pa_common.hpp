@@ -19,9 +19,11 @@ namespace pa {
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
-// Finite floor used as the initial running maximum: exp2(s - floor) of a
-// masked score (-inf) is exactly 0 and no (-inf) - (-inf) NaN can appear.
-constexpr float kScoreFloor = -3.402823466e+38f;
+// Finite floor used as the initial running maximum: exp2 of a masked score
+// (-inf) minus the floor is exactly 0 and no (-inf) - (-inf) NaN can appear.
+// -1e30 is also the reference's own "masked" threshold
+// (csrc/src/paged_kernels.cpp:79), and floor * scale stays finite.
+constexpr float kScoreFloor = -1e30f;
 
 struct bf16_t {
   uint16_t bits;

@@ -22,6 +22,8 @@ struct DecodeArgs {
   void* output;             // [T, H_q, D]
   float* part_acc;          // [items, H_q, D]
   float* part_ml;           // [items, H_q, 2]
+  const int32_t* merge_items;  // first item of every multi-partition sequence
+  int64_t num_merge;
   int32_t block_table_stride;
   int32_t num_kv_heads;
   int32_t total_blocks;
@@ -73,6 +75,7 @@ struct PackArgs {
   int64_t* position_ids;
   int64_t* gather_slots;
   int32_t* decode_items;
+  int32_t* merge_items;
   int32_t* prefill_items;
   int32_t num_seqs;
   int32_t block_size;
@@ -82,6 +85,7 @@ struct PackArgs {
   int64_t max_query_tokens;
   int64_t max_context_tokens;
   int64_t max_decode_items;
+  int64_t max_merge_items;
   int64_t max_prefill_items;
 };
 

@@ -11,8 +11,10 @@
 //   position_ids restart at every sequence: start .. start+count-1
 //     (paged_attention.py:81-90).
 // In addition it emits the work lists of the attention kernels: decode
-// items (seq, partition) for sequences with exactly one new token and
-// prefill items (seq, query tile) for the others, both ordered by sequence.
+// items (seq, partition) for sequences with exactly one new token, the
+// merge list (index of the first decode item of every such sequence with
+// more than one partition) and prefill items (seq, query tile) for the
+// multi-token sequences, all ordered by sequence.
 //
 // Each workgroup computes its own prefix sums by reducing over the
 // sequences before it (B is at most a few thousand, so this is cheaper than
@@ -40,37 +42,45 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
   const int wave = tid / kWave;
 
   // Prefix sums over sequences [0, seq).
-  int64_t tok = 0, ctx = 0, ditems = 0, pitems = 0;
+  int64_t tok = 0, ctx = 0, ditems = 0, pitems = 0, mitems = 0;
   for (int k = tid; k < seq; k += kPackThreads) {
     const int64_t cnt = nonneg(a.new_token_counts[k]);
     const int64_t c = nonneg(a.start_positions[k]) + cnt;
     tok += cnt;
     ctx += c;
-    if (cnt == 1) ditems += (c + a.partition - 1) / a.partition;
-    else if (cnt > 1) pitems += (cnt + a.prefill_tile - 1) / a.prefill_tile;
+    if (cnt == 1) {
+      const int64_t np = (c + a.partition - 1) / a.partition;
+      ditems += np;
+      mitems += np > 1 ? 1 : 0;
+    } else if (cnt > 1) {
+      pitems += (cnt + a.prefill_tile - 1) / a.prefill_tile;
+    }
   }
-  __shared__ int64_t s_red[4][kPackThreads / kWave];
+  __shared__ int64_t s_red[5][kPackThreads / kWave];
 #pragma unroll
   for (int o = kWave / 2; o >= 1; o >>= 1) {
     tok += __shfl_xor(tok, o, kWave);
     ctx += __shfl_xor(ctx, o, kWave);
     ditems += __shfl_xor(ditems, o, kWave);
     pitems += __shfl_xor(pitems, o, kWave);
+    mitems += __shfl_xor(mitems, o, kWave);
   }
   if (lane == 0) {
     s_red[0][wave] = tok;
     s_red[1][wave] = ctx;
     s_red[2][wave] = ditems;
     s_red[3][wave] = pitems;
+    s_red[4][wave] = mitems;
   }
   __syncthreads();
-  tok = ctx = ditems = pitems = 0;
+  tok = ctx = ditems = pitems = mitems = 0;
 #pragma unroll
   for (int w = 0; w < kPackThreads / kWave; ++w) {
     tok += s_red[0][w];
     ctx += s_red[1][w];
     ditems += s_red[2][w];
     pitems += s_red[3][w];
+    mitems += s_red[4][w];
   }
 
   const int64_t start = nonneg(a.start_positions[seq]);
@@ -120,6 +130,9 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
   }
 
   // Attention work lists.
+  if (count == 1 && a.merge_items != nullptr && tid == 0 && mitems < a.max_merge_items &&
+      clen > a.partition)
+    a.merge_items[mitems] = static_cast<int32_t>(ditems);
   if (count == 1 && a.decode_items != nullptr) {
     const int64_t nparts = (clen + a.partition - 1) / a.partition;
     for (int64_t p = tid; p < nparts; p += kPackThreads) {

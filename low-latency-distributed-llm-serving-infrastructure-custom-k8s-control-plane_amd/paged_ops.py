@@ -91,6 +91,7 @@ class PackedStep:
     scatter_slots: torch.Tensor  # int64 [T]
     position_ids: torch.Tensor  # int64 [T]
     decode_items: torch.Tensor  # int32 [num_decode_items, 2]
+    merge_items: torch.Tensor  # int32 [num_merge_items]
     prefill_items: torch.Tensor  # int32 [num_prefill_items, 2]
     block_size: int
     partition_size: int
@@ -98,6 +99,7 @@ class PackedStep:
     num_query_tokens: int
     num_context_tokens: int
     num_decode_items: int
+    num_merge_items: int
     num_prefill_items: int
     num_decode_seqs: int
     num_prefill_seqs: int
@@ -116,6 +118,8 @@ class PackedStep:
         return self._gather_slots
 
     def workspace(self, num_query_heads: int, head_dim: int, device: torch.device) -> torch.Tensor:
+        """Decode workspace (split-K partials), reused across the layers of the
+        step; calls that share it must not overlap in time."""
         need = decode_workspace_bytes(self.num_decode_items, num_query_heads, head_dim)
         ws = self._workspace
         if ws is None or ws.numel() < need or ws.device != device:
@@ -130,19 +134,21 @@ def work_counts(
     partition_size: int,
     prefill_tile: int,
 ):
-    """Host-side sizes of a step: (T, C, decode items, prefill items, #decode, #prefill)."""
-    t = c = ditems = pitems = ndec = npre = 0
+    """Host-side sizes of a step:
+    (T, C, decode items, merge items, prefill items, #decode seqs, #prefill seqs)."""
+    t = c = ditems = mitems = pitems = ndec = npre = 0
     for start, count in zip(start_positions, new_token_counts):
         ctx = start + count
         t += count
         c += ctx
         if count == 1:
             ditems += -(-ctx // partition_size)
+            mitems += ctx > partition_size
             ndec += 1
         elif count > 1:
             pitems += -(-count // prefill_tile)
             npre += 1
-    return t, c, ditems, pitems, ndec, npre
+    return t, c, ditems, mitems, pitems, ndec, npre
 
 
 def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Tensor]:
@@ -160,6 +166,7 @@ def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Ten
         max_query_tokens=step.num_query_tokens,
         max_context_tokens=step.num_context_tokens,
         max_decode_items=step.num_decode_items,
+        max_merge_items=step.num_merge_items,
         max_prefill_items=step.num_prefill_items,
     )
     status = lib.pa_pack(
@@ -174,6 +181,7 @@ def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Ten
         _ptr(step.position_ids),
         _ptr(gather),
         _ptr(step.decode_items),
+        _ptr(step.merge_items),
         _ptr(step.prefill_items),
         _stream(device),
     )
@@ -209,7 +217,8 @@ def pack_step(
         raise ValueError("start_positions / new_token_counts must have one entry per block-table row")
     if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
         raise ValueError("start positions and token counts must be non-negative")
-    t, c, ditems, pitems, ndec, npre = work_counts(start_positions, new_token_counts, partition_size, prefill_tile)
+    t, c, ditems, mitems, pitems, ndec, npre = work_counts(
+        start_positions, new_token_counts, partition_size, prefill_tile)
     if start_positions_dev is None:
         start_positions_dev = torch.tensor(list(start_positions), dtype=torch.int64).to(device, non_blocking=True)
     if new_token_counts_dev is None:
@@ -224,6 +233,7 @@ def pack_step(
         scatter_slots=torch.empty(t, dtype=torch.int64, device=device),
         position_ids=torch.empty(t, dtype=torch.int64, device=device),
         decode_items=torch.empty((ditems, 2), dtype=torch.int32, device=device),
+        merge_items=torch.empty((mitems,), dtype=torch.int32, device=device),
         prefill_items=torch.empty((pitems, 2), dtype=torch.int32, device=device),
         block_size=int(block_size),
         partition_size=int(partition_size),
@@ -231,6 +241,7 @@ def pack_step(
         num_query_tokens=t,
         num_context_tokens=c,
         num_decode_items=ditems,
+        num_merge_items=mitems,
         num_prefill_items=pitems,
         num_decode_seqs=ndec,
         num_prefill_seqs=npre,
@@ -302,6 +313,7 @@ def reshape_and_cache(
 
 
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
+    """Bytes pa_decode needs for its split-K partials."""
     if num_decode_items <= 0:
         return 0
     rows = num_decode_items * num_query_heads
@@ -393,6 +405,8 @@ def decode(
         step.cu_seqlens.data_ptr(),
         _ptr(step.decode_items),
         step.num_decode_items,
+        _ptr(step.merge_items),
+        step.num_merge_items,
         float(scaling),
         out.data_ptr(),
         ws.data_ptr(),

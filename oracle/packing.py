@@ -121,15 +121,22 @@ def scatter_layer_kv(cache: np.ndarray, layer_idx: int, rows: np.ndarray, slots:
 
 
 def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, prefill_tile: int
-               ) -> Tuple[np.ndarray, np.ndarray]:
-    """(seq, partition) pairs of single-token sequences and (seq, query tile)
-    pairs of multi-token ones, ordered by sequence -- the attention work
-    lists the GPU packing kernel emits alongside the reference outputs."""
+               ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Attention work lists the GPU packing kernel emits alongside the
+    reference outputs, all ordered by sequence: (seq, partition) pairs of
+    single-token sequences, the index of the first such pair of every
+    sequence spanning more than one partition, and (seq, query tile) pairs
+    of multi-token sequences."""
     dec: List[Tuple[int, int]] = []
+    merge: List[int] = []
     pre: List[Tuple[int, int]] = []
     for i, (s, c) in enumerate(zip(starts, counts)):
         if c == 1:
-            dec += [(i, p) for p in range(-(-(s + c) // partition))]
+            nparts = -(-(s + c) // partition)
+            if nparts > 1:
+                merge.append(len(dec))
+            dec += [(i, p) for p in range(nparts)]
         elif c > 1:
             pre += [(i, q) for q in range(-(-c // prefill_tile))]
-    return (np.asarray(dec, dtype=np.int32).reshape(-1, 2), np.asarray(pre, dtype=np.int32).reshape(-1, 2))
+    return (np.asarray(dec, dtype=np.int32).reshape(-1, 2), np.asarray(merge, dtype=np.int32),
+            np.asarray(pre, dtype=np.int32).reshape(-1, 2))

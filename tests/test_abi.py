@@ -39,7 +39,7 @@ def test_struct_layouts():
     native = pkg("_native")
     assert ctypes.sizeof(native.PagedAttentionDims) == 32
     assert ctypes.sizeof(native.PaStepDims) == 12 * 4 + 2 * 8
-    assert ctypes.sizeof(native.PaPackDims) == 6 * 4 + 4 * 8
+    assert ctypes.sizeof(native.PaPackDims) == 6 * 4 + 5 * 8
 
 
 def test_error_strings():
@@ -54,7 +54,7 @@ def test_invalid_arguments_rejected_before_launch():
     dims = native.PaStepDims(num_seqs=1, num_query_tokens=1, num_query_heads=6, num_kv_heads=4, head_dim=64,
                              block_size=16, total_blocks=8, num_layers=1, max_blocks_per_seq=1,
                              partition_size=512, dtype=native.PA_DTYPE_BF16, q_token_stride=384, q_head_stride=64)
-    rc = lib.pa_decode(None, None, None, 0, dims, None, None, None, None, 1, 1.0, None, None, 0, None)
+    rc = lib.pa_decode(None, None, None, 0, dims, None, None, None, None, 1, None, 0, 1.0, None, None, 0, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT
     assert b"multiple of num_kv_heads" in lib.pa_last_error_message()
     dims.num_query_heads = 8
@@ -64,7 +64,7 @@ def test_invalid_arguments_rejected_before_launch():
     rc = lib.pa_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 2, 8, 4, 4, 1, 0, 7, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
-    rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None)
+    rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT
 
 
@@ -85,7 +85,7 @@ def test_workspace_size():
     native = pkg("_native")
     lib = native.load_library()
     ops = pkg("paged_ops")
-    dims = native.PaStepDims(num_query_heads=32, head_dim=128)
+    dims = native.PaStepDims(num_query_heads=32, num_kv_heads=8, head_dim=128)
     assert lib.pa_decode_workspace_size(dims, 925) == ops.decode_workspace_bytes(925, 32, 128)
     assert lib.pa_decode_workspace_size(dims, 0) == 0
 

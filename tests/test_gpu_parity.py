@@ -94,7 +94,7 @@ def golden_case(name):
 
 def _pack_expect(starts, counts, lists, bs, partition, tile):
     ctx = [s + c for s, c in zip(starts, counts)]
-    dec, pre = op.work_items(starts, counts, partition, tile)
+    dec, merge, pre = op.work_items(starts, counts, partition, tile)
     return dict(
         cu_seqlens=op.cumulative_offsets(counts),
         cu_context_offsets=op.cumulative_offsets(ctx),
@@ -103,13 +103,14 @@ def _pack_expect(starts, counts, lists, bs, partition, tile):
         position_ids=op.position_ids(starts, counts)[0],
         gather_slots=op.build_slot_mapping(lists, ctx, bs, [0] * len(ctx), ctx),
         decode_items=dec,
+        merge_items=merge,
         prefill_items=pre,
     )
 
 
 def _check_pack(step, exp):
     for name in ("cu_seqlens", "cu_context_offsets", "context_lens", "scatter_slots", "position_ids",
-                 "decode_items", "prefill_items"):
+                 "decode_items", "merge_items", "prefill_items"):
         got = getattr(step, name).cpu().numpy()
         assert got.dtype == exp[name].dtype, name
         assert np.array_equal(got.reshape(exp[name].shape), exp[name]), name
@@ -256,9 +257,12 @@ def test_decode_fp32_matches_oracle(device):
     check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=True)
 
 
-@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (16, 16, 64, torch.bfloat16),
-                                            (16, 2, 64, torch.float32), (8, 4, 128, torch.float32),
-                                            (12, 4, 32, torch.bfloat16)])
+@pytest.mark.parametrize("hq,hkv,d,dtype", [
+    (32, 8, 128, torch.bfloat16), (64, 8, 128, torch.bfloat16), (8, 4, 128, torch.bfloat16),
+    (4, 4, 128, torch.bfloat16), (16, 16, 64, torch.bfloat16), (8, 4, 64, torch.bfloat16),
+    (32, 8, 64, torch.bfloat16), (16, 2, 64, torch.bfloat16), (16, 2, 64, torch.float32),
+    (8, 4, 128, torch.float32), (8, 8, 128, torch.float32), (32, 8, 128, torch.float32),
+    (8, 1, 64, torch.float32), (12, 4, 32, torch.bfloat16), (12, 4, 128, torch.bfloat16)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
