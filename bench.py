@@ -105,6 +105,19 @@ def cpu_baseline(w, t, budget_s: float):
     }
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel on `workload`, from the
+    committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled
+    by what the counter reads for a copy of known size); None if absent."""
+    path = REPO / "profiles" / "pmc_traffic.json"
+    try:
+        table = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = table.get(workload)
+    return int(entry["traffic_bytes"]) if entry else None
+
+
 def calibrate_copy(device, nbytes: int = 1 << 30, reps: int = 5) -> None:
     """A plain device-to-device copy of known size (for scaling the PMC
     FETCH_SIZE / WRITE_SIZE counters of the profiled kernels)."""
@@ -151,15 +164,33 @@ def main() -> int:
     t = wl.make_tensors(w, device, seed=args.seed)
     table = torch.from_numpy(w.block_table_array()).to(device)
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
-    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
+                            num_kv_heads=w.num_kv_heads)
     out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
     stream = torch.cuda.current_stream(device)
 
     def decode_step():
         ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
 
+    def partition_kernel_ms(steps, warmup):
+        """Average duration of the dominant kernel (the split-K partition
+        kernel): the step is issued as pa_decode's two phases and HIP events
+        on the launch stream bracket every partition launch."""
+        pairs = []
+        for i in range(warmup + steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1)
+            b.record(stream)
+            ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2)
+            if i >= warmup:
+                pairs.append((a, b))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
     def full_step():
-        s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile)
+        s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
+                            num_kv_heads=w.num_kv_heads)
         ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
         ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
 
@@ -177,10 +208,13 @@ def main() -> int:
         return start.elapsed_time(stop) / steps  # ms
 
     ms = timed(decode_step, args.steps, args.warmup)
+    kernel_ms = partition_kernel_ms(args.steps, args.warmup)
     full_ms = timed(full_step, max(5, args.steps // 5), 2)
 
     kv_bytes = wl.decode_bytes(w)
     gbs = kv_bytes / (ms * 1e-3) / 1e9
+    kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
+    traffic = measured_traffic(w.name)
     tokens_per_s = w.num_query_tokens / (ms * 1e-3)
     result = {
         "metric": METRIC,
@@ -211,11 +245,14 @@ def main() -> int:
         "full_step_ms": round(full_ms, 5),
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gbs, 2),
+            "kernel": "decode_partition_kernel",
+            "achieved": round(kernel_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel_ms": round(kernel_ms, 5),
+            "algorithmic_bytes": kv_bytes,
         },
     }
     if args.config == 5:

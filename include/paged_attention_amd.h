@@ -40,8 +40,11 @@ enum {
 /* Element type tags for K/V/query/output buffers. */
 enum { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1, PA_DTYPE_F16 = 2 };
 
-/* Default split-K partition of the decode kernel, in context tokens. */
-#define PA_DECODE_PARTITION 512
+/* Default split-K partition of the decode kernel, in context tokens, and the
+ * largest one its fast path takes (larger or non-multiple-of-32 partitions
+ * run on the generic kernel). */
+#define PA_DECODE_PARTITION 1024
+#define PA_DECODE_MAX_PARTITION 2048
 
 /* ---- (0) reference ABI, device pointers -------------------------------- */
 
@@ -200,6 +203,27 @@ int pa_decode(const void *query, const void *key_cache,
               int64_t num_decode_items, const int32_t *merge_items,
               int64_t num_merge_items, float scaling, void *output,
               void *workspace, size_t workspace_bytes, void *stream);
+
+/* Phases of pa_decode, for callers that launch them separately. */
+enum { PA_DECODE_PHASE_PARTITIONS = 1, PA_DECODE_PHASE_MERGE = 2 };
+
+/*
+ * pa_decode split in its two launches (same arguments and rules).  The
+ * partition phase writes the final rows of single-partition sequences and
+ * the split-K partials of the others into `workspace`; the merge phase then
+ * combines those partials (a no-op when every sequence fits one partition
+ * or the step runs on the generic kernel).  pa_decode(...) equals
+ * pa_decode_phases(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE, ...),
+ * and a partition call followed by a merge call on one stream gives the same
+ * bits.  No reference counterpart: the reference's decode is one CPU call.
+ */
+int pa_decode_phases(int32_t phases, const void *query, const void *key_cache,
+                     const void *value_cache, int32_t layer_idx, PaStepDims dims,
+                     const int32_t *block_tables, const int32_t *context_lens,
+                     const int64_t *cu_seqlens, const int32_t *decode_items,
+                     int64_t num_decode_items, const int32_t *merge_items,
+                     int64_t num_merge_items, float scaling, void *output,
+                     void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- (d) causal chunked prefill ----------------------------------------- */
 

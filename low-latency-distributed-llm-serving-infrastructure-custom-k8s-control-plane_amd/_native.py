@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -26,7 +26,10 @@ PA_DTYPE_F32 = 0
 PA_DTYPE_BF16 = 1
 PA_DTYPE_F16 = 2
 
-PA_DECODE_PARTITION = 512
+PA_DECODE_PARTITION = 1024
+PA_DECODE_MAX_PARTITION = 2048
+PA_DECODE_PHASE_PARTITIONS = 1
+PA_DECODE_PHASE_MERGE = 2
 
 #: Every symbol the header declares; tests check the library exports them all.
 EXPORTED_SYMBOLS = (
@@ -36,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "pa_reshape_and_cache",
     "pa_decode_workspace_size",
     "pa_decode",
+    "pa_decode_phases",
     "pa_prefill",
     "pa_error_string",
     "pa_last_error_message",
@@ -111,6 +115,10 @@ _SIGNATURES = {
     "pa_decode": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
+    ),
+    "pa_decode_phases": (
+        ctypes.c_int,
+        [_i32, _vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
     ),
     "pa_prefill": (
         ctypes.c_int,

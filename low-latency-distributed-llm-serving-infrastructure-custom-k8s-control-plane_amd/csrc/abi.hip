@@ -69,7 +69,7 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 extern "C" {
 
-int pa_abi_version(void) { return 2; }
+int pa_abi_version(void) { return 3; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -240,6 +240,22 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
               const int32_t* decode_items, int64_t num_decode_items,
               const int32_t* merge_items, int64_t num_merge_items, float scaling,
               void* output, void* workspace, size_t workspace_bytes, void* stream) {
+  return pa_decode_phases(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE, query, key_cache,
+                          value_cache, layer_idx, dims, block_tables, context_lens, cu_seqlens,
+                          decode_items, num_decode_items, merge_items, num_merge_items, scaling,
+                          output, workspace, workspace_bytes, stream);
+}
+
+int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
+                     const void* value_cache, int32_t layer_idx, PaStepDims dims,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const int64_t* cu_seqlens, const int32_t* decode_items,
+                     int64_t num_decode_items, const int32_t* merge_items,
+                     int64_t num_merge_items, float scaling, void* output, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (phases <= 0 || (phases & ~(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE)) != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: phases must be a non-empty mask of "
+                "PA_DECODE_PHASE_PARTITIONS and PA_DECODE_PHASE_MERGE, got %d", phases);
   int rc = check_step(dims, "pa_decode");
   if (rc != PA_OK) return rc;
   if (layer_idx < 0 || layer_idx >= dims.num_layers)
@@ -287,12 +303,16 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
     a.log2_block_size = log2_bs;
     a.partition = dims.partition_size;
     a.scale_log2e = scaling * pa::kLog2e;
-    return from_hip(pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, s),
-                    "pa_decode");
+    return from_hip(
+        pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s),
+        "pa_decode");
   }
   if (!pa::generic_supported(dims.dtype, dims.head_dim))
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: head_dim %d / dtype %d not supported",
                 dims.head_dim, dims.dtype);
+  // The generic kernel finishes every row in one pass: it is the partition
+  // phase, and the merge phase has nothing to do.
+  if (!(phases & PA_DECODE_PHASE_PARTITIONS)) return PA_OK;
   pa::GenericArgs a{};
   a.query = query;
   a.q_token_stride = dims.q_token_stride;

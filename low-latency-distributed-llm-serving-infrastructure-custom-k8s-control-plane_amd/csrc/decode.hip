@@ -1,5 +1,6 @@
 // Paged-attention decode for gfx950: one workgroup per
-// (sequence, 512-token context partition, KV head), split-K merge after.
+// (sequence, context partition of up to 2048 tokens, KV head), split-K merge
+// after.
 //
 // The workgroup (4 waves) serves the G = H_q / H_kv query heads that share
 // one KV head, so every K/V row of the partition is read from HBM once.
@@ -39,7 +40,7 @@ namespace pa {
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeWaves = kDecodeThreads / kWave;
 // Largest split-K partition (context tokens per workgroup) the kernel takes.
-constexpr int kMaxPartition = 2048;
+constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #ifndef PA_DECODE_TILE
 #define PA_DECODE_TILE 32  // context tokens per wave iteration (at least 2 rows per group)
 #endif
@@ -674,26 +675,30 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
 // ---- host-side dispatch ------------------------------------------------
 
 template <typename T, int D, int G>
-static hipError_t launch_decode_t(const DecodeArgs& a, int64_t num_items, hipStream_t stream) {
+static hipError_t launch_decode_t(const DecodeArgs& a, int64_t num_items, int phases,
+                                  hipStream_t stream) {
   const int64_t grid = num_items * a.num_kv_heads;
   const int64_t merge_grid = a.num_merge * a.num_kv_heads;
-  hipLaunchKernelGGL((decode_partition_kernel<T, D, G>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(kDecodeThreads), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  if (merge_grid <= 0) return hipSuccess;
+  if (phases & PA_DECODE_PHASE_PARTITIONS) {
+    hipLaunchKernelGGL((decode_partition_kernel<T, D, G>), dim3(static_cast<uint32_t>(grid)),
+                       dim3(kDecodeThreads), 0, stream, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(static_cast<uint32_t>(merge_grid)),
                      dim3(kDecodeThreads), 0, stream, a, G, D);
   return hipGetLastError();
 }
 
 template <typename T, int D>
-static hipError_t launch_decode_g(const DecodeArgs& a, int G, int64_t num_items, hipStream_t s) {
+static hipError_t launch_decode_g(const DecodeArgs& a, int G, int64_t num_items, int phases,
+                                  hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode_t<T, D, 1>(a, num_items, s);
-    case 2: return launch_decode_t<T, D, 2>(a, num_items, s);
-    case 4: return launch_decode_t<T, D, 4>(a, num_items, s);
-    case 8: return launch_decode_t<T, D, 8>(a, num_items, s);
+    case 1: return launch_decode_t<T, D, 1>(a, num_items, phases, s);
+    case 2: return launch_decode_t<T, D, 2>(a, num_items, phases, s);
+    case 4: return launch_decode_t<T, D, 4>(a, num_items, phases, s);
+    case 8: return launch_decode_t<T, D, 8>(a, num_items, phases, s);
     default: return hipErrorNotSupported;
   }
 }
@@ -709,14 +714,14 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
-                         int64_t num_items, hipStream_t stream) {
+                         int64_t num_items, int phases, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return launch_decode_g<bf16_t, 128>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_decode_g<bf16_t, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_decode_g<bf16_t, 128>(a, group, num_items, phases, stream);
+    if (head_dim == 64) return launch_decode_g<bf16_t, 64>(a, group, num_items, phases, stream);
   } else if (dtype == PA_DTYPE_F32) {
-    if (head_dim == 128) return launch_decode_g<float, 128>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_decode_g<float, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_decode_g<float, 128>(a, group, num_items, phases, stream);
+    if (head_dim == 64) return launch_decode_g<float, 64>(a, group, num_items, phases, stream);
   }
   return hipErrorNotSupported;
 }

@@ -126,8 +126,9 @@ struct PrefillArgs {
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition);
+// phases: PA_DECODE_PHASE_PARTITIONS and/or PA_DECODE_PHASE_MERGE.
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
-                         int64_t num_items, hipStream_t stream);
+                         int64_t num_items, int phases, hipStream_t stream);
 
 bool generic_supported(int dtype, int head_dim);
 hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStream_t stream);

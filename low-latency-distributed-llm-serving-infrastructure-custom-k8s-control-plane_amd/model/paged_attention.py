@@ -15,7 +15,6 @@ from __future__ import annotations
 from typing import List, Optional, Sequence as SequenceABC
 
 import torch
-import torch.nn.functional as F
 
 from .. import paged_ops
 from ..memory.manager import PagedKVCacheManager
@@ -86,6 +85,7 @@ class PagedStepContext:
                     self.new_token_counts,
                     store.block_size,
                     prefill_tile=prefill_tile,
+                    num_kv_heads=store.num_heads,
                 )
                 self.scatter_slots = self.packed.scatter_slots
             else:
@@ -111,6 +111,7 @@ class PagedStepContext:
                 self.new_token_counts,
                 self.store.block_size,
                 prefill_tile=tile,
+                partition_size=self.packed.partition_size,
                 start_positions_dev=self.packed.start_positions,
                 new_token_counts_dev=self.packed.new_token_counts,
             )
@@ -207,25 +208,13 @@ def paged_attention_forward(
 
     scale = scaling if scaling is not None else module.scaling
     backend = _BACKEND
-    if backend is not None and backend.supports(context, query.shape[2]):
-        return backend.attend(query, store, layer_idx, context, scale, dropout), None
+    if backend is not None and not backend.supports(context, query.shape[2]):
+        backend = _get_fallback_backend()
     if backend is not None:
-        return _get_fallback_backend().attend(query, store, layer_idx, context, scale, dropout), None
+        return backend.attend(query, store, layer_idx, context, scale, dropout), None
+    from .attention_backends import dense_sdpa
 
-    context_keys = store.gather_layer_keys(layer_idx, context.gather_slots)
-    context_values = store.gather_layer_values(layer_idx, context.gather_slots)
-    context_keys = context_keys.unsqueeze(0).transpose(1, 2)
-    context_values = context_values.unsqueeze(0).transpose(1, 2)
-    attn_output = F.scaled_dot_product_attention(
-        query,
-        context_keys,
-        context_values,
-        attn_mask=context.attention_mask(query.device),
-        dropout_p=dropout,
-        scale=scale,
-        enable_gqa=context_keys.shape[1] != query.shape[1],
-    )
-    return attn_output.transpose(1, 2).contiguous(), None
+    return dense_sdpa(query, store, layer_idx, context, scale, dropout), None
 
 
 def register_paged_attention(model) -> None:

@@ -22,7 +22,7 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _native
-from ._native import PA_DECODE_PARTITION
+from ._native import PA_DECODE_PARTITION, PA_DECODE_MAX_PARTITION
 
 _DTYPES = {
     torch.float32: _native.PA_DTYPE_F32,
@@ -151,6 +151,33 @@ def work_counts(
     return t, c, ditems, mitems, pitems, ndec, npre
 
 
+# Fewest decode workgroups (partitions x KV heads) a step should launch:
+# eight per compute unit of the 256 on MI355X.
+_MIN_DECODE_WORKGROUPS = 2048
+
+
+def choose_partition(
+    start_positions: Sequence[int],
+    new_token_counts: Sequence[int],
+    num_kv_heads: int = 8,
+) -> int:
+    """Split-K partition for the decode sequences of a step.
+
+    The default partition (1024 tokens) keeps the number of partials and the
+    per-workgroup set-up small; when the step's decode work would launch
+    fewer than 2048 workgroups it is halved (down to 256 tokens) so short
+    batches still spread over the whole chip.
+    """
+    ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
+    p = PA_DECODE_PARTITION
+    while p > 256:
+        items = sum(-(-x // p) for x in ctx)
+        if items * max(int(num_kv_heads), 1) >= _MIN_DECODE_WORKGROUPS:
+            break
+        p //= 2
+    return p
+
+
 def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Tensor]:
     lib = _native.load_library()
     device = _require_device(step.block_tables)
@@ -196,7 +223,8 @@ def pack_step(
     block_size: int,
     *,
     prefill_tile: int = 32,
-    partition_size: int = PA_DECODE_PARTITION,
+    partition_size: Optional[int] = None,
+    num_kv_heads: int = 8,
     with_gather: bool = False,
     start_positions_dev: Optional[torch.Tensor] = None,
     new_token_counts_dev: Optional[torch.Tensor] = None,
@@ -206,6 +234,8 @@ def pack_step(
     ``block_tables``: int32 [B, max_blocks] device tensor (-1 padded).
     ``start_positions`` / ``new_token_counts``: the host lists of the step
     (also uploaded unless device copies are passed in).
+    ``partition_size``: decode split-K partition in tokens; by default
+    :func:`choose_partition` picks it from the step and ``num_kv_heads``.
     """
     device = _require_device(block_tables)
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
@@ -217,6 +247,10 @@ def pack_step(
         raise ValueError("start_positions / new_token_counts must have one entry per block-table row")
     if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
         raise ValueError("start positions and token counts must be non-negative")
+    if partition_size is None:
+        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads)
+    if partition_size <= 0:
+        raise ValueError("partition_size must be positive")
     t, c, ditems, mitems, pitems, ndec, npre = work_counts(
         start_positions, new_token_counts, partition_size, prefill_tile)
     if start_positions_dev is None:
@@ -381,10 +415,13 @@ def decode(
     step: PackedStep,
     scaling: float,
     out: Optional[torch.Tensor] = None,
+    phases: int = _native.PA_DECODE_PHASE_PARTITIONS | _native.PA_DECODE_PHASE_MERGE,
 ) -> torch.Tensor:
     """Split-K paged decode for the single-token sequences of ``step``.
 
     Returns (or fills) ``out`` [T, H_q, D]; rows of other tokens are untouched.
+    ``phases`` launches only the partition and/or the merge phase (a merge
+    call must follow a partition call of the same step and workspace).
     """
     q = _query_view(query)
     device = _require_device(q, key_cache, value_cache, step.block_tables)
@@ -394,7 +431,8 @@ def decode(
     dims = _step_dims(q, key_cache, step)
     ws = step.workspace(int(q.shape[1]), int(q.shape[2]), device)
     lib = _native.load_library()
-    status = lib.pa_decode(
+    status = lib.pa_decode_phases(
+        int(phases),
         q.data_ptr(),
         key_cache.data_ptr(),
         value_cache.data_ptr(),

@@ -193,14 +193,15 @@ def make_tensors(w: StepWorkload, device: torch.device, seed: int = 0) -> StepTe
 
 
 def decode_bytes(w: StepWorkload) -> int:
-    """Algorithmic HBM bytes of one decode launch:
-    K+V once per (context token, KV head) + q and out rows + block-table
-    entries + one context length per sequence."""
+    """Algorithmic HBM bytes of one decode launch over the single-token
+    sequences of the step: K+V once per (context token, KV head) + q and out
+    rows + block-table entries + one context length per sequence."""
     e = torch.tensor([], dtype=w.dtype).element_size()
-    kv = w.num_context_tokens * 2 * w.num_kv_heads * w.head_dim * e
-    qo = w.num_seqs * w.num_query_heads * w.head_dim * 2 * e
-    bt = sum(-(-c // w.block_size) for c in w.context_lens) * 4
-    return kv + qo + bt + 4 * w.num_seqs
+    ctx = [s + n for s, n in zip(w.start_positions, w.new_token_counts) if n == 1]
+    kv = sum(ctx) * 2 * w.num_kv_heads * w.head_dim * e
+    qo = len(ctx) * w.num_query_heads * w.head_dim * 2 * e
+    bt = sum(-(-c // w.block_size) for c in ctx) * 4
+    return kv + qo + bt + 4 * len(ctx)
 
 
 def decode_flops(w: StepWorkload) -> int:

@@ -63,6 +63,11 @@ def test_invalid_arguments_rejected_before_launch():
     assert b"Layer index 3 out of range" in lib.pa_last_error_message()
     rc = lib.pa_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 2, 8, 4, 4, 1, 0, 7, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT
+    for phases in (0, 4, -1):
+        rc = lib.pa_decode_phases(phases, None, None, None, 0, dims, None, None, None, None, 1, None, 0, 1.0,
+                                  None, None, 0, None)
+        assert rc == native.PA_ERR_INVALID_ARGUMENT
+        assert b"phases must be" in lib.pa_last_error_message()
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
     rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT

@@ -39,11 +39,12 @@ def log(msg):
 # helpers
 
 
-def pack_workload(w, device, prefill_tile=None, with_gather=False):
+def pack_workload(w, device, prefill_tile=None, with_gather=False, partition=None):
     table = torch.from_numpy(w.block_table_array()).to(device)
     tile = prefill_tile or ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     return ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
-                         prefill_tile=tile, with_gather=with_gather)
+                         prefill_tile=tile, with_gather=with_gather, partition_size=partition,
+                         num_kv_heads=w.num_kv_heads)
 
 
 def oracle_rows(w, t, seqs):
@@ -124,7 +125,8 @@ def test_pack_matches_oracle_on_workloads(device, cfg):
     log(f"pack cfg{cfg}: B={w.num_seqs} T={w.num_query_tokens} C={w.num_context_tokens}")
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     step = pack_workload(w, device, with_gather=True)
-    exp = _pack_expect(w.start_positions, w.new_token_counts, w.block_lists, w.block_size, 512, tile)
+    exp = _pack_expect(w.start_positions, w.new_token_counts, w.block_lists, w.block_size,
+                       step.partition_size, tile)
     _check_pack(step, exp)
 
 
@@ -142,8 +144,9 @@ def test_pack_matches_oracle_on_ragged_edges(device, seed):
         lists.append([int(x) for x in perm[off : off + n]])
         off += n
     table = torch.from_numpy(op.build_block_tables(lists, [s + c for s, c in zip(starts, counts)])[0]).to(device)
-    step = ops.pack_step(table, starts, counts, bs, prefill_tile=16, with_gather=True)
-    _check_pack(step, _pack_expect(starts, counts, lists, bs, 512, 16))
+    partition = [None, 32, 512, 100][seed]
+    step = ops.pack_step(table, starts, counts, bs, prefill_tile=16, with_gather=True, partition_size=partition)
+    _check_pack(step, _pack_expect(starts, counts, lists, bs, step.partition_size, 16))
 
 
 def test_pack_empty_batch(device):
@@ -280,6 +283,40 @@ def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=dtype == torch.float32)
 
 
+@pytest.mark.parametrize("partition", [32, 256, 1024, 2048, 96, 100, 4096])
+def test_decode_partition_sizes(device, partition):
+    """Every split-K partition gives the oracle's result: multiples of 32 up
+    to 2048 on the fast kernel, others (100, 4096) on the generic one."""
+    rng = np.random.Generator(np.random.PCG64(partition))
+    ctx = [1, 31, 32, 33, 100, 2047, 2048, 2049, 5000]
+    need = [-(-c // 16) for c in ctx]
+    perm = rng.permutation(sum(need))
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    w = wl.StepWorkload("decode_partitions", 32, 8, 128, 16, torch.bfloat16, 1.0, [c - 1 for c in ctx],
+                        [1] * len(ctx), lists, sum(need))
+    t = wl.make_tensors(w, device, seed=6)
+    step = pack_workload(w, device, partition=partition)
+    log(f"decode partition={partition} items={step.num_decode_items} merges={step.num_merge_items}")
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=False)
+
+
+def test_decode_phases_equal_one_call(device):
+    """Partition phase then merge phase (two launches) gives pa_decode's bits."""
+    w = wl.llama3_8b_gqa_decode(seed=2)
+    t = wl.make_tensors(w, device, seed=2)
+    step = pack_workload(w, device, partition=512)
+    assert step.num_merge_items > 0
+    whole = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    split = torch.zeros_like(whole)
+    ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=split, phases=1)
+    ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=split, phases=2)
+    assert torch.equal(whole.view(torch.int16), split.view(torch.int16))
+
+
 def test_decode_properties_full_size(device):
     """Size-independent properties on the whole GQA batch: the output depends
     only on logical context (moving blocks + table gives identical bits) and
@@ -309,7 +346,9 @@ def test_decode_properties_full_size(device):
                          [w.start_positions[i] for i in sub], [1] * len(sub), [w.block_lists[i] for i in sub],
                          w.total_blocks)
     q_sub = t.query[:, :, 10:20]
-    alone = ops.decode(q_sub, t.key_cache, t.value_cache, 0, pack_workload(w3, device), w.scaling)
+    # (the same split-K partition: a different one changes the rounding)
+    alone = ops.decode(q_sub, t.key_cache, t.value_cache, 0,
+                       pack_workload(w3, device, partition=step.partition_size), w.scaling)
     assert torch.equal(alone.view(torch.int16), base[10:20].view(torch.int16))
 
 

@@ -1,0 +1,304 @@
+"""Host-side operator API on the CPU: backend selection and dispatch, step
+bookkeeping, KV-cache manager errors, and the host helpers that size the
+GPU work lists.
+
+These follow the reference's own unit tests case by case
+(tests/unit/test_attention_backends.py, tests/unit/test_kv_cache.py), with
+the known answers those tests hold.  The torch SDPA backend checked here is
+the reference's own fallback interface; the HIP path is covered by the GPU
+parity tests.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import pkg
+from oracle import packing as op
+
+paged_attention = pkg("model.paged_attention")
+backends = pkg("model.attention_backends")
+manager_mod = pkg("memory.manager")
+sequence_mod = pkg("scheduler.sequence")
+ops = pkg("paged_ops")
+
+NUM_LAYERS = 4
+NUM_KV_HEADS = 2
+HEAD_DIM = 8
+BLOCK_SIZE = 4
+AVAILABLE = backends.__name__ + ".native_kernel_available"
+
+
+@pytest.fixture
+def store():
+    return manager_mod.PagedKVCacheManager(total_blocks=8, block_size=BLOCK_SIZE, num_heads=NUM_KV_HEADS,
+                                           head_dim=HEAD_DIM, num_layers=NUM_LAYERS, device="cpu")
+
+
+def _prefill_step(store, prompt_lens):
+    seqs = []
+    for i, n in enumerate(prompt_lens):
+        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        store.allocate_prefix_blocks(seq)
+        seqs.append(seq)
+    return seqs, paged_attention.PagedStepContext(store, seqs, [0] * len(seqs), list(prompt_lens))
+
+
+class _Layer:
+    layer_idx = 0
+    scaling = 0.35
+
+    def __init__(self, context):
+        self.paged_context = context
+
+
+# ---- select_backend (attention_backends.py:120-144) -----------------------
+
+
+def test_auto_selects_torch_without_native_library(monkeypatch):
+    monkeypatch.delenv("LLM_PAGED_BACKEND", raising=False)
+    monkeypatch.setattr(AVAILABLE, lambda: False)
+    assert isinstance(backends.select_backend(), backends.TorchSdpBackend)
+
+
+def test_auto_prefers_native_when_available(monkeypatch):
+    monkeypatch.delenv("LLM_PAGED_BACKEND", raising=False)
+    monkeypatch.setattr(AVAILABLE, lambda: True)
+    assert isinstance(backends.select_backend(), backends.NativePagedBackend)
+
+
+def test_torch_backend_can_always_be_requested(monkeypatch):
+    monkeypatch.setenv("LLM_PAGED_BACKEND", "torch")
+    assert isinstance(backends.select_backend(), backends.TorchSdpBackend)
+
+
+def test_native_request_without_library_raises(monkeypatch):
+    monkeypatch.setenv("LLM_PAGED_BACKEND", "native")
+    monkeypatch.setattr(AVAILABLE, lambda: False)
+    with pytest.raises(RuntimeError):
+        backends.select_backend()
+
+
+def test_unknown_backend_name_raises(monkeypatch):
+    monkeypatch.setenv("LLM_PAGED_BACKEND", "flash")
+    with pytest.raises(ValueError):
+        backends.select_backend()
+
+
+def test_hip_is_an_alias_of_native(monkeypatch):
+    monkeypatch.setenv("LLM_PAGED_BACKEND", "hip")
+    monkeypatch.setattr(AVAILABLE, lambda: True)
+    assert isinstance(backends.select_backend(), backends.NativePagedBackend)
+
+
+def test_native_kernel_unavailable_without_rocm_device():
+    if torch.cuda.is_available():
+        pytest.skip("a ROCm device is visible")
+    assert backends.native_kernel_available() is False
+
+
+# ---- supports / attend / dispatch ------------------------------------------
+
+
+def test_native_backend_refuses_cpu_store(store):
+    # The HIP backend serves every step shape of a GPU store; a CPU store has
+    # no packed step, so the hook falls back (attention_backends.py:85-86
+    # refuses prefill shapes in the reference for the same effect).
+    _, prefill = _prefill_step(store, [4, 2])
+    assert prefill.packed is None
+    assert backends.NativePagedBackend().supports(prefill, prefill.num_query_tokens) is False
+    assert backends.TorchSdpBackend().supports(prefill, prefill.num_query_tokens) is True
+
+
+def test_native_attend_reports_missing_library(store, monkeypatch):
+    _, context = _prefill_step(store, [4, 2])
+    monkeypatch.setattr(AVAILABLE, lambda: False)
+    with pytest.raises(RuntimeError):
+        backends.NativePagedBackend().attend(torch.randn(1, NUM_KV_HEADS, 6, HEAD_DIM), store, 0, context,
+                                             0.35, 0.0)
+
+
+def test_dispatch_falls_back_when_backend_refuses_shape(store, monkeypatch):
+    _, context = _prefill_step(store, [4, 2])
+    q, k, v = (torch.randn(1, NUM_KV_HEADS, 6, HEAD_DIM) for _ in range(3))
+
+    class Refusing(backends.NativePagedBackend):
+        calls = 0
+
+        def supports(self, context, num_query_tokens):
+            return False
+
+        def attend(self, *args, **kwargs):
+            Refusing.calls += 1
+            raise AssertionError("attend must not run for a refused shape")
+
+    monkeypatch.setattr(paged_attention, "_BACKEND", Refusing())
+    out, weights = paged_attention.paged_attention_forward(_Layer(context), q, k, v, None, dropout=0.0,
+                                                           scaling=0.35)
+    assert Refusing.calls == 0
+    assert out.shape == (1, 6, NUM_KV_HEADS, HEAD_DIM)
+    assert weights is None
+
+
+def test_dispatch_routes_supported_shape_to_backend(store, monkeypatch):
+    _, context = _prefill_step(store, [4, 2])
+    q, k, v = (torch.randn(1, NUM_KV_HEADS, 6, HEAD_DIM) for _ in range(3))
+
+    class Recording(backends.TorchSdpBackend):
+        calls = 0
+
+        def attend(self, *args, **kwargs):
+            Recording.calls += 1
+            return super().attend(*args, **kwargs)
+
+    monkeypatch.setattr(paged_attention, "_BACKEND", Recording())
+    paged_attention.paged_attention_forward(_Layer(context), q, k, v, None, dropout=0.0, scaling=0.35)
+    assert Recording.calls == 1
+
+
+def test_inline_path_equals_installed_torch_backend(store, monkeypatch):
+    _, context = _prefill_step(store, [4, 2])
+    torch.manual_seed(3)
+    q, k, v = (torch.randn(1, NUM_KV_HEADS, 6, HEAD_DIM) for _ in range(3))
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    inline, _ = paged_attention.paged_attention_forward(_Layer(context), q, k, v, None, scaling=0.35)
+    monkeypatch.setattr(paged_attention, "_BACKEND", backends.TorchSdpBackend())
+    routed, _ = paged_attention.paged_attention_forward(_Layer(context), q, k, v, None, scaling=0.35)
+    assert torch.equal(inline, routed)
+
+
+# ---- step bookkeeping (test_attention_backends.py:175-243) ----------------
+
+
+def test_cu_seqlens_and_context_offsets(store):
+    _, context = _prefill_step(store, [4, 2, 3])
+    assert context.cu_seqlens.tolist() == [0, 4, 6, 9]
+    assert context.cu_context_offsets.tolist() == [0, 4, 6, 9]
+    assert context.context_lens == [4, 2, 3]
+    assert context.num_query_tokens == 9 and context.num_context_tokens == 9
+
+
+def test_position_ids_prefill_and_decode(store):
+    _, context = _prefill_step(store, [4, 2])
+    assert context.position_ids(torch.device("cpu")).tolist() == [[0, 1, 2, 3, 0, 1]]
+    seqs = []
+    other = manager_mod.PagedKVCacheManager(total_blocks=8, block_size=BLOCK_SIZE, num_heads=NUM_KV_HEADS,
+                                            head_dim=HEAD_DIM, num_layers=NUM_LAYERS, device="cpu")
+    for i, n in enumerate([4, 2]):
+        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        other.allocate_prefix_blocks(seq)
+        other.allocate_slot_for_next_token(seq)
+        seqs.append(seq)
+    starts = [s.block_table.get_tokens_count() - 1 for s in seqs]
+    decode = paged_attention.PagedStepContext(other, seqs, starts, [1, 1])
+    assert decode.position_ids(torch.device("cpu")).tolist() == [[4, 2]]
+
+
+def test_attention_mask_matches_oracle(store):
+    _, context = _prefill_step(store, [4, 2])
+    mask = context.attention_mask(torch.device("cpu"))
+    assert mask.shape == (1, 1, 6, 6)
+    assert mask.numpy().tolist() == op.attention_mask([0, 0], [4, 2]).tolist()
+
+
+def test_scatter_then_gather_round_trip(store):
+    _, context = _prefill_step(store, [4, 2])
+    torch.manual_seed(123)
+    kv = torch.randn(context.num_context_tokens, NUM_LAYERS, NUM_KV_HEADS, HEAD_DIM)
+    store.scatter_kv(kv, kv, context.scatter_slots)
+    for layer in range(NUM_LAYERS):
+        assert torch.equal(store.gather_layer_keys(layer, context.gather_slots), kv[:, layer])
+        assert torch.equal(store.gather_layer_values(layer, context.gather_slots), kv[:, layer])
+
+
+@pytest.mark.parametrize("num_query_heads", [NUM_KV_HEADS, 6])
+def test_torch_backend_matches_closed_form_attention(store, num_query_heads):
+    _, context = _prefill_step(store, [4, 2])
+    torch.manual_seed(42)
+    kv = torch.randn(context.num_context_tokens, NUM_LAYERS, NUM_KV_HEADS, HEAD_DIM)
+    store.scatter_kv(kv, kv, context.scatter_slots)
+    q = torch.randn(1, num_query_heads, context.num_query_tokens, HEAD_DIM)
+    out = backends.TorchSdpBackend().attend(q, store, 0, context, 0.35, 0.0)
+    assert out.shape == (1, context.num_query_tokens, num_query_heads, HEAD_DIM)
+    # float64 softmax attention written out, GQA by head repetition
+    k = store.gather_layer_keys(0, context.gather_slots).double()  # [C, Hkv, D]
+    rep = num_query_heads // NUM_KV_HEADS
+    k = k.repeat_interleave(rep, dim=1).transpose(0, 1)  # [Hq, C, D]
+    mask = context.attention_mask(torch.device("cpu"))[0, 0]
+    s = torch.einsum("htd,hcd->htc", q[0].double(), k) * 0.35
+    s = s.masked_fill(~mask, float("-inf"))
+    want = torch.einsum("htc,hcd->thd", torch.softmax(s, dim=-1), k)
+    assert torch.allclose(out[0].double(), want, atol=1e-6)
+
+
+# ---- manager errors (test_kv_cache.py:50-62,206-225) ----------------------
+
+
+def _kv_manager():
+    return manager_mod.PagedKVCacheManager(total_blocks=10, block_size=4, num_heads=2, head_dim=8,
+                                           device="cpu", num_layers=1)
+
+
+def test_slot_mapping_requires_block_table():
+    with pytest.raises(ValueError, match="no block table"):
+        _kv_manager().build_slot_mapping([sequence_mod.Sequence(seq_id=5, prompt_token_ids=[1])], [0], [1])
+
+
+def test_single_token_write_requires_block_table():
+    token = torch.zeros(1, 2, 8)
+    with pytest.raises(ValueError, match="no block table"):
+        _kv_manager().write_single_token_kv(sequence_mod.Sequence(seq_id=4, prompt_token_ids=[1]), token, token)
+
+
+def test_slot_mapping_range_and_length_errors():
+    m = _kv_manager()
+    seq = sequence_mod.Sequence(seq_id=1, prompt_token_ids=[1, 2, 3, 4])
+    m.allocate_prefix_blocks(seq)
+    with pytest.raises(ValueError):
+        m.build_slot_mapping([seq], [0], [5])
+    with pytest.raises(ValueError):
+        m.build_slot_mapping([seq], [0, 1], [4])
+    slots = m.build_slot_mapping([seq], [0], [2])
+    with pytest.raises(ValueError):
+        m.scatter_kv(torch.randn(2, 2, 8), torch.randn(2, 2, 8), slots)
+
+
+def test_manager_slots_and_tables_match_oracle():
+    m = _kv_manager()
+    seqs = []
+    for i, n in enumerate([3, 7, 1]):
+        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        m.allocate_prefix_blocks(seq)
+        seqs.append(seq)
+    lists = [s.block_table.get_physical_blocks() for s in seqs]
+    counts = [3, 7, 1]
+    got = m.build_slot_mapping(seqs, [0, 2, 0], [3, 5, 1])
+    assert got.tolist() == op.build_slot_mapping(lists, counts, 4, [0, 2, 0], [3, 5, 1]).tolist()
+    table, lens = m.build_block_tables(seqs)
+    want_table, want_lens = op.build_block_tables(lists, counts)
+    assert table.cpu().tolist() == want_table.tolist() and lens.cpu().tolist() == want_lens.tolist()
+
+
+# ---- host sizing of the GPU work lists -------------------------------------
+
+
+@pytest.mark.parametrize("partition,tile", [(512, 32), (1024, 16), (32, 128), (100, 4)])
+def test_work_counts_match_oracle_work_lists(partition, tile):
+    starts = [0, 600, 1100, 0, 7, 2047, 5000]
+    counts = [300, 1, 1, 5, 1, 1, 0]
+    t, c, ditems, mitems, pitems, ndec, npre = ops.work_counts(starts, counts, partition, tile)
+    dec, merge, pre = op.work_items(starts, counts, partition, tile)
+    assert (t, c) == (sum(counts), sum(s + n for s, n in zip(starts, counts)))
+    assert (ditems, mitems, pitems) == (len(dec), len(merge), len(pre))
+    assert (ndec, npre) == (4, 2)
+
+
+def test_choose_partition_fills_the_chip():
+    # 256 long decodes x 8 KV heads already fill the chip at the default.
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8) == 1024
+    # fewer sequences get smaller partitions, never below 256
+    assert ops.choose_partition([4095] * 32, [1] * 32, 8) == 512
+    assert ops.choose_partition([3000] * 4, [1] * 4, 8) == 256
+    # prefill rows do not count as decode work
+    assert ops.choose_partition([0, 3000], [500, 1], 8) == 256
+    assert ops.choose_partition([], [], 8) == 256
