@@ -41,6 +41,11 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions: the MFMA kernels keep their accumulators in
+# architectural VGPRs (no AGPR copies around the softmax rescale).
+EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH") or os.environ.get("ROCM_HOME") or "/opt/rocm"
     path = Path(rocm) / "bin" / "hipcc"
@@ -54,7 +59,8 @@ def _hipcc() -> str:
 
 def _compile(hipcc: str, source: str) -> Path:
     obj = BUILD_DIR / (Path(source).stem + ".o")
-    cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c", str(CSRC / source), "-o", str(obj)]
+    cmd = [hipcc, *HIP_FLAGS, *EXTRA_FLAGS.get(source, []), f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c",
+           str(CSRC / source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source}:\n{proc.stdout}\n{proc.stderr}")

@@ -1,21 +1,37 @@
 // Causal chunked prefill over the paged cache with gfx950 MFMA tiles.
 //
-// One workgroup (4 waves) per (sequence, query tile, KV head).  The tile
+// One workgroup (8 waves) per (sequence, query tile, KV head).  The tile
 // holds 128 query rows = (128 / G) query tokens x the G query heads that
-// share the KV head; wave w owns rows [32w, 32w + 32).  The context is
-// walked in tiles of 32 tokens staged through LDS (K row-major, V
-// transposed), with flash-style online softmax in fp32.
+// share the KV head.  The context is walked in stages of 64 tokens; wave w
+// owns rows [32 (w%4), 32 (w%4) + 32) and the 32-token half w/4 of every
+// stage, with flash-style online softmax in fp32, so the two waves of a row
+// group split the context and merge their partial results through LDS at
+// the end (this halves the longest chain of a causal tile).
 //
 // Both products are computed transposed so that a lane owns one query row:
-//   S^T[kv][row] = sum_d K[kv][d] Q[row][d]     (A = K from LDS, B = Q regs)
-//   O^T[d][row] += sum_kv V^T[d][kv] P^T[kv][row] (A = V^T from LDS, B = P)
+//   S^T[kv][row] = sum_d K[kv][d] Q[row][d]       (A = K from LDS, B = Q regs)
+//   O^T[d][row] += sum_kv V^T[d][kv] P^T[kv][row]  (A = V^T, B = P^T regs)
 // with v_mfma_f32_32x32x16_bf16.  In the 32x32 accumulator lane l holds
 // column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4), i = 0..15, so the
 // softmax max/sum of a query row needs only its own 16 values plus the
-// partner lane l ^ 32.  The P^T values a lane already holds are exactly the
-// B operand of the PV product once the context index inside each 16-token
-// step is permuted (bits 2 and 3 swapped); V^T is stored in LDS in that
-// permuted order so each A operand is one 16-byte LDS read.
+// partner lane l ^ 32, and the probabilities a lane holds are the B operand
+// of the PV product with the context index of k-slot j being
+// 8*(j/4) + 4*(l/32) + (j%4) inside each 16-token step.
+//
+// K and V are staged row-major in LDS (16-byte stores).  The V^T operand is
+// read with the gfx950 LDS transpose read ds_read_b64_tr_b16: inside each
+// group of 16 lanes, lane i receives element j from the 8-byte word
+// addressed by lane (i/4 + 4j), element i%4.  Lane i of a group therefore
+// addresses V[kv0 + (i/4)][d0 + 4*(i%4)] and receives V[kv0 + j][d0 + i],
+// j = 0..3: four context tokens of its own output column.
+//
+// Pipeline: stage t+1 sits in registers while stage t is computed from LDS;
+// at the top of each iteration it is stored to the other LDS buffer, the
+// loads of stage t+2 are issued (block ids fetched one iteration earlier),
+// so one barrier per stage suffices and global latency overlaps the MFMAs.
+// Masking is applied only to tiles that cross the causal diagonal or the end
+// of the context, and the accumulator is rescaled only when some row's
+// maximum grew by more than 2^8 over the reference maximum in use.
 //
 // Reference: the block-diagonal causal mask of app/model/paged_attention.py:
 // 92-118 applied by SDPA (paged_attention.py:170-178); query token j of a
@@ -27,40 +43,54 @@ namespace pa {
 
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4v __attribute__((ext_vector_type(4)));
 
-constexpr int kPrefillThreads = 256;
+constexpr int kPrefillThreads = 512;  // 4 row groups x 2 context halves
 constexpr int kPrefillRows = 128;  // query rows per workgroup
-constexpr int kKvTile = 32;        // context tokens per LDS tile
+constexpr int kKvTile = 32;        // context tokens per wave per stage
+constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
+constexpr float kLazyRescale = 8.f;  // log2 headroom before the row maximum moves
 
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
                                                  __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
 }
 
-// Position of context index kv (0..31) inside a V^T LDS row: bits 2 and 3
-// swapped, so the 8 values one lane feeds to an MFMA step are contiguous.
-__device__ __forceinline__ int vt_pos(int kv) {
-  return (kv & ~12) | ((kv & 4) << 1) | ((kv & 8) >> 1);
+// ds_read_b64_tr_b16 at an LDS address (see the header comment).
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4v lds_i16x4;
+  const i16x4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(uint2, r);
 }
 
 template <int D, int G>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
-  constexpr int MTOK = kPrefillRows / G;   // query tokens per workgroup
-  constexpr int KS = D / 16;               // MFMA k-steps for QK^T
-  constexpr int DB = D / 32;               // 32-wide d blocks of the output
-  constexpr int KPAD = 8;                  // bf16 padding per K row
-  constexpr int VPAD = 8;                  // bf16 padding per V^T row
-  constexpr int CHUNKS = D / 8;            // 16-byte pieces per row
+  constexpr int MTOK = kPrefillRows / G;  // query tokens per workgroup
+  constexpr int KS = D / 16;              // MFMA k-steps of QK^T
+  constexpr int DB = D / 32;              // 32-wide d blocks of the output
+  constexpr int CHUNKS = D / 8;           // 16-byte pieces per row
+  constexpr int PIECES = kStage * CHUNKS / kPrefillThreads;  // per thread, K and V each
+  // LDS row strides (elements): K rows 4 banks apart (conflict-free 16-byte
+  // reads of 16 rows), V rows 16 banks apart (conflict-free transpose reads).
+  constexpr int KSTR = D + 8;
+  constexpr int VSTR = D + 32;
+  static_assert(PIECES >= 1 && kStage * CHUNKS % kPrefillThreads == 0, "stage / thread mismatch");
+  constexpr int kStageElems = kStage * (KSTR + VSTR);
+  static_assert(2 * kStageElems * 2 >= 4 * (16 * (D / 32) + 2) * kWave * 4, "merge scratch must fit");
 
-  __shared__ uint16_t s_k[kKvTile][D + KPAD];
-  __shared__ uint16_t s_vt[D][kKvTile + VPAD];
+  // Two stage buffers (K rows then V rows); reused for the final merge.
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[2 * kStageElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  const int rg = wave & 3;   // row group
+  const int kh = wave >> 2;  // context half of every stage
   const int hkv = a.num_kv_heads;
-  const int64_t item = blockIdx.x / hkv;
-  const int kvh = blockIdx.x - static_cast<int>(item) * hkv;
+  // Highest item first: the last query tiles of a sequence see the most context.
+  const int64_t blk_id = static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x;
+  const int64_t item = blk_id / hkv;
+  const int kvh = static_cast<int>(blk_id - item * hkv);
   const int seq = a.items[2 * item];
   const int qt = a.items[2 * item + 1];
   const int64_t first = a.cu_seqlens[seq];
@@ -74,9 +104,11 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int bs_mask = (1 << log2_bs) - 1;
   const int64_t row_stride = static_cast<int64_t>(hkv) * D;
   const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.key_cache) + kvh * D;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.value_cache) + kvh * D;
 
   // This lane's query row.
-  const int row = wave * 32 + (lane & 31);
+  const int row = rg * 32 + (lane & 31);
   const int half = lane >> 5;
   const int g = row / MTOK;
   const int tok = row - g * MTOK;
@@ -93,6 +125,67 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       qreg[ks] = row_live ? ld16(qrow + ks * 16 + half * 8) : make_uint4(0, 0, 0, 0);
   }
 
+  const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
+  const int ntiles = (kv_end + kKvTile - 1) / kKvTile;
+  const int nstages = (kv_end + kStage - 1) / kStage;
+  // Tiles below this index need no mask for any row of the workgroup.
+  const int first_masked = min(start + tok0 + 1, kv_end) / kKvTile;
+  const float scale = a.scale_log2e;
+
+  // ---- staging: thread piece p covers stage row tid/CHUNKS + p*rows_per_pass
+  constexpr int kRowsPerPass = kPrefillThreads / CHUNKS;
+  const int ld_row = tid / CHUNKS;
+  const int ld_ch = tid - ld_row * CHUNKS;
+  uint4 kr[PIECES], vr[PIECES];
+  int blk[PIECES];  // block ids of the tile two ahead of the one being stored
+
+  auto fetch_blocks = [&](int tile) {
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) {
+      const int pos = tile * kStage + ld_row + p * kRowsPerPass;
+      const int col = pos >> log2_bs;
+      int b = -1;
+      if (pos < kv_end && col < a.block_table_stride) b = bt[col];
+      blk[p] = (b >= 0 && b < a.total_blocks) ? b : -1;
+    }
+  };
+  auto load_tile = [&](int tile) {
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) {
+      const int pos = tile * kStage + ld_row + p * kRowsPerPass;
+      kr[p] = make_uint4(0, 0, 0, 0);
+      vr[p] = make_uint4(0, 0, 0, 0);
+      if (blk[p] >= 0) {
+        const int64_t off = ((static_cast<int64_t>(blk[p]) << log2_bs) | (pos & bs_mask)) * row_stride +
+                            ld_ch * 8;
+        kr[p] = ld16(kbase + off);
+        vr[p] = ld16(vbase + off);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* sk = s_lds + buf * kStageElems;
+    uint16_t* sv = sk + kStage * KSTR;
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) {
+      const int r = ld_row + p * kRowsPerPass;
+      *reinterpret_cast<uint4*>(&sk[r * KSTR + ld_ch * 8]) = kr[p];
+      *reinterpret_cast<uint4*>(&sv[r * VSTR + ld_ch * 8]) = vr[p];
+    }
+  };
+
+  // Prologue: stage 0 into LDS buffer 0, stage 1 in registers, block ids of
+  // stage 2.
+  fetch_blocks(0);
+  load_tile(0);
+  store_tile(0);
+  if (nstages > 1) {
+    fetch_blocks(1);
+    load_tile(1);
+  }
+  if (nstages > 2) fetch_blocks(2);
+  __syncthreads();
+
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -100,80 +193,69 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
   float m = kScoreFloor, l = 0.f;
 
-  const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
-  const float scale = a.scale_log2e;
+  // Per-lane LDS offsets of the MFMA operands (inside this wave's half).
+  const int k_off = (kh * kKvTile + (lane & 31)) * KSTR + half * 8;
+  const int li = lane & 15;
+  const int v_off = kStage * KSTR + (kh * kKvTile + 4 * half + (li >> 2)) * VSTR +
+                    16 * ((lane >> 4) & 1) + 4 * (li & 3);
 
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kKvTile) {
-    // ---- stage K (row-major) and V (transposed, permuted) into LDS ----
-#pragma unroll
-    for (int it = 0; it < (kKvTile * CHUNKS) / kPrefillThreads; ++it) {
-      const int idx = it * kPrefillThreads + tid;
-      const int kv = idx / CHUNKS;
-      const int ch = idx - kv * CHUNKS;
-      const int pos = kv0 + kv;
-      uint4 kq = make_uint4(0, 0, 0, 0), vq = make_uint4(0, 0, 0, 0);
-      if (pos < kv_end) {
-        const int col = pos >> log2_bs;
-        const int b = col < a.block_table_stride ? bt[col] : -1;
-        if (b >= 0 && b < a.total_blocks) {
-          const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | (pos & bs_mask);
-          const uint16_t* kr = reinterpret_cast<const uint16_t*>(a.key_cache) +
-                               slot * row_stride + kvh * D + ch * 8;
-          const uint16_t* vr = reinterpret_cast<const uint16_t*>(a.value_cache) +
-                               slot * row_stride + kvh * D + ch * 8;
-          kq = ld16(kr);
-          vq = ld16(vr);
-        }
-      }
-      *reinterpret_cast<uint4*>(&s_k[kv][ch * 8]) = kq;
-      const int vp = vt_pos(kv);
-      const uint32_t w[4] = {vq.x, vq.y, vq.z, vq.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s_vt[ch * 8 + 2 * e][vp] = static_cast<uint16_t>(w[e] & 0xffffu);
-        s_vt[ch * 8 + 2 * e + 1][vp] = static_cast<uint16_t>(w[e] >> 16);
-      }
-    }
-    __syncthreads();
+  for (int st = 0; st < nstages; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nstages) store_tile(buf ^ 1);
+    if (st + 2 < nstages) load_tile(st + 2);
+    if (st + 3 < nstages) fetch_blocks(st + 3);
+    const int t = 2 * st + kh;  // this wave's 32-token tile
+    if (t < ntiles) {
 
-    // ---- S^T = K Q^T --------------------------------------------------
+    // ---- S^T = K Q^T ------------------------------------------------------
+    const uint16_t* sk = s_lds + buf * kStageElems;
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint4 ka = *reinterpret_cast<const uint4*>(&s_k[lane & 31][ks * 16 + half * 8]);
-      s = mfma32(ka, qreg[ks], s);
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      s = mfma32(*reinterpret_cast<const uint4*>(sk + k_off + ks * 16), qreg[ks], s);
 
-    // ---- online softmax for this lane's row ---------------------------
-    float tmax = kScoreFloor;
+    // ---- online softmax (unscaled scores; exp2 folds the scale) -----------
+    const int kv0 = t * kKvTile;
+    if (t >= first_masked) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
-      float v = s[i] * scale;
-      if (kv > qpos || kv >= kv_end) v = -INFINITY;
-      s[i] = v;
-      tmax = fmaxf(tmax, v);
+      for (int i = 0; i < 16; ++i) {
+        const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (kv > qpos || kv >= kv_end) s[i] = -INFINITY;
+      }
     }
+    float tmax = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m, tmax);
-    const float alpha = fast_exp2(m - m_new);
+    // Lazy rescale: the reference maximum m of a row moves only when the
+    // tile's maximum exceeds it by more than kLazyRescale (log2 units), so
+    // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
+    // same softmax.
+    const bool grow = (tmax - m) * scale > kLazyRescale;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? tmax : m;
+      const float alpha = fast_exp2((m - m_new) * scale);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+      m = m_new;
+    }
+    const float msc = m * scale;
     float rsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[i] = fast_exp2(s[i] - m_new);
+      s[i] = fast_exp2(fmaf(s[i], scale, -msc));
       rsum += s[i];
     }
     rsum += __shfl_xor(rsum, 32, kWave);
-    l = l * alpha + rsum;
-    m = m_new;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+    l += rsum;
 
-    // ---- O^T += V^T P^T -------------------------------------------------
+    // ---- O^T += V^T P^T ---------------------------------------------------
+    const uint16_t* sv = s_lds + buf * kStageElems;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       uint4 pb;
@@ -183,12 +265,41 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       pb.w = pack_bf16x2(s[8 * ks + 6], s[8 * ks + 7]);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const uint4 va =
-            *reinterpret_cast<const uint4*>(&s_vt[db * 32 + (lane & 31)][ks * 16 + half * 8]);
-        acc[db] = mfma32(va, pb, acc[db]);
+        const uint16_t* p0 = sv + v_off + ks * 16 * VSTR + db * 32;
+        const uint2 lo = lds_read_tr16(p0);
+        const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
+        acc[db] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, acc[db]);
       }
     }
+    }  // t < ntiles
     __syncthreads();
+  }
+
+  // ---- merge the two context halves of every row group ---------------------
+  // (the loop ended on a barrier, so the stage buffers are free)
+  float* scratch = reinterpret_cast<float*>(s_lds) + rg * (16 * DB + 2) * kWave;
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) scratch[(db * 16 + i) * kWave + lane] = acc[db][i];
+    scratch[(16 * DB) * kWave + lane] = m;
+    scratch[(16 * DB + 1) * kWave + lane] = l;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  {
+    const float m2 = scratch[(16 * DB) * kWave + lane];
+    const float l2 = scratch[(16 * DB + 1) * kWave + lane];
+    const float mm = fmaxf(m, m2);
+    const float a1 = fast_exp2((m - mm) * scale);
+    const float a2 = fast_exp2((m2 - mm) * scale);
+    l = l * a1 + l2 * a2;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        acc[db][i] = acc[db][i] * a1 + scratch[(db * 16 + i) * kWave + lane] * a2;
   }
 
   if (!row_live) return;
