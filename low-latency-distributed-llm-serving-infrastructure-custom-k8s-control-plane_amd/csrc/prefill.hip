@@ -137,26 +137,28 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int ld_row = tid / CHUNKS;
   const int ld_ch = tid - ld_row * CHUNKS;
   uint4 kr[PIECES], vr[PIECES];
-  int blk[PIECES];  // block ids of the tile two ahead of the one being stored
+  // Raw block-table entries of the stage two ahead of the one being stored.
+  // The fetch is unconditional (column clamped into the row) and the entry is
+  // checked only when used, so issuing it never waits on earlier loads.
+  int blk[PIECES];
+  const int last_col = a.block_table_stride - 1;
 
   auto fetch_blocks = [&](int tile) {
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int pos = tile * kStage + ld_row + p * kRowsPerPass;
-      const int col = pos >> log2_bs;
-      int b = -1;
-      if (pos < kv_end && col < a.block_table_stride) b = bt[col];
-      blk[p] = (b >= 0 && b < a.total_blocks) ? b : -1;
+      blk[p] = bt[min(pos >> log2_bs, last_col)];
     }
   };
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int pos = tile * kStage + ld_row + p * kRowsPerPass;
+      const int b = blk[p];
       kr[p] = make_uint4(0, 0, 0, 0);
       vr[p] = make_uint4(0, 0, 0, 0);
-      if (blk[p] >= 0) {
-        const int64_t off = ((static_cast<int64_t>(blk[p]) << log2_bs) | (pos & bs_mask)) * row_stride +
+      if (pos < kv_end && (pos >> log2_bs) <= last_col && b >= 0 && b < a.total_blocks) {
+        const int64_t off = ((static_cast<int64_t>(b) << log2_bs) | (pos & bs_mask)) * row_stride +
                             ld_ch * 8;
         kr[p] = ld16(kbase + off);
         vr[p] = ld16(vbase + off);
@@ -207,14 +209,29 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     const int t = 2 * st + kh;  // this wave's 32-token tile
     if (t < ntiles) {
 
-    // ---- S^T = K Q^T ------------------------------------------------------
+    // All LDS operands of the tile are read up front (the V^T reads do not
+    // depend on the softmax), so their latency overlaps the MFMAs and exps.
     const uint16_t* sk = s_lds + buf * kStageElems;
+    uint4 ka[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(sk + k_off + ks * 16);
+    uint4 va[2][DB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint16_t* p0 = sk + v_off + ks * 16 * VSTR + db * 32;
+        const uint2 lo = lds_read_tr16(p0);
+        const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
+        va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+
+    // ---- S^T = K Q^T ------------------------------------------------------
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      s = mfma32(*reinterpret_cast<const uint4*>(sk + k_off + ks * 16), qreg[ks], s);
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(ka[ks], qreg[ks], s);
 
     // ---- online softmax (unscaled scores; exp2 folds the scale) -----------
     const int kv0 = t * kKvTile;
@@ -255,7 +272,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     l += rsum;
 
     // ---- O^T += V^T P^T ---------------------------------------------------
-    const uint16_t* sv = s_lds + buf * kStageElems;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       uint4 pb;
@@ -264,12 +280,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       pb.z = pack_bf16x2(s[8 * ks + 4], s[8 * ks + 5]);
       pb.w = pack_bf16x2(s[8 * ks + 6], s[8 * ks + 7]);
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint16_t* p0 = sv + v_off + ks * 16 * VSTR + db * 32;
-        const uint2 lo = lds_read_tr16(p0);
-        const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
-        acc[db] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, acc[db]);
-      }
+      for (int db = 0; db < DB; ++db) acc[db] = mfma32(va[ks][db], pb, acc[db]);
     }
     }  // t < ntiles
     __syncthreads();
