@@ -139,9 +139,10 @@ typedef struct {
  *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
  *   decode_items int32 pairs (seq, partition) for every sequence with one
  *   new token, ordered by sequence then partition (may be NULL),
- *   merge_items int32: index in decode_items of the first item of every
- *   single-token sequence whose context spans more than one partition,
- *   ordered by sequence (may be NULL),
+ *   merge_items int32 [., 4]: (index in decode_items of the first item,
+ *   partition count, sequence, 0) of every single-token sequence whose
+ *   context spans more than one partition, ordered by sequence (may be
+ *   NULL; 16-byte aligned),
  *   prefill_items int32 pairs (seq, query tile) for every sequence with more
  *   than one new token (may be NULL).
  * Writes past a capacity in PaPackDims are dropped, never performed.

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1

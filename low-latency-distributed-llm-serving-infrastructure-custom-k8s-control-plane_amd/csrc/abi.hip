@@ -69,7 +69,7 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 extern "C" {
 
-int pa_abi_version(void) { return 3; }
+int pa_abi_version(void) { return 4; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -152,6 +152,8 @@ int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
        scatter_slots == nullptr || position_ids == nullptr ||
        (block_tables == nullptr && dims.max_blocks_per_seq > 0)))
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: missing input or output buffer");
+  if (!aligned16(merge_items))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: merge_items must be 16-byte aligned");
   pa::PackArgs a{};
   a.block_tables = block_tables;
   a.start_positions = start_positions;
@@ -266,6 +268,8 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
   if (num_merge_items < 0 || (num_merge_items > 0 && merge_items == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items is required when num_merge_items > 0");
+  if (!aligned16(merge_items))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items must be 16-byte aligned");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = dims.num_query_heads / dims.num_kv_heads;
   const int eb = elem_bytes(dims.dtype);

@@ -577,98 +577,63 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   }
 }
 
-// Combines the split-K partials of every multi-partition sequence.  One
-// workgroup per (first work item of a sequence, KV head); the items of a
-// sequence are contiguous in `items` (pa_pack orders them that way).
 // Combines the split-K partials (max, sum, unnormalised acc) of one
 // multi-partition sequence for the G heads of one KV head.  One workgroup
-// per (entry of the merge list, KV head); the merge list holds the first
-// decode item of every sequence with more than one partition, and the
-// items of a sequence are contiguous (pa_pack orders them that way).
-//  phase A  wave w takes heads w, w+4, ...: lane p reads (max, sum) of
-//           partition p, the wave reduces them, and each lane writes its
-//           partition's weight exp2(max_p - max) / sum to LDS;
-//  phase B  every thread owns G*D/256 outputs and accumulates the weighted
-//           partials over the partitions.
+// per (entry of the merge list, KV head); an entry is (first decode item,
+// partition count, sequence, 0), written by pa_pack, and the items of a
+// sequence are contiguous.  Every thread owns G*D/256 outputs and merges
+// the partitions in one pass with a running maximum (the stored maxima are
+// already in the exp2 domain): no LDS and no barrier, so the only
+// dependent global round trips are the entry and then the partials.
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
-  constexpr int kMaxW = 4096;  // LDS weights: partitions x heads per pass
-  __shared__ float s_w[kMaxW];
   const int hkv = a.num_kv_heads;
   const int64_t m = blockIdx.x / hkv;
-  const int kvh = blockIdx.x - static_cast<int>(m) * hkv;
-  const int64_t first = a.merge_items[m];
-  const int seq = a.items[2 * first];
-  int nparts = (a.context_lens[seq] + a.partition - 1) / a.partition;
+  const int kvh = static_cast<int>(blockIdx.x - m * hkv);
+  const int4 e = reinterpret_cast<const int4*>(a.merge_items)[m];
+  const int64_t first = e.x;
+  int nparts = e.y;
   if (first + nparts > a.num_items) nparts = static_cast<int>(a.num_items - first);
   if (nparts <= 1) return;
   const int hq = hkv * G;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int chunk = kMaxW / G;
-  const int64_t stride = static_cast<int64_t>(hq) * D;
-  T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[seq] * hq + kvh * G) * D;
-  const float* acc_base = a.part_acc + (first * hq + kvh * G) * static_cast<int64_t>(D);
-
-  // Phase A over all partitions first: global max and normaliser per head.
-  __shared__ float s_max[64];
-  __shared__ float s_inv[64];
-  for (int g = wave; g < G; g += kDecodeWaves) {
-    const int h = kvh * G + g;
-    float mx = kScoreFloor;
-    for (int p = lane; p < nparts; p += kWave) mx = fmaxf(mx, a.part_ml[((first + p) * hq + h) * 2]);
-    mx = wave_max(mx);
-    float l = 0.f;
-    for (int p = lane; p < nparts; p += kWave) {
-      const float* ml = a.part_ml + ((first + p) * hq + h) * 2;
-      const float w = fast_exp2(ml[0] - mx);
-      l = fmaf(ml[1], w, l);
-      if (p < chunk) s_w[p * G + g] = w;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      s_max[g] = mx;
-      s_inv[g] = l > 0.f ? 1.f / l : 0.f;
-    }
-  }
-  float o[8];  // up to 8 outputs per thread (G * D <= 2048)
+  const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
+  const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
+  T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
+  for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
+    const int h = kvh * G + i / D;
+    const float* ml = a.part_ml + first * ml_stride + 2 * h;
+    const float* acc = a.part_acc + first * stride + static_cast<int64_t>(kvh) * G * D + i;
+    float mx = kScoreFloor, sum = 0.f, o = 0.f;
+    int p = 0;
+    for (; p + 4 <= nparts; p += 4) {
+      float mp[4], lp[4], xp[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = 0.f;
-  for (int c0 = 0; c0 < nparts; c0 += chunk) {
-    const int pn = min(chunk, nparts - c0);
-    if (c0 > 0) {  // weights of a further chunk (contexts past chunk*partition)
-      __syncthreads();
-      for (int i = tid; i < pn * G; i += kDecodeThreads) {
-        const int p = i / G, g = i - (i / G) * G;
-        s_w[i] = fast_exp2(a.part_ml[((first + c0 + p) * hq + kvh * G + g) * 2] - s_max[g]);
+      for (int u = 0; u < 4; ++u) {
+        mp[u] = ml[(p + u) * ml_stride];
+        lp[u] = ml[(p + u) * ml_stride + 1];
+        xp[u] = acc[(p + u) * stride];
       }
-    }
-    __syncthreads();
+      const float mn = fmaxf(fmaxf(mx, mp[0]), fmaxf(fmaxf(mp[1], mp[2]), mp[3]));
+      const float r = fast_exp2(mx - mn);
+      sum *= r;
+      o *= r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = tid + j * kDecodeThreads;
-      if (i >= G * D) break;
-      const int g = i / D;
-      const float* src = acc_base + c0 * stride + i;
-      float acc = 0.f;
-      int p = 0;
-      for (; p + 4 <= pn; p += 4) {
-        const float x0 = src[(p + 0) * stride], x1 = src[(p + 1) * stride];
-        const float x2 = src[(p + 2) * stride], x3 = src[(p + 3) * stride];
-        acc = fmaf(x0, s_w[(p + 0) * G + g], acc);
-        acc = fmaf(x1, s_w[(p + 1) * G + g], acc);
-        acc = fmaf(x2, s_w[(p + 2) * G + g], acc);
-        acc = fmaf(x3, s_w[(p + 3) * G + g], acc);
+      for (int u = 0; u < 4; ++u) {
+        const float w = fast_exp2(mp[u] - mn);
+        sum = fmaf(lp[u], w, sum);
+        o = fmaf(xp[u], w, o);
       }
-      for (; p < pn; ++p) acc = fmaf(src[p * stride], s_w[p * G + g], acc);
-      o[j] += acc;
+      mx = mn;
     }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = tid + j * kDecodeThreads;
-    if (i < G * D) store_scalar<T>(out + i, o[j] * s_inv[i / D]);
+    for (; p < nparts; ++p) {
+      const float mp = ml[p * ml_stride], lp = ml[p * ml_stride + 1], xp = acc[p * stride];
+      const float mn = fmaxf(mx, mp);
+      const float r = fast_exp2(mx - mn), w = fast_exp2(mp - mn);
+      sum = fmaf(lp, w, sum * r);
+      o = fmaf(xp, w, o * r);
+      mx = mn;
+    }
+    store_scalar<T>(out + i, sum > 0.f ? o / sum : 0.f);
   }
 }
 

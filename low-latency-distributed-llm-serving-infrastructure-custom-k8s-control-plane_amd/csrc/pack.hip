@@ -12,9 +12,9 @@
 //     (paged_attention.py:81-90).
 // In addition it emits the work lists of the attention kernels: decode
 // items (seq, partition) for sequences with exactly one new token, the
-// merge list (index of the first decode item of every such sequence with
-// more than one partition) and prefill items (seq, query tile) for the
-// multi-token sequences, all ordered by sequence.
+// merge list ((first decode item, partition count, sequence, 0) of every
+// such sequence with more than one partition) and prefill items (seq, query
+// tile) for the multi-token sequences, all ordered by sequence.
 //
 // Each workgroup computes its own prefix sums by reducing over the
 // sequences before it (B is at most a few thousand, so this is cheaper than
@@ -131,8 +131,14 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
 
   // Attention work lists.
   if (count == 1 && a.merge_items != nullptr && tid == 0 && mitems < a.max_merge_items &&
-      clen > a.partition)
-    a.merge_items[mitems] = static_cast<int32_t>(ditems);
+      clen > a.partition) {
+    int4 e;
+    e.x = static_cast<int32_t>(ditems);
+    e.y = static_cast<int32_t>((clen + a.partition - 1) / a.partition);
+    e.z = seq;
+    e.w = 0;
+    reinterpret_cast<int4*>(a.merge_items)[mitems] = e;
+  }
   if (count == 1 && a.decode_items != nullptr) {
     const int64_t nparts = (clen + a.partition - 1) / a.partition;
     for (int64_t p = tid; p < nparts; p += kPackThreads) {

@@ -91,7 +91,7 @@ class PackedStep:
     scatter_slots: torch.Tensor  # int64 [T]
     position_ids: torch.Tensor  # int64 [T]
     decode_items: torch.Tensor  # int32 [num_decode_items, 2]
-    merge_items: torch.Tensor  # int32 [num_merge_items]
+    merge_items: torch.Tensor  # int32 [num_merge_items, 4]: (first item, parts, seq, 0)
     prefill_items: torch.Tensor  # int32 [num_prefill_items, 2]
     block_size: int
     partition_size: int
@@ -267,7 +267,7 @@ def pack_step(
         scatter_slots=torch.empty(t, dtype=torch.int64, device=device),
         position_ids=torch.empty(t, dtype=torch.int64, device=device),
         decode_items=torch.empty((ditems, 2), dtype=torch.int32, device=device),
-        merge_items=torch.empty((mitems,), dtype=torch.int32, device=device),
+        merge_items=torch.empty((mitems, 4), dtype=torch.int32, device=device),
         prefill_items=torch.empty((pitems, 2), dtype=torch.int32, device=device),
         block_size=int(block_size),
         partition_size=int(partition_size),

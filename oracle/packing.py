@@ -124,19 +124,19 @@ def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, pre
                ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Attention work lists the GPU packing kernel emits alongside the
     reference outputs, all ordered by sequence: (seq, partition) pairs of
-    single-token sequences, the index of the first such pair of every
-    sequence spanning more than one partition, and (seq, query tile) pairs
-    of multi-token sequences."""
+    single-token sequences, (index of the first such pair, partition count,
+    seq, 0) of every sequence spanning more than one partition, and
+    (seq, query tile) pairs of multi-token sequences."""
     dec: List[Tuple[int, int]] = []
-    merge: List[int] = []
+    merge: List[Tuple[int, int, int, int]] = []
     pre: List[Tuple[int, int]] = []
     for i, (s, c) in enumerate(zip(starts, counts)):
         if c == 1:
             nparts = -(-(s + c) // partition)
             if nparts > 1:
-                merge.append(len(dec))
+                merge.append((len(dec), nparts, i, 0))
             dec += [(i, p) for p in range(nparts)]
         elif c > 1:
             pre += [(i, q) for q in range(-(-c // prefill_tile))]
-    return (np.asarray(dec, dtype=np.int32).reshape(-1, 2), np.asarray(merge, dtype=np.int32),
+    return (np.asarray(dec, dtype=np.int32).reshape(-1, 2), np.asarray(merge, dtype=np.int32).reshape(-1, 4),
             np.asarray(pre, dtype=np.int32).reshape(-1, 2))

@@ -144,5 +144,5 @@ def test_scatter_is_bit_exact_on_raw_bits():
 def test_work_items():
     dec, merge, pre = op.work_items([0, 600, 1100, 0, 7], [300, 1, 1, 5, 1], 512, 32)
     assert dec.tolist() == [[1, 0], [1, 1], [2, 0], [2, 1], [2, 2], [4, 0]]
-    assert merge.tolist() == [0, 2]
+    assert merge.tolist() == [[0, 2, 1, 0], [2, 3, 2, 0]]
     assert pre.tolist() == [[0, q] for q in range(10)] + [[3, 0]]
