@@ -138,11 +138,14 @@ typedef struct {
  *   cu_seqlens [B+1], cu_context_offsets [B+1], context_lens int32 [B],
  *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
  *   decode_items int32 pairs (seq, partition) for every sequence with one
- *   new token, ordered by sequence then partition (may be NULL),
- *   merge_items int32 [., 4]: (index in decode_items of the first item,
- *   partition count, sequence, 0) of every single-token sequence whose
- *   context spans more than one partition, ordered by sequence (may be
- *   NULL; 16-byte aligned),
+ *   new token: all full partitions first (by sequence, then partition),
+ *   then the partial last partitions from longest to shortest (ties by
+ *   sequence), so short work ends the launch (may be NULL),
+ *   merge_items int32 [., 4]: (index in decode_items of the sequence's first
+ *   full partition, number of full partitions, sequence, index of its
+ *   partial partition or -1) for every single-token sequence whose context
+ *   spans more than one partition, ordered by sequence (may be NULL;
+ *   16-byte aligned),
  *   prefill_items int32 pairs (seq, query tile) for every sequence with more
  *   than one new token (may be NULL).
  * Writes past a capacity in PaPackDims are dropped, never performed.

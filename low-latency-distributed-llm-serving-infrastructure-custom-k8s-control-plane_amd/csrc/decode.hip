@@ -579,12 +579,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
 
 // Combines the split-K partials (max, sum, unnormalised acc) of one
 // multi-partition sequence for the G heads of one KV head.  One workgroup
-// per (entry of the merge list, KV head); an entry is (first decode item,
-// partition count, sequence, 0), written by pa_pack, and the items of a
-// sequence are contiguous.  Every thread owns G*D/256 outputs and merges
-// the partitions in one pass with a running maximum (the stored maxima are
-// already in the exp2 domain): no LDS and no barrier, so the only
-// dependent global round trips are the entry and then the partials.
+// per (entry of the merge list, KV head); an entry, written by pa_pack, is
+// (first full-partition item, number of full partitions, sequence, item of
+// the partial last partition or -1): the full partitions of a sequence are
+// contiguous items, its partial one sits among the short work at the end.
+// Every thread owns G*D/256 outputs and merges the partitions in one pass
+// with a running maximum (the stored maxima are already in the exp2
+// domain): no LDS and no barrier, so the only dependent global round trips
+// are the entry and then the partials.
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
   const int hkv = a.num_kv_heads;
@@ -592,26 +594,29 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const int kvh = static_cast<int>(blockIdx.x - m * hkv);
   const int4 e = reinterpret_cast<const int4*>(a.merge_items)[m];
   const int64_t first = e.x;
-  int nparts = e.y;
-  if (first + nparts > a.num_items) nparts = static_cast<int>(a.num_items - first);
-  if (nparts <= 1) return;
+  const int nfull = static_cast<int>(min(static_cast<int64_t>(e.y), a.num_items - first));
+  const bool has_rem = e.w >= 0 && e.w < a.num_items;
+  const int nparts = nfull + (has_rem ? 1 : 0);
+  if (nfull < 0 || nparts <= 1) return;
+  auto item_of = [&](int p) -> int64_t { return p < nfull ? first + p : static_cast<int64_t>(e.w); };
   const int hq = hkv * G;
   const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
   const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
   T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
   for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
     const int h = kvh * G + i / D;
-    const float* ml = a.part_ml + first * ml_stride + 2 * h;
-    const float* acc = a.part_acc + first * stride + static_cast<int64_t>(kvh) * G * D + i;
+    const float* ml = a.part_ml + 2 * h;
+    const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
     float mx = kScoreFloor, sum = 0.f, o = 0.f;
     int p = 0;
     for (; p + 4 <= nparts; p += 4) {
       float mp[4], lp[4], xp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        mp[u] = ml[(p + u) * ml_stride];
-        lp[u] = ml[(p + u) * ml_stride + 1];
-        xp[u] = acc[(p + u) * stride];
+        const int64_t it = item_of(p + u);
+        mp[u] = ml[it * ml_stride];
+        lp[u] = ml[it * ml_stride + 1];
+        xp[u] = acc[it * stride];
       }
       const float mn = fmaxf(fmaxf(mx, mp[0]), fmaxf(fmaxf(mp[1], mp[2]), mp[3]));
       const float r = fast_exp2(mx - mn);
@@ -626,7 +631,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
       mx = mn;
     }
     for (; p < nparts; ++p) {
-      const float mp = ml[p * ml_stride], lp = ml[p * ml_stride + 1], xp = acc[p * stride];
+      const int64_t it = item_of(p);
+      const float mp = ml[it * ml_stride], lp = ml[it * ml_stride + 1], xp = acc[it * stride];
       const float mn = fmaxf(mx, mp);
       const float r = fast_exp2(mx - mn), w = fast_exp2(mp - mn);
       sum = fmaf(lp, w, sum * r);

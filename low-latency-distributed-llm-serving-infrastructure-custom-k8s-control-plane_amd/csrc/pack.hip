@@ -11,13 +11,15 @@
 //   position_ids restart at every sequence: start .. start+count-1
 //     (paged_attention.py:81-90).
 // In addition it emits the work lists of the attention kernels: decode
-// items (seq, partition) for sequences with exactly one new token, the
-// merge list ((first decode item, partition count, sequence, 0) of every
-// such sequence with more than one partition) and prefill items (seq, query
-// tile) for the multi-token sequences, all ordered by sequence.
+// items (seq, partition) for sequences with exactly one new token -- every
+// full partition first (by sequence), then the partial last partitions from
+// longest to shortest -- the merge list ((first full item, number of full
+// partitions, sequence, item of the partial one or -1) of every such
+// sequence with more than one partition, by sequence) and prefill items
+// (seq, query tile) for the multi-token sequences, by sequence.
 //
-// Each workgroup computes its own prefix sums by reducing over the
-// sequences before it (B is at most a few thousand, so this is cheaper than
+// Each workgroup computes its own prefix sums and ranks by reducing over
+// the other sequences (B is at most a few thousand, so this is cheaper than
 // a separate scan launch), then writes its sequence's entries.
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
@@ -41,51 +43,61 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
 
-  // Prefix sums over sequences [0, seq).
-  int64_t tok = 0, ctx = 0, ditems = 0, pitems = 0, mitems = 0;
-  for (int k = tid; k < seq; k += kPackThreads) {
-    const int64_t cnt = nonneg(a.new_token_counts[k]);
-    const int64_t c = nonneg(a.start_positions[k]) + cnt;
-    tok += cnt;
-    ctx += c;
-    if (cnt == 1) {
-      const int64_t np = (c + a.partition - 1) / a.partition;
-      ditems += np;
-      mitems += np > 1 ? 1 : 0;
-    } else if (cnt > 1) {
-      pitems += (cnt + a.prefill_tile - 1) / a.prefill_tile;
-    }
-  }
-  __shared__ int64_t s_red[5][kPackThreads / kWave];
-#pragma unroll
-  for (int o = kWave / 2; o >= 1; o >>= 1) {
-    tok += __shfl_xor(tok, o, kWave);
-    ctx += __shfl_xor(ctx, o, kWave);
-    ditems += __shfl_xor(ditems, o, kWave);
-    pitems += __shfl_xor(pitems, o, kWave);
-    mitems += __shfl_xor(mitems, o, kWave);
-  }
-  if (lane == 0) {
-    s_red[0][wave] = tok;
-    s_red[1][wave] = ctx;
-    s_red[2][wave] = ditems;
-    s_red[3][wave] = pitems;
-    s_red[4][wave] = mitems;
-  }
-  __syncthreads();
-  tok = ctx = ditems = pitems = mitems = 0;
-#pragma unroll
-  for (int w = 0; w < kPackThreads / kWave; ++w) {
-    tok += s_red[0][w];
-    ctx += s_red[1][w];
-    ditems += s_red[2][w];
-    pitems += s_red[3][w];
-    mitems += s_red[4][w];
-  }
-
   const int64_t start = nonneg(a.start_positions[seq]);
   const int64_t count = nonneg(a.new_token_counts[seq]);
   const int64_t clen = start + count;
+  // Decode partitions of this sequence: `nfull` full ones and, when the
+  // context is not a multiple of the partition, one remainder of `rlen`.
+  const int64_t P = a.partition;
+  const int64_t nfull = count == 1 ? clen / P : 0;
+  const int64_t rlen = count == 1 ? clen % P : 0;
+
+  // One pass over all sequences: prefix sums over [0, seq) plus the totals
+  // that place the decode items (all full partitions first, by sequence;
+  // then the remainders from longest to shortest, ties by sequence, so the
+  // short work lands at the end of the launch).
+  int64_t tok = 0, ctx = 0, pitems = 0, mitems = 0, fulls = 0, total_full = 0, rank = 0;
+  for (int k = tid; k < a.num_seqs; k += kPackThreads) {
+    const int64_t cnt = nonneg(a.new_token_counts[k]);
+    const int64_t c = nonneg(a.start_positions[k]) + cnt;
+    const int64_t kf = cnt == 1 ? c / P : 0;
+    const int64_t kr = cnt == 1 ? c % P : 0;
+    total_full += kf;
+    if (rlen > 0 && kr > 0 && (kr > rlen || (kr == rlen && k < seq))) ++rank;
+    if (k < seq) {
+      tok += cnt;
+      ctx += c;
+      fulls += kf;
+      if (cnt == 1) {
+        mitems += kf + (kr > 0 ? 1 : 0) > 1 ? 1 : 0;
+      } else if (cnt > 1) {
+        pitems += (cnt + a.prefill_tile - 1) / a.prefill_tile;
+      }
+    }
+  }
+  constexpr int kSums = 7;
+  __shared__ int64_t s_red[kSums][kPackThreads / kWave];
+  int64_t v[kSums] = {tok, ctx, pitems, mitems, fulls, total_full, rank};
+#pragma unroll
+  for (int i = 0; i < kSums; ++i) {
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) v[i] += __shfl_xor(v[i], o, kWave);
+    if (lane == 0) s_red[i][wave] = v[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSums; ++i) {
+    v[i] = 0;
+#pragma unroll
+    for (int w = 0; w < kPackThreads / kWave; ++w) v[i] += s_red[i][w];
+  }
+  tok = v[0];
+  ctx = v[1];
+  pitems = v[2];
+  mitems = v[3];
+  fulls = v[4];
+  total_full = v[5];
+  rank = v[6];
   const int64_t bs = a.block_size;
   const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
 
@@ -130,22 +142,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
   }
 
   // Attention work lists.
+  const int64_t rem_idx = rlen > 0 ? total_full + rank : -1;
   if (count == 1 && a.merge_items != nullptr && tid == 0 && mitems < a.max_merge_items &&
-      clen > a.partition) {
+      nfull + (rlen > 0 ? 1 : 0) > 1) {
     int4 e;
-    e.x = static_cast<int32_t>(ditems);
-    e.y = static_cast<int32_t>((clen + a.partition - 1) / a.partition);
+    e.x = static_cast<int32_t>(fulls);
+    e.y = static_cast<int32_t>(nfull);
     e.z = seq;
-    e.w = 0;
+    e.w = static_cast<int32_t>(rem_idx);
     reinterpret_cast<int4*>(a.merge_items)[mitems] = e;
   }
   if (count == 1 && a.decode_items != nullptr) {
-    const int64_t nparts = (clen + a.partition - 1) / a.partition;
-    for (int64_t p = tid; p < nparts; p += kPackThreads) {
-      const int64_t idx = ditems + p;
+    for (int64_t p = tid; p < nfull; p += kPackThreads) {
+      const int64_t idx = fulls + p;
       if (idx >= a.max_decode_items) break;
       a.decode_items[2 * idx] = seq;
       a.decode_items[2 * idx + 1] = static_cast<int32_t>(p);
+    }
+    if (tid == 0 && rem_idx >= 0 && rem_idx < a.max_decode_items) {
+      a.decode_items[2 * rem_idx] = seq;
+      a.decode_items[2 * rem_idx + 1] = static_cast<int32_t>(nfull);
     }
   } else if (count > 1 && a.prefill_items != nullptr) {
     const int64_t ntiles = (count + a.prefill_tile - 1) / a.prefill_tile;

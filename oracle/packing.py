@@ -123,19 +123,37 @@ def scatter_layer_kv(cache: np.ndarray, layer_idx: int, rows: np.ndarray, slots:
 def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, prefill_tile: int
                ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Attention work lists the GPU packing kernel emits alongside the
-    reference outputs, all ordered by sequence: (seq, partition) pairs of
-    single-token sequences, (index of the first such pair, partition count,
-    seq, 0) of every sequence spanning more than one partition, and
-    (seq, query tile) pairs of multi-token sequences."""
-    dec: List[Tuple[int, int]] = []
+    reference outputs.
+
+    decode: (seq, partition) of single-token sequences -- every full
+    partition first, by sequence then partition, then the partial last
+    partitions by decreasing length (ties by sequence);
+    merge: (first full item, number of full partitions, seq, item of the
+    partial partition or -1) of every sequence with more than one
+    partition, by sequence;
+    prefill: (seq, query tile) of multi-token sequences, by sequence.
+    """
+    full: List[Tuple[int, int]] = []
+    rems: List[Tuple[int, int, int]] = []  # (length, seq, partition)
+    first_full = {}
+    for i, (s, c) in enumerate(zip(starts, counts)):
+        if c == 1:
+            ctx = s + c
+            first_full[i] = len(full)
+            full += [(i, p) for p in range(ctx // partition)]
+            if ctx % partition:
+                rems.append((ctx % partition, i, ctx // partition))
+    rems.sort(key=lambda r: (-r[0], r[1]))
+    rem_index = {seq: len(full) + k for k, (_, seq, _) in enumerate(rems)}
+    dec = full + [(seq, p) for _, seq, p in rems]
     merge: List[Tuple[int, int, int, int]] = []
     pre: List[Tuple[int, int]] = []
     for i, (s, c) in enumerate(zip(starts, counts)):
         if c == 1:
-            nparts = -(-(s + c) // partition)
-            if nparts > 1:
-                merge.append((len(dec), nparts, i, 0))
-            dec += [(i, p) for p in range(nparts)]
+            nfull = (s + c) // partition
+            rem = rem_index.get(i, -1)
+            if nfull + (rem >= 0) > 1:
+                merge.append((first_full[i], nfull, i, rem))
         elif c > 1:
             pre += [(i, q) for q in range(-(-c // prefill_tile))]
     return (np.asarray(dec, dtype=np.int32).reshape(-1, 2), np.asarray(merge, dtype=np.int32).reshape(-1, 4),

@@ -142,7 +142,27 @@ def test_scatter_is_bit_exact_on_raw_bits():
 
 
 def test_work_items():
-    dec, merge, pre = op.work_items([0, 600, 1100, 0, 7], [300, 1, 1, 5, 1], 512, 32)
-    assert dec.tolist() == [[1, 0], [1, 1], [2, 0], [2, 1], [2, 2], [4, 0]]
-    assert merge.tolist() == [[0, 2, 1, 0], [2, 3, 2, 0]]
+    # contexts of the decode sequences 1, 2, 4, 5: 601, 1101, 8, 1024
+    dec, merge, pre = op.work_items([0, 600, 1100, 0, 7, 1023], [300, 1, 1, 5, 1, 1], 512, 32)
+    # full partitions by sequence, then partial ones longest first (89, 77, 8)
+    assert dec.tolist() == [[1, 0], [2, 0], [2, 1], [5, 0], [5, 1], [1, 1], [2, 2], [4, 0]]
+    assert merge.tolist() == [[0, 1, 1, 5], [1, 2, 2, 6], [3, 2, 5, -1]]
     assert pre.tolist() == [[0, q] for q in range(10)] + [[3, 0]]
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_work_items_cover_every_partition_once(seed):
+    rng = np.random.default_rng(seed)
+    b = 50
+    starts = [int(x) for x in rng.integers(0, 5000, size=b)]
+    counts = [int(rng.choice([0, 1, 1, 1, 7])) for _ in range(b)]
+    part = int(rng.choice([32, 256, 512, 1000]))
+    dec, merge, _ = op.work_items(starts, counts, part, 16)
+    want = sorted((i, p) for i, (s, c) in enumerate(zip(starts, counts)) if c == 1
+                  for p in range(-(-(s + c) // part)))
+    assert sorted(map(tuple, dec.tolist())) == want
+    length = [min(part, starts[s] + 1 - p * part) for s, p in dec.tolist()]
+    assert length == sorted(length, reverse=True)
+    for first, nfull, seq, rem in merge.tolist():
+        items = [tuple(x) for x in dec[first : first + nfull].tolist()] + ([tuple(dec[rem])] if rem >= 0 else [])
+        assert items == [(seq, p) for p in range(-(-(starts[seq] + 1) // part))]
