@@ -43,8 +43,8 @@ enum { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1, PA_DTYPE_F16 = 2 };
 /* Default split-K partition of the decode kernel, in context tokens, and the
  * largest one its fast path takes (larger or non-multiple-of-32 partitions
  * run on the generic kernel). */
-#define PA_DECODE_PARTITION 1024
-#define PA_DECODE_MAX_PARTITION 2048
+#define PA_DECODE_PARTITION 2048
+#define PA_DECODE_MAX_PARTITION 4096
 
 /* ---- (0) reference ABI, device pointers -------------------------------- */
 

@@ -26,8 +26,8 @@ PA_DTYPE_F32 = 0
 PA_DTYPE_BF16 = 1
 PA_DTYPE_F16 = 2
 
-PA_DECODE_PARTITION = 1024
-PA_DECODE_MAX_PARTITION = 2048
+PA_DECODE_PARTITION = 2048
+PA_DECODE_MAX_PARTITION = 4096
 PA_DECODE_PHASE_PARTITIONS = 1
 PA_DECODE_PHASE_MERGE = 2
 

@@ -1,5 +1,5 @@
 // Paged-attention decode for gfx950: one workgroup per
-// (sequence, context partition of up to 2048 tokens, KV head), split-K merge
+// (sequence, context partition of up to 4096 tokens, KV head), split-K merge
 // after.
 //
 // The workgroup (4 waves) serves the G = H_q / H_kv query heads that share

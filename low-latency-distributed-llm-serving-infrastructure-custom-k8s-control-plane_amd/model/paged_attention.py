@@ -75,8 +75,8 @@ class PagedStepContext:
             # reference (scatter range, then the whole context).
             store.check_slot_ranges(self.sequences, self.start_positions, self.new_token_counts)
             store.check_slot_ranges(self.sequences, [0] * len(self.sequences), self.context_lens)
+            hq = getattr(store, "num_query_heads", None) or store.num_heads
             if prefill_tile is None:
-                hq = getattr(store, "num_query_heads", None) or store.num_heads
                 prefill_tile = paged_ops.prefill_tile_for(hq, store.num_heads)
             if self.sequences:
                 self.packed = paged_ops.pack_step(
@@ -86,6 +86,7 @@ class PagedStepContext:
                     store.block_size,
                     prefill_tile=prefill_tile,
                     num_kv_heads=store.num_heads,
+                    num_query_heads=hq,
                 )
                 self.scatter_slots = self.packed.scatter_slots
             else:

@@ -22,7 +22,7 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _native
-from ._native import PA_DECODE_PARTITION, PA_DECODE_MAX_PARTITION
+from ._native import PA_DECODE_MAX_PARTITION
 
 _DTYPES = {
     torch.float32: _native.PA_DTYPE_F32,
@@ -151,28 +151,36 @@ def work_counts(
     return t, c, ditems, mitems, pitems, ndec, npre
 
 
-# Fewest decode workgroups (partitions x KV heads) a step should launch:
-# eight per compute unit of the 256 on MI355X.
-_MIN_DECODE_WORKGROUPS = 2048
+# Decode workgroups resident per compute unit (256 CUs on MI355X): the
+# single-query-head kernel fits five, the grouped ones four.
+_DECODE_CUS = 256
+
+
+def _resident_decode_workgroups(group: int) -> int:
+    return _DECODE_CUS * (5 if group == 1 else 4)
 
 
 def choose_partition(
     start_positions: Sequence[int],
     new_token_counts: Sequence[int],
     num_kv_heads: int = 8,
+    num_query_heads: Optional[int] = None,
 ) -> int:
     """Split-K partition for the decode sequences of a step.
 
-    The default partition (1024 tokens) keeps the number of partials and the
-    per-workgroup set-up small; when the step's decode work would launch
-    fewer than 2048 workgroups it is halved (down to 256 tokens) so short
-    batches still spread over the whole chip.
+    The largest of 4096, 2048, 1024, 512 and 256 tokens whose decode launch
+    (partitions x KV heads) still gives every resident workgroup slot of the
+    chip two workgroups: long partitions keep the number of partials, merges
+    and per-workgroup set-ups low, and pa_pack orders the work longest first
+    so the short remainders fill the end of the launch.
     """
+    hkv = max(int(num_kv_heads), 1)
+    group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
+    need = 2 * _resident_decode_workgroups(group)
     ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
-    p = PA_DECODE_PARTITION
+    p = PA_DECODE_MAX_PARTITION
     while p > 256:
-        items = sum(-(-x // p) for x in ctx)
-        if items * max(int(num_kv_heads), 1) >= _MIN_DECODE_WORKGROUPS:
+        if sum(-(-x // p) for x in ctx) * hkv >= need:
             break
         p //= 2
     return p
@@ -225,6 +233,7 @@ def pack_step(
     prefill_tile: int = 32,
     partition_size: Optional[int] = None,
     num_kv_heads: int = 8,
+    num_query_heads: Optional[int] = None,
     with_gather: bool = False,
     start_positions_dev: Optional[torch.Tensor] = None,
     new_token_counts_dev: Optional[torch.Tensor] = None,
@@ -235,7 +244,7 @@ def pack_step(
     ``start_positions`` / ``new_token_counts``: the host lists of the step
     (also uploaded unless device copies are passed in).
     ``partition_size``: decode split-K partition in tokens; by default
-    :func:`choose_partition` picks it from the step and ``num_kv_heads``.
+    :func:`choose_partition` picks it from the step and the head counts.
     """
     device = _require_device(block_tables)
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
@@ -248,7 +257,7 @@ def pack_step(
     if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
         raise ValueError("start positions and token counts must be non-negative")
     if partition_size is None:
-        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads)
+        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads, num_query_heads)
     if partition_size <= 0:
         raise ValueError("partition_size must be positive")
     t, c, ditems, mitems, pitems, ndec, npre = work_counts(

@@ -44,7 +44,7 @@ def pack_workload(w, device, prefill_tile=None, with_gather=False, partition=Non
     tile = prefill_tile or ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     return ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
                          prefill_tile=tile, with_gather=with_gather, partition_size=partition,
-                         num_kv_heads=w.num_kv_heads)
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
 
 
 def oracle_rows(w, t, seqs):
@@ -283,12 +283,12 @@ def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=dtype == torch.float32)
 
 
-@pytest.mark.parametrize("partition", [32, 256, 1024, 2048, 96, 100, 4096])
+@pytest.mark.parametrize("partition", [32, 256, 1024, 2048, 4096, 96, 100, 8192])
 def test_decode_partition_sizes(device, partition):
     """Every split-K partition gives the oracle's result: multiples of 32 up
-    to 2048 on the fast kernel, others (100, 4096) on the generic one."""
+    to 4096 on the fast kernel, others (100, 8192) on the generic one."""
     rng = np.random.Generator(np.random.PCG64(partition))
-    ctx = [1, 31, 32, 33, 100, 2047, 2048, 2049, 5000]
+    ctx = [1, 31, 32, 33, 100, 2047, 2048, 2049, 5000, 4096, 9000]
     need = [-(-c // 16) for c in ctx]
     perm = rng.permutation(sum(need))
     lists, off = [], 0

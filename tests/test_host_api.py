@@ -294,11 +294,13 @@ def test_work_counts_match_oracle_work_lists(partition, tile):
 
 
 def test_choose_partition_fills_the_chip():
-    # 256 long decodes x 8 KV heads already fill the chip at the default.
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8) == 1024
+    # 256 decodes x 8 KV heads give two workgroups per resident slot at 4096
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32) == 4096
+    # the single-head kernel has more resident slots, so it splits more
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8) == 2048
     # fewer sequences get smaller partitions, never below 256
-    assert ops.choose_partition([4095] * 32, [1] * 32, 8) == 512
-    assert ops.choose_partition([3000] * 4, [1] * 4, 8) == 256
+    assert ops.choose_partition([4095] * 32, [1] * 32, 8, 32) == 512
+    assert ops.choose_partition([3000] * 4, [1] * 4, 8, 32) == 256
     # prefill rows do not count as decode work
-    assert ops.choose_partition([0, 3000], [500, 1], 8) == 256
+    assert ops.choose_partition([0, 3000], [500, 1], 8, 32) == 256
     assert ops.choose_partition([], [], 8) == 256
