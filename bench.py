@@ -11,10 +11,14 @@ value   = algorithmic KV-read GB/s = decode bytes / mean step time, where
           decode bytes = sum_i ctx_i * 2 * H_kv * D * 2 (K+V read once per
           KV head) + q and out rows + block-table entries + context lengths;
 tokens/s = sequences / mean step time (one token per sequence per layer).
-Also reported: the roofline fraction against 8 TB/s, the full step time
-(GPU packing + K/V write of the step's 256 tokens + decode), and the
-reference CPU kernel timed on a bounded sample of the same workload on this
-host's cores.
+roofline = the dominant kernel (the split-K partition kernel), its
+          algorithmic bytes over its own launch time, measured with HIP
+          events around each partition launch on its stream; traffic = its
+          HBM bytes per launch from the committed rocprofv3 PMC summary.
+Also reported: the full step time (GPU packing + K/V write of the step's
+tokens + attention), the reference CPU kernel timed on a bounded sample of
+the same workload on this host's cores, and for --config 5 (mixed prefill +
+decode step) the prefill kernel's TFLOP/s against the bf16 MFMA peak.
 
 python bench.py [--steps K] [--warmup W] [--config 3|4|5] [--no-cpu-baseline]
 """
@@ -188,6 +192,19 @@ def main() -> int:
         torch.cuda.synchronize()
         return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
 
+    def prefill_kernel_ms(steps, warmup):
+        """Average duration of the prefill kernel alone (HIP events on its stream)."""
+        pairs = []
+        for i in range(warmup + steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+            b.record(stream)
+            if i >= warmup:
+                pairs.append((a, b))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
     def full_step():
         s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
                           num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
@@ -257,7 +274,15 @@ def main() -> int:
     }
     if args.config == 5:
         pf = wl.prefill_flops(w)
-        result["prefill_gflop"] = round(pf / 1e9, 2)
+        pms = prefill_kernel_ms(args.steps, args.warmup)
+        result["prefill"] = {
+            "kernel": "prefill_kernel",
+            "gflop": round(pf / 1e9, 2),
+            "kernel_ms": round(pms, 5),
+            "tflops": round(pf / (pms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(pf / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        }
+        result["mixed_tokens_per_s"] = round(w.num_query_tokens / (ms * 1e-3), 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, t, args.cpu_budget)
     print(json.dumps(result), flush=True)
