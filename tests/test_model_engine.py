@@ -1,0 +1,239 @@
+"""End-to-end: a transformers Llama GQA model served through the paged hook.
+
+Mirrors the reference's model-level checks (tests/correctness/
+test_paged_attention.py:48-84: paged greedy generation equals the model's own
+generation) on an offline, random-init tiny Llama built from a config with a
+fixed seed, as tests/fuzz/test_allocator_scheduler_fuzzing.py:309-323 does.
+No checkpoint is downloaded.
+
+Every engine step is teacher-forced on the same token stream as a plain
+no-cache forward of the whole sequence, and the step's logits are compared
+with that forward's logits at the same positions; greedy tokens are compared
+where the top-2 margin exceeds the tolerance (a random model has near-ties).
+An fp32 model is held to an absolute tolerance.  A bf16 model is compared
+with an fp32 copy of itself: over the rows of a step, its largest and its
+mean error may be at most 1.5x (+0.02 / +0.01) those of the model's own bf16
+SDPA forward over the same rows.
+
+CPU tests run the reference's inline SDPA path over a CPU store.  GPU tests
+install the HIP backend (decode split-K + MFMA prefill, packing and K/V write
+on the device) over an HBM store, and run ragged multi-sequence and mixed
+prefill + decode steps.
+"""
+
+import copy
+
+import pytest
+import torch
+
+from helpers import pkg
+
+transformers = pytest.importorskip("transformers")
+
+paged_attention = pkg("model.paged_attention")
+backends = pkg("model.attention_backends")
+manager_mod = pkg("memory.manager")
+sequence_mod = pkg("scheduler.sequence")
+
+BLOCK_SIZE = 16
+
+
+def tiny_llama(dtype, device, seed=0, head_dim=64, layers=2):
+    cfg = transformers.LlamaConfig(
+        vocab_size=512,
+        hidden_size=8 * head_dim,
+        intermediate_size=1024,
+        num_hidden_layers=layers,
+        num_attention_heads=8,
+        num_key_value_heads=2,
+        max_position_embeddings=4096,
+        initializer_range=0.08,
+    )
+    torch.manual_seed(seed)
+    model = transformers.LlamaForCausalLM(cfg).to(device=device, dtype=dtype)
+    model.eval()
+    return model
+
+
+def reference_logits(model, ids, device):
+    """Logits of a plain forward of the whole sequence (model's own attention)."""
+    cfg_impl = model.config._attn_implementation
+    model.config._attn_implementation = "sdpa"
+    try:
+        with torch.inference_mode():
+            out = model(torch.tensor([ids], device=device), use_cache=False).logits[0].float()
+    finally:
+        model.config._attn_implementation = cfg_impl
+    return out
+
+
+class Reference:
+    """Reference logits of a sequence and the error bound a paged step must meet."""
+
+    def __init__(self, model, device, tol):
+        self.model, self.device, self.tol = model, device, tol
+        self.exact = None
+        if model.dtype != torch.float32:
+            self.exact = copy.deepcopy(model).float()
+
+    def __call__(self, ids):
+        """(logits to compare with, per-row error of the model's own forward or
+        None when the absolute tolerance applies)."""
+        own = reference_logits(self.model, ids, self.device)
+        if self.exact is None:
+            return own, None
+        exact = reference_logits(self.exact, ids, self.device)
+        return exact, (own - exact).abs()
+
+
+class Engine:
+    """The reference engine's step loop (app/engine/llm_engine.py:175-204),
+    reduced to what the attention path needs: one flat forward per step over
+    any mix of prefill chunks and decodes."""
+
+    def __init__(self, model, device, total_blocks=256):
+        self.model = model
+        self.device = device
+        self.store = manager_mod.PagedKVCacheManager.from_model_config(
+            model.config, total_blocks=total_blocks, block_size=BLOCK_SIZE, dtype=model.dtype, device=device)
+        paged_attention.register_paged_attention(model)
+        self.next_id = 1
+
+    def add(self, prompt):
+        seq = sequence_mod.Sequence(seq_id=self.next_id, prompt_token_ids=list(prompt))
+        self.next_id += 1
+        self.store.allocate_prefix_blocks(seq)
+        return seq
+
+    def step(self, entries):
+        """entries: (seq, start, tokens) -> per-entry logits [len(tokens), V]."""
+        seqs, starts, toks = [], [], []
+        for seq, start, tokens in entries:
+            while seq.block_table.get_tokens_count() < start + len(tokens):
+                self.store.allocate_slot_for_next_token(seq)
+            seqs.append(seq)
+            starts.append(start)
+            toks.append(list(tokens))
+        ctx = paged_attention.PagedStepContext(self.store, seqs, starts, [len(t) for t in toks])
+        flat = torch.tensor([[t for ts in toks for t in ts]], dtype=torch.long, device=self.device)
+        with torch.inference_mode():
+            logits = paged_attention.run_paged_forward(self.model, ctx, flat)[0].float()
+        out, off = [], 0
+        for ts in toks:
+            out.append(logits[off : off + len(ts)])
+            off += len(ts)
+        return out
+
+
+def check_logits(got, ref, tol):
+    want, own_err = ref
+    err = (got - want).abs()
+    if own_err is None:
+        bound = tol
+        assert err.max().item() <= bound, f"max |logit diff| {err.max().item():.3e} > {bound:.1e}"
+    else:
+        bound = 1.5 * own_err.max().item() + 0.02
+        assert err.max().item() <= bound, (
+            f"max |logit diff| {err.max().item():.3e} > 1.5 x bf16 SDPA's {own_err.max().item():.3e} + 0.02")
+        assert err.mean().item() <= 1.5 * own_err.mean().item() + 0.01, (
+            f"mean |logit diff| {err.mean().item():.3e} vs bf16 SDPA's {own_err.mean().item():.3e}")
+    top2 = torch.topk(want, 2, dim=-1).values
+    decisive = (top2[:, 0] - top2[:, 1]) > 4 * bound
+    assert torch.equal(got.argmax(-1)[decisive], want.argmax(-1)[decisive])
+
+
+def _rows(ref, a, b):
+    return ref[0][a:b], (None if ref[1] is None else ref[1][a:b])
+
+
+def run_scenario(model, device, tol, prompts, decode_steps, late_prompt=None):
+    torch.manual_seed(123)
+    vocab = model.config.vocab_size
+    streams = [list(p) + torch.randint(0, vocab, (decode_steps,)).tolist() for p in prompts]
+    eng = Engine(model, device)
+    reference = Reference(model, device, tol)
+    seqs = [eng.add(p) for p in prompts]
+    # step 0: all prompts prefilled together (ragged)
+    outs = eng.step([(s, 0, p) for s, p in zip(seqs, prompts)])
+    refs = [reference(st) for st in streams]
+    for o, r, p in zip(outs, refs, prompts):
+        check_logits(o, _rows(r, 0, len(p)), tol)
+    late = None
+    for k in range(decode_steps):
+        entries = [(s, len(p) + k, [st[len(p) + k]]) for s, p, st in zip(seqs, prompts, streams)
+                   if len(p) + k < len(st)]
+        if late_prompt is not None and k == decode_steps // 2:
+            late = eng.add(late_prompt)
+            entries.append((late, 0, list(late_prompt)))  # a prefill mixed with decodes
+        outs = eng.step(entries)
+        for (s, pos, tok), o in zip(entries, outs):
+            if s is late:
+                check_logits(o, reference(list(late_prompt)), tol)
+            else:
+                i = seqs.index(s)
+                check_logits(o, _rows(refs[i], pos, pos + 1), tol)
+    return eng
+
+
+# ---------------------------------------------------------------------------
+# CPU: the reference's inline path over a CPU store
+
+
+def test_cpu_paged_generation_matches_model(monkeypatch):
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    model = tiny_llama(torch.float32, "cpu")
+    run_scenario(model, "cpu", 1e-4, prompts=[[5, 9, 2, 7, 1], [3, 3, 8]], decode_steps=4)
+
+
+def test_cpu_cache_holds_history_for_every_layer(monkeypatch):
+    # tests/correctness/test_paged_attention.py:87-119
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    model = tiny_llama(torch.float32, "cpu", layers=3)
+    eng = Engine(model, "cpu", total_blocks=32)
+    prompt = list(range(1, 20))
+    seq = eng.add(prompt)
+    eng.step([(seq, 0, prompt)])
+    assert eng.store.key_cache.shape == (3, 32, BLOCK_SIZE, 2, 64)
+    empty = paged_attention.PagedStepContext(eng.store, [seq], [0], [0])
+    assert empty.gather_slots.numel() == 0
+    full = paged_attention.PagedStepContext(eng.store, [seq], [0], [len(prompt)])
+    for layer in range(3):
+        keys = eng.store.gather_layer_keys(layer, full.gather_slots)
+        assert keys.shape == (len(prompt), 2, 64)
+        assert torch.isfinite(keys).all() and keys.abs().sum() > 0
+
+
+# ---------------------------------------------------------------------------
+# GPU: the HIP backend installed behind the same hook
+
+
+@pytest.fixture
+def native(monkeypatch):
+    backend = backends.select_backend("native")
+    assert isinstance(backend, backends.NativePagedBackend)
+    monkeypatch.setattr(paged_attention, "_BACKEND", backend)
+    return backend
+
+
+class _NoFallback(backends.TorchSdpBackend):
+    def attend(self, *args, **kwargs):
+        raise AssertionError("the HIP backend refused a step of a GPU store")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-3), (torch.bfloat16, None)])
+def test_gpu_engine_matches_model(native, monkeypatch, dtype, tol):
+    monkeypatch.setattr(paged_attention, "_FALLBACK_BACKEND", _NoFallback())
+    model = tiny_llama(dtype, "cuda")
+    prompts = [list(range(3, 40)), [7, 1, 4], list(range(100, 300)), [11] * 70]
+    run_scenario(model, "cuda", tol, prompts, decode_steps=6, late_prompt=list(range(50, 95)))
+
+
+@pytest.mark.gpu
+def test_gpu_engine_long_context_split_k(native, monkeypatch):
+    """A prompt longer than the decode partition (split-K + merge path)."""
+    monkeypatch.setattr(paged_attention, "_FALLBACK_BACKEND", _NoFallback())
+    model = tiny_llama(torch.bfloat16, "cuda", head_dim=128)
+    torch.manual_seed(7)
+    prompt = torch.randint(0, 512, (2500,)).tolist()
+    run_scenario(model, "cuda", None, [prompt, prompt[:300]], decode_steps=3)
