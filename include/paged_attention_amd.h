@@ -181,6 +181,25 @@ int pa_reshape_and_cache(const void *key, const void *value,
                          int32_t num_layers, int32_t layer_idx, int32_t dtype,
                          void *stream);
 
+/*
+ * Replaces: KVCacheMemoryStrategy.copy_blocks (app/memory/strategies.py:
+ * 50-56; CPU 88-90, CUDA 117-122: one torch copy per block).  For every
+ * (src block, dst block) pair of block_mapping (int64 [num_pairs, 2]) and
+ * every layer, copies the block (block_bytes = bs * H_kv * D * element
+ * bytes) of src_cache (L, src_total_blocks, bs, H_kv, D) into dst_cache
+ * (L, dst_total_blocks, bs, H_kv, D); call once for the keys and once for
+ * the values.  Both caches must be device-accessible; pairs with an index
+ * outside its cache are skipped.  When the two caches are one, no pair's
+ * destination may be another pair's source.  (The reference indexes
+ * dim 0 of its caches with the block id, which selects a layer; this copies
+ * the named physical block of every layer.)
+ */
+int pa_copy_blocks(const void *src_cache, void *dst_cache,
+                   const int64_t *block_mapping, int64_t num_pairs,
+                   int32_t num_layers, int64_t src_total_blocks,
+                   int64_t dst_total_blocks, int64_t block_bytes,
+                   void *stream);
+
 /* ---- (c) paged-attention decode (split-K) ------------------------------ */
 
 /* Bytes of workspace pa_decode needs for `num_decode_items` work items (the

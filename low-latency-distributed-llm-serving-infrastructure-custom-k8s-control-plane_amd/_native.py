@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "pa_last_error",
     "pa_pack",
     "pa_reshape_and_cache",
+    "pa_copy_blocks",
     "pa_decode_workspace_size",
     "pa_decode",
     "pa_decode_phases",
@@ -111,6 +112,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
+    "pa_copy_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _vp]),
     "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
     "pa_decode": (
         ctypes.c_int,

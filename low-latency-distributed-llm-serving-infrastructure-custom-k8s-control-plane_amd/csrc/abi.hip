@@ -69,7 +69,7 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 extern "C" {
 
-int pa_abi_version(void) { return 4; }
+int pa_abi_version(void) { return 5; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -213,6 +213,35 @@ int pa_reshape_and_cache(const void* key, const void* value, int64_t key_token_s
   a.head_dim = head_dim;
   return from_hip(pa::launch_cache_write(a, dtype, static_cast<hipStream_t>(stream)),
                   "pa_reshape_and_cache");
+}
+
+int pa_copy_blocks(const void* src_cache, void* dst_cache, const int64_t* block_mapping,
+                   int64_t num_pairs, int32_t num_layers, int64_t src_total_blocks,
+                   int64_t dst_total_blocks, int64_t block_bytes, void* stream) {
+  if (num_pairs < 0 || num_layers < 0 || src_total_blocks < 0 || dst_total_blocks < 0 ||
+      block_bytes < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_copy_blocks: negative size");
+  if (num_pairs == 0 || num_layers == 0 || block_bytes == 0) return PA_OK;
+  if (src_cache == nullptr || dst_cache == nullptr || block_mapping == nullptr)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_copy_blocks: missing cache or block mapping");
+  if (block_bytes % 4 != 0 || (reinterpret_cast<uintptr_t>(src_cache) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(dst_cache) & 3u) != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_copy_blocks: caches and block size must be 4-byte aligned");
+  if (num_pairs * static_cast<int64_t>(num_layers) > 0x7fffffffLL)
+    return fail(PA_ERR_UNSUPPORTED, "pa_copy_blocks: too many blocks in one call");
+  pa::CopyBlocksArgs a{};
+  a.src = src_cache;
+  a.dst = dst_cache;
+  a.block_mapping = block_mapping;
+  a.num_pairs = num_pairs;
+  a.src_total_blocks = src_total_blocks;
+  a.dst_total_blocks = dst_total_blocks;
+  a.block_bytes = block_bytes;
+  a.num_layers = num_layers;
+  const bool vec16 = block_bytes % 16 == 0 && aligned16(src_cache) && aligned16(dst_cache);
+  return from_hip(pa::launch_copy_blocks(a, vec16, static_cast<hipStream_t>(stream)),
+                  "pa_copy_blocks");
 }
 
 namespace {

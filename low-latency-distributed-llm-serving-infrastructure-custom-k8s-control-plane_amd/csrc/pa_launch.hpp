@@ -105,6 +105,18 @@ struct CacheWriteArgs {
   int32_t head_dim;
 };
 
+// KV block copy (copy_blocks).
+struct CopyBlocksArgs {
+  const void* src;              // cache (L, N_src, bs, H_kv, D)
+  void* dst;                    // cache (L, N_dst, bs, H_kv, D)
+  const int64_t* block_mapping;  // [num_pairs, 2]: (src block, dst block)
+  int64_t num_pairs;
+  int64_t src_total_blocks;
+  int64_t dst_total_blocks;
+  int64_t block_bytes;          // bs * H_kv * D * element bytes
+  int32_t num_layers;
+};
+
 // Causal chunked prefill over block tables (MFMA tiles).
 struct PrefillArgs {
   const void* query;
@@ -136,6 +148,7 @@ hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStrea
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
 hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_copy_blocks(const CopyBlocksArgs& a, bool vec16, hipStream_t stream);
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size);
 int prefill_tile_for(int group);

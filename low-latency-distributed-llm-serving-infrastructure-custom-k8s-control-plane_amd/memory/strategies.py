@@ -125,10 +125,14 @@ class DeviceKVCacheStrategy(KVCacheMemoryStrategy):
         return key_cache, value_cache
 
     def copy_blocks(self, src_cache, dst_cache, physical_blocks):
+        """Copy the named physical blocks (every layer) from src_cache into
+        dst_cache with the HIP block-copy kernel, on the current stream."""
         if not physical_blocks:
             return
-        idx = torch.as_tensor(list(physical_blocks), dtype=torch.long, device=dst_cache.device)
-        dst_cache.index_copy_(1, idx, src_cache.index_select(1, idx.to(src_cache.device)).to(dst_cache.device))
+        from .. import paged_ops
+
+        ids = [int(b) for b in physical_blocks]
+        paged_ops.copy_blocks(src_cache, dst_cache, [(b, b) for b in ids])
 
     def sync(self) -> None:
         torch.cuda.current_stream(self._device).synchronize()

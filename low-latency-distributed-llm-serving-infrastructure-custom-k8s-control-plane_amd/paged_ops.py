@@ -355,6 +355,42 @@ def reshape_and_cache(
 # (c)/(d) attention
 
 
+def copy_blocks(src_cache: torch.Tensor, dst_cache: torch.Tensor, block_mapping) -> None:
+    """Copy physical blocks between two device caches of one layout, every
+    layer at once (pa_copy_blocks).
+
+    ``block_mapping``: (src block, dst block) pairs, an int64 [n, 2] tensor or
+    a sequence of pairs; ``src_cache`` / ``dst_cache``: (L, N, bs, H_kv, D)
+    contiguous device tensors of the same dtype and block shape.
+    """
+    if src_cache.dim() != 5 or dst_cache.dim() != 5:
+        raise ValueError("caches must be 5-D (layers, blocks, block_size, heads, dim)")
+    if src_cache.dtype != dst_cache.dtype or src_cache.shape[0] != dst_cache.shape[0] or \
+            src_cache.shape[2:] != dst_cache.shape[2:]:
+        raise ValueError("caches differ in dtype, layer count or block shape")
+    if not (src_cache.is_contiguous() and dst_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    device = _require_device(src_cache, dst_cache)
+    mapping = torch.as_tensor(block_mapping, dtype=torch.int64)
+    mapping = mapping.reshape(-1, 2).to(device, non_blocking=True).contiguous()
+    if mapping.shape[0] == 0:
+        return
+    block_bytes = src_cache[0, 0].numel() * src_cache.element_size()
+    lib = _native.load_library()
+    status = lib.pa_copy_blocks(
+        src_cache.data_ptr(),
+        dst_cache.data_ptr(),
+        mapping.data_ptr(),
+        int(mapping.shape[0]),
+        int(src_cache.shape[0]),
+        int(src_cache.shape[1]),
+        int(dst_cache.shape[1]),
+        int(block_bytes),
+        _stream(device),
+    )
+    _native.check(status, "pa_copy_blocks")
+
+
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
     """Bytes pa_decode needs for its split-K partials."""
     if num_decode_items <= 0:

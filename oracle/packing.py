@@ -120,6 +120,17 @@ def scatter_layer_kv(cache: np.ndarray, layer_idx: int, rows: np.ndarray, slots:
     flat[slots] = rows
 
 
+def copy_blocks(src: np.ndarray, dst: np.ndarray, mapping: Sequence[Tuple[int, int]]) -> None:
+    """dst[:, d] = src[:, s] for every (s, d) pair in order, all layers of the
+    (L, N, bs, H, D) caches; pairs with an index outside its cache are
+    skipped.  The intent of KVCacheMemoryStrategy.copy_blocks
+    (app/memory/strategies.py:88-90, 117-122) -- copy the named physical
+    blocks -- on this layout; raw bits, so the copy is exact."""
+    for s_blk, d_blk in mapping:
+        if 0 <= s_blk < src.shape[1] and 0 <= d_blk < dst.shape[1]:
+            dst[:, d_blk] = src[:, s_blk]
+
+
 def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, prefill_tile: int
                ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Attention work lists the GPU packing kernel emits alongside the

@@ -68,6 +68,11 @@ def test_invalid_arguments_rejected_before_launch():
                                   None, None, 0, None)
         assert rc == native.PA_ERR_INVALID_ARGUMENT
         assert b"phases must be" in lib.pa_last_error_message()
+    rc = lib.pa_copy_blocks(None, None, None, -1, 1, 1, 1, 16, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    rc = lib.pa_copy_blocks(None, None, None, 1, 1, 1, 1, 16, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT and b"missing" in lib.pa_last_error_message()
+    assert lib.pa_copy_blocks(None, None, None, 0, 1, 1, 1, 16, None) == native.PA_OK
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
     rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT

@@ -353,6 +353,45 @@ def test_decode_properties_full_size(device):
 
 
 # ---------------------------------------------------------------------------
+# block copy (copy_blocks)
+
+
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (3, 40, 16, 8, 128)), (torch.float32, (2, 33, 16, 2, 64)),
+                                         (torch.bfloat16, (2, 9, 2, 1, 6))])
+def test_copy_blocks_bit_exact(device, dtype, shape):
+    gen = torch.Generator().manual_seed(11)
+    src = torch.randn(shape, generator=gen).to(dtype)
+    dst_shape = (shape[0], shape[1] + 5) + shape[2:]
+    dst = torch.randn(dst_shape, generator=gen).to(dtype)
+    n = shape[1]
+    mapping = [(int(s), int(d)) for s, d in zip(torch.randperm(n, generator=gen)[: n // 2],
+                                                  torch.randperm(n + 5, generator=gen)[: n // 2])]
+    mapping += [(n + 3, 0), (0, n + 9), (-1, 1)]  # out of range: skipped
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    want = dst.view(bits).numpy().copy()
+    op.copy_blocks(src.view(bits).numpy(), want, mapping)
+    log(f"copy_blocks {dtype} {shape} pairs={len(mapping)}")
+    src_d, dst_d = src.to(device), dst.to(device)
+    ops.copy_blocks(src_d, dst_d, mapping)
+    torch.cuda.synchronize()
+    assert np.array_equal(dst_d.cpu().view(bits).numpy(), want)
+    assert torch.equal(src_d.cpu().view(bits), src.view(bits))
+
+
+def test_device_strategy_copy_blocks(device):
+    strategies = pkg("memory.strategies")
+    strat = strategies.DeviceKVCacheStrategy(device.index or 0)
+    k_src, _ = strat.allocate_cache(12, 16, 2, 4, 64, torch.bfloat16)
+    k_dst, _ = strat.allocate_cache(12, 16, 2, 4, 64, torch.bfloat16)
+    k_src.copy_(torch.randn(k_src.shape, device=device).to(torch.bfloat16))
+    strat.copy_blocks(k_src, k_dst, [3, 7, 11])
+    strat.sync()
+    for b in range(12):
+        want = k_src[:, b] if b in (3, 7, 11) else torch.zeros_like(k_src[:, b])
+        assert torch.equal(k_dst[:, b].view(torch.int16), want.view(torch.int16))
+
+
+# ---------------------------------------------------------------------------
 # (d) prefill
 
 

@@ -166,3 +166,16 @@ def test_work_items_cover_every_partition_once(seed):
     for first, nfull, seq, rem in merge.tolist():
         items = [tuple(x) for x in dec[first : first + nfull].tolist()] + ([tuple(dec[rem])] if rem >= 0 else [])
         assert items == [(seq, p) for p in range(-(-(starts[seq] + 1) // part))]
+
+
+def test_copy_blocks_brute_force():
+    rng = np.random.default_rng(3)
+    src = rng.integers(0, 2**16, size=(3, 10, 4, 2, 6), dtype=np.uint16)
+    dst = rng.integers(0, 2**16, size=(3, 7, 4, 2, 6), dtype=np.uint16)
+    before = dst.copy()
+    mapping = [(2, 0), (9, 6), (11, 1), (0, 7), (-1, 2), (5, 3)]
+    op.copy_blocks(src, dst, mapping)
+    for layer in range(3):
+        for blk in range(7):
+            want = {0: src[layer, 2], 6: src[layer, 9], 3: src[layer, 5]}.get(blk, before[layer, blk])
+            assert np.array_equal(dst[layer, blk], want)
