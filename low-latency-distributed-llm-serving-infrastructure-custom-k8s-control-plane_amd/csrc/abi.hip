@@ -387,7 +387,8 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
   const int eb = elem_bytes(dims.dtype);
   const bool fast =
       pa::prefill_fast_path_supported(dims.dtype, dims.head_dim, group, dims.block_size) &&
-      prefill_tile == pa::prefill_tile_for(group) && aligned16(query) && aligned16(key_cache) &&
+      prefill_tile == pa::prefill_tile_for(group) && dims.max_blocks_per_seq > 0 &&
+      aligned16(query) && aligned16(key_cache) &&
       aligned16(value_cache) && aligned16(output) && (dims.q_token_stride * eb) % 16 == 0 &&
       (dims.q_head_stride * eb) % 16 == 0;
   if (fast) {
