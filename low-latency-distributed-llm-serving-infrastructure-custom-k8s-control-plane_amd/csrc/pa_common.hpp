@@ -118,6 +118,19 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Combine every lane with its partner lane ^ 32 in the other half of the
+// wave.  gfx950 v_permlane32_swap with both operands = x leaves, at every
+// lane position, element 0 = the value of half 0 and element 1 = the value
+// of half 1, so one VALU op replaces an LDS permute round trip.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));

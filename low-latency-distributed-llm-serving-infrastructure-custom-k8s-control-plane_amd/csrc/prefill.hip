@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     float tmax = s[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    tmax = max_halves(tmax);
     // Lazy rescale: the reference maximum m of a row moves only when the
     // tile's maximum exceeds it by more than kLazyRescale (log2 units), so
     // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       s[i] = fast_exp2(fmaf(s[i], scale, -msc));
       rsum += s[i];
     }
-    rsum += __shfl_xor(rsum, 32, kWave);
+    rsum = sum_halves(rsum);
     l += rsum;
 
     // ---- O^T += V^T P^T ---------------------------------------------------
