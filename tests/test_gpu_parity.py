@@ -283,6 +283,32 @@ def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=dtype == torch.float32)
 
 
+@pytest.mark.parametrize("bs", [1, 2, 4, 8, 32, 64, 256, 12])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_sizes_mixed_step(device, bs, dtype):
+    """Decode (every K/V addressing path: per-lane, wave-uniform, 16-row
+    runs) and prefill over block sizes from 1 to 256 tokens, plus a
+    non-power-of-two size that takes the generic kernel, in one mixed step."""
+    starts = [0, 6, 32, 99, 599, 2999, 50]
+    counts = [1, 1, 1, 1, 1, 1, 90]
+    ctx = [s + c for s, c in zip(starts, counts)]
+    rng = np.random.Generator(np.random.PCG64(bs))
+    need = [-(-c // bs) for c in ctx]
+    perm = rng.permutation(sum(need) + 2)
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    hq, hkv, d = (16, 4, 128) if dtype == torch.bfloat16 else (8, 4, 64)
+    w = wl.StepWorkload("block_sizes", hq, hkv, d, bs, dtype, 1.0, starts, counts, lists, sum(need) + 2)
+    t = wl.make_tensors(w, device, seed=bs)
+    step = pack_workload(w, device, partition=256)
+    log(f"block size {bs} {dtype}: decode items {step.num_decode_items}, prefill items {step.num_prefill_items}")
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=dtype == torch.float32)
+
+
 @pytest.mark.parametrize("partition", [32, 256, 1024, 2048, 4096, 96, 100, 8192])
 def test_decode_partition_sizes(device, partition):
     """Every split-K partition gives the oracle's result: multiples of 32 up
