@@ -17,10 +17,11 @@ roofline = the dominant kernel (the split-K partition kernel), its
           HBM bytes per launch from the committed rocprofv3 PMC summary.
 Also reported: the full step time (GPU packing + K/V write of the step's
 tokens + attention), the reference CPU kernel timed on a bounded sample of
-the same workload on this host's cores, and for --config 5 (mixed prefill +
+the same workload on this host's cores, and for --workload mixed_step (prefill +
 decode step) the prefill kernel's TFLOP/s against the bf16 MFMA peak.
 
-python bench.py [--steps K] [--warmup W] [--config 3|4|5] [--no-cpu-baseline]
+python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+                [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step]
 """
 
 from __future__ import annotations
@@ -141,7 +142,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=4, choices=[3, 4, 5])
+    ap.add_argument("--workload", default="llama3_8b_gqa_decode",
+                    choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -164,7 +166,8 @@ def main() -> int:
         calibrate_copy(device)
         return 0
 
-    w = wl.CONFIGS[args.config](seed=args.seed)
+    w = wl.WORKLOADS[args.workload](seed=args.seed)
+    mixed = args.workload == "mixed_step"
     t = wl.make_tensors(w, device, seed=args.seed)
     table = torch.from_numpy(w.block_table_array()).to(device)
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
@@ -272,7 +275,7 @@ def main() -> int:
             "algorithmic_bytes": kv_bytes,
         },
     }
-    if args.config == 5:
+    if mixed:
         pf = wl.prefill_flops(w)
         pms = prefill_kernel_ms(args.steps, args.warmup)
         result["prefill"] = {

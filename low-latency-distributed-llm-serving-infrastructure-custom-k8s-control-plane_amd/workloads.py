@@ -148,12 +148,12 @@ def mixed_step(seed: int = 0) -> StepWorkload:
     return StepWorkload("mixed_step", 32, 8, 128, BLOCK_SIZE, torch.bfloat16, 1.0, starts, counts, lists, total)
 
 
-CONFIGS = {
-    1: fp32_mha_decode,
-    2: kv_write_pack,
-    3: llama7b_mha_decode,
-    4: llama3_8b_gqa_decode,
-    5: mixed_step,
+WORKLOADS = {
+    "fp32_mha_decode": fp32_mha_decode,
+    "kv_write_pack": kv_write_pack,
+    "llama7b_mha_decode": llama7b_mha_decode,
+    "llama3_8b_gqa_decode": llama3_8b_gqa_decode,
+    "mixed_step": mixed_step,
 }
 
 

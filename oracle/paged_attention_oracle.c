@@ -1,7 +1,7 @@
 /*
  * ORACLE -- test infrastructure only.  Nothing in the product path links or
  * calls this file; only tests/, __graft_entry__.smoke() and the cpu_baseline
- * leg of bench.py load it, and only as the checker.
+ * leg of bench.py load it, and only to check the HIP path against.
  *
  * CPU restatement of the reference paged-attention kernel
  * (csrc/src/paged_kernels.cpp:7-105, ABI csrc/include/paged_kernels.h:11-34).

@@ -119,10 +119,10 @@ def _check_pack(step, exp):
     assert g.dtype == np.int64 and np.array_equal(g, exp["gather_slots"])
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 5])
-def test_pack_matches_oracle_on_workloads(device, cfg):
-    w = wl.CONFIGS[cfg](seed=cfg)
-    log(f"pack cfg{cfg}: B={w.num_seqs} T={w.num_query_tokens} C={w.num_context_tokens}")
+@pytest.mark.parametrize("seed,name", [(1, "fp32_mha_decode"), (2, "kv_write_pack"), (5, "mixed_step")])
+def test_pack_matches_oracle_on_workloads(device, seed, name):
+    w = wl.WORKLOADS[name](seed=seed)
+    log(f"pack {name}: B={w.num_seqs} T={w.num_query_tokens} C={w.num_context_tokens}")
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     step = pack_workload(w, device, with_gather=True)
     exp = _pack_expect(w.start_positions, w.new_token_counts, w.block_lists, w.block_size,
@@ -237,14 +237,15 @@ def test_block_table_path_matches_golden(device, name):
 # (c) decode at full size
 
 
-@pytest.mark.parametrize("cfg,subset", [(3, [0, 1, 17, 33, 63]), (4, [0, 5, 100, 200, 255])])
-def test_decode_bf16_full_size(device, cfg, subset):
-    w = wl.CONFIGS[cfg](seed=cfg)
+@pytest.mark.parametrize("seed,name,subset", [(3, "llama7b_mha_decode", [0, 1, 17, 33, 63]),
+                                              (4, "llama3_8b_gqa_decode", [0, 5, 100, 200, 255])])
+def test_decode_bf16_full_size(device, seed, name, subset):
+    w = wl.WORKLOADS[name](seed=seed)
     longest = int(np.argmax(w.context_lens))
     shortest = int(np.argmin(w.context_lens))
     seqs = sorted(set(subset + [longest, shortest]))
-    log(f"decode cfg{cfg}: B={w.num_seqs} C={w.num_context_tokens} checking seqs {seqs}")
-    t = wl.make_tensors(w, device, seed=cfg)
+    log(f"decode {name}: B={w.num_seqs} C={w.num_context_tokens} checking seqs {seqs}")
+    t = wl.make_tensors(w, device, seed=seed)
     step = pack_workload(w, device)
     out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
