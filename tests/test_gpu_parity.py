@@ -331,6 +331,27 @@ def test_decode_partition_sizes(device, partition):
     check_rows(w, out, oracle_rows(w, t, range(len(ctx))), fp32=False)
 
 
+def test_decode_extremes(device):
+    """A 131072-token context next to 2048 short decodes (64-bit offsets, a
+    32-partition merge, a grid of ~2100 items)."""
+    rng = np.random.Generator(np.random.PCG64(77))
+    ctx = [131072] + [int(x) for x in rng.integers(1, 200, size=2048)]
+    need = [-(-c // 16) for c in ctx]
+    perm = rng.permutation(sum(need))
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    w = wl.StepWorkload("extremes", 32, 8, 128, 16, torch.bfloat16, 1.0, [c - 1 for c in ctx], [1] * len(ctx),
+                        lists, sum(need))
+    t = wl.make_tensors(w, device, seed=77)
+    step = pack_workload(w, device)
+    log(f"extremes: partition {step.partition_size}, items {step.num_decode_items}, merges {step.num_merge_items}")
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, [0, 1, 2, 1000, 2048]), fp32=False)
+
+
 def test_decode_phases_equal_one_call(device):
     """Partition phase then merge phase (two launches) gives pa_decode's bits."""
     w = wl.llama3_8b_gqa_decode(seed=2)
