@@ -53,7 +53,7 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #define PA_DECODE_NT 1  // non-temporal K/V loads
 #endif
 #ifndef PA_DECODE_MIN_WAVES
-#define PA_DECODE_MIN_WAVES 4  // occupancy floor per SIMD (0 = compiler choice)
+#define PA_DECODE_MIN_WAVES 4  // occupancy floor per SIMD for groups of up to 4 heads
 #endif
 // Occupancy floor for a group of G query heads: the register budget of the
 // wider groups does not fit four waves per SIMD without spilling.
