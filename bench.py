@@ -104,7 +104,8 @@ def cpu_baseline(w, t, budget_s: float):
         "kind": kind,
         "sample": (f"first {len(sample)} of {w.num_seqs} sequences ({sum(c for *_, c in sample)} context tokens), "
                    f"one call per sequence (T=1, all-ones mask; OpenMP parallelism capped at T*H_q="
-                   f"{w.num_query_heads} rows), fp32 up-casts of the bf16 values, median of 5 passes after a "
+                   f"{w.num_query_heads} rows), {'fp32 up-casts of the bf16' if e == 2 else 'the fp32'} values, "
+                   f"median of 5 passes after a "
                    f"warm-up ({med:.2f} s/pass kernel time, steady_clock around the C call); "
                    f"host {cpu_model()}, nproc {os.cpu_count()}, OMP_NUM_THREADS {threads}"),
     }
@@ -121,6 +122,129 @@ def measured_traffic(workload: str):
         return None
     entry = table.get(workload)
     return int(entry["traffic_bytes"]) if entry else None
+
+
+def workload_config(w, **extra):
+    cfg = {
+        "workload": w.name,
+        "num_seqs": w.num_seqs,
+        "num_query_heads": w.num_query_heads,
+        "num_kv_heads": w.num_kv_heads,
+        "head_dim": w.head_dim,
+        "block_size": w.block_size,
+        "context_tokens": w.num_context_tokens,
+        "query_tokens": w.num_query_tokens,
+    }
+    cfg.update(extra)
+    return cfg
+
+
+def bench_kv_write_pack(args, w, t, device):
+    """The integer side of a step: the GPU packing kernel over the step's
+    block tables plus the K/V write of its new tokens (32 sequences: 24
+    decodes and 8 prompts of 64-256 tokens, 32 KV heads, D 128, bf16).
+
+    value   = algorithmic GB/s of the step: new K and V rows read + cache
+              rows written (4 * T * H_kv * D * 2 bytes) + the int64 slots
+              read by the write and the packing outputs written;
+    roofline = the K/V write kernel alone, timed with HIP events;
+    cpu_baseline = the NumPy restatement (slot mapping + scatter) on the same
+              step, one host thread."""
+    import time
+
+    import numpy as np
+    import torch
+
+    from oracle import packing as op
+
+    ops = pkg("paged_ops")
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
+    stream = torch.cuda.current_stream(device)
+    e = t.new_keys.element_size()
+    T, B = w.num_query_tokens, w.num_seqs
+    write_bytes = 4 * T * w.num_kv_heads * w.head_dim * e + 8 * T
+    pack_bytes = (8 * 2 + 8 * 2) * B + 16 * T + 4 * B + 4 * table.numel()
+    total = write_bytes + pack_bytes
+
+    def step_fn():
+        ops._run_pack(step)
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+
+    for _ in range(args.warmup):
+        step_fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(args.steps):
+        step_fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    pairs = []
+    for i in range(args.warmup + args.steps):
+        x, y = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        x.record(stream)
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+        y.record(stream)
+        if i >= args.warmup:
+            pairs.append((x, y))
+    torch.cuda.synchronize()
+    kms = sum(x.elapsed_time(y) for x, y in pairs) / len(pairs)
+    result = {
+        "metric": "paged KV write + ragged packing GB/s (% HBM peak), 1 GPU",
+        "value": round(total / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V, random non-contiguous block tables)",
+        "config": workload_config(w),
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "cache_write_vec_kernel",
+            "achieved": round(write_bytes / (kms * 1e-3) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(write_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel_ms": round(kms, 5),
+            "algorithmic_bytes": write_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        ctx = [s + c for s, c in zip(w.start_positions, w.new_token_counts)]
+        shape = (1, w.total_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+        kcache, vcache = np.zeros(shape, dtype=np.uint16), np.zeros(shape, dtype=np.uint16)
+        krows = t.new_keys.view(torch.int16).cpu().numpy().view(np.uint16)
+        vrows = t.new_values.view(torch.int16).cpu().numpy().view(np.uint16)
+        passes = []
+        for _ in range(6):
+            t0 = time.perf_counter()
+            slots = op.build_slot_mapping(w.block_lists, ctx, w.block_size, w.start_positions, w.new_token_counts)
+            op.cumulative_offsets(w.new_token_counts)
+            op.scatter_layer_kv(kcache, 0, krows, slots)
+            op.scatter_layer_kv(vcache, 0, vrows, slots)
+            passes.append(time.perf_counter() - t0)
+        med = sorted(passes[1:])[2]
+        result["cpu_baseline"] = {
+            "value": round(total / med / 1e9, 4),
+            "unit": "GB/s",
+            "tokens_per_s": round(T / med, 1),
+            "cores": 1,
+            "kind": "port",
+            "sample": (f"the whole step ({T} new tokens of {B} sequences): NumPy slot mapping + cu_seqlens + "
+                       f"K and V scatter into a host cache, median of 5 passes after a warm-up "
+                       f"({med * 1e3:.2f} ms/pass); host {cpu_model()}"),
+        }
+    return result
 
 
 def calibrate_copy(device, nbytes: int = 1 << 30, reps: int = 5) -> None:
@@ -143,7 +267,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3_8b_gqa_decode",
-                    choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step"])
+                    choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step", "fp32_mha_decode",
+                             "kv_write_pack"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -169,6 +294,10 @@ def main() -> int:
     w = wl.WORKLOADS[args.workload](seed=args.seed)
     mixed = args.workload == "mixed_step"
     t = wl.make_tensors(w, device, seed=args.seed)
+    if args.workload == "kv_write_pack":
+        result = bench_kv_write_pack(args, w, t, device)
+        print(json.dumps(result), flush=True)
+        return 0
     table = torch.from_numpy(w.block_table_array()).to(device)
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
@@ -249,17 +378,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) K/V/Q, random non-contiguous block tables)",
-        "config": {
-            "workload": w.name,
-            "num_seqs": w.num_seqs,
-            "num_query_heads": w.num_query_heads,
-            "num_kv_heads": w.num_kv_heads,
-            "head_dim": w.head_dim,
-            "block_size": w.block_size,
-            "context_tokens": w.num_context_tokens,
-            "query_tokens": w.num_query_tokens,
-            "partition": step.partition_size,
-        },
+        "config": workload_config(w, partition=step.partition_size),
         "tokens_per_s": round(tokens_per_s, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "full_step_ms": round(full_ms, 5),
