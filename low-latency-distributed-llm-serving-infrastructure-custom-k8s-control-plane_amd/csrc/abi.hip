@@ -388,6 +388,7 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
   const bool fast =
       pa::prefill_fast_path_supported(dims.dtype, dims.head_dim, group, dims.block_size) &&
       prefill_tile == pa::prefill_tile_for(group) && dims.max_blocks_per_seq > 0 &&
+      static_cast<int64_t>(dims.block_size) * dims.num_kv_heads * dims.head_dim * eb <= 0xffffffffLL &&
       aligned16(query) && aligned16(key_cache) &&
       aligned16(value_cache) && aligned16(output) && (dims.q_token_stride * eb) % 16 == 0 &&
       (dims.q_head_stride * eb) % 16 == 0;

@@ -25,10 +25,13 @@
 // addresses V[kv0 + (i/4)][d0 + 4*(i%4)] and receives V[kv0 + j][d0 + i],
 // j = 0..3: four context tokens of its own output column.
 //
-// Pipeline: stage t+1 sits in registers while stage t is computed from LDS;
-// at the top of each iteration it is stored to the other LDS buffer, the
-// loads of stage t+2 are issued (block ids fetched one iteration earlier),
-// so one barrier per stage suffices and global latency overlaps the MFMAs.
+// Pipeline (one barrier per 64-token stage): three LDS stage buffers hold
+// stage t (its V is read), stage t+1 (its K is read: the scores of the next
+// tile are computed while this tile's exponentials run) and stage t+2 (being
+// stored from registers).  Stages t+3 and t+4 are in flight in two register
+// sets, and block ids are fetched two stages before their rows.  Every
+// global load is unconditional, so the compiler's memory-counter waits are
+// exact and never drain the younger stage.
 // Masking is applied only to tiles that cross the causal diagonal or the end
 // of the context, and the accumulator is rescaled only when some row's
 // maximum grew by more than 2^8 over the reference maximum in use.
@@ -50,6 +53,7 @@ constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kKvTile = 32;        // context tokens per wave per stage
 constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
 constexpr float kLazyRescale = 8.f;  // log2 headroom before the row maximum moves
+constexpr int kStageBufs = 3;       // LDS stage buffers in flight
 
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
@@ -76,10 +80,11 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   constexpr int VSTR = D + 32;
   static_assert(PIECES >= 1 && kStage * CHUNKS % kPrefillThreads == 0, "stage / thread mismatch");
   constexpr int kStageElems = kStage * (KSTR + VSTR);
-  static_assert(2 * kStageElems * 2 >= 4 * (16 * (D / 32) + 2) * kWave * 4, "merge scratch must fit");
+  static_assert(kStageBufs * kStageElems * 2 >= 4 * (16 * (D / 32) + 2) * kWave * 4,
+                "merge scratch must fit");
 
-  // Two stage buffers (K rows then V rows); reused for the final merge.
-  __shared__ __attribute__((aligned(16))) uint16_t s_lds[2 * kStageElems];
+  // Three stage buffers (K rows then V rows); reused for the final merge.
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[kStageBufs * kStageElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -102,10 +107,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   if (ntok <= 0) return;
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
-  const int64_t row_stride = static_cast<int64_t>(hkv) * D;
+  // Byte strides of a cache row and a cache block (the host keeps a block
+  // under 4 GiB, so a row offset is one 32 x 32 -> 64-bit multiply-add).
+  const uint32_t row_bytes = static_cast<uint32_t>(hkv) * D * 2;
+  const uint32_t block_bytes = row_bytes << log2_bs;
   const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.key_cache) + kvh * D;
-  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.value_cache) + kvh * D;
+  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * D * 2;
+  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * D * 2;
 
   // This lane's query row.
   const int row = rg * 32 + (lane & 31);
@@ -126,66 +134,87 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   }
 
   const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
+  // Positions that have a block-table column (the rest are never read).
+  const int kv_read = static_cast<int>(
+      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(a.block_table_stride) << log2_bs));
   const int ntiles = (kv_end + kKvTile - 1) / kKvTile;
   const int nstages = (kv_end + kStage - 1) / kStage;
   // Tiles below this index need no mask for any row of the workgroup.
   const int first_masked = min(start + tok0 + 1, kv_end) / kKvTile;
   const float scale = a.scale_log2e;
 
-  // ---- staging: thread piece p covers stage row tid/CHUNKS + p*rows_per_pass
+  // ---- staging: thread piece p covers stage row ld_row + p*kRowsPerPass,
+  // 16 bytes at chunk ld_ch, of K and of V.  Every load is issued
+  // unconditionally (no branch around a memory instruction), so the memory
+  // counter waits stay exact and two stages are in flight in registers:
+  //  - rows past the readable context re-read its last row (finite; their
+  //    scores are masked);
+  //  - an out-of-pool block id reads block 0 and is zeroed before it
+  //    reaches LDS (the reference leaves such ids undefined).
+  // Block ids are fetched two iterations before their rows are loaded.
   constexpr int kRowsPerPass = kPrefillThreads / CHUNKS;
   const int ld_row = tid / CHUNKS;
-  const int ld_ch = tid - ld_row * CHUNKS;
-  uint4 kr[PIECES], vr[PIECES];
-  // Raw block-table entries of the stage two ahead of the one being stored.
-  // The fetch is unconditional (column clamped into the row) and the entry is
-  // checked only when used, so issuing it never waits on earlier loads.
-  int blk[PIECES];
-  const int last_col = a.block_table_stride - 1;
+  const uint32_t lane_bytes = static_cast<uint32_t>(tid - ld_row * CHUNKS) * 16;
+  const int ld_col = (tid - ld_row * CHUNKS) * 8;
 
-  auto fetch_blocks = [&](int tile) {
+  auto row_of = [&](int stage, int p) {
+    return min(stage * kStage + ld_row + p * kRowsPerPass, kv_read - 1);
+  };
+  auto fetch_blocks = [&](int stage, int* out) {
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) out[p] = bt[row_of(stage, p) >> log2_bs];
+  };
+  auto load_tile = [&](int stage, const int* bl, uint4* kd, uint4* vd, uint32_t& bad) {
+    bad = 0;
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
-      const int pos = tile * kStage + ld_row + p * kRowsPerPass;
-      blk[p] = bt[min(pos >> log2_bs, last_col)];
+      const int pos = row_of(stage, p);
+      const bool ok = static_cast<uint32_t>(bl[p]) < static_cast<uint32_t>(a.total_blocks);
+      const uint32_t b = ok ? static_cast<uint32_t>(bl[p]) : 0u;
+      const uint64_t off = static_cast<uint64_t>(b) * block_bytes +
+                           (static_cast<uint32_t>(pos & bs_mask) * row_bytes + lane_bytes);
+      kd[p] = ld16(kbase + off);
+      vd[p] = ld16(vbase + off);
+      bad |= ok ? 0u : (1u << p);
     }
   };
-  auto load_tile = [&](int tile) {
+  auto store_tile = [&](int off, uint4* kd, uint4* vd, uint32_t bad) {
+    if (__builtin_amdgcn_ballot_w64(bad != 0) != 0) {
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int pos = tile * kStage + ld_row + p * kRowsPerPass;
-      const int b = blk[p];
-      kr[p] = make_uint4(0, 0, 0, 0);
-      vr[p] = make_uint4(0, 0, 0, 0);
-      if (pos < kv_end && (pos >> log2_bs) <= last_col && b >= 0 && b < a.total_blocks) {
-        const int64_t off = ((static_cast<int64_t>(b) << log2_bs) | (pos & bs_mask)) * row_stride +
-                            ld_ch * 8;
-        kr[p] = ld16(kbase + off);
-        vr[p] = ld16(vbase + off);
-      }
+      for (int p = 0; p < PIECES; ++p)
+        if ((bad >> p) & 1u) kd[p] = vd[p] = make_uint4(0, 0, 0, 0);
     }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* sk = s_lds + buf * kStageElems;
+    uint16_t* sk = s_lds + off;
     uint16_t* sv = sk + kStage * KSTR;
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int r = ld_row + p * kRowsPerPass;
-      *reinterpret_cast<uint4*>(&sk[r * KSTR + ld_ch * 8]) = kr[p];
-      *reinterpret_cast<uint4*>(&sv[r * VSTR + ld_ch * 8]) = vr[p];
+      *reinterpret_cast<uint4*>(&sk[r * KSTR + ld_col]) = kd[p];
+      *reinterpret_cast<uint4*>(&sv[r * VSTR + ld_col]) = vd[p];
     }
   };
 
-  // Prologue: stage 0 into LDS buffer 0, stage 1 in registers, block ids of
-  // stage 2.
-  fetch_blocks(0);
-  load_tile(0);
-  store_tile(0);
-  if (nstages > 1) {
-    fetch_blocks(1);
-    load_tile(1);
-  }
-  if (nstages > 2) fetch_blocks(2);
+  // Two register stages (X: even iterations, Y: odd) and their block ids.
+  uint4 kx[PIECES], vx[PIECES], ky[PIECES], vy[PIECES];
+  int bx[PIECES], by[PIECES];
+  uint32_t badx, bady;
+
+  // Prologue: stages 0 and 1 into LDS buffers 0 and 1, stages 2 and 3 in
+  // registers, block ids of stages 4 and 5.
+  fetch_blocks(0, bx);
+  fetch_blocks(1, by);
+  load_tile(0, bx, kx, vx, badx);
+  load_tile(1, by, ky, vy, bady);
+  fetch_blocks(2, bx);
+  fetch_blocks(3, by);
+  store_tile(0, kx, vx, badx);
+  store_tile(kStageElems, ky, vy, bady);
+  // (same issue order as the loop, so its memory counter waits hold on
+  // entry too)
+  load_tile(2, bx, kx, vx, badx);
+  fetch_blocks(4, bx);
+  load_tile(3, by, ky, vy, bady);
+  fetch_blocks(5, by);
   __syncthreads();
 
   f32x16 acc[DB];
@@ -201,89 +230,125 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int v_off = kStage * KSTR + (kh * kKvTile + 4 * half + (li >> 2)) * VSTR +
                     16 * ((lane >> 4) & 1) + 4 * (li & 3);
 
-  for (int st = 0; st < nstages; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nstages) store_tile(buf ^ 1);
-    if (st + 2 < nstages) load_tile(st + 2);
-    if (st + 3 < nstages) fetch_blocks(st + 3);
-    const int t = 2 * st + kh;  // this wave's 32-token tile
-    if (t < ntiles) {
-
-    // All LDS operands of the tile are read up front (the V^T reads do not
-    // depend on the softmax), so their latency overlaps the MFMAs and exps.
-    const uint16_t* sk = s_lds + buf * kStageElems;
+  // The scores of stage st+1 are computed while stage st's are turned into
+  // probabilities: the QK MFMAs of the next tile are interleaved with the
+  // exponentials of this one, so the matrix pipe and the VALU overlap inside
+  // a wave.  Stage buffers rotate through LDS offsets kept in scalars.
+  f32x16 s_cur;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s_cur[i] = 0.f;
+  int off_cur = 0, off_next = kStageElems, off_store = 2 * kStageElems;
+  if (kh < ntiles) {
     uint4 ka[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(sk + k_off + ks * 16);
-    uint4 va[2][DB];
+    for (int ks = 0; ks < KS; ++ks)
+      ka[ks] = *reinterpret_cast<const uint4*>(s_lds + k_off + ks * 16);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < KS; ++ks) s_cur = mfma32(ka[ks], qreg[ks], s_cur);
+  }
+
+  // One pipeline step: stage st+2 registers -> LDS, stage st+4 loads issued
+  // into the same registers, block ids of stage st+6, then the tile of
+  // stage st.  Returns the scores of stage st+1.
+  auto step = [&](int st, uint4* kd, uint4* vd, int* bl, uint32_t& bad, const f32x16& s_in) {
+    store_tile(off_store, kd, vd, bad);
+    load_tile(st + 4, bl, kd, vd, bad);
+    fetch_blocks(st + 6, bl);
+    const int t = 2 * st + kh;  // this wave's 32-token tile
+    f32x16 s_next = s_in;
+    if (t < ntiles) {
+      // LDS operands: V^T of this stage, K of the next one (read even when
+      // there is no next tile: the stale scores are never used).
+      const uint16_t* sv = s_lds + off_cur + v_off;
+      uint4 va[2][DB];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint16_t* p0 = sk + v_off + ks * 16 * VSTR + db * 32;
-        const uint2 lo = lds_read_tr16(p0);
-        const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
-        va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const uint16_t* p0 = sv + ks * 16 * VSTR + db * 32;
+          const uint2 lo = lds_read_tr16(p0);
+          const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
+          va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      const uint16_t* sk = s_lds + off_next + k_off;
+      uint4 ka[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(sk + ks * 16);
+
+      // ---- online softmax of s_in (unscaled scores; exp2 folds the scale)
+      f32x16 s = s_in;
+      const int kv0 = t * kKvTile;
+      if (t >= first_masked) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
+          if (kv > qpos || kv >= kv_end) s[i] = -INFINITY;
+        }
       }
-
-    // ---- S^T = K Q^T ------------------------------------------------------
-    f32x16 s;
+      float tmax = s[0];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+      for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+      tmax = max_halves(tmax);
+      // Lazy rescale: the reference maximum m of a row moves only when the
+      // tile's maximum exceeds it by more than kLazyRescale (log2 units), so
+      // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
+      // same softmax.
+      const bool grow = (tmax - m) * scale > kLazyRescale;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = grow ? tmax : m;
+        const float alpha = fast_exp2((m - m_new) * scale);
+        l *= alpha;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(ka[ks], qreg[ks], s);
-
-    // ---- online softmax (unscaled scores; exp2 folds the scale) -----------
-    const int kv0 = t * kKvTile;
-    if (t >= first_masked) {
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (kv > qpos || kv >= kv_end) s[i] = -INFINITY;
+          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+        m = m_new;
       }
-    }
-    float tmax = s[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-    tmax = max_halves(tmax);
-    // Lazy rescale: the reference maximum m of a row moves only when the
-    // tile's maximum exceeds it by more than kLazyRescale (log2 units), so
-    // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
-    // same softmax.
-    const bool grow = (tmax - m) * scale > kLazyRescale;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float m_new = grow ? tmax : m;
-      const float alpha = fast_exp2((m - m_new) * scale);
-      l *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-      m = m_new;
-    }
-    const float msc = m * scale;
-    float rsum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] = fast_exp2(fmaf(s[i], scale, -msc));
-      rsum += s[i];
-    }
-    rsum = sum_halves(rsum);
-    l += rsum;
+      const float msc = m * scale;
 
-    // ---- O^T += V^T P^T ---------------------------------------------------
+      // ---- interleaved: S_next = K_next Q^T | P = exp2(S - m) | O^T += V^T P^T
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint4 pb;
-      pb.x = pack_bf16x2(s[8 * ks + 0], s[8 * ks + 1]);
-      pb.y = pack_bf16x2(s[8 * ks + 2], s[8 * ks + 3]);
-      pb.z = pack_bf16x2(s[8 * ks + 4], s[8 * ks + 5]);
-      pb.w = pack_bf16x2(s[8 * ks + 6], s[8 * ks + 7]);
+      for (int i = 0; i < 16; ++i) s_next[i] = 0.f;
+      float rsum = 0.f;
+      uint4 pb[2];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] = mfma32(va[ks][db], pb, acc[db]);
-    }
+      for (int ks = 0; ks < KS; ++ks) {
+        s_next = mfma32(ka[ks], qreg[ks], s_next);
+        // two (D = 128) or four (D = 64) probabilities per QK step
+#pragma unroll
+        for (int j = ks * 16 / KS; j < (ks + 1) * 16 / KS; ++j) {
+          s[j] = fast_exp2(fmaf(s[j], scale, -msc));
+          rsum += s[j];
+        }
+        if ((ks + 1) * 16 / KS % 8 == 0) {
+          const int c = (ks + 1) * 16 / KS / 8 - 1;
+          pb[c].x = pack_bf16x2(s[8 * c + 0], s[8 * c + 1]);
+          pb[c].y = pack_bf16x2(s[8 * c + 2], s[8 * c + 3]);
+          pb[c].z = pack_bf16x2(s[8 * c + 4], s[8 * c + 5]);
+          pb[c].w = pack_bf16x2(s[8 * c + 6], s[8 * c + 7]);
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] = mfma32(va[ks][db], pb[ks], acc[db]);
+      rsum = sum_halves(rsum);
+      l += rsum;
     }  // t < ntiles
+    const int o = off_cur;
+    off_cur = off_next;
+    off_next = off_store;
+    off_store = o;
     __syncthreads();
+    return s_next;
+  };
+
+  // Two steps per trip so that the register stages and block-id sets
+  // alternate by name.  A trailing step past the last stage computes
+  // nothing (its tiles are past ntiles) and only reloads clamped rows.
+  for (int st = 0; st < nstages; st += 2) {
+    const f32x16 s_mid = step(st, kx, vx, bx, badx, s_cur);
+    s_cur = step(st + 1, ky, vy, by, bady, s_mid);
   }
 
   // ---- merge the two context halves of every row group ---------------------
