@@ -91,7 +91,9 @@ class PackedStep:
     scatter_slots: torch.Tensor  # int64 [T]
     position_ids: torch.Tensor  # int64 [T]
     decode_items: torch.Tensor  # int32 [num_decode_items, 2]
-    merge_items: torch.Tensor  # int32 [num_merge_items, 4]: (first item, parts, seq, 0)
+    # int32 [num_merge_items, 4]: (first full-partition item, full partitions,
+    # seq, remainder item or -1)
+    merge_items: torch.Tensor
     prefill_items: torch.Tensor  # int32 [num_prefill_items, 2]
     block_size: int
     partition_size: int
@@ -230,7 +232,7 @@ def pack_step(
     new_token_counts: Sequence[int],
     block_size: int,
     *,
-    prefill_tile: int = 32,
+    prefill_tile: Optional[int] = None,
     partition_size: Optional[int] = None,
     num_kv_heads: int = 8,
     num_query_heads: Optional[int] = None,
@@ -245,6 +247,8 @@ def pack_step(
     (also uploaded unless device copies are passed in).
     ``partition_size``: decode split-K partition in tokens; by default
     :func:`choose_partition` picks it from the step and the head counts.
+    ``prefill_tile``: query tokens per prefill work item; by default the
+    MFMA kernel's tile for the head counts (:func:`prefill_tile_for`).
     """
     device = _require_device(block_tables)
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
@@ -256,6 +260,10 @@ def pack_step(
         raise ValueError("start_positions / new_token_counts must have one entry per block-table row")
     if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
         raise ValueError("start positions and token counts must be non-negative")
+    if prefill_tile is None:
+        prefill_tile = prefill_tile_for(int(num_query_heads or 4 * num_kv_heads), int(num_kv_heads))
+    if prefill_tile <= 0:
+        raise ValueError("prefill_tile must be positive")
     if partition_size is None:
         partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads, num_query_heads)
     if partition_size <= 0:
