@@ -664,7 +664,11 @@ static hipError_t launch_decode_g(const DecodeArgs& a, int G, int64_t num_items,
   switch (G) {
     case 1: return launch_decode_t<T, D, 1>(a, num_items, phases, s);
     case 2: return launch_decode_t<T, D, 2>(a, num_items, phases, s);
+    case 3: return launch_decode_t<T, D, 3>(a, num_items, phases, s);
     case 4: return launch_decode_t<T, D, 4>(a, num_items, phases, s);
+    case 5: return launch_decode_t<T, D, 5>(a, num_items, phases, s);
+    case 6: return launch_decode_t<T, D, 6>(a, num_items, phases, s);
+    case 7: return launch_decode_t<T, D, 7>(a, num_items, phases, s);
     case 8: return launch_decode_t<T, D, 8>(a, num_items, phases, s);
     default: return hipErrorNotSupported;
   }
@@ -674,7 +678,7 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
                                 int partition) {
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
-  if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+  if (group < 1 || group > 8) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;
   return true;

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int half = lane >> 5;
   const int g = row / MTOK;
   const int tok = row - g * MTOK;
-  const bool row_live = tok < ntok;
+  // Rows past G * MTOK (when G does not divide 128) belong to no head.
+  const bool row_live = tok < ntok && g < G;
   const int qpos = start + tok0 + tok;  // causal limit (inclusive)
   const int h = kvh * G + g;
 
@@ -397,7 +398,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
   if (dtype != PA_DTYPE_BF16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
-  if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+  if (group < 1 || group > 8) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   return true;
 }
@@ -411,7 +412,11 @@ static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_
   switch (group) {
     case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(kPrefillThreads), 0, s, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((prefill_kernel<D, 3>), grid, dim3(kPrefillThreads), 0, s, a); break;
     case 4: hipLaunchKernelGGL((prefill_kernel<D, 4>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((prefill_kernel<D, 5>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((prefill_kernel<D, 6>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((prefill_kernel<D, 7>), grid, dim3(kPrefillThreads), 0, s, a); break;
     case 8: hipLaunchKernelGGL((prefill_kernel<D, 8>), grid, dim3(kPrefillThreads), 0, s, a); break;
     default: return hipErrorNotSupported;
   }

@@ -67,7 +67,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 def prefill_tile_for(num_query_heads: int, num_kv_heads: int) -> int:
     """Query tokens per prefill work item (128 query rows per workgroup)."""
     group = num_query_heads // num_kv_heads
-    return max(1, 128 // group) if group in (1, 2, 4, 8) else 128
+    return 128 // group if 1 <= group <= 8 else 128
 
 
 # ---------------------------------------------------------------------------

@@ -266,7 +266,10 @@ def test_decode_fp32_matches_oracle(device):
     (4, 4, 128, torch.bfloat16), (16, 16, 64, torch.bfloat16), (8, 4, 64, torch.bfloat16),
     (32, 8, 64, torch.bfloat16), (16, 2, 64, torch.bfloat16), (16, 2, 64, torch.float32),
     (8, 4, 128, torch.float32), (8, 8, 128, torch.float32), (32, 8, 128, torch.float32),
-    (8, 1, 64, torch.float32), (12, 4, 32, torch.bfloat16), (12, 4, 128, torch.bfloat16)])
+    (8, 1, 64, torch.float32), (12, 4, 32, torch.bfloat16), (12, 4, 128, torch.bfloat16),
+    # groups that are not powers of two (9/3/64 is SmolLM-135M's shape)
+    (9, 3, 64, torch.bfloat16), (9, 3, 64, torch.float32), (10, 2, 128, torch.bfloat16),
+    (12, 2, 64, torch.bfloat16), (28, 4, 128, torch.bfloat16), (14, 2, 128, torch.float32)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
@@ -443,7 +446,8 @@ def test_device_strategy_copy_blocks(device):
 # (d) prefill
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 2, 64), (8, 1, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 2, 64), (8, 1, 64),
+                                     (9, 3, 64), (12, 4, 128), (10, 2, 128), (12, 2, 64), (28, 4, 128)])
 def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]

@@ -38,14 +38,14 @@ sequence_mod = pkg("scheduler.sequence")
 BLOCK_SIZE = 16
 
 
-def tiny_llama(dtype, device, seed=0, head_dim=64, layers=2):
+def tiny_llama(dtype, device, seed=0, head_dim=64, layers=2, heads=8, kv_heads=2):
     cfg = transformers.LlamaConfig(
         vocab_size=512,
-        hidden_size=8 * head_dim,
+        hidden_size=heads * head_dim,
         intermediate_size=1024,
         num_hidden_layers=layers,
-        num_attention_heads=8,
-        num_key_value_heads=2,
+        num_attention_heads=heads,
+        num_key_value_heads=kv_heads,
         max_position_embeddings=4096,
         initializer_range=0.08,
     )
@@ -237,3 +237,13 @@ def test_gpu_engine_long_context_split_k(native, monkeypatch):
     torch.manual_seed(7)
     prompt = torch.randint(0, 512, (2500,)).tolist()
     run_scenario(model, "cuda", None, [prompt, prompt[:300]], decode_steps=3)
+
+
+@pytest.mark.gpu
+def test_gpu_engine_smollm_head_shape(native, monkeypatch):
+    """9 query heads over 3 KV heads of 64 (SmolLM-135M's attention shape, the
+    reference's test model): a group of three on the HIP decode and prefill."""
+    monkeypatch.setattr(paged_attention, "_FALLBACK_BACKEND", _NoFallback())
+    model = tiny_llama(torch.bfloat16, "cuda", heads=9, kv_heads=3)
+    prompts = [list(range(3, 60)), [7, 1, 4], list(range(100, 230))]
+    run_scenario(model, "cuda", None, prompts, decode_steps=4, late_prompt=list(range(50, 90)))
