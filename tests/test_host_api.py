@@ -304,3 +304,7 @@ def test_choose_partition_fills_the_chip():
     # prefill rows do not count as decode work
     assert ops.choose_partition([0, 3000], [500, 1], 8, 32) == 256
     assert ops.choose_partition([], [], 8) == 256
+    # a small step whose contexts all fit 512 tokens skips the merge launch
+    assert ops.choose_partition([15, 300, 511], [1, 1, 1], 8, 8) == 512
+    assert ops.choose_partition([15, 300, 512], [1, 1, 1], 8, 8) == 256
+    assert ops.choose_partition([15, 200, 255], [1, 1, 1], 8, 8) == 256
