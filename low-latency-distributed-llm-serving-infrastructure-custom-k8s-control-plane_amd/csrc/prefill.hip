@@ -18,20 +18,25 @@
 // of the PV product with the context index of k-slot j being
 // 8*(j/4) + 4*(l/32) + (j%4) inside each 16-token step.
 //
-// K and V are staged row-major in LDS (16-byte stores).  The V^T operand is
+// K and V go from HBM straight into LDS with the gfx950 direct loads
+// (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i), into
+// unpadded rows whose 16-byte chunks are XOR-swizzled (chunk_swizzle) so that
+// the operand reads below are free of bank conflicts.  The V^T operand is
 // read with the gfx950 LDS transpose read ds_read_b64_tr_b16: inside each
 // group of 16 lanes, lane i receives element j from the 8-byte word
 // addressed by lane (i/4 + 4j), element i%4.  Lane i of a group therefore
 // addresses V[kv0 + (i/4)][d0 + 4*(i%4)] and receives V[kv0 + j][d0 + i],
 // j = 0..3: four context tokens of its own output column.
 //
-// Pipeline (one barrier per 64-token stage): three LDS stage buffers hold
+// Pipeline (one barrier per 64-token stage): four LDS stage buffers hold
 // stage t (its V is read), stage t+1 (its K is read: the scores of the next
-// tile are computed while this tile's exponentials run) and stage t+2 (being
-// stored from registers).  Stages t+3 and t+4 are in flight in two register
-// sets, and block ids are fetched two stages before their rows.  Every
-// global load is unconditional, so the compiler's memory-counter waits are
-// exact and never drain the younger stage.
+// tile are computed while this tile's exponentials run), stage t+2 (landed)
+// and stage t+3 (being copied).  The block ids of a stage are copied into an
+// LDS ring two stages before its rows.  The copies are issued from inline
+// assembly, every step the same number per wave, and each wave waits for
+// its own copies with an exact s_waitcnt vmcnt before the barrier that
+// publishes them (the compiler would otherwise drain every copy before each
+// LDS read, as it cannot tell the buffers apart).
 // Masking is applied only to tiles that cross the causal diagonal or the end
 // of the context, and the accumulator is rescaled only when some row's
 // maximum grew by more than 2^8 over the reference maximum in use.
@@ -53,7 +58,10 @@ constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kKvTile = 32;        // context tokens per wave per stage
 constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
 constexpr float kLazyRescale = 8.f;  // log2 headroom before the row maximum moves
-constexpr int kStageBufs = 3;       // LDS stage buffers in flight
+constexpr int kStageBufs = 4;       // LDS stage buffers in flight
+constexpr int kPrefillWaves = kPrefillThreads / 64;
+constexpr int kIdRing = 8;          // block-id slots (one per stage in flight)
+constexpr int kIdSlotBytes = 256;   // up to 64 table entries per stage
 
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
@@ -67,28 +75,59 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Direct global -> LDS loads.  Each lane's 16 (or 4) bytes land at
+// lds_base + 16 * lane (4 * lane); lds_base must be wave-uniform.  They are
+// issued from inline assembly so that the compiler, which cannot tell the
+// stage buffers apart, does not drain them before every LDS read; the
+// kernel waits for them itself (s_waitcnt vmcnt) before the barrier that
+// publishes a stage.
+__device__ __forceinline__ void dma16(uint32_t lds_base, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds_base, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_base), "v"(src)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Swizzle of the 16-byte chunks of an unpadded LDS row: chunk c of row r sits
+// at position c ^ chunk_swizzle(r).  It keeps the 16-byte K reads (16 rows,
+// one chunk) and the transpose reads of V (4 rows x 4 chunks per 32 lanes)
+// free of bank conflicts.
+template <int CHUNKS>
+__device__ __forceinline__ int chunk_swizzle(int r) {
+  if constexpr (CHUNKS == 16) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
   constexpr int MTOK = kPrefillRows / G;  // query tokens per workgroup
   constexpr int KS = D / 16;              // MFMA k-steps of QK^T
   constexpr int DB = D / 32;              // 32-wide d blocks of the output
   constexpr int CHUNKS = D / 8;           // 16-byte pieces per row
-  constexpr int PIECES = kStage * CHUNKS / kPrefillThreads;  // per thread, K and V each
-  // LDS row strides (elements): K rows 4 banks apart (conflict-free 16-byte
-  // reads of 16 rows), V rows 16 banks apart (conflict-free transpose reads).
-  constexpr int KSTR = D + 8;
-  constexpr int VSTR = D + 32;
-  static_assert(PIECES >= 1 && kStage * CHUNKS % kPrefillThreads == 0, "stage / thread mismatch");
-  constexpr int kStageElems = kStage * (KSTR + VSTR);
-  static_assert(kStageBufs * kStageElems * 2 >= 4 * (16 * (D / 32) + 2) * kWave * 4,
-                "merge scratch must fit");
+  constexpr int ROW_BYTES = D * 2;
+  constexpr int kRowsPerDma = kWave / CHUNKS;             // rows one wave load covers
+  constexpr int kDmaPerWave = kStage / kPrefillWaves / kRowsPerDma;  // per tensor
+  constexpr int kRegionBytes = kStage * ROW_BYTES;        // K (or V) rows of a stage
+  constexpr int kStageBytes = 2 * kRegionBytes;
+  constexpr int kIdsOff = kStageBufs * kStageBytes;       // block-id ring
+  static_assert(kDmaPerWave >= 1, "stage / wave mismatch");
+  static_assert(kStageBufs * kStageBytes >= 4 * (16 * DB + 2) * kWave * 4, "merge scratch must fit");
 
-  // Three stage buffers (K rows then V rows); reused for the final merge.
-  __shared__ __attribute__((aligned(16))) uint16_t s_lds[kStageBufs * kStageElems];
+  // Four stage buffers (K rows, then V rows, swizzled) and the block-id ring;
+  // the stage buffers are reused for the final merge.
+  __shared__ __attribute__((aligned(16))) char s_lds[kIdsOff + kIdRing * kIdSlotBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  // Wave-uniform (scalar): branches on it are whole-wave branches, and the
+  // copy counts each wave waits on are exact.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int rg = wave & 3;   // row group
   const int kh = wave >> 2;  // context half of every stage
   const int hkv = a.num_kv_heads;
@@ -109,11 +148,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int bs_mask = (1 << log2_bs) - 1;
   // Byte strides of a cache row and a cache block (the host keeps a block
   // under 4 GiB, so a row offset is one 32 x 32 -> 64-bit multiply-add).
-  const uint32_t row_bytes = static_cast<uint32_t>(hkv) * D * 2;
+  const uint32_t row_bytes = static_cast<uint32_t>(hkv) * ROW_BYTES;
   const uint32_t block_bytes = row_bytes << log2_bs;
   const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
-  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * D * 2;
-  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * D * 2;
+  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * ROW_BYTES;
+  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * ROW_BYTES;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_lds));
 
   // This lane's query row.
   const int row = rg * 32 + (lane & 31);
@@ -143,79 +183,62 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // Tiles below this index need no mask for any row of the workgroup.
   const int first_masked = min(start + tok0 + 1, kv_end) / kKvTile;
   const float scale = a.scale_log2e;
+  const int last_col = a.block_table_stride - 1;
 
-  // ---- staging: thread piece p covers stage row ld_row + p*kRowsPerPass,
-  // 16 bytes at chunk ld_ch, of K and of V.  Every load is issued
-  // unconditionally (no branch around a memory instruction), so the memory
-  // counter waits stay exact and two stages are in flight in registers:
-  //  - rows past the readable context re-read its last row (finite; their
-  //    scores are masked);
-  //  - an out-of-pool block id reads block 0 and is zeroed before it
-  //    reaches LDS (the reference leaves such ids undefined).
-  // Block ids are fetched two iterations before their rows are loaded.
-  constexpr int kRowsPerPass = kPrefillThreads / CHUNKS;
-  const int ld_row = tid / CHUNKS;
-  const uint32_t lane_bytes = static_cast<uint32_t>(tid - ld_row * CHUNKS) * 16;
-  const int ld_col = (tid - ld_row * CHUNKS) * 8;
-
-  auto row_of = [&](int stage, int p) {
-    return min(stage * kStage + ld_row + p * kRowsPerPass, kv_read - 1);
+  // ---- staging ---------------------------------------------------------------
+  // Block ids: wave 0 copies the table entries a stage needs (at most 64)
+  // into slot (stage & 7) of an LDS ring, five stages ahead of use.  K/V:
+  // every wave copies rows [8 w, 8 w + 8) of a stage (lane -> row
+  // lane / CHUNKS of its load, chunk position lane % CHUNKS, fetching the
+  // chunk that the swizzle puts there), three stages ahead.  Rows past the
+  // readable context re-read its last row (finite; their scores are
+  // masked); an out-of-pool block id reads block 0 (the reference leaves
+  // such ids undefined).  Every copy is issued unconditionally, so each
+  // wave's outstanding count is the same every step.
+  auto dma_ids = [&](int stage) {
+    const int col = min(((stage * kStage) >> log2_bs) + lane, last_col);
+    dma4(lds0 + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes, bt + col);
   };
-  auto fetch_blocks = [&](int stage, int* out) {
+  const int dma_row0 = wave * (kStage / kPrefillWaves) + lane / CHUNKS;  // + j * kRowsPerDma
+  auto dma_kv = [&](int stage, int buf_off) {
+    const int col0 = (stage * kStage) >> log2_bs;
+    const int* ids = reinterpret_cast<const int*>(s_lds + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes);
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) out[p] = bt[row_of(stage, p) >> log2_bs];
-  };
-  auto load_tile = [&](int stage, const int* bl, uint4* kd, uint4* vd, uint32_t& bad) {
-    bad = 0;
-#pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int pos = row_of(stage, p);
-      const bool ok = static_cast<uint32_t>(bl[p]) < static_cast<uint32_t>(a.total_blocks);
-      const uint32_t b = ok ? static_cast<uint32_t>(bl[p]) : 0u;
-      const uint64_t off = static_cast<uint64_t>(b) * block_bytes +
-                           (static_cast<uint32_t>(pos & bs_mask) * row_bytes + lane_bytes);
-      kd[p] = ld16(kbase + off);
-      vd[p] = ld16(vbase + off);
-      bad |= ok ? 0u : (1u << p);
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int r = dma_row0 + j * kRowsPerDma;  // row inside the stage
+      const int pos = min(stage * kStage + r, kv_read - 1);
+      // (clamped: past the last stage pos may precede the stage's first column)
+      const int b = ids[min(max((pos >> log2_bs) - col0, 0), kIdSlotBytes / 4 - 1)];
+      const uint32_t bb = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks)
+                              ? static_cast<uint32_t>(b) : 0u;
+      const int chunk = (lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(r);
+      const uint64_t off = static_cast<uint64_t>(bb) * block_bytes +
+                           (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk * 16);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          lds0 + buf_off + (r - lane / CHUNKS) * ROW_BYTES);
+      dma16(dst, kbase + off);
+      dma16(dst + kRegionBytes, vbase + off);
     }
   };
-  auto store_tile = [&](int off, uint4* kd, uint4* vd, uint32_t bad) {
-    if (__builtin_amdgcn_ballot_w64(bad != 0) != 0) {
-#pragma unroll
-      for (int p = 0; p < PIECES; ++p)
-        if ((bad >> p) & 1u) kd[p] = vd[p] = make_uint4(0, 0, 0, 0);
-    }
-    uint16_t* sk = s_lds + off;
-    uint16_t* sv = sk + kStage * KSTR;
-#pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int r = ld_row + p * kRowsPerPass;
-      *reinterpret_cast<uint4*>(&sk[r * KSTR + ld_col]) = kd[p];
-      *reinterpret_cast<uint4*>(&sv[r * VSTR + ld_col]) = vd[p];
-    }
+  // Outstanding copies a wave leaves behind the stage it must see landed:
+  // its K/V copies of one stage plus, for wave 0, one id copy.
+  auto wait_stage = [&]() {
+    if (wave == 0) wait_vmcnt<2 * kDmaPerWave + 1>();
+    else wait_vmcnt<2 * kDmaPerWave>();
   };
 
-  // Two register stages (X: even iterations, Y: odd) and their block ids.
-  uint4 kx[PIECES], vx[PIECES], ky[PIECES], vy[PIECES];
-  int bx[PIECES], by[PIECES];
-  uint32_t badx, bady;
-
-  // Prologue: stages 0 and 1 into LDS buffers 0 and 1, stages 2 and 3 in
-  // registers, block ids of stages 4 and 5.
-  fetch_blocks(0, bx);
-  fetch_blocks(1, by);
-  load_tile(0, bx, kx, vx, badx);
-  load_tile(1, by, ky, vy, bady);
-  fetch_blocks(2, bx);
-  fetch_blocks(3, by);
-  store_tile(0, kx, vx, badx);
-  store_tile(kStageElems, ky, vy, bady);
-  // (same issue order as the loop, so its memory counter waits hold on
-  // entry too)
-  load_tile(2, bx, kx, vx, badx);
-  fetch_blocks(4, bx);
-  load_tile(3, by, ky, vy, bady);
-  fetch_blocks(5, by);
+  // Prologue: ids of stages 0-4, then K/V of stages 0-2 (the loop's step st
+  // copies K/V of stage st+3 and ids of stage st+5).
+  if (wave == 0) {
+#pragma unroll
+    for (int s = 0; s < 5; ++s) dma_ids(s);
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+  dma_kv(0, 0);
+  dma_kv(1, kStageBytes);
+  dma_kv(2, 2 * kStageBytes);
+  wait_vmcnt<2 * kDmaPerWave>();  // stages 0 and 1 landed
   __syncthreads();
 
   f32x16 acc[DB];
@@ -225,56 +248,71 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
   float m = kScoreFloor, l = 0.f;
 
-  // Per-lane LDS offsets of the MFMA operands (inside this wave's half).
-  const int k_off = (kh * kKvTile + (lane & 31)) * KSTR + half * 8;
+  // Per-lane byte offsets of the MFMA operands inside a stage buffer (this
+  // wave's half of the stage; chunk positions follow the swizzle).
+  const int k_row = kh * kKvTile + (lane & 31);
+  int k_off[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    k_off[ks] = k_row * ROW_BYTES + (((half + 2 * ks) ^ chunk_swizzle<CHUNKS>(k_row)) * 16);
   const int li = lane & 15;
-  const int v_off = kStage * KSTR + (kh * kKvTile + 4 * half + (li >> 2)) * VSTR +
-                    16 * ((lane >> 4) & 1) + 4 * (li & 3);
+  int v_off[2][DB];  // [8-row half][d block]; +16 rows per k-step is added below
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) {
+    const int r = kh * kKvTile + 4 * half + (li >> 2) + 8 * hi;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int col = 16 * ((lane >> 4) & 1) + 4 * (li & 3) + 32 * db;  // element
+      v_off[hi][db] = kRegionBytes + r * ROW_BYTES +
+                      (((col >> 3) ^ chunk_swizzle<CHUNKS>(r)) * 16) + (col & 7) * 2;
+    }
+  }
+  auto read_k = [&](int buf_off, uint4* ka) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(s_lds + buf_off + k_off[ks]);
+  };
+  auto read_vt = [&](int buf_off, uint4 (*va)[DB]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const char* base = s_lds + buf_off + ks * 16 * ROW_BYTES;
+        const uint2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + v_off[0][db]));
+        const uint2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + v_off[1][db]));
+        va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+  };
 
   // The scores of stage st+1 are computed while stage st's are turned into
   // probabilities: the QK MFMAs of the next tile are interleaved with the
   // exponentials of this one, so the matrix pipe and the VALU overlap inside
-  // a wave.  Stage buffers rotate through LDS offsets kept in scalars.
+  // a wave.  Stage buffers rotate through byte offsets kept in scalars:
+  // stage st (V read), st+1 (K read), st+2 (landed), st+3 (being copied).
+  // (computed unconditionally -- unused when the wave has no tile -- so the
+  // query loads are complete on every path into the loop and the compiler
+  // adds no memory-counter wait inside it)
   f32x16 s_cur;
 #pragma unroll
   for (int i = 0; i < 16; ++i) s_cur[i] = 0.f;
-  int off_cur = 0, off_next = kStageElems, off_store = 2 * kStageElems;
-  if (kh < ntiles) {
+  {
     uint4 ka[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      ka[ks] = *reinterpret_cast<const uint4*>(s_lds + k_off + ks * 16);
+    read_k(0, ka);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) s_cur = mfma32(ka[ks], qreg[ks], s_cur);
   }
+  int off_cur = 0, off_next = kStageBytes, off_land = 2 * kStageBytes, off_copy = 3 * kStageBytes;
 
-  // One pipeline step: stage st+2 registers -> LDS, stage st+4 loads issued
-  // into the same registers, block ids of stage st+6, then the tile of
-  // stage st.  Returns the scores of stage st+1.
-  auto step = [&](int st, uint4* kd, uint4* vd, int* bl, uint32_t& bad, const f32x16& s_in) {
-    store_tile(off_store, kd, vd, bad);
-    load_tile(st + 4, bl, kd, vd, bad);
-    fetch_blocks(st + 6, bl);
+  auto step = [&](int st, const f32x16& s_in) {
+    dma_kv(st + 3, off_copy);
+    if (wave == 0) dma_ids(st + 5);
     const int t = 2 * st + kh;  // this wave's 32-token tile
     f32x16 s_next = s_in;
     if (t < ntiles) {
       // LDS operands: V^T of this stage, K of the next one (read even when
       // there is no next tile: the stale scores are never used).
-      const uint16_t* sv = s_lds + off_cur + v_off;
-      uint4 va[2][DB];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const uint16_t* p0 = sv + ks * 16 * VSTR + db * 32;
-          const uint2 lo = lds_read_tr16(p0);
-          const uint2 hi = lds_read_tr16(p0 + 8 * VSTR);
-          va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-      const uint16_t* sk = s_lds + off_next + k_off;
-      uint4 ka[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(sk + ks * 16);
+      uint4 va[2][DB], ka[KS];
+      read_vt(off_cur, va);
+      read_k(off_next, ka);
 
       // ---- online softmax of s_in (unscaled scores; exp2 folds the scale)
       f32x16 s = s_in;
@@ -338,22 +376,28 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     }  // t < ntiles
     const int o = off_cur;
     off_cur = off_next;
-    off_next = off_store;
-    off_store = o;
+    off_next = off_land;
+    off_land = off_copy;
+    off_copy = o;
+    // Stage st+2 (read as K next step) and the ids of stage st+4 must have
+    // landed before the barrier publishes them.
+    wait_stage();
     __syncthreads();
     return s_next;
   };
 
-  // Two steps per trip so that the register stages and block-id sets
-  // alternate by name.  A trailing step past the last stage computes
-  // nothing (its tiles are past ntiles) and only reloads clamped rows.
+  // Two steps per trip (the compiler then keeps the scores in place).  A
+  // trailing step past the last stage computes nothing and only copies
+  // clamped rows into a free buffer.
   for (int st = 0; st < nstages; st += 2) {
-    const f32x16 s_mid = step(st, kx, vx, bx, badx, s_cur);
-    s_cur = step(st + 1, ky, vy, by, bady, s_mid);
+    const f32x16 s_mid = step(st, s_cur);
+    s_cur = step(st + 1, s_mid);
   }
+  // Let every copy land before the buffers are reused for the merge.
+  wait_vmcnt<0>();
+  __syncthreads();
 
   // ---- merge the two context halves of every row group ---------------------
-  // (the loop ended on a barrier, so the stage buffers are free)
   float* scratch = reinterpret_cast<float*>(s_lds) + rg * (16 * DB + 2) * kWave;
   if (kh == 1) {
 #pragma unroll
