@@ -238,12 +238,21 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   const int lig = lane % L;  // lane within its row group
   const int gi = lane / L;   // row group within the wave
   constexpr int QCHUNKS = G * D / CE;  // 16-byte pieces of the G query rows
+  constexpr int GH = G >= 2 ? G / 2 : 1;  // query heads per real KV head when paired
+  constexpr int HC = D / CE / 2;          // 16-byte pieces of a real head when paired
   for (int i = tid; i < QCHUNKS; i += kDecodeThreads) {
     const int g = i / (D / CE);
     const int c = i - g * (D / CE);
     const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                     static_cast<int64_t>(kvh * G + g) * a.q_head_stride;
-    s_q[i] = ld16(qrow + c * CE);
+    if (a.pair) {
+      // Query head g belongs to real KV head g / GH of the pair: its D/2
+      // elements go into that half of the row, zeros into the other, so the
+      // D-wide dot products give exactly the real head's scores.
+      s_q[i] = (c / HC) == (g / GH) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
+    } else {
+      s_q[i] = ld16(qrow + c * CE);
+    }
   }
   __syncthreads();
 
@@ -561,7 +570,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
       l = fmaf(s_l[w][g], f, l);
     }
     if (nparts <= 1) {
-      store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
+      if (!a.pair) {
+        store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
+      } else if (((i - g * D) / (D / 2)) == (g / GH)) {
+        // Only the half of the paired row that belongs to the head's own KV
+        // head is its output (the other half weighted the partner's V).
+        T* out_pair = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G + g) * (D / 2);
+        store_scalar<T>(out_pair + (i - g * D) % (D / 2), l > 0.f ? o / l : 0.f);
+      }
     } else {
       pacc[i] = o;
       if (i % D == 0) {
@@ -599,8 +615,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
   const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
   T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
+  const int gh = G >= 2 ? G / 2 : 1;  // query heads per real KV head when paired
   for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
     const int h = kvh * G + i / D;
+    // Paired KV heads: only the own half of a row is output (see the
+    // partition kernel).
+    if (a.pair && ((i % D) / (D / 2)) != ((i / D) / gh)) continue;
     const float* ml = a.part_ml + 2 * h;
     const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
     float mx = kScoreFloor, sum = 0.f, o = 0.f;
@@ -635,7 +655,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
       o = fmaf(xp, w, o * r);
       mx = mn;
     }
-    store_scalar<T>(out + i, sum > 0.f ? o / sum : 0.f);
+    const float r = sum > 0.f ? o / sum : 0.f;
+    if (a.pair)
+      store_scalar<T>(reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + h) * (D / 2) +
+                          (i % D) % (D / 2), r);
+    else
+      store_scalar<T>(out + i, r);
   }
 }
 

@@ -30,6 +30,10 @@ struct DecodeArgs {
   int32_t log2_block_size;
   int32_t partition;
   float scale_log2e;
+  // 1: two adjacent real KV heads of D/2 run as one of D (G counts the query
+  // heads of both); queries are staged into their half, outputs written from
+  // it.  Partials keep the paired layout.
+  int32_t pair;
 };
 
 // Generic one-wave-per-(query token, head) attention: any head_dim <= 256,

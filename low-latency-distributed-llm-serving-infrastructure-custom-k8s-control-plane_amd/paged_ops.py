@@ -407,11 +407,13 @@ def copy_blocks(src_cache: torch.Tensor, dst_cache: torch.Tensor, block_mapping)
 
 
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
-    """Bytes pa_decode needs for its split-K partials."""
+    """Bytes pa_decode needs for its split-K partials (heads of 64 may run as
+    pairs, whose partial rows are 128 wide: reserved for every dtype)."""
     if num_decode_items <= 0:
         return 0
     rows = num_decode_items * num_query_heads
-    acc = (rows * head_dim * 4 + 255) & ~255
+    dim = 128 if head_dim == 64 else head_dim
+    acc = (rows * dim * 4 + 255) & ~255
     ml = (rows * 2 * 4 + 255) & ~255
     return acc + ml
 
