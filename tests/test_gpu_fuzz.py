@@ -1,0 +1,70 @@
+"""Randomised parity of a whole step on the GPU against the oracle.
+
+Each seed draws a head layout (H_kv in {1, 2, 3, 4, 8}, group 1-8, D 64 or
+128), a dtype (bf16 or fp32), a block size (1-64), a ragged batch of decodes
+(contexts 1-700) and prefill chunks (2-90 tokens at starts 0-400) and a
+split-K partition (automatic or 32-512 tokens).  The step is packed, its new
+K/V rows are written into a random non-contiguous pool, decode and prefill
+run, and every output row is compared with the oracle run on the cache the
+GPU read (fp32 to 1e-4 absolute, bf16 to the relative bound of the parity
+tests).  This covers the combinations the fixed-shape tests do not name:
+paired and unpaired heads of 64, groups that do not divide 128, tiny blocks
+with short partitions, and prefill chunks beside split-K decodes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import pkg
+from test_gpu_parity import check_rows, log, oracle_rows
+
+pytestmark = pytest.mark.gpu
+
+ops = pkg("paged_ops")
+wl = pkg("workloads")
+
+
+def random_case(seed):
+    rng = np.random.Generator(np.random.PCG64(1000 + seed))
+    hkv = int(rng.choice([1, 2, 3, 4, 8]))
+    group = int(rng.integers(1, 9))
+    d = int(rng.choice([64, 128]))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float32
+    bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
+    starts, counts = [], []
+    for _ in range(int(rng.integers(1, 11))):
+        if rng.random() < 0.6:
+            c = int(rng.integers(1, 700))
+            starts.append(c - 1)
+            counts.append(1)
+        else:
+            starts.append(int(rng.integers(0, 400)))
+            counts.append(int(rng.integers(2, 90)))
+    ctx = [s + c for s, c in zip(starts, counts)]
+    need = [-(-c // bs) for c in ctx]
+    pool = sum(need) + 5
+    perm = rng.permutation(pool)
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    partition = int(rng.choice([0, 32, 64, 256, 512]))
+    w = wl.StepWorkload(f"fuzz{seed}", hkv * group, hkv, d, bs, dtype, 1.0, starts, counts, lists, pool)
+    return w, (partition or None)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_steps_match_oracle(device, seed):
+    w, partition = random_case(seed)
+    log(f"fuzz seed={seed}: H_q={w.num_query_heads} H_kv={w.num_kv_heads} D={w.head_dim} {w.dtype} "
+        f"bs={w.block_size} B={w.num_seqs} counts={w.new_token_counts} partition={partition}")
+    t = wl.make_tensors(w, device, seed=seed)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         partition_size=partition, num_kv_heads=w.num_kv_heads,
+                         num_query_heads=w.num_query_heads)
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=w.dtype == torch.float32)
