@@ -57,8 +57,12 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #endif
 // Occupancy floor for a group of G query heads: the register budget of the
 // wider groups does not fit four waves per SIMD without spilling.
+#ifndef PA_DECODE_MIN_WAVES_WIDE
+#define PA_DECODE_MIN_WAVES_WIDE 2  // the same for wider groups or rows
+#endif
 #define PA_DECODE_OCCUPANCY(T, D, G) \
-  __attribute__((amdgpu_waves_per_eu(((G) <= 4 && (D) * sizeof(T) <= 256) ? PA_DECODE_MIN_WAVES : 2)))
+  __attribute__((amdgpu_waves_per_eu(((G) <= 4 && (D) * sizeof(T) <= 256) ? PA_DECODE_MIN_WAVES \
+                                                                          : PA_DECODE_MIN_WAVES_WIDE)))
 
 typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
