@@ -307,7 +307,8 @@ def main() -> int:
     table = torch.from_numpy(w.block_table_array()).to(device)
     tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
-                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
+                         head_dim=w.head_dim, dtype=w.dtype)
     out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
     stream = torch.cuda.current_stream(device)
 
@@ -345,7 +346,8 @@ def main() -> int:
 
     def full_step():
         s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
-                          num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
+                          num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
+                          head_dim=w.head_dim, dtype=w.dtype)
         ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
         ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
 

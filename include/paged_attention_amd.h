@@ -206,6 +206,17 @@ int pa_copy_blocks(const void *src_cache, void *dst_cache,
  * split-K partials).  Calls that share a workspace must not overlap in time. */
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
 
+/* KV heads that one pa_decode workgroup reads together: 2 when two adjacent
+ * KV heads run as one (bf16, an even KV head count, head_dim 64 with groups
+ * of up to 4 query heads or head_dim 128 with groups of up to 2: each token's
+ * rows of the two heads are read as one row of twice the length), else 1;
+ * 0 for head counts pa_decode rejects.  A host choosing the split-K
+ * partition size from the launch width divides the KV head count by it.
+ * (No counterpart in the reference, whose CPU kernel has no workgroups.) */
+int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim,
+                                         int32_t num_kv_heads,
+                                         int32_t num_query_heads);
+
 /*
  * Replaces: NativePagedBackend.attend for decode steps
  * (app/model/attention_backends.py:88-117) and the paged_attention kernel

@@ -245,15 +245,11 @@ int pa_copy_blocks(const void* src_cache, void* dst_cache, const int64_t* block_
 }
 
 namespace {
-// bf16 heads of 64 with an even KV head count and groups of 1 or 2 run as
-// pairs of KV heads: one 256-byte row per token instead of two 128-byte ones
-// (cfg-4 lengths, 16/16/64: 0.60 -> 0.76 of HBM peak).  Groups of 4 would
-// become 8-head groups, whose VALU load outweighs the longer rows
-// (32/8/64: 0.55 -> 0.49), so they stay unpaired.
+// Two adjacent KV heads run as one workgroup reading one row of twice the
+// length per token (pa::decode_pairs_heads has the shapes).
 bool decode_pairs(const PaStepDims& d) {
   const int group = d.num_kv_heads > 0 ? d.num_query_heads / d.num_kv_heads : 0;
-  return d.dtype == PA_DTYPE_BF16 && d.head_dim == 64 && d.num_kv_heads % 2 == 0 &&
-         group >= 1 && group <= 2;
+  return pa::decode_pairs_heads(d.dtype, d.head_dim, d.num_kv_heads, group);
 }
 struct DecodeWorkspaceLayout {
   size_t acc, ml, total;
@@ -264,8 +260,7 @@ DecodeWorkspaceLayout decode_workspace_layout(const PaStepDims& dims, int64_t it
   DecodeWorkspaceLayout w{0, 0, 0};
   if (items <= 0 || dims.num_query_heads <= 0 || dims.head_dim <= 0) return w;
   const size_t rows = static_cast<size_t>(items) * dims.num_query_heads;
-  const size_t dim = decode_pairs(dims) ? 2 * dims.head_dim : dims.head_dim;  // paired rows
-  w.acc = (rows * dim * sizeof(float) + 255) & ~size_t(255);
+  w.acc = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
   w.ml = (rows * 2 * sizeof(float) + 255) & ~size_t(255);
   w.total = w.acc + w.ml;
   return w;
@@ -274,6 +269,13 @@ DecodeWorkspaceLayout decode_workspace_layout(const PaStepDims& dims, int64_t it
 
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items) {
   return decode_workspace_layout(dims, num_decode_items).total;
+}
+
+int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
+                                         int32_t num_query_heads) {
+  if (num_kv_heads <= 0 || num_query_heads <= 0 || num_query_heads % num_kv_heads != 0) return 0;
+  return pa::decode_pairs_heads(dtype, head_dim, num_kv_heads, num_query_heads / num_kv_heads) ? 2
+                                                                                                : 1;
 }
 
 int pa_decode(const void* query, const void* key_cache, const void* value_cache,
@@ -315,10 +317,8 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
   const int eb = elem_bytes(dims.dtype);
   const int log2_bs = log2_exact(dims.block_size);
   const bool pair = decode_pairs(dims);
-  const int k_dim = pair ? 2 * dims.head_dim : dims.head_dim;  // kernel's head dim
-  const int k_group = pair ? 2 * group : group;                // and group
   const bool fast =
-      pa::decode_fast_path_supported(dims.dtype, k_dim, k_group, dims.block_size,
+      pa::decode_fast_path_supported(dims.dtype, dims.head_dim, group, dims.block_size,
                                      dims.partition_size) &&
       aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&
       (dims.q_token_stride * eb) % 16 == 0 && (dims.q_head_stride * eb) % 16 == 0;
@@ -352,7 +352,7 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
     a.scale_log2e = scaling * pa::kLog2e;
     a.pair = pair ? 1 : 0;
     return from_hip(
-        pa::launch_decode(a, dims.dtype, k_dim, k_group, num_decode_items, phases, s),
+        pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s),
         "pa_decode");
   }
   if (!pa::generic_supported(dims.dtype, dims.head_dim))

@@ -60,9 +60,12 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #ifndef PA_DECODE_MIN_WAVES_WIDE
 #define PA_DECODE_MIN_WAVES_WIDE 2  // the same for wider groups or rows
 #endif
-#define PA_DECODE_OCCUPANCY(T, D, G) \
-  __attribute__((amdgpu_waves_per_eu(((G) <= 4 && (D) * sizeof(T) <= 256) ? PA_DECODE_MIN_WAVES \
-                                                                          : PA_DECODE_MIN_WAVES_WIDE)))
+// GA: query heads whose accumulators one lane holds (G, or G/2 when paired,
+// whose rows of up to 512 bytes come in half-length tiles).
+#define PA_DECODE_OCCUPANCY(T, D, GA, PAIR)                                        \
+  __attribute__((amdgpu_waves_per_eu(((GA) <= 4 && ((D) * sizeof(T) <= 256 || (PAIR))) \
+                                         ? PA_DECODE_MIN_WAVES                       \
+                                         : PA_DECODE_MIN_WAVES_WIDE)))
 
 typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -138,6 +141,27 @@ struct VRaw<8> {
   using type = uint2;
 };
 
+// Dot product of one 16-byte piece of K with the matching piece of q.
+template <typename T>
+__device__ __forceinline__ float piece_dot(uint4 q, uint4 k, float acc) {
+  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
+    acc = dot2_bf16(q.x, k.x, acc);
+    acc = dot2_bf16(q.y, k.y, acc);
+    acc = dot2_bf16(q.z, k.z, acc);
+    acc = dot2_bf16(q.w, k.w, acc);
+  } else {
+    acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
+    acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
+    acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
+    acc = fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
+  }
+  return acc;
+}
+
+// 32-bit word w of a lane's V piece (a bf16 pair).
+__device__ __forceinline__ uint32_t v_word(uint32_t v, int) { return v; }
+__device__ __forceinline__ uint32_t v_word(uint2 v, int w) { return w == 0 ? v.x : v.y; }
+
 // Dot product of one lane's K slice (two 16-byte pieces) with its q slice.
 template <typename T>
 __device__ __forceinline__ float slice_dot(const uint4 (&q)[2], const uint4 (&k)[2]) {
@@ -183,9 +207,18 @@ __device__ __forceinline__ float across_groups_max(float x) {
   return x;
 }
 
-template <typename T, int D, int G>
-__global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void decode_partition_kernel(DecodeArgs a) {
-  using S = DecodeShape<T, D, (G > 4 ? PA_DECODE_TILE_WIDE : PA_DECODE_TILE)>;
+// PAIR: two adjacent real KV heads of D/2 run as one head of D with the G
+// query heads of both (the first G/2 belong to the first real head).  A
+// lane's first K piece lies in the first real head's half of the row and its
+// second piece in the second's, so each query head dots only its own piece;
+// in the PV layout lanes [0, 32) hold the first half, and each lane
+// accumulates only the G/2 heads of its half.
+template <typename T, int D, int G, bool PAIR>
+__global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G / 2 : G), PAIR) void decode_partition_kernel(DecodeArgs a) {
+  // Tiles of 16 tokens for wide groups and for paired rows of 512 bytes (the
+  // same bytes per tile as 32 tokens of 256-byte rows).
+  using S = DecodeShape<T, D, ((G > 4 || (PAIR && D * sizeof(T) > 256)) ? PA_DECODE_TILE_WIDE
+                                                                          : PA_DECODE_TILE)>;
   using VR = typename VRaw<S::kPvBytes>::type;
   constexpr int L = S::kL;
   constexpr int GPW = S::kGpw;
@@ -198,13 +231,17 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   // p staging per wave: bf16 pairs [16 pairs][G] or fp32 [32 tokens][G]
   constexpr int kTile = S::kTile;
   constexpr int PWORDS = BF16 ? (kTile / 2) * G : kTile * G;
+  constexpr int GA = PAIR ? G / 2 : G;    // heads a lane accumulates
+  constexpr int OUT_D = PAIR ? D / 2 : D;  // output elements per query head
+  static_assert(!PAIR || (BF16 && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
+                "pairs: bf16, an even head count, one V row per wave load");
 
   __shared__ int s_blk[kMaxPartition + 2];
   __shared__ uint4 s_q[G * D * S::kE / 16];
   __shared__ uint32_t s_p[kDecodeWaves][PWORDS];
   __shared__ float s_m[kDecodeWaves][G];
   __shared__ float s_l[kDecodeWaves][G];
-  __shared__ float s_acc[kDecodeWaves][G * D];
+  __shared__ float s_acc[kDecodeWaves][G * OUT_D];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -242,18 +279,16 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   const int lig = lane % L;  // lane within its row group
   const int gi = lane / L;   // row group within the wave
   constexpr int QCHUNKS = G * D / CE;  // 16-byte pieces of the G query rows
-  constexpr int GH = G >= 2 ? G / 2 : 1;  // query heads per real KV head when paired
-  constexpr int HC = D / CE / 2;          // 16-byte pieces of a real head when paired
+  constexpr int HC = D / CE / 2;  // 16-byte pieces of a real head when paired
   for (int i = tid; i < QCHUNKS; i += kDecodeThreads) {
     const int g = i / (D / CE);
     const int c = i - g * (D / CE);
     const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                     static_cast<int64_t>(kvh * G + g) * a.q_head_stride;
-    if (a.pair) {
-      // Query head g belongs to real KV head g / GH of the pair: its D/2
-      // elements go into that half of the row, zeros into the other, so the
-      // D-wide dot products give exactly the real head's scores.
-      s_q[i] = (c / HC) == (g / GH) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
+    if constexpr (PAIR) {
+      // Query head g belongs to real KV head g / GA of the pair: its D/2
+      // elements go into that half of the row (the other half is never read).
+      s_q[i] = (c / HC) == (g / GA) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
     } else {
       s_q[i] = ld16(qrow + c * CE);
     }
@@ -263,13 +298,15 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   const float scale = a.scale_log2e;
   const int sub = lane / S::kLp;  // V row of this lane within a wave load
   const int lp = lane % S::kLp;   // head-dimension slice of this lane
-  float m[G], acc[G][PE];
+  // Paired: which real head's half of the row the lane's V slice lies in.
+  const int hh = PAIR ? lp / (S::kLp / 2) : 0;
+  float m[G], acc[GA][PE];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kScoreFloor;
+  for (int g = 0; g < G; ++g) m[g] = kScoreFloor;
 #pragma unroll
-    for (int e = 0; e < PE; ++e) acc[g][e] = 0.f;
-  }
+  for (int j = 0; j < GA; ++j)
+#pragma unroll
+    for (int e = 0; e < PE; ++e) acc[j][e] = 0.f;
 
   // ---- per-tile work ------------------------------------------------------
   // Softmax exponentials are spread over the lanes of a row group: lane lig
@@ -400,11 +437,19 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       uint4 qg[2];
-      qg[0] = s_q[g * (D / CE) + lig];
-      qg[1] = s_q[g * (D / CE) + L + lig];
+      if constexpr (PAIR) {
+        // The head's own half: piece 0 of every lane for the first G/2
+        // heads, piece 1 for the others.
+        qg[0] = s_q[g * (D / CE) + (g / GA) * L + lig];
+      } else {
+        qg[0] = s_q[g * (D / CE) + lig];
+        qg[1] = s_q[g * (D / CE) + L + lig];
+      }
 #pragma unroll
       for (int i = 0; i < TPG; ++i) {
-        float v = group_sum<L>(slice_dot<T>(qg, kb[i]));
+        float v;
+        if constexpr (PAIR) v = group_sum<L>(piece_dot<T>(qg[0], kb[i][g / GA], 0.f));
+        else v = group_sum<L>(slice_dot<T>(qg, kb[i]));
         if (!full) v = kok[i] ? v : -INFINITY;
         s[i][g] = v;
         tmax[g] = fmaxf(tmax[g], v);
@@ -419,13 +464,18 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
       moved |= m_new[g] != m[g];
     }
     if (moved) {  // wave-uniform
+      float alpha[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float alpha = fast_exp2((m[g] - m_new[g]) * scale);
-        lsum[g] *= alpha;
-#pragma unroll
-        for (int e = 0; e < PE; ++e) acc[g][e] *= alpha;
+        alpha[g] = fast_exp2((m[g] - m_new[g]) * scale);
+        lsum[g] *= alpha[g];
         m[g] = m_new[g];
+      }
+#pragma unroll
+      for (int j = 0; j < GA; ++j) {
+        const float al = PAIR ? (hh ? alpha[GA + j] : alpha[j]) : alpha[j];
+#pragma unroll
+        for (int e = 0; e < PE; ++e) acc[j][e] *= al;
       }
     }
     float mneg[G];
@@ -476,16 +526,20 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
         if (((R * u) % (2 * GPW)) >= GPW) continue;
         const int t = R * u + sub;
         const int pidx = (t / (2 * GPW)) * GPW + (t % GPW);
-        uint32_t pw[G];
+        uint32_t pw[GA];
 #pragma unroll
-        for (int g = 0; g < G; ++g) pw[g] = sp[pidx * G + g];
-        const uint32_t va = vb[u], vbb = vb[u + PARTNER];
-        const uint32_t lo = __builtin_amdgcn_perm(vbb, va, 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(vbb, va, 0x07060302u);
+        for (int j = 0; j < GA; ++j) pw[j] = sp[pidx * G + (PAIR ? hh * GA + j : j)];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          acc[g][0] = dot2_bf16(pw[g], lo, acc[g][0]);
-          acc[g][1] = dot2_bf16(pw[g], hi, acc[g][1]);
+        for (int w = 0; w < PE / 2; ++w) {
+          // Element 2w (lo) and 2w+1 (hi) of tokens t and t + GPW, paired.
+          const uint32_t va = v_word(vb[u], w), vbb = v_word(vb[u + PARTNER], w);
+          const uint32_t lo = __builtin_amdgcn_perm(vbb, va, 0x05040100u);
+          const uint32_t hi = __builtin_amdgcn_perm(vbb, va, 0x07060302u);
+#pragma unroll
+          for (int j = 0; j < GA; ++j) {
+            acc[j][2 * w] = dot2_bf16(pw[j], lo, acc[j][2 * w]);
+            acc[j][2 * w + 1] = dot2_bf16(pw[j], hi, acc[j][2 * w + 1]);
+          }
         }
       }
     } else {
@@ -500,7 +554,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
           v[1] = __uint_as_float(vb[u].y);
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GA; ++g) {
           const float p = __uint_as_float(sp[t * G + g]);
 #pragma unroll
           for (int e = 0; e < PE; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e]);
@@ -538,14 +592,18 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
 #pragma unroll
   for (int o = kWave / 2; o >= S::kLp; o >>= 1)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int j = 0; j < GA; ++j)
 #pragma unroll
-      for (int e = 0; e < PE; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, kWave);
+      for (int e = 0; e < PE; ++e) acc[j][e] += __shfl_xor(acc[j][e], o, kWave);
   if (sub == 0) {
+    // s_acc rows hold OUT_D elements: when paired, the half of the row that
+    // belongs to the head's own real KV head (the lane's slice lies in the
+    // half of real head hh, whose query heads are hh*GA .. hh*GA + GA-1).
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int j = 0; j < GA; ++j)
 #pragma unroll
-      for (int e = 0; e < PE; ++e) s_acc[wave][g * D + lp * PE + e] = acc[g][e];
+      for (int e = 0; e < PE; ++e)
+        s_acc[wave][(PAIR ? hh * GA + j : j) * OUT_D + lp * PE - hh * OUT_D + e] = acc[j][e];
   }
   if (lane < G) {
 #pragma unroll
@@ -557,12 +615,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
   }
   __syncthreads();
 
+  // Outputs and partials use the real layout [.., H_q, OUT_D]: a pair's G
+  // query heads are the real heads kvh*G .. kvh*G + G-1.
   const int hq = hkv * G;
   const int nparts = (ctx + a.partition - 1) / a.partition;
-  float* pacc = a.part_acc + (item * hq + kvh * G) * D;
-  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * D;
-  for (int i = tid; i < G * D; i += kDecodeThreads) {
-    const int g = i / D;
+  float* pacc = a.part_acc + (item * hq + kvh * G) * OUT_D;
+  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * OUT_D;
+  for (int i = tid; i < G * OUT_D; i += kDecodeThreads) {
+    const int g = i / OUT_D;
     float mx = s_m[0][g];
 #pragma unroll
     for (int w = 1; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
@@ -574,17 +634,10 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, G) void d
       l = fmaf(s_l[w][g], f, l);
     }
     if (nparts <= 1) {
-      if (!a.pair) {
-        store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
-      } else if (((i - g * D) / (D / 2)) == (g / GH)) {
-        // Only the half of the paired row that belongs to the head's own KV
-        // head is its output (the other half weighted the partner's V).
-        T* out_pair = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G + g) * (D / 2);
-        store_scalar<T>(out_pair + (i - g * D) % (D / 2), l > 0.f ? o / l : 0.f);
-      }
+      store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
     } else {
       pacc[i] = o;
-      if (i % D == 0) {
+      if (i % OUT_D == 0) {
         float* pml = a.part_ml + (item * hq + kvh * G + g) * 2;
         pml[0] = mx;
         pml[1] = l;
@@ -619,12 +672,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
   const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
   T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
-  const int gh = G >= 2 ? G / 2 : 1;  // query heads per real KV head when paired
   for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
     const int h = kvh * G + i / D;
-    // Paired KV heads: only the own half of a row is output (see the
-    // partition kernel).
-    if (a.pair && ((i % D) / (D / 2)) != ((i / D) / gh)) continue;
     const float* ml = a.part_ml + 2 * h;
     const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
     float mx = kScoreFloor, sum = 0.f, o = 0.f;
@@ -660,30 +709,28 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
       mx = mn;
     }
     const float r = sum > 0.f ? o / sum : 0.f;
-    if (a.pair)
-      store_scalar<T>(reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + h) * (D / 2) +
-                          (i % D) % (D / 2), r);
-    else
-      store_scalar<T>(out + i, r);
+    store_scalar<T>(out + i, r);
   }
 }
 
 // ---- host-side dispatch ------------------------------------------------
 
-template <typename T, int D, int G>
+// D, G: the kernel's head dim and group (twice the real ones when paired).
+template <typename T, int D, int G, bool PAIR>
 static hipError_t launch_decode_t(const DecodeArgs& a, int64_t num_items, int phases,
                                   hipStream_t stream) {
   const int64_t grid = num_items * a.num_kv_heads;
   const int64_t merge_grid = a.num_merge * a.num_kv_heads;
   if (phases & PA_DECODE_PHASE_PARTITIONS) {
-    hipLaunchKernelGGL((decode_partition_kernel<T, D, G>), dim3(static_cast<uint32_t>(grid)),
+    hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR>), dim3(static_cast<uint32_t>(grid)),
                        dim3(kDecodeThreads), 0, stream, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
+  // Partials are in the real layout: rows of D/2 when paired.
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(static_cast<uint32_t>(merge_grid)),
-                     dim3(kDecodeThreads), 0, stream, a, G, D);
+                     dim3(kDecodeThreads), 0, stream, a, G, PAIR ? D / 2 : D);
   return hipGetLastError();
 }
 
@@ -691,16 +738,51 @@ template <typename T, int D>
 static hipError_t launch_decode_g(const DecodeArgs& a, int G, int64_t num_items, int phases,
                                   hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode_t<T, D, 1>(a, num_items, phases, s);
-    case 2: return launch_decode_t<T, D, 2>(a, num_items, phases, s);
-    case 3: return launch_decode_t<T, D, 3>(a, num_items, phases, s);
-    case 4: return launch_decode_t<T, D, 4>(a, num_items, phases, s);
-    case 5: return launch_decode_t<T, D, 5>(a, num_items, phases, s);
-    case 6: return launch_decode_t<T, D, 6>(a, num_items, phases, s);
-    case 7: return launch_decode_t<T, D, 7>(a, num_items, phases, s);
-    case 8: return launch_decode_t<T, D, 8>(a, num_items, phases, s);
+    case 1: return launch_decode_t<T, D, 1, false>(a, num_items, phases, s);
+    case 2: return launch_decode_t<T, D, 2, false>(a, num_items, phases, s);
+    case 3: return launch_decode_t<T, D, 3, false>(a, num_items, phases, s);
+    case 4: return launch_decode_t<T, D, 4, false>(a, num_items, phases, s);
+    case 5: return launch_decode_t<T, D, 5, false>(a, num_items, phases, s);
+    case 6: return launch_decode_t<T, D, 6, false>(a, num_items, phases, s);
+    case 7: return launch_decode_t<T, D, 7, false>(a, num_items, phases, s);
+    case 8: return launch_decode_t<T, D, 8, false>(a, num_items, phases, s);
     default: return hipErrorNotSupported;
   }
+}
+
+// Paired heads of real dim D/2, real group G/2.
+template <int D>
+static hipError_t launch_decode_pair(const DecodeArgs& a, int G, int64_t num_items, int phases,
+                                     hipStream_t s) {
+  switch (G) {
+    case 2: return launch_decode_t<bf16_t, D, 2, true>(a, num_items, phases, s);
+    case 4: return launch_decode_t<bf16_t, D, 4, true>(a, num_items, phases, s);
+    case 6: return launch_decode_t<bf16_t, D, 6, true>(a, num_items, phases, s);
+    case 8: return launch_decode_t<bf16_t, D, 8, true>(a, num_items, phases, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+// Largest real group run as pairs, per real head dim (bf16; 0 = never).
+// Kernel time on 256 lognormal contexts (median 1024) with 8 KV heads,
+// unpaired -> paired, each at its best partition:
+//   D 64:  G 1 0.180 -> 0.141 ms, G 2 0.181 -> 0.140, G 3 0.183 -> 0.147,
+//          G 4 0.183 -> 0.149;
+//   D 128: G 1 0.267 -> 0.254, G 2 0.267 -> 0.259, but G 4 0.270 -> 0.277:
+//          the scores of eight heads summed over 16-lane groups cost more
+//          VALU than the longer rows save.
+#ifndef PA_DECODE_PAIR_MAX_GROUP_D64
+#define PA_DECODE_PAIR_MAX_GROUP_D64 4
+#endif
+#ifndef PA_DECODE_PAIR_MAX_GROUP_D128
+#define PA_DECODE_PAIR_MAX_GROUP_D128 2
+#endif
+
+bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group) {
+  if (dtype != PA_DTYPE_BF16 || num_kv_heads % 2 != 0 || group < 1) return false;
+  if (head_dim == 64) return group <= PA_DECODE_PAIR_MAX_GROUP_D64;
+  if (head_dim == 128) return group <= PA_DECODE_PAIR_MAX_GROUP_D128;
+  return false;
 }
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
@@ -716,6 +798,12 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
                          int64_t num_items, int phases, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
+  if (a.pair) {
+    if (dtype != PA_DTYPE_BF16 || group < 1 || group > 4) return hipErrorNotSupported;
+    if (head_dim == 64) return launch_decode_pair<128>(a, 2 * group, num_items, phases, stream);
+    if (head_dim == 128) return launch_decode_pair<256>(a, 2 * group, num_items, phases, stream);
+    return hipErrorNotSupported;
+  }
   if (dtype == PA_DTYPE_BF16) {
     if (head_dim == 128) return launch_decode_g<bf16_t, 128>(a, group, num_items, phases, stream);
     if (head_dim == 64) return launch_decode_g<bf16_t, 64>(a, group, num_items, phases, stream);

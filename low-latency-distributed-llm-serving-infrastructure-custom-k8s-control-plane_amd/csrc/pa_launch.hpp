@@ -31,8 +31,8 @@ struct DecodeArgs {
   int32_t partition;
   float scale_log2e;
   // 1: two adjacent real KV heads of D/2 run as one of D (G counts the query
-  // heads of both); queries are staged into their half, outputs written from
-  // it.  Partials keep the paired layout.
+  // heads of both).  Every query head reads only its own half of the rows;
+  // outputs and partials use the real layout [.., H_q, D/2].
   int32_t pair;
 };
 
@@ -142,7 +142,11 @@ struct PrefillArgs {
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition);
-// phases: PA_DECODE_PHASE_PARTITIONS and/or PA_DECODE_PHASE_MERGE.
+// Whether two adjacent KV heads of this shape run as one workgroup
+// (DecodeArgs::pair; the KV head count must then be even).
+bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group);
+// phases: PA_DECODE_PHASE_PARTITIONS and/or PA_DECODE_PHASE_MERGE.  head_dim
+// and group are the real ones; a.num_kv_heads counts pairs when a.pair.
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
                          int64_t num_items, int phases, hipStream_t stream);
 

@@ -87,6 +87,8 @@ class PagedStepContext:
                     prefill_tile=prefill_tile,
                     num_kv_heads=store.num_heads,
                     num_query_heads=hq,
+                    head_dim=store.head_dim,
+                    dtype=store.dtype,
                 )
                 self.scatter_slots = self.packed.scatter_slots
             else:

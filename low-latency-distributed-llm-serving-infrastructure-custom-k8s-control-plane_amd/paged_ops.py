@@ -162,19 +162,30 @@ def _resident_decode_workgroups(group: int) -> int:
     return _DECODE_CUS * (5 if group == 1 else 4)
 
 
+def decode_kv_heads_per_workgroup(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
+                                  num_query_heads: int) -> int:
+    """KV heads one decode workgroup reads together (2 when adjacent KV heads
+    run as pairs, else 1; 0 for head counts the decode rejects)."""
+    lib = _native.load_library()
+    return int(lib.pa_decode_kv_heads_per_workgroup(dtype_code(dtype), int(head_dim), int(num_kv_heads),
+                                                    int(num_query_heads)))
+
+
 def choose_partition(
     start_positions: Sequence[int],
     new_token_counts: Sequence[int],
     num_kv_heads: int = 8,
     num_query_heads: Optional[int] = None,
+    kv_heads_per_workgroup: int = 1,
 ) -> int:
     """Split-K partition for the decode sequences of a step.
 
     The largest of 4096, 2048, 1024, 512 and 256 tokens whose decode launch
-    (partitions x KV heads) still gives every resident workgroup slot of the
-    chip two workgroups: long partitions keep the number of partials, merges
-    and per-workgroup set-ups low, and pa_pack orders the work longest first
-    so the short remainders fill the end of the launch.
+    (partitions x KV heads / kv_heads_per_workgroup) still gives every
+    resident workgroup slot of the chip two workgroups: long partitions keep
+    the number of partials, merges and per-workgroup set-ups low, and pa_pack
+    orders the work longest first so the short remainders fill the end of
+    the launch.
 
     A step too small for that rule at any size keeps 256, unless every
     context fits one partition of at most 512 tokens: then that size is
@@ -185,10 +196,11 @@ def choose_partition(
     hkv = max(int(num_kv_heads), 1)
     group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
     need = 2 * _resident_decode_workgroups(group)
+    width = max(hkv // max(int(kv_heads_per_workgroup), 1), 1)  # workgroups per item
     ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
     p = PA_DECODE_MAX_PARTITION
     while p > 256:
-        if sum(-(-x // p) for x in ctx) * hkv >= need:
+        if sum(-(-x // p) for x in ctx) * width >= need:
             return p
         p //= 2
     longest = max(ctx, default=0)
@@ -243,6 +255,8 @@ def pack_step(
     partition_size: Optional[int] = None,
     num_kv_heads: int = 8,
     num_query_heads: Optional[int] = None,
+    head_dim: Optional[int] = None,
+    dtype: Optional[torch.dtype] = None,
     with_gather: bool = False,
     start_positions_dev: Optional[torch.Tensor] = None,
     new_token_counts_dev: Optional[torch.Tensor] = None,
@@ -253,7 +267,9 @@ def pack_step(
     ``start_positions`` / ``new_token_counts``: the host lists of the step
     (also uploaded unless device copies are passed in).
     ``partition_size``: decode split-K partition in tokens; by default
-    :func:`choose_partition` picks it from the step and the head counts.
+    :func:`choose_partition` picks it from the step and the head counts
+    (and, when ``head_dim`` and the cache ``dtype`` are given, from how many
+    KV heads one decode workgroup reads).
     ``prefill_tile``: query tokens per prefill work item; by default the
     MFMA kernel's tile for the head counts (:func:`prefill_tile_for`).
     """
@@ -272,7 +288,12 @@ def pack_step(
     if prefill_tile <= 0:
         raise ValueError("prefill_tile must be positive")
     if partition_size is None:
-        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads, num_query_heads)
+        per_wg = 1
+        if head_dim is not None and dtype is not None:
+            hq = int(num_query_heads or 4 * num_kv_heads)
+            per_wg = max(decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, hq), 1)
+        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads, num_query_heads,
+                                          per_wg)
     if partition_size <= 0:
         raise ValueError("partition_size must be positive")
     t, c, ditems, mitems, pitems, ndec, npre = work_counts(
@@ -407,13 +428,12 @@ def copy_blocks(src_cache: torch.Tensor, dst_cache: torch.Tensor, block_mapping)
 
 
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
-    """Bytes pa_decode needs for its split-K partials (heads of 64 may run as
-    pairs, whose partial rows are 128 wide: reserved for every dtype)."""
+    """Bytes pa_decode needs for its split-K partials: fp32 acc[items, H_q, D]
+    and (max, sum)[items, H_q], each rounded up to 256 bytes."""
     if num_decode_items <= 0:
         return 0
     rows = num_decode_items * num_query_heads
-    dim = 128 if head_dim == 64 else head_dim
-    acc = (rows * dim * 4 + 255) & ~255
+    acc = (rows * head_dim * 4 + 255) & ~255
     ml = (rows * 2 * 4 + 255) & ~255
     return acc + ml
 

@@ -98,6 +98,28 @@ def test_workspace_size():
     dims = native.PaStepDims(num_query_heads=32, num_kv_heads=8, head_dim=128)
     assert lib.pa_decode_workspace_size(dims, 925) == ops.decode_workspace_bytes(925, 32, 128)
     assert lib.pa_decode_workspace_size(dims, 0) == 0
+    # paired heads keep the real partial layout
+    dims = native.PaStepDims(num_query_heads=16, num_kv_heads=4, head_dim=64, dtype=native.PA_DTYPE_BF16)
+    assert lib.pa_decode_workspace_size(dims, 77) == ops.decode_workspace_bytes(77, 16, 64)
+
+
+def test_kv_heads_per_workgroup():
+    native = pkg("_native")
+    lib = native.load_library()
+    bf16, f32 = native.PA_DTYPE_BF16, native.PA_DTYPE_F32
+    # (dtype, head_dim, H_kv, H_q) -> KV heads per decode workgroup
+    cases = {
+        (bf16, 64, 8, 8): 2, (bf16, 64, 8, 16): 2, (bf16, 64, 8, 24): 2, (bf16, 64, 8, 32): 2,
+        (bf16, 64, 8, 40): 1,  # groups above 4 stay single
+        (bf16, 64, 3, 9): 1,  # an odd KV head count cannot pair
+        (bf16, 128, 8, 8): 2, (bf16, 128, 32, 32): 2, (bf16, 128, 8, 16): 2,
+        (bf16, 128, 8, 32): 1,  # 32/8 heads of 128 run single
+        (f32, 64, 8, 8): 1, (f32, 128, 8, 16): 1, (native.PA_DTYPE_F16, 64, 8, 8): 1,
+        (bf16, 96, 8, 8): 1,
+        (bf16, 64, 0, 8): 0, (bf16, 64, 8, 12): 0, (bf16, 64, 8, 0): 0,
+    }
+    for (dtype, d, hkv, hq), want in cases.items():
+        assert lib.pa_decode_kv_heads_per_workgroup(dtype, d, hkv, hq) == want, (dtype, d, hkv, hq)
 
 
 def test_product_path_fails_loudly_without_library(monkeypatch, tmp_path):

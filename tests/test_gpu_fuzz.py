@@ -63,7 +63,7 @@ def test_random_steps_match_oracle(device, seed):
     table = torch.from_numpy(w.block_table_array()).to(device)
     step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
                          partition_size=partition, num_kv_heads=w.num_kv_heads,
-                         num_query_heads=w.num_query_heads)
+                         num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
     ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()

@@ -44,7 +44,8 @@ def pack_workload(w, device, prefill_tile=None, with_gather=False, partition=Non
     tile = prefill_tile or ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
     return ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
                          prefill_tile=tile, with_gather=with_gather, partition_size=partition,
-                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
+                         head_dim=w.head_dim, dtype=w.dtype)
 
 
 def oracle_rows(w, t, seqs):
@@ -269,7 +270,10 @@ def test_decode_fp32_matches_oracle(device):
     (8, 1, 64, torch.float32), (12, 4, 32, torch.bfloat16), (12, 4, 128, torch.bfloat16),
     # groups that are not powers of two (9/3/64 is SmolLM-135M's shape)
     (9, 3, 64, torch.bfloat16), (9, 3, 64, torch.float32), (10, 2, 128, torch.bfloat16),
-    (12, 2, 64, torch.bfloat16), (28, 4, 128, torch.bfloat16), (14, 2, 128, torch.float32)])
+    (12, 2, 64, torch.bfloat16), (28, 4, 128, torch.bfloat16), (14, 2, 128, torch.float32),
+    # paired KV heads (bf16, even H_kv): heads of 64 with groups of 3 and 4,
+    # heads of 128 with a group of 2
+    (24, 8, 64, torch.bfloat16), (16, 8, 128, torch.bfloat16)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]

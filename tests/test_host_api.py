@@ -308,3 +308,6 @@ def test_choose_partition_fills_the_chip():
     assert ops.choose_partition([15, 300, 511], [1, 1, 1], 8, 8) == 512
     assert ops.choose_partition([15, 300, 512], [1, 1, 1], 8, 8) == 256
     assert ops.choose_partition([15, 200, 255], [1, 1, 1], 8, 8) == 256
+    # paired KV heads halve the launch width: the same step splits further
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, kv_heads_per_workgroup=2) == 2048
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, kv_heads_per_workgroup=2) == 1024
