@@ -207,15 +207,24 @@ int pa_copy_blocks(const void *src_cache, void *dst_cache,
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
 
 /* KV heads that one pa_decode workgroup reads together: 2 when two adjacent
- * KV heads run as one (bf16, an even KV head count, head_dim 64 with groups
- * of up to 4 query heads or head_dim 128 with groups of up to 2: each token's
- * rows of the two heads are read as one row of twice the length), else 1;
+ * KV heads run as one (bf16, an even KV head count, head_dim 64 or 128 and
+ * groups of up to 4 query heads: each token's rows of the two heads are
+ * read as one row of twice the length), else 1;
  * 0 for head counts pa_decode rejects.  A host choosing the split-K
  * partition size from the launch width divides the KV head count by it.
  * (No counterpart in the reference, whose CPU kernel has no workgroups.) */
 int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim,
                                          int32_t num_kv_heads,
                                          int32_t num_query_heads);
+
+/* Decode workgroups of this shape that one compute unit of the current
+ * device holds at once (the HIP occupancy calculator on the kernel pa_decode
+ * launches for it), or 0 for a shape without a tuned kernel or on a HIP
+ * error (pa_last_error_message then says which).  With the CU count it gives
+ * the resident width a host's split-K partition choice aims to fill.  (No
+ * counterpart in the reference.) */
+int32_t pa_decode_workgroups_per_cu(int32_t dtype, int32_t head_dim,
+                                    int32_t num_kv_heads, int32_t num_query_heads);
 
 /*
  * Replaces: NativePagedBackend.attend for decode steps

@@ -278,6 +278,24 @@ int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim, int32_
                                                                                                 : 1;
 }
 
+int32_t pa_decode_workgroups_per_cu(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
+                                    int32_t num_query_heads) {
+  if (pa_decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, num_query_heads) == 0) {
+    fail(PA_ERR_INVALID_ARGUMENT, "pa_decode_workgroups_per_cu: bad head counts %d / %d",
+         num_query_heads, num_kv_heads);
+    return 0;
+  }
+  const int group = num_query_heads / num_kv_heads;
+  const bool pair = pa::decode_pairs_heads(dtype, head_dim, num_kv_heads, group);
+  int per_cu = 0;
+  const hipError_t err = pa::decode_workgroups_per_cu(dtype, head_dim, group, pair, &per_cu);
+  if (err != hipSuccess) {
+    from_hip(err, "pa_decode_workgroups_per_cu");
+    return 0;
+  }
+  return per_cu;
+}
+
 int pa_decode(const void* query, const void* key_cache, const void* value_cache,
               int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
               const int32_t* context_lens, const int64_t* cu_seqlens,

@@ -60,12 +60,16 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #ifndef PA_DECODE_MIN_WAVES_WIDE
 #define PA_DECODE_MIN_WAVES_WIDE 2  // the same for wider groups or rows
 #endif
+#ifndef PA_DECODE_MIN_WAVES_PAIR512
+#define PA_DECODE_MIN_WAVES_PAIR512 3  // the same for paired rows of 512 bytes
+#endif
 // GA: query heads whose accumulators one lane holds (G, or G/2 when paired,
 // whose rows of up to 512 bytes come in half-length tiles).
-#define PA_DECODE_OCCUPANCY(T, D, GA, PAIR)                                        \
-  __attribute__((amdgpu_waves_per_eu(((GA) <= 4 && ((D) * sizeof(T) <= 256 || (PAIR))) \
-                                         ? PA_DECODE_MIN_WAVES                       \
-                                         : PA_DECODE_MIN_WAVES_WIDE)))
+#define PA_DECODE_OCCUPANCY(T, D, GA, PAIR)                                                  \
+  __attribute__((amdgpu_waves_per_eu(                                                        \
+      ((GA) <= 4 && (PAIR) && (D) * sizeof(T) > 256) ? PA_DECODE_MIN_WAVES_PAIR512           \
+      : ((GA) <= 4 && ((D) * sizeof(T) <= 256 || (PAIR))) ? PA_DECODE_MIN_WAVES              \
+                                                          : PA_DECODE_MIN_WAVES_WIDE)))
 
 typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -141,21 +145,14 @@ struct VRaw<8> {
   using type = uint2;
 };
 
-// Dot product of one 16-byte piece of K with the matching piece of q.
+// Dot product of one 16-byte piece of K with the matching piece of q (bf16).
 template <typename T>
-__device__ __forceinline__ float piece_dot(uint4 q, uint4 k, float acc) {
-  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
-    acc = dot2_bf16(q.x, k.x, acc);
-    acc = dot2_bf16(q.y, k.y, acc);
-    acc = dot2_bf16(q.z, k.z, acc);
-    acc = dot2_bf16(q.w, k.w, acc);
-  } else {
-    acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
-    acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
-    acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
-    acc = fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
-  }
-  return acc;
+__device__ __forceinline__ float piece_dot(uint4 q, uint4 k) {
+  static_assert(Elem<T>::kDtype == PA_DTYPE_BF16, "paired heads are bf16");
+  float acc = dot2_bf16(q.x, k.x, 0.f);
+  acc = dot2_bf16(q.y, k.y, acc);
+  acc = dot2_bf16(q.z, k.z, acc);
+  return dot2_bf16(q.w, k.w, acc);
 }
 
 // 32-bit word w of a lane's V piece (a bf16 pair).
@@ -208,10 +205,16 @@ __device__ __forceinline__ float across_groups_max(float x) {
 }
 
 // PAIR: two adjacent real KV heads of D/2 run as one head of D with the G
-// query heads of both (the first G/2 belong to the first real head).  A
-// lane's first K piece lies in the first real head's half of the row and its
-// second piece in the second's, so each query head dots only its own piece;
-// in the PV layout lanes [0, 32) hold the first half, and each lane
+// query heads of both (the first G/2 belong to the first real head); every
+// query head reads only its own real head's half of the rows.  QK layout:
+//  - rows of 512 bytes ("split"): the first half of a row group's lanes holds
+//    the first real head's half of the row (two pieces per lane, as for an
+//    unpaired row), the second half the other's; a lane scores the G/2 heads
+//    of its own real head, summed over L/2 lanes.
+//  - rows of 256 bytes: every lane's first piece lies in the first real
+//    head's half and its second piece in the other's (so each wave load still
+//    reads 128-byte runs); each head dots its own piece, summed over L lanes.
+// PV layout: lanes [0, 32) hold the first half of the row, and each lane
 // accumulates only the G/2 heads of its half.
 template <typename T, int D, int G, bool PAIR>
 __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G / 2 : G), PAIR) void decode_partition_kernel(DecodeArgs a) {
@@ -309,14 +312,26 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     for (int e = 0; e < PE; ++e) acc[j][e] = 0.f;
 
   // ---- per-tile work ------------------------------------------------------
-  // Softmax exponentials are spread over the lanes of a row group: lane lig
-  // owns "combos" c = lig + L*r, each one (token pair, head) for bf16 or
-  // (token, head) for fp32, and computes, sums and stages only those.
-  constexpr int NC = (BF16 ? TPG / 2 : TPG) * G;  // combos per row group
-  constexpr int CPL = (NC + L - 1) / L;           // combos per lane
-  float lsum[G];  // this lane's share of the softmax denominators
+  // A lane computes the scores of NS query heads, summed over LS lanes: all
+  // G over the row group, or, in the split pair layout, the G/2 of its own
+  // real head over its half of the group.  Its K pieces are kp0 and
+  // kp0 + KP1 (16-byte pieces of the row).
+  constexpr bool SPLIT = PAIR && D * sizeof(T) > 256;
+  constexpr int NS = SPLIT ? GA : G;
+  constexpr int LS = SPLIT ? L / 2 : L;
+  constexpr int KP1 = SPLIT ? L / 2 : L;
+  const int khalf = SPLIT ? lig / LS : 0;              // real head of the lane's pieces
+  const int kp0 = SPLIT ? khalf * L + lig % LS : lig;  // first 16-byte piece of the lane
+  const int gq0 = SPLIT ? khalf * GA : 0;              // first query head it scores
+  // Softmax exponentials are spread over the LS lanes that share those
+  // scores: lane lig owns "combos" k = lig % LS + LS*r, each one (token pair,
+  // head) for bf16 or (token, head) for fp32, and computes, sums and stages
+  // only those.
+  constexpr int NC = (BF16 ? TPG / 2 : TPG) * NS;  // combos per lane group
+  constexpr int CPL = (NC + LS - 1) / LS;          // combos per lane
+  float lsum[NS];  // this lane's share of the softmax denominators of its NS heads
 #pragma unroll
-  for (int g = 0; g < G; ++g) lsum[g] = 0.f;
+  for (int j = 0; j < NS; ++j) lsum[j] = 0.f;
 
   uint4 kb[TPG][2];
   bool kok[TPG];
@@ -328,7 +343,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   };
   // Per-lane element offset of its K slice within a wave load: row group gi
   // reads row gi of the load (GPW consecutive tokens).
-  const int64_t koff = static_cast<int64_t>(gi) * row_stride + lig * CE;
+  const int64_t koff = static_cast<int64_t>(gi) * row_stride + kp0 * CE;
   const bool k_uniform = log2_bs >= S::kLog2Gpw;  // a load's GPW tokens share a block
   auto issue_k = [&](int tile, int blk_lane) {
     const int t0 = tile * kTile;
@@ -346,7 +361,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
               (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + GPW * i) & bs_mask);
           const T* row = kbase + slot0 * row_stride + koff;
           kb[i][0] = kv_load<uint4>(row);
-          kb[i][1] = kv_load<uint4>(row + L * CE);
+          kb[i][1] = kv_load<uint4>(row + KP1 * CE);
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -358,8 +373,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         if (kok[i]) {
           const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
           const T* row = kbase + slot * row_stride;
-          kb[i][0] = kv_load<uint4>(row + lig * CE);
-          kb[i][1] = kv_load<uint4>(row + (L + lig) * CE);
+          kb[i][0] = kv_load<uint4>(row + kp0 * CE);
+          kb[i][1] = kv_load<uint4>(row + (kp0 + KP1) * CE);
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -430,37 +445,46 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // Scores stay unscaled (the max commutes with the positive scale); the
   // scale is applied inside the exponent: p = exp2(s * scale - max * scale).
   auto qk_softmax = [&](bool full) {
-    float s[TPG][G];
-    float tmax[G];
+    float s[TPG][NS];
+    float tmax[NS];
 #pragma unroll
-    for (int g = 0; g < G; ++g) tmax[g] = -INFINITY;
+    for (int j = 0; j < NS; ++j) tmax[j] = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int j = 0; j < NS; ++j) {
       uint4 qg[2];
-      if constexpr (PAIR) {
-        // The head's own half: piece 0 of every lane for the first G/2
-        // heads, piece 1 for the others.
-        qg[0] = s_q[g * (D / CE) + (g / GA) * L + lig];
+      if constexpr (PAIR && !SPLIT) {
+        // Head j's own piece: piece 0 for the first G/2 heads, piece 1 after.
+        qg[0] = s_q[j * (D / CE) + (j / GA) * L + lig];
       } else {
-        qg[0] = s_q[g * (D / CE) + lig];
-        qg[1] = s_q[g * (D / CE) + L + lig];
+        qg[0] = s_q[(gq0 + j) * (D / CE) + kp0];
+        qg[1] = s_q[(gq0 + j) * (D / CE) + kp0 + KP1];
       }
 #pragma unroll
       for (int i = 0; i < TPG; ++i) {
         float v;
-        if constexpr (PAIR) v = group_sum<L>(piece_dot<T>(qg[0], kb[i][g / GA], 0.f));
-        else v = group_sum<L>(slice_dot<T>(qg, kb[i]));
+        if constexpr (PAIR && !SPLIT) v = group_sum<L>(piece_dot<T>(qg[0], kb[i][j / GA]));
+        else v = group_sum<LS>(slice_dot<T>(qg, kb[i]));
         if (!full) v = kok[i] ? v : -INFINITY;
-        s[i][g] = v;
-        tmax[g] = fmaxf(tmax[g], v);
+        s[i][j] = v;
+        tmax[j] = fmaxf(tmax[j], v);
       }
     }
+    // Tile maxima over the row groups.  In the split pair layout head g's is
+    // held by lane 0, or, for the second real head, by lane LS (the first
+    // lane of the second half of row group 0).
     bool moved = false;
     float m_new[G];
+    float red[NS];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      m_new[g] = __int_as_float(__builtin_amdgcn_readfirstlane(
-          __float_as_int(fmaxf(m[g], across_groups_max<L>(tmax[g])))));
+      if constexpr (SPLIT) {
+        if (g < GA) red[g] = across_groups_max<L>(tmax[g]);
+        m_new[g] = fmaxf(m[g], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red[g % GA]),
+                                                                          g < GA ? 0 : LS)));
+      } else {
+        m_new[g] = __int_as_float(__builtin_amdgcn_readfirstlane(
+            __float_as_int(fmaxf(m[g], across_groups_max<L>(tmax[g])))));
+      }
       moved |= m_new[g] != m[g];
     }
     if (moved) {  // wave-uniform
@@ -468,8 +492,12 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         alpha[g] = fast_exp2((m[g] - m_new[g]) * scale);
-        lsum[g] *= alpha[g];
+        if constexpr (!SPLIT) lsum[g] *= alpha[g];
         m[g] = m_new[g];
+      }
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int j = 0; j < GA; ++j) lsum[j] *= khalf ? alpha[GA + j] : alpha[j];
       }
 #pragma unroll
       for (int j = 0; j < GA; ++j) {
@@ -484,33 +512,34 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     uint32_t* sp = s_p[wave];
 #pragma unroll
     for (int r = 0; r < CPL; ++r) {
-      const int c = lig + L * r;
-      if (NC % L != 0 && c >= NC) break;
+      const int c = (SPLIT ? lig % LS : lig) + LS * r;
+      if (NC % LS != 0 && c >= NC) break;
       float sa = -INFINITY, sb = -INFINITY, mc = 0.f;  // mc: -max * scale of the head
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
         const bool mine = c == cc;
         if constexpr (BF16) {
-          sa = mine ? s[2 * (cc / G)][cc % G] : sa;
-          sb = mine ? s[2 * (cc / G) + 1][cc % G] : sb;
+          sa = mine ? s[2 * (cc / NS)][cc % NS] : sa;
+          sb = mine ? s[2 * (cc / NS) + 1][cc % NS] : sb;
         } else {
-          sa = mine ? s[cc / G][cc % G] : sa;
+          sa = mine ? s[cc / NS][cc % NS] : sa;
         }
       }
-      const int g = c % G;
+      const int g = SPLIT ? gq0 + c % NS : c % G;
+      const int jl = SPLIT ? c % NS : g;  // its slot in lsum
 #pragma unroll
       for (int gg = 0; gg < G; ++gg) mc = g == gg ? mneg[gg] : mc;
       if constexpr (BF16) {
         const float pa = fast_exp2(fmaf(sa, scale, mc));
         const float pb = fast_exp2(fmaf(sb, scale, mc));
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) lsum[gg] += g == gg ? pa + pb : 0.f;
-        sp[((c / G) * GPW + gi) * G + g] = pack_bf16x2(pa, pb);
+        for (int gg = 0; gg < NS; ++gg) lsum[gg] += jl == gg ? pa + pb : 0.f;
+        sp[((c / NS) * GPW + gi) * G + g] = pack_bf16x2(pa, pb);
       } else {
         const float pa = fast_exp2(fmaf(sa, scale, mc));
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) lsum[gg] += g == gg ? pa : 0.f;
-        sp[(gi + GPW * (c / G)) * G + g] = __float_as_uint(pa);
+        for (int gg = 0; gg < NS; ++gg) lsum[gg] += jl == gg ? pa : 0.f;
+        sp[(gi + GPW * (c / NS)) * G + g] = __float_as_uint(pa);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -581,12 +610,13 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 
   // ---- combine the waves -------------------------------------------------
   // Each (token, head) exponential was summed by exactly one lane.
+  float ltot[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float l = lsum[g];
+    float l = SPLIT ? (khalf == g / GA ? lsum[g % NS] : 0.f) : lsum[g % NS];
 #pragma unroll
     for (int o = kWave / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
-    lsum[g] = l;
+    ltot[g] = l;
   }
   // V rows of one wave load that hold different tokens -> add them up.
 #pragma unroll
@@ -610,7 +640,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     for (int g = 0; g < G; ++g)
       if (lane == g) {
         s_m[wave][g] = m[g] * scale;
-        s_l[wave][g] = lsum[g];
+        s_l[wave][g] = ltot[g];
       }
   }
   __syncthreads();
@@ -648,14 +678,16 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 
 // Combines the split-K partials (max, sum, unnormalised acc) of one
 // multi-partition sequence for the G heads of one KV head.  One workgroup
-// per (entry of the merge list, KV head); an entry, written by pa_pack, is
-// (first full-partition item, number of full partitions, sequence, item of
-// the partial last partition or -1): the full partitions of a sequence are
-// contiguous items, its partial one sits among the short work at the end.
-// Every thread owns G*D/256 outputs and merges the partitions in one pass
-// with a running maximum (the stored maxima are already in the exp2
-// domain): no LDS and no barrier, so the only dependent global round trips
-// are the entry and then the partials.
+// per (entry of the merge list, KV head, 256 of the G*D outputs); an entry,
+// written by pa_pack, is (first full-partition item, number of full
+// partitions, sequence, item of the partial last partition or -1): the full
+// partitions of a sequence are contiguous items, its partial one sits among
+// the short work at the end.  Every thread owns one output and merges the
+// partitions in one pass with a running maximum (the stored maxima are
+// already in the exp2 domain): no LDS and no barrier, so the only dependent
+// global round trips are the entry and then the partials.  (With several
+// outputs per thread their round trips queued one behind the other: eight
+// heads of 128 at partition 2048 took 19 us.)
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
   const int hkv = a.num_kv_heads;
@@ -672,20 +704,31 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
   const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
   T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
-  for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
+  {
+    const int i = static_cast<int>(blockIdx.y) * kDecodeThreads + static_cast<int>(threadIdx.x);
+    if (i >= G * D) return;
     const int h = kvh * G + i / D;
     const float* ml = a.part_ml + 2 * h;
     const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
     float mx = kScoreFloor, sum = 0.f, o = 0.f;
-    int p = 0;
-    for (; p + 4 <= nparts; p += 4) {
+    // Four partitions per round trip; slots past the last one read the
+    // first partition again and are given no weight.
+    for (int p = 0; p < nparts; p += 4) {
       float mp[4], lp[4], xp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t it = item_of(p + u);
+        const int64_t it = item_of(p + u < nparts ? p + u : 0);
         mp[u] = ml[it * ml_stride];
         lp[u] = ml[it * ml_stride + 1];
         xp[u] = acc[it * stride];
+      }
+#pragma unroll
+      for (int u = 1; u < 4; ++u) {
+        if (p + u >= nparts) {
+          mp[u] = kScoreFloor;
+          lp[u] = 0.f;
+          xp[u] = 0.f;
+        }
       }
       const float mn = fmaxf(fmaxf(mx, mp[0]), fmaxf(fmaxf(mp[1], mp[2]), mp[3]));
       const float r = fast_exp2(mx - mn);
@@ -699,15 +742,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
       }
       mx = mn;
     }
-    for (; p < nparts; ++p) {
-      const int64_t it = item_of(p);
-      const float mp = ml[it * ml_stride], lp = ml[it * ml_stride + 1], xp = acc[it * stride];
-      const float mn = fmaxf(mx, mp);
-      const float r = fast_exp2(mx - mn), w = fast_exp2(mp - mn);
-      sum = fmaf(lp, w, sum * r);
-      o = fmaf(xp, w, o * r);
-      mx = mn;
-    }
     const float r = sum > 0.f ? o / sum : 0.f;
     store_scalar<T>(out + i, r);
   }
@@ -715,52 +749,86 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
 
 // ---- host-side dispatch ------------------------------------------------
 
-// D, G: the kernel's head dim and group (twice the real ones when paired).
-template <typename T, int D, int G, bool PAIR>
-static hipError_t launch_decode_t(const DecodeArgs& a, int64_t num_items, int phases,
-                                  hipStream_t stream) {
-  const int64_t grid = num_items * a.num_kv_heads;
-  const int64_t merge_grid = a.num_merge * a.num_kv_heads;
-  if (phases & PA_DECODE_PHASE_PARTITIONS) {
-    hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR>), dim3(static_cast<uint32_t>(grid)),
-                       dim3(kDecodeThreads), 0, stream, a);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+// Launches both phases of one kernel instance.  D, G: the kernel's head dim
+// and group (twice the real ones when paired).
+struct LaunchOp {
+  const DecodeArgs& a;
+  int64_t num_items;
+  int phases;
+  hipStream_t stream;
+  template <typename T, int D, int G, bool PAIR>
+  hipError_t run() const {
+    const int64_t grid = num_items * a.num_kv_heads;
+    const int64_t merge_grid = a.num_merge * a.num_kv_heads;
+    if (phases & PA_DECODE_PHASE_PARTITIONS) {
+      hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR>), dim3(static_cast<uint32_t>(grid)),
+                         dim3(kDecodeThreads), 0, stream, a);
+      const hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
+    // Partials are in the real layout: rows of D/2 when paired.
+    constexpr int kOutD = PAIR ? D / 2 : D;
+    constexpr int kChunks = (G * kOutD + kDecodeThreads - 1) / kDecodeThreads;
+    hipLaunchKernelGGL((decode_merge_kernel<T>),
+                       dim3(static_cast<uint32_t>(merge_grid), kChunks), dim3(kDecodeThreads), 0,
+                       stream, a, G, kOutD);
+    return hipGetLastError();
   }
-  if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
-  // Partials are in the real layout: rows of D/2 when paired.
-  hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(static_cast<uint32_t>(merge_grid)),
-                     dim3(kDecodeThreads), 0, stream, a, G, PAIR ? D / 2 : D);
-  return hipGetLastError();
+};
+
+// Resident partition workgroups per CU of one kernel instance.
+struct OccupancyOp {
+  int* per_cu;
+  template <typename T, int D, int G, bool PAIR>
+  hipError_t run() const {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_partition_kernel<T, D, G, PAIR>,
+                                                        kDecodeThreads, 0);
+  }
+};
+
+template <typename T, int D, int G, bool PAIR, typename Op>
+static hipError_t visit_one(const Op& op) {
+  if constexpr (PAIR && G % 2 != 0) {
+    return hipErrorNotSupported;  // a pair's group is even
+  } else {
+    return op.template run<T, D, G, PAIR>();
+  }
 }
 
-template <typename T, int D>
-static hipError_t launch_decode_g(const DecodeArgs& a, int G, int64_t num_items, int phases,
-                                  hipStream_t s) {
+template <typename T, int D, bool PAIR, typename Op>
+static hipError_t visit_group(int G, const Op& op) {
   switch (G) {
-    case 1: return launch_decode_t<T, D, 1, false>(a, num_items, phases, s);
-    case 2: return launch_decode_t<T, D, 2, false>(a, num_items, phases, s);
-    case 3: return launch_decode_t<T, D, 3, false>(a, num_items, phases, s);
-    case 4: return launch_decode_t<T, D, 4, false>(a, num_items, phases, s);
-    case 5: return launch_decode_t<T, D, 5, false>(a, num_items, phases, s);
-    case 6: return launch_decode_t<T, D, 6, false>(a, num_items, phases, s);
-    case 7: return launch_decode_t<T, D, 7, false>(a, num_items, phases, s);
-    case 8: return launch_decode_t<T, D, 8, false>(a, num_items, phases, s);
+    case 1: return visit_one<T, D, 1, PAIR>(op);
+    case 2: return visit_one<T, D, 2, PAIR>(op);
+    case 3: return visit_one<T, D, 3, PAIR>(op);
+    case 4: return visit_one<T, D, 4, PAIR>(op);
+    case 5: return visit_one<T, D, 5, PAIR>(op);
+    case 6: return visit_one<T, D, 6, PAIR>(op);
+    case 7: return visit_one<T, D, 7, PAIR>(op);
+    case 8: return visit_one<T, D, 8, PAIR>(op);
     default: return hipErrorNotSupported;
   }
 }
 
-// Paired heads of real dim D/2, real group G/2.
-template <int D>
-static hipError_t launch_decode_pair(const DecodeArgs& a, int G, int64_t num_items, int phases,
-                                     hipStream_t s) {
-  switch (G) {
-    case 2: return launch_decode_t<bf16_t, D, 2, true>(a, num_items, phases, s);
-    case 4: return launch_decode_t<bf16_t, D, 4, true>(a, num_items, phases, s);
-    case 6: return launch_decode_t<bf16_t, D, 6, true>(a, num_items, phases, s);
-    case 8: return launch_decode_t<bf16_t, D, 8, true>(a, num_items, phases, s);
-    default: return hipErrorNotSupported;
+// The kernel instance of a real shape: paired heads of D run as the
+// instance of head dim 2D and group 2G.
+template <typename Op>
+static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, const Op& op) {
+  if (pair) {
+    if (dtype != PA_DTYPE_BF16 || group < 1 || group > 4) return hipErrorNotSupported;
+    if (head_dim == 64) return visit_group<bf16_t, 128, true>(2 * group, op);
+    if (head_dim == 128) return visit_group<bf16_t, 256, true>(2 * group, op);
+    return hipErrorNotSupported;
   }
+  if (dtype == PA_DTYPE_BF16) {
+    if (head_dim == 128) return visit_group<bf16_t, 128, false>(group, op);
+    if (head_dim == 64) return visit_group<bf16_t, 64, false>(group, op);
+  } else if (dtype == PA_DTYPE_F32) {
+    if (head_dim == 128) return visit_group<float, 128, false>(group, op);
+    if (head_dim == 64) return visit_group<float, 64, false>(group, op);
+  }
+  return hipErrorNotSupported;
 }
 
 // Largest real group run as pairs, per real head dim (bf16; 0 = never).
@@ -768,14 +836,14 @@ static hipError_t launch_decode_pair(const DecodeArgs& a, int G, int64_t num_ite
 // unpaired -> paired, each at its best partition:
 //   D 64:  G 1 0.180 -> 0.141 ms, G 2 0.181 -> 0.140, G 3 0.183 -> 0.147,
 //          G 4 0.183 -> 0.149;
-//   D 128: G 1 0.267 -> 0.254, G 2 0.267 -> 0.259, but G 4 0.270 -> 0.277:
-//          the scores of eight heads summed over 16-lane groups cost more
-//          VALU than the longer rows save.
+//   D 128: G 1 0.267 -> 0.253, G 2 0.267 -> 0.259, G 3 0.269 -> 0.261,
+//          G 4 0.271 -> 0.267 (three waves per SIMD: the eight heads' state
+//          does not fit the register budget of four without spilling).
 #ifndef PA_DECODE_PAIR_MAX_GROUP_D64
 #define PA_DECODE_PAIR_MAX_GROUP_D64 4
 #endif
 #ifndef PA_DECODE_PAIR_MAX_GROUP_D128
-#define PA_DECODE_PAIR_MAX_GROUP_D128 2
+#define PA_DECODE_PAIR_MAX_GROUP_D128 4
 #endif
 
 bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group) {
@@ -798,20 +866,12 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
                          int64_t num_items, int phases, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
-  if (a.pair) {
-    if (dtype != PA_DTYPE_BF16 || group < 1 || group > 4) return hipErrorNotSupported;
-    if (head_dim == 64) return launch_decode_pair<128>(a, 2 * group, num_items, phases, stream);
-    if (head_dim == 128) return launch_decode_pair<256>(a, 2 * group, num_items, phases, stream);
-    return hipErrorNotSupported;
-  }
-  if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return launch_decode_g<bf16_t, 128>(a, group, num_items, phases, stream);
-    if (head_dim == 64) return launch_decode_g<bf16_t, 64>(a, group, num_items, phases, stream);
-  } else if (dtype == PA_DTYPE_F32) {
-    if (head_dim == 128) return launch_decode_g<float, 128>(a, group, num_items, phases, stream);
-    if (head_dim == 64) return launch_decode_g<float, 64>(a, group, num_items, phases, stream);
-  }
-  return hipErrorNotSupported;
+  return visit_decode(dtype, head_dim, group, a.pair != 0, LaunchOp{a, num_items, phases, stream});
+}
+
+hipError_t decode_workgroups_per_cu(int dtype, int head_dim, int group, bool pair, int* per_cu) {
+  *per_cu = 0;
+  return visit_decode(dtype, head_dim, group, pair, OccupancyOp{per_cu});
 }
 
 }  // namespace pa

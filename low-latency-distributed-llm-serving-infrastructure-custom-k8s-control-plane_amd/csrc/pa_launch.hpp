@@ -149,6 +149,9 @@ bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group);
 // and group are the real ones; a.num_kv_heads counts pairs when a.pair.
 hipError_t launch_decode(const DecodeArgs& a, int dtype, int head_dim, int group,
                          int64_t num_items, int phases, hipStream_t stream);
+// Resident partition workgroups per CU of the kernel launch_decode runs for
+// a shape (the HIP occupancy calculator on the current device).
+hipError_t decode_workgroups_per_cu(int dtype, int head_dim, int group, bool pair, int* per_cu);
 
 bool generic_supported(int dtype, int head_dim);
 hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStream_t stream);

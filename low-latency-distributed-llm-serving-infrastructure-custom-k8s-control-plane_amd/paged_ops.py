@@ -153,13 +153,8 @@ def work_counts(
     return t, c, ditems, mitems, pitems, ndec, npre
 
 
-# Decode workgroups resident per compute unit (256 CUs on MI355X): the
-# single-query-head kernel fits five, the grouped ones four.
+# Compute units of an MI355X; pack_step uses the device's own count.
 _DECODE_CUS = 256
-
-
-def _resident_decode_workgroups(group: int) -> int:
-    return _DECODE_CUS * (5 if group == 1 else 4)
 
 
 def decode_kv_heads_per_workgroup(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
@@ -171,21 +166,37 @@ def decode_kv_heads_per_workgroup(dtype: torch.dtype, head_dim: int, num_kv_head
                                                     int(num_query_heads)))
 
 
+def decode_workgroups_per_cu(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
+                             num_query_heads: int) -> int:
+    """Decode workgroups of this shape one compute unit of the current device
+    holds at once (the occupancy of the kernel pa_decode launches; 0 for a
+    shape without a tuned kernel)."""
+    lib = _native.load_library()
+    return int(lib.pa_decode_workgroups_per_cu(dtype_code(dtype), int(head_dim), int(num_kv_heads),
+                                               int(num_query_heads)))
+
+
 def choose_partition(
     start_positions: Sequence[int],
     new_token_counts: Sequence[int],
     num_kv_heads: int = 8,
     num_query_heads: Optional[int] = None,
     kv_heads_per_workgroup: int = 1,
+    workgroups_per_cu: Optional[int] = None,
+    compute_units: int = _DECODE_CUS,
 ) -> int:
     """Split-K partition for the decode sequences of a step.
 
     The largest of 4096, 2048, 1024, 512 and 256 tokens whose decode launch
     (partitions x KV heads / kv_heads_per_workgroup) still gives every
-    resident workgroup slot of the chip two workgroups: long partitions keep
-    the number of partials, merges and per-workgroup set-ups low, and pa_pack
+    resident workgroup slot of the chip (compute_units x workgroups_per_cu;
+    without the occupancy, five per CU for one query head per KV head and
+    four for groups) one and a half workgroups: long partitions keep the
+    number of partials, merges and per-workgroup set-ups low, and pa_pack
     orders the work longest first so the short remainders fill the end of
-    the launch.
+    the launch.  On 256 lognormal contexts (median 1024) the rule picks the
+    fastest partition of every measured shape: 4096 for 32/8 heads of 128,
+    2048 for the same heads paired (three workgroups per CU), 1024 for 8/8.
 
     A step too small for that rule at any size keeps 256, unless every
     context fits one partition of at most 512 tokens: then that size is
@@ -195,7 +206,8 @@ def choose_partition(
     """
     hkv = max(int(num_kv_heads), 1)
     group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
-    need = 2 * _resident_decode_workgroups(group)
+    per_cu = int(workgroups_per_cu or 0) or (5 if group == 1 else 4)
+    need = 3 * int(compute_units) * per_cu // 2
     width = max(hkv // max(int(kv_heads_per_workgroup), 1), 1)  # workgroups per item
     ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
     p = PA_DECODE_MAX_PARTITION
@@ -288,12 +300,14 @@ def pack_step(
     if prefill_tile <= 0:
         raise ValueError("prefill_tile must be positive")
     if partition_size is None:
-        per_wg = 1
+        per_wg, per_cu = 1, None
         if head_dim is not None and dtype is not None:
             hq = int(num_query_heads or 4 * num_kv_heads)
             per_wg = max(decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, hq), 1)
-        partition_size = choose_partition(start_positions, new_token_counts, num_kv_heads, num_query_heads,
-                                          per_wg)
+            per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq) or None
+        partition_size = choose_partition(
+            start_positions, new_token_counts, num_kv_heads, num_query_heads, per_wg, per_cu,
+            torch.cuda.get_device_properties(device).multi_processor_count)
     if partition_size <= 0:
         raise ValueError("partition_size must be positive")
     t, c, ditems, mitems, pitems, ndec, npre = work_counts(

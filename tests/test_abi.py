@@ -112,8 +112,8 @@ def test_kv_heads_per_workgroup():
         (bf16, 64, 8, 8): 2, (bf16, 64, 8, 16): 2, (bf16, 64, 8, 24): 2, (bf16, 64, 8, 32): 2,
         (bf16, 64, 8, 40): 1,  # groups above 4 stay single
         (bf16, 64, 3, 9): 1,  # an odd KV head count cannot pair
-        (bf16, 128, 8, 8): 2, (bf16, 128, 32, 32): 2, (bf16, 128, 8, 16): 2,
-        (bf16, 128, 8, 32): 1,  # 32/8 heads of 128 run single
+        (bf16, 128, 8, 8): 2, (bf16, 128, 32, 32): 2, (bf16, 128, 8, 16): 2, (bf16, 128, 8, 32): 2,
+        (bf16, 128, 8, 48): 1,
         (f32, 64, 8, 8): 1, (f32, 128, 8, 16): 1, (native.PA_DTYPE_F16, 64, 8, 8): 1,
         (bf16, 96, 8, 8): 1,
         (bf16, 64, 0, 8): 0, (bf16, 64, 8, 12): 0, (bf16, 64, 8, 0): 0,

@@ -359,6 +359,20 @@ def test_decode_extremes(device):
     check_rows(w, out, oracle_rows(w, t, [0, 1, 2, 1000, 2048]), fp32=False)
 
 
+def test_decode_occupancy_query(device):
+    """The resident workgroups per CU of every tuned decode kernel, as the
+    partition choice reads them; unsupported shapes report 0."""
+    for dtype in (torch.bfloat16, torch.float32):
+        for d in (64, 128):
+            for g in range(1, 9):
+                per_cu = ops.decode_workgroups_per_cu(dtype, d, 8, 8 * g)
+                log(f"occupancy {dtype} D={d} G={g}: {per_cu} per CU, "
+                    f"{ops.decode_kv_heads_per_workgroup(dtype, d, 8, 8 * g)} KV heads per workgroup")
+                assert 1 <= per_cu <= 8
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 96, 8, 8) == 0
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 8, 80) == 0
+
+
 def test_decode_phases_equal_one_call(device):
     """Partition phase then merge phase (two launches) gives pa_decode's bits."""
     w = wl.llama3_8b_gqa_decode(seed=2)

@@ -297,7 +297,8 @@ def test_choose_partition_fills_the_chip():
     # 256 decodes x 8 KV heads give two workgroups per resident slot at 4096
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32) == 4096
     # the single-head kernel has more resident slots, so it splits more
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8) == 2048
+    assert ops.choose_partition([3000] * 896, [1] * 896, 2, 2) == 2048
+    assert ops.choose_partition([3000] * 896, [1] * 896, 2, 8) == 4096
     # fewer sequences get smaller partitions, never below 256
     assert ops.choose_partition([4095] * 32, [1] * 32, 8, 32) == 512
     assert ops.choose_partition([3000] * 4, [1] * 4, 8, 32) == 256
@@ -310,4 +311,9 @@ def test_choose_partition_fills_the_chip():
     assert ops.choose_partition([15, 200, 255], [1, 1, 1], 8, 8) == 256
     # paired KV heads halve the launch width: the same step splits further
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, kv_heads_per_workgroup=2) == 2048
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, kv_heads_per_workgroup=2) == 1024
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, kv_heads_per_workgroup=2) == 2048
+    # the kernel's occupancy sets the resident slots: fewer slots, longer partitions
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 2, workgroups_per_cu=2) == 4096
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 2, workgroups_per_cu=8) == 1024
+    # a chip with fewer compute units fills at longer partitions
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, 2, compute_units=128) == 4096
