@@ -166,14 +166,24 @@ def decode_kv_heads_per_workgroup(dtype: torch.dtype, head_dim: int, num_kv_head
                                                     int(num_query_heads)))
 
 
+# (library, device, shape) -> workgroups per CU: the occupancy query is a
+# function of the kernel and the device only, and pack_step runs every step.
+_OCCUPANCY_CACHE: dict = {}
+
+
 def decode_workgroups_per_cu(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
                              num_query_heads: int) -> int:
     """Decode workgroups of this shape one compute unit of the current device
     holds at once (the occupancy of the kernel pa_decode launches; 0 for a
-    shape without a tuned kernel)."""
+    shape without a tuned kernel).  Cached per library, device and shape."""
     lib = _native.load_library()
-    return int(lib.pa_decode_workgroups_per_cu(dtype_code(dtype), int(head_dim), int(num_kv_heads),
-                                               int(num_query_heads)))
+    key = (id(lib), torch.cuda.current_device(), dtype, int(head_dim), int(num_kv_heads), int(num_query_heads))
+    per_cu = _OCCUPANCY_CACHE.get(key)
+    if per_cu is None:
+        per_cu = int(lib.pa_decode_workgroups_per_cu(dtype_code(dtype), int(head_dim), int(num_kv_heads),
+                                                     int(num_query_heads)))
+        _OCCUPANCY_CACHE[key] = per_cu
+    return per_cu
 
 
 def choose_partition(
@@ -304,7 +314,8 @@ def pack_step(
         if head_dim is not None and dtype is not None:
             hq = int(num_query_heads or 4 * num_kv_heads)
             per_wg = max(decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, hq), 1)
-            per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq) or None
+            with torch.cuda.device(device):  # the occupancy of the step's own device
+                per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq) or None
         partition_size = choose_partition(
             start_positions, new_token_counts, num_kv_heads, num_query_heads, per_wg, per_cu,
             torch.cuda.get_device_properties(device).multi_processor_count)
