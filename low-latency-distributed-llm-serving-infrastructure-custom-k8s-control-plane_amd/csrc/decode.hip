@@ -1,6 +1,8 @@
 // Paged-attention decode for gfx950: one workgroup per
 // (sequence, context partition of up to 4096 tokens, KV head), split-K merge
-// after.
+// after.  For bf16 with an even KV head count and up to 4 query heads per KV
+// head, two adjacent KV heads run as one workgroup that reads each token's
+// rows of both heads as one row of twice the length (see PAIR below).
 //
 // The workgroup (4 waves) serves the G = H_q / H_kv query heads that share
 // one KV head, so every K/V row of the partition is read from HBM once.
