@@ -71,14 +71,17 @@ def cpu_baseline(w, t, budget_s: float):
     kind = "reference" if oa.reference_available() else "port"
     q_all = t.query[0].transpose(0, 1)
     e = 2 if w.dtype == torch.bfloat16 else 4
+    qbase = np.concatenate([[0], np.cumsum(w.new_token_counts)])  # first query token of each sequence
     sample, spent = [], 0.0
     for i in range(w.num_seqs):
+        if w.new_token_counts[i] != 1:
+            continue  # decode sequences only (a mixed step's prefill chunks are not decode work)
         blocks = torch.tensor(w.block_lists[i], dtype=torch.long, device=t.key_cache.device)
         k = t.key_cache[:, blocks].float().cpu().numpy()
         v = t.value_cache[:, blocks].float().cpu().numpy()
         ctx = w.context_lens[i]
         slots = np.arange(len(w.block_lists[i]) * w.block_size, dtype=np.int64)[:ctx]
-        q = q_all[i : i + 1].float().cpu().numpy().transpose(1, 0, 2)
+        q = q_all[qbase[i] : qbase[i] + 1].float().cpu().numpy().transpose(1, 0, 2)
         _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [w.start_positions[i]], [1], slots, w.scaling,
                                                   kind=kind)
         sample.append((q, k, v, slots, w.start_positions[i], ctx))
@@ -102,7 +105,8 @@ def cpu_baseline(w, t, budget_s: float):
         "tokens_per_s": round(len(sample) / med, 2),
         "cores": threads,
         "kind": kind,
-        "sample": (f"first {len(sample)} of {w.num_seqs} sequences ({sum(c for *_, c in sample)} context tokens), "
+        "sample": (f"first {len(sample)} of {sum(1 for c in w.new_token_counts if c == 1)} decode sequences "
+                   f"({sum(c for *_, c in sample)} context tokens), "
                    f"one call per sequence (T=1, all-ones mask; OpenMP parallelism capped at T*H_q="
                    f"{w.num_query_heads} rows), {'fp32 up-casts of the bf16' if e == 2 else 'the fp32'} values, "
                    f"median of 5 passes after a "
