@@ -206,16 +206,26 @@ int pa_copy_blocks(const void *src_cache, void *dst_cache,
  * split-K partials).  Calls that share a workspace must not overlap in time. */
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
 
-/* KV heads that one pa_decode workgroup reads together: 2 when two adjacent
- * KV heads run as one (bf16, an even KV head count, head_dim 64 or 128 and
- * groups of up to 4 query heads: each token's rows of the two heads are
- * read as one row of twice the length), else 1;
- * 0 for head counts pa_decode rejects.  A host choosing the split-K
- * partition size from the launch width divides the KV head count by it.
+/* Partition workgroups pa_decode launches per decode work item:
+ *  - num_kv_heads / 2 when two adjacent KV heads run as one workgroup
+ *    (bf16, an even KV head count, head_dim 64 or 128 and groups of up to 4
+ *    query heads: each token's rows of the two heads are read as one row of
+ *    twice the length);
+ *  - num_kv_heads x the sub-groups of a group of more than 8 query heads
+ *    (the fewest equal sub-groups of at most 8; each re-reads the K/V);
+ *  - num_kv_heads otherwise; 0 for head counts pa_decode rejects.
+ * A host choosing the split-K partition size from the launch width uses it.
  * (No counterpart in the reference, whose CPU kernel has no workgroups.) */
-int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim,
-                                         int32_t num_kv_heads,
-                                         int32_t num_query_heads);
+int32_t pa_decode_workgroups_per_item(int32_t dtype, int32_t head_dim,
+                                      int32_t num_kv_heads, int32_t num_query_heads);
+
+/* Query tokens per pa_prefill work item (the `prefill_tile` given to pa_pack
+ * and pa_prefill) that the MFMA prefill kernel takes for these head counts:
+ * 128 query rows over the query heads of one workgroup, i.e. 128 / group,
+ * or 128 / (sub-group) for groups above 8; 0 for bad head counts.  Another
+ * tile is still correct but runs the generic kernel.  (No counterpart in
+ * the reference.) */
+int32_t pa_prefill_tile(int32_t num_query_heads, int32_t num_kv_heads);
 
 /* Decode workgroups of this shape that one compute unit of the current
  * device holds at once (the HIP occupancy calculator on the kernel pa_decode

@@ -39,8 +39,9 @@ EXPORTED_SYMBOLS = (
     "pa_reshape_and_cache",
     "pa_copy_blocks",
     "pa_decode_workspace_size",
-    "pa_decode_kv_heads_per_workgroup",
+    "pa_decode_workgroups_per_item",
     "pa_decode_workgroups_per_cu",
+    "pa_prefill_tile",
     "pa_decode",
     "pa_decode_phases",
     "pa_prefill",
@@ -116,8 +117,9 @@ _SIGNATURES = {
     ),
     "pa_copy_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _vp]),
     "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
-    "pa_decode_kv_heads_per_workgroup": (_i32, [_i32, _i32, _i32, _i32]),
+    "pa_decode_workgroups_per_item": (_i32, [_i32, _i32, _i32, _i32]),
     "pa_decode_workgroups_per_cu": (_i32, [_i32, _i32, _i32, _i32]),
+    "pa_prefill_tile": (_i32, [_i32, _i32]),
     "pa_decode": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz, _vp],

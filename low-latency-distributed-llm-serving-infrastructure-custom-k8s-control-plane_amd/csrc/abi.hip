@@ -271,21 +271,33 @@ size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items) {
   return decode_workspace_layout(dims, num_decode_items).total;
 }
 
-int32_t pa_decode_kv_heads_per_workgroup(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
-                                         int32_t num_query_heads) {
+int32_t pa_decode_workgroups_per_item(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
+                                      int32_t num_query_heads) {
   if (num_kv_heads <= 0 || num_query_heads <= 0 || num_query_heads % num_kv_heads != 0) return 0;
-  return pa::decode_pairs_heads(dtype, head_dim, num_kv_heads, num_query_heads / num_kv_heads) ? 2
-                                                                                                : 1;
+  const int group = num_query_heads / num_kv_heads;
+  if (pa::decode_pairs_heads(dtype, head_dim, num_kv_heads, group)) return num_kv_heads / 2;
+  if (!pa::decode_fast_path_supported(dtype, head_dim, group, 16, 32)) return num_kv_heads;
+  return num_kv_heads * pa::decode_sub_groups(group);
+}
+
+int32_t pa_prefill_tile(int32_t num_query_heads, int32_t num_kv_heads) {
+  if (num_kv_heads <= 0 || num_query_heads <= 0 || num_query_heads % num_kv_heads != 0) return 0;
+  return pa::prefill_tile_for(num_query_heads / num_kv_heads);
 }
 
 int32_t pa_decode_workgroups_per_cu(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
                                     int32_t num_query_heads) {
-  if (pa_decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, num_query_heads) == 0) {
+  if (pa_decode_workgroups_per_item(dtype, head_dim, num_kv_heads, num_query_heads) == 0) {
     fail(PA_ERR_INVALID_ARGUMENT, "pa_decode_workgroups_per_cu: bad head counts %d / %d",
          num_query_heads, num_kv_heads);
     return 0;
   }
   const int group = num_query_heads / num_kv_heads;
+  if (!pa::decode_fast_path_supported(dtype, head_dim, group, 16, 32)) {
+    fail(PA_ERR_UNSUPPORTED, "pa_decode_workgroups_per_cu: no tuned decode kernel for dtype %d, "
+         "head_dim %d, %d query heads per KV head", dtype, head_dim, group);
+    return 0;
+  }
   const bool pair = pa::decode_pairs_heads(dtype, head_dim, num_kv_heads, group);
   int per_cu = 0;
   const hipError_t err = pa::decode_workgroups_per_cu(dtype, head_dim, group, pair, &per_cu);
@@ -324,7 +336,8 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
     return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
                 dims.num_layers);
   if (num_decode_items <= 0 || dims.num_seqs == 0) return PA_OK;
-  if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) > 0x7fffffffLL)
+  if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) *
+          pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
   if (num_merge_items < 0 || (num_merge_items > 0 && merge_items == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items is required when num_merge_items > 0");
@@ -369,6 +382,8 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
     a.partition = dims.partition_size;
     a.scale_log2e = scaling * pa::kLog2e;
     a.pair = pair ? 1 : 0;
+    a.group = pair ? 2 * group : group;
+    a.sub_groups = pair ? 1 : pa::decode_sub_groups(group);
     return from_hip(
         pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s),
         "pa_decode");
@@ -413,7 +428,8 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
     return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
                 dims.num_layers);
   if (num_prefill_items <= 0 || dims.num_seqs == 0) return PA_OK;
-  if (num_prefill_items * static_cast<int64_t>(dims.num_kv_heads) > 0x7fffffffLL)
+  if (num_prefill_items * static_cast<int64_t>(dims.num_kv_heads) *
+          pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill: too many work items");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = dims.num_query_heads / dims.num_kv_heads;
@@ -442,6 +458,8 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
     a.total_blocks = dims.total_blocks;
     a.log2_block_size = log2_exact(dims.block_size);
     a.scale_log2e = scaling * pa::kLog2e;
+    a.group = group;
+    a.sub_groups = pa::decode_sub_groups(group);
     return from_hip(
         pa::launch_prefill(a, dims.dtype, dims.head_dim, group, num_prefill_items, s),
         "pa_prefill");

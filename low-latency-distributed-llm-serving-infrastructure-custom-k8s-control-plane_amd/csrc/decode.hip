@@ -40,6 +40,7 @@
 namespace pa {
 
 constexpr int kDecodeThreads = 256;
+constexpr int kMaxDecodeGroup = 8;  // query heads one unpaired workgroup serves
 constexpr int kDecodeWaves = kDecodeThreads / kWave;
 // Largest split-K partition (context tokens per workgroup) the kernel takes.
 constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
@@ -252,8 +253,13 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int hkv = a.num_kv_heads;
-  const int64_t item = blockIdx.x / hkv;
-  const int kvh = blockIdx.x - static_cast<int>(item) * hkv;
+  // Workgroup -> (item, KV head, sub-group of G of the head's a.group query
+  // heads; one sub-group unless a.group exceeds the largest kernel group).
+  const int units = hkv * a.sub_groups;
+  const int64_t item = blockIdx.x / units;
+  const int unit = static_cast<int>(blockIdx.x - item * units);
+  const int kvh = unit / a.sub_groups;
+  const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
   const int seq = a.items[2 * item];
   const int part = a.items[2 * item + 1];
   const int ctx = a.context_lens[seq];
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     const int g = i / (D / CE);
     const int c = i - g * (D / CE);
     const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
-                    static_cast<int64_t>(kvh * G + g) * a.q_head_stride;
+                    static_cast<int64_t>(h0 + g) * a.q_head_stride;
     if constexpr (PAIR) {
       // Query head g belongs to real KV head g / GA of the pair: its D/2
       // elements go into that half of the row (the other half is never read).
@@ -647,12 +653,13 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   }
   __syncthreads();
 
-  // Outputs and partials use the real layout [.., H_q, OUT_D]: a pair's G
-  // query heads are the real heads kvh*G .. kvh*G + G-1.
-  const int hq = hkv * G;
+  // Outputs and partials use the real layout [.., H_q, OUT_D]: this
+  // workgroup's G query heads are the real heads h0 .. h0 + G-1 (for a pair,
+  // those of both of its KV heads).
+  const int hq = hkv * a.group;
   const int nparts = (ctx + a.partition - 1) / a.partition;
-  float* pacc = a.part_acc + (item * hq + kvh * G) * OUT_D;
-  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + kvh * G) * OUT_D;
+  float* pacc = a.part_acc + (item * hq + h0) * OUT_D;
+  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + h0) * OUT_D;
   for (int i = tid; i < G * OUT_D; i += kDecodeThreads) {
     const int g = i / OUT_D;
     float mx = s_m[0][g];
@@ -670,7 +677,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     } else {
       pacc[i] = o;
       if (i % OUT_D == 0) {
-        float* pml = a.part_ml + (item * hq + kvh * G + g) * 2;
+        float* pml = a.part_ml + (item * hq + h0 + g) * 2;
         pml[0] = mx;
         pml[1] = l;
       }
@@ -760,7 +767,7 @@ struct LaunchOp {
   hipStream_t stream;
   template <typename T, int D, int G, bool PAIR>
   hipError_t run() const {
-    const int64_t grid = num_items * a.num_kv_heads;
+    const int64_t grid = num_items * a.num_kv_heads * a.sub_groups;
     const int64_t merge_grid = a.num_merge * a.num_kv_heads;
     if (phases & PA_DECODE_PHASE_PARTITIONS) {
       hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR>), dim3(static_cast<uint32_t>(grid)),
@@ -769,12 +776,13 @@ struct LaunchOp {
       if (err != hipSuccess) return err;
     }
     if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
-    // Partials are in the real layout: rows of D/2 when paired.
+    // Partials are in the real layout: rows of D/2 when paired; all a.group
+    // query heads of a KV head (or pair) merge in one workgroup row.
     constexpr int kOutD = PAIR ? D / 2 : D;
-    constexpr int kChunks = (G * kOutD + kDecodeThreads - 1) / kDecodeThreads;
+    const int chunks = (a.group * kOutD + kDecodeThreads - 1) / kDecodeThreads;
     hipLaunchKernelGGL((decode_merge_kernel<T>),
-                       dim3(static_cast<uint32_t>(merge_grid), kChunks), dim3(kDecodeThreads), 0,
-                       stream, a, G, kOutD);
+                       dim3(static_cast<uint32_t>(merge_grid), static_cast<uint32_t>(chunks)),
+                       dim3(kDecodeThreads), 0, stream, a, a.group, kOutD);
     return hipGetLastError();
   }
 };
@@ -814,7 +822,8 @@ static hipError_t visit_group(int G, const Op& op) {
 }
 
 // The kernel instance of a real shape: paired heads of D run as the
-// instance of head dim 2D and group 2G.
+// instance of head dim 2D and group 2G; a group above the largest kernel
+// group runs as decode_sub_groups(group) workgroups per KV head.
 template <typename Op>
 static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, const Op& op) {
   if (pair) {
@@ -823,12 +832,14 @@ static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, co
     if (head_dim == 128) return visit_group<bf16_t, 256, true>(2 * group, op);
     return hipErrorNotSupported;
   }
+  if (group < 1) return hipErrorNotSupported;
+  const int g = group / decode_sub_groups(group);
   if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return visit_group<bf16_t, 128, false>(group, op);
-    if (head_dim == 64) return visit_group<bf16_t, 64, false>(group, op);
+    if (head_dim == 128) return visit_group<bf16_t, 128, false>(g, op);
+    if (head_dim == 64) return visit_group<bf16_t, 64, false>(g, op);
   } else if (dtype == PA_DTYPE_F32) {
-    if (head_dim == 128) return visit_group<float, 128, false>(group, op);
-    if (head_dim == 64) return visit_group<float, 64, false>(group, op);
+    if (head_dim == 128) return visit_group<float, 128, false>(g, op);
+    if (head_dim == 64) return visit_group<float, 64, false>(g, op);
   }
   return hipErrorNotSupported;
 }
@@ -855,11 +866,18 @@ bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group) {
   return false;
 }
 
+int decode_sub_groups(int group) {
+  // The fewest equal sub-groups of at most kMaxDecodeGroup query heads.
+  int n = (group + kMaxDecodeGroup - 1) / kMaxDecodeGroup;
+  while (n < group && group % n != 0) ++n;
+  return n > 0 ? n : 1;
+}
+
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition) {
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
-  if (group < 1 || group > 8) return false;
+  if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;
   return true;

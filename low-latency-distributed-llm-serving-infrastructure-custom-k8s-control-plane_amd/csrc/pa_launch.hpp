@@ -34,6 +34,11 @@ struct DecodeArgs {
   // heads of both).  Every query head reads only its own half of the rows;
   // outputs and partials use the real layout [.., H_q, D/2].
   int32_t pair;
+  // Query heads per num_kv_heads unit (for a pair, those of both heads) and
+  // the workgroups that share them (1 unless the group is split because it
+  // exceeds the largest kernel group; each then re-reads the unit's K/V).
+  int32_t group;
+  int32_t sub_groups;
 };
 
 // Generic one-wave-per-(query token, head) attention: any head_dim <= 256,
@@ -138,10 +143,21 @@ struct PrefillArgs {
   int32_t total_blocks;
   int32_t log2_block_size;
   float scale_log2e;
+  // Query heads per KV head and the workgroups that share them (1 unless
+  // the group exceeds the largest kernel group; each serves group /
+  // sub_groups heads and walks the context itself).
+  int32_t group;
+  int32_t sub_groups;
 };
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition);
+// Largest query-head group the decode serves (split into sub-groups of at
+// most 8 heads above 8).
+constexpr int kMaxDecodeQueryGroup = 64;
+// Workgroups sharing one KV head's query heads: the fewest equal sub-groups
+// of at most 8 heads.
+int decode_sub_groups(int group);
 // Whether two adjacent KV heads of this shape run as one workgroup
 // (DecodeArgs::pair; the KV head count must then be even).
 bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group);

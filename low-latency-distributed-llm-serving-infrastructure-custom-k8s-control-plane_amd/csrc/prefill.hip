@@ -137,8 +137,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int hkv = a.num_kv_heads;
   // Highest item first: the last query tiles of a sequence see the most context.
   const int64_t blk_id = static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x;
-  const int64_t item = blk_id / hkv;
-  const int kvh = static_cast<int>(blk_id - item * hkv);
+  // -> (item, KV head, sub-group of G of the head's a.group query heads).
+  const int units = hkv * a.sub_groups;
+  const int64_t item = blk_id / units;
+  const int unit = static_cast<int>(blk_id - item * units);
+  const int kvh = unit / a.sub_groups;
+  const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
   const int seq = a.items[2 * item];
   const int qt = a.items[2 * item + 1];
   const int64_t first = a.cu_seqlens[seq];
@@ -167,7 +171,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // Rows past G * MTOK (when G does not divide 128) belong to no head.
   const bool row_live = tok < ntok && g < G;
   const int qpos = start + tok0 + tok;  // causal limit (inclusive)
-  const int h = kvh * G + g;
+  const int h = h0 + g;
 
   uint4 qreg[KS];
   {
@@ -431,7 +435,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   if (!row_live) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = reinterpret_cast<uint16_t*>(a.output) +
-                   ((first + tok0 + tok) * (hkv * G) + h) * static_cast<int64_t>(D);
+                   ((first + tok0 + tok) * (hkv * a.group) + h) * static_cast<int64_t>(D);
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -447,18 +451,22 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
   if (dtype != PA_DTYPE_BF16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
-  if (group < 1 || group > 8) return false;
+  if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   return true;
 }
 
-int prefill_tile_for(int group) { return group > 0 ? kPrefillRows / group : kPrefillRows; }
+// Query tokens per work item: 128 rows over the heads of one workgroup (a
+// sub-group of at most 8 when the group is larger).
+int prefill_tile_for(int group) {
+  return group > 0 ? kPrefillRows / (group / decode_sub_groups(group)) : kPrefillRows;
+}
 
 template <int D>
 static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items,
                                    hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads));
-  switch (group) {
+  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
+  switch (group / a.sub_groups) {
     case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(kPrefillThreads), 0, s, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(kPrefillThreads), 0, s, a); break;
     case 3: hipLaunchKernelGGL((prefill_kernel<D, 3>), grid, dim3(kPrefillThreads), 0, s, a); break;

@@ -65,9 +65,10 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def prefill_tile_for(num_query_heads: int, num_kv_heads: int) -> int:
-    """Query tokens per prefill work item (128 query rows per workgroup)."""
-    group = num_query_heads // num_kv_heads
-    return 128 // group if 1 <= group <= 8 else 128
+    """Query tokens per prefill work item: the tile the MFMA prefill kernel
+    takes (128 query rows over one workgroup's heads; pa_prefill_tile)."""
+    lib = _native.load_library()
+    return int(lib.pa_prefill_tile(int(num_query_heads), int(num_kv_heads))) or 128
 
 
 # ---------------------------------------------------------------------------
@@ -157,13 +158,14 @@ def work_counts(
 _DECODE_CUS = 256
 
 
-def decode_kv_heads_per_workgroup(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
-                                  num_query_heads: int) -> int:
-    """KV heads one decode workgroup reads together (2 when adjacent KV heads
-    run as pairs, else 1; 0 for head counts the decode rejects)."""
+def decode_workgroups_per_item(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
+                               num_query_heads: int) -> int:
+    """Partition workgroups the decode launches per work item: half the KV
+    heads when adjacent heads run as pairs, KV heads x sub-groups for groups
+    of more than 8 query heads, else the KV heads (0 for rejected counts)."""
     lib = _native.load_library()
-    return int(lib.pa_decode_kv_heads_per_workgroup(dtype_code(dtype), int(head_dim), int(num_kv_heads),
-                                                    int(num_query_heads)))
+    return int(lib.pa_decode_workgroups_per_item(dtype_code(dtype), int(head_dim), int(num_kv_heads),
+                                                 int(num_query_heads)))
 
 
 # (library, device, shape) -> workgroups per CU: the occupancy query is a
@@ -191,14 +193,14 @@ def choose_partition(
     new_token_counts: Sequence[int],
     num_kv_heads: int = 8,
     num_query_heads: Optional[int] = None,
-    kv_heads_per_workgroup: int = 1,
+    workgroups_per_item: Optional[int] = None,
     workgroups_per_cu: Optional[int] = None,
     compute_units: int = _DECODE_CUS,
 ) -> int:
     """Split-K partition for the decode sequences of a step.
 
     The largest of 4096, 2048, 1024, 512 and 256 tokens whose decode launch
-    (partitions x KV heads / kv_heads_per_workgroup) still gives every
+    (partitions x workgroups_per_item, by default the KV heads) still gives every
     resident workgroup slot of the chip (compute_units x workgroups_per_cu;
     without the occupancy, five per CU for one query head per KV head and
     four for groups) one and a half workgroups: long partitions keep the
@@ -218,7 +220,7 @@ def choose_partition(
     group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
     per_cu = int(workgroups_per_cu or 0) or (5 if group == 1 else 4)
     need = 3 * int(compute_units) * per_cu // 2
-    width = max(hkv // max(int(kv_heads_per_workgroup), 1), 1)  # workgroups per item
+    width = max(int(workgroups_per_item or hkv), 1)  # workgroups per item
     ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
     p = PA_DECODE_MAX_PARTITION
     while p > 256:
@@ -310,14 +312,14 @@ def pack_step(
     if prefill_tile <= 0:
         raise ValueError("prefill_tile must be positive")
     if partition_size is None:
-        per_wg, per_cu = 1, None
+        per_item, per_cu = None, None
         if head_dim is not None and dtype is not None:
             hq = int(num_query_heads or 4 * num_kv_heads)
-            per_wg = max(decode_kv_heads_per_workgroup(dtype, head_dim, num_kv_heads, hq), 1)
+            per_item = decode_workgroups_per_item(dtype, head_dim, num_kv_heads, hq) or None
             with torch.cuda.device(device):  # the occupancy of the step's own device
                 per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq) or None
         partition_size = choose_partition(
-            start_positions, new_token_counts, num_kv_heads, num_query_heads, per_wg, per_cu,
+            start_positions, new_token_counts, num_kv_heads, num_query_heads, per_item, per_cu,
             torch.cuda.get_device_properties(device).multi_processor_count)
     if partition_size <= 0:
         raise ValueError("partition_size must be positive")

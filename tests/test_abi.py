@@ -103,23 +103,42 @@ def test_workspace_size():
     assert lib.pa_decode_workspace_size(dims, 77) == ops.decode_workspace_bytes(77, 16, 64)
 
 
-def test_kv_heads_per_workgroup():
+def test_workgroups_per_item():
     native = pkg("_native")
     lib = native.load_library()
     bf16, f32 = native.PA_DTYPE_BF16, native.PA_DTYPE_F32
-    # (dtype, head_dim, H_kv, H_q) -> KV heads per decode workgroup
+    # (dtype, head_dim, H_kv, H_q) -> decode partition workgroups per work item
     cases = {
-        (bf16, 64, 8, 8): 2, (bf16, 64, 8, 16): 2, (bf16, 64, 8, 24): 2, (bf16, 64, 8, 32): 2,
-        (bf16, 64, 8, 40): 1,  # groups above 4 stay single
-        (bf16, 64, 3, 9): 1,  # an odd KV head count cannot pair
-        (bf16, 128, 8, 8): 2, (bf16, 128, 32, 32): 2, (bf16, 128, 8, 16): 2, (bf16, 128, 8, 32): 2,
-        (bf16, 128, 8, 48): 1,
-        (f32, 64, 8, 8): 1, (f32, 128, 8, 16): 1, (native.PA_DTYPE_F16, 64, 8, 8): 1,
-        (bf16, 96, 8, 8): 1,
+        # pairs of adjacent KV heads: half the KV heads
+        (bf16, 64, 8, 8): 4, (bf16, 64, 8, 16): 4, (bf16, 64, 8, 24): 4, (bf16, 64, 8, 32): 4,
+        (bf16, 128, 8, 8): 4, (bf16, 128, 32, 32): 16, (bf16, 128, 8, 16): 4, (bf16, 128, 8, 32): 4,
+        # one per KV head: groups of 5-8, an odd KV head count, fp32
+        (bf16, 64, 8, 40): 8, (bf16, 128, 8, 48): 8, (bf16, 64, 3, 9): 3,
+        (f32, 64, 8, 8): 8, (f32, 128, 8, 16): 8,
+        # groups above 8: the fewest equal sub-groups of at most 8 heads
+        (bf16, 128, 8, 128): 16, (bf16, 128, 4, 48): 8, (f32, 64, 2, 22): 22, (bf16, 128, 1, 64): 8,
+        (bf16, 64, 2, 18): 6,
+        # no tuned kernel (the generic one runs a workgroup per KV head's rows)
+        (native.PA_DTYPE_F16, 64, 8, 8): 8, (bf16, 96, 8, 8): 8, (bf16, 128, 1, 72): 1,
+        # rejected head counts
         (bf16, 64, 0, 8): 0, (bf16, 64, 8, 12): 0, (bf16, 64, 8, 0): 0,
     }
     for (dtype, d, hkv, hq), want in cases.items():
-        assert lib.pa_decode_kv_heads_per_workgroup(dtype, d, hkv, hq) == want, (dtype, d, hkv, hq)
+        assert lib.pa_decode_workgroups_per_item(dtype, d, hkv, hq) == want, (dtype, d, hkv, hq)
+
+
+def test_prefill_tile():
+    lib = pkg("_native").load_library()
+    ops = pkg("paged_ops")
+    # 128 query rows over one workgroup's heads; groups above 8 split into the
+    # fewest equal sub-groups of at most 8 heads
+    cases = {(8, 8): 128, (32, 8): 32, (24, 8): 42, (64, 8): 16, (9, 3): 42, (7, 1): 18,
+             (96, 8): 21, (128, 8): 16, (9, 1): 42, (64, 1): 16, (11, 1): 128,
+             (0, 8): 0, (12, 8): 0, (8, 0): 0}
+    for (hq, hkv), want in cases.items():
+        assert lib.pa_prefill_tile(hq, hkv) == want, (hq, hkv)
+    assert ops.prefill_tile_for(128, 8) == 16
+    assert ops.prefill_tile_for(12, 8) == 128  # rejected counts: one workgroup row of tokens
 
 
 def test_product_path_fails_loudly_without_library(monkeypatch, tmp_path):

@@ -273,7 +273,9 @@ def test_decode_fp32_matches_oracle(device):
     (12, 2, 64, torch.bfloat16), (28, 4, 128, torch.bfloat16), (14, 2, 128, torch.float32),
     # paired KV heads (bf16, even H_kv): heads of 64 with groups of 3 and 4,
     # heads of 128 with a group of 2
-    (24, 8, 64, torch.bfloat16), (16, 8, 128, torch.bfloat16)])
+    (24, 8, 64, torch.bfloat16), (16, 8, 128, torch.bfloat16),
+    # groups above 8 as sub-groups of at most 8 (16 = 2 x 8, 12 = 2 x 6, 11 = 11 x 1)
+    (32, 2, 128, torch.bfloat16), (24, 2, 64, torch.bfloat16), (11, 1, 64, torch.float32)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
@@ -367,10 +369,11 @@ def test_decode_occupancy_query(device):
             for g in range(1, 9):
                 per_cu = ops.decode_workgroups_per_cu(dtype, d, 8, 8 * g)
                 log(f"occupancy {dtype} D={d} G={g}: {per_cu} per CU, "
-                    f"{ops.decode_kv_heads_per_workgroup(dtype, d, 8, 8 * g)} KV heads per workgroup")
+                    f"{ops.decode_workgroups_per_item(dtype, d, 8, 8 * g)} workgroups per item")
                 assert 1 <= per_cu <= 8
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 2, 32) >= 1  # group 16: two sub-groups
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 96, 8, 8) == 0
-    assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 8, 80) == 0
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 1, 72) == 0
 
 
 def test_decode_phases_equal_one_call(device):
@@ -465,7 +468,9 @@ def test_device_strategy_copy_blocks(device):
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 2, 64), (8, 1, 64),
-                                     (9, 3, 64), (12, 4, 128), (10, 2, 128), (12, 2, 64), (28, 4, 128)])
+                                     (9, 3, 64), (12, 4, 128), (10, 2, 128), (12, 2, 64), (28, 4, 128),
+                                     # groups above 8: sub-groups of 8 and of 6 query heads
+                                     (32, 2, 128), (24, 2, 64)])
 def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]

@@ -310,10 +310,13 @@ def test_choose_partition_fills_the_chip():
     assert ops.choose_partition([15, 300, 512], [1, 1, 1], 8, 8) == 256
     assert ops.choose_partition([15, 200, 255], [1, 1, 1], 8, 8) == 256
     # paired KV heads halve the launch width: the same step splits further
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, kv_heads_per_workgroup=2) == 2048
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, kv_heads_per_workgroup=2) == 2048
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, workgroups_per_item=4) == 2048
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, workgroups_per_item=4) == 2048
+    # split query-head groups widen it
+    assert ops.choose_partition([3000] * 64, [1] * 64, 8, 128, workgroups_per_item=16) == 2048
+    assert ops.choose_partition([3000] * 64, [1] * 64, 8, 128) == 1024
     # the kernel's occupancy sets the resident slots: fewer slots, longer partitions
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 2, workgroups_per_cu=2) == 4096
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 2, workgroups_per_cu=8) == 1024
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 4, workgroups_per_cu=2) == 4096
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 4, workgroups_per_cu=8) == 1024
     # a chip with fewer compute units fills at longer partitions
-    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, 2, compute_units=128) == 4096
+    assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, 4, compute_units=128) == 4096
