@@ -208,7 +208,7 @@ size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
 
 /* Partition workgroups pa_decode launches per decode work item:
  *  - num_kv_heads / 2 when two adjacent KV heads run as one workgroup
- *    (bf16, an even KV head count, head_dim 64 or 128 and groups of up to 4
+ *    (bf16 or fp16, an even KV head count, head_dim 64 or 128 and groups of up to 4
  *    query heads: each token's rows of the two heads are read as one row of
  *    twice the length);
  *  - num_kv_heads x the sub-groups of a group of more than 8 query heads

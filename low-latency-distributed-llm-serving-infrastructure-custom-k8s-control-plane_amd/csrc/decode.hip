@@ -1,6 +1,6 @@
 // Paged-attention decode for gfx950: one workgroup per
 // (sequence, context partition of up to 4096 tokens, KV head), split-K merge
-// after.  For bf16 with an even KV head count and up to 4 query heads per KV
+// after.  For bf16/fp16 with an even KV head count and up to 4 query heads per KV
 // head, two adjacent KV heads run as one workgroup that reads each token's
 // rows of both heads as one row of twice the length (see PAIR below).
 //
@@ -13,8 +13,9 @@
 //  K (QK layout)  a "row group" of kL lanes holds one token's K row, each
 //                 lane two 16-byte pieces (the group's loads cover the row
 //                 contiguously); a wave covers 64 / kL tokens per load.
-//                 Dots with the G query slices use v_dot2_f32_bf16 (bf16)
-//                 and a DPP butterfly sums each group.
+//                 Dots with the G query slices use v_dot2_f32_bf16 /
+//                 v_dot2_f32_f16 (16-bit types) and a DPP butterfly sums
+//                 each group.
 //  V (PV layout)  one wave load covers whole V rows (one 256-byte row for
 //                 bf16 D=128, 4 bytes per lane), so the row address of a
 //                 load is wave-uniform and is formed in scalar registers
@@ -22,9 +23,9 @@
 //                 owns a fixed slice of the head dimension for all G heads.
 //  softmax        per tile: wave-wide max per head (DPP + shuffles), rescale
 //                 of the running sum / accumulator only when the max moved,
-//                 p = exp2(s - max) staged in LDS.  For bf16 the p of two
-//                 tokens are packed as a bf16 pair and the PV product uses
-//                 v_dot2_f32_bf16 on the matching V pair (one v_perm_b32 per
+//                 p = exp2(s - max) staged in LDS.  For bf16/fp16 the p of
+//                 two tokens are packed as a pair of the cache type and the
+//                 PV product uses v_dot2 on the matching V pair (one v_perm_b32 per
 //                 two elements); fp32 keeps fp32 FMAs throughout.
 //
 // At the end the four waves combine (max, sum, acc) through LDS.  A sequence
@@ -107,16 +108,10 @@ __device__ __forceinline__ uint32_t kv_load<uint32_t>(const void* p) {
 #endif
 }
 
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a),
-                                         __builtin_bit_cast(bf16x2v, b), c, false);
-}
 
 template <typename T, int D, int TILE>
 struct DecodeShape {
-  static constexpr bool kBf16 = Elem<T>::kDtype == PA_DTYPE_BF16;
+  static constexpr bool kHalf = Elem<T>::kBytes == 2;  // bf16 or fp16
   static constexpr int kE = Elem<T>::kBytes;
   static constexpr int kRowBytes = D * kE;
   // QK layout
@@ -148,17 +143,18 @@ struct VRaw<8> {
   using type = uint2;
 };
 
-// Dot product of one 16-byte piece of K with the matching piece of q (bf16).
+// Dot product of one 16-byte piece of K with the matching piece of q
+// (16-bit elements).
 template <typename T>
 __device__ __forceinline__ float piece_dot(uint4 q, uint4 k) {
-  static_assert(Elem<T>::kDtype == PA_DTYPE_BF16, "paired heads are bf16");
-  float acc = dot2_bf16(q.x, k.x, 0.f);
-  acc = dot2_bf16(q.y, k.y, acc);
-  acc = dot2_bf16(q.z, k.z, acc);
-  return dot2_bf16(q.w, k.w, acc);
+  static_assert(Elem<T>::kBytes == 2, "paired heads have 16-bit elements");
+  float acc = dot2_half<T>(q.x, k.x, 0.f);
+  acc = dot2_half<T>(q.y, k.y, acc);
+  acc = dot2_half<T>(q.z, k.z, acc);
+  return dot2_half<T>(q.w, k.w, acc);
 }
 
-// 32-bit word w of a lane's V piece (a bf16 pair).
+// 32-bit word w of a lane's V piece (a pair of 16-bit elements).
 __device__ __forceinline__ uint32_t v_word(uint32_t v, int) { return v; }
 __device__ __forceinline__ uint32_t v_word(uint2 v, int w) { return w == 0 ? v.x : v.y; }
 
@@ -166,13 +162,13 @@ __device__ __forceinline__ uint32_t v_word(uint2 v, int w) { return w == 0 ? v.x
 template <typename T>
 __device__ __forceinline__ float slice_dot(const uint4 (&q)[2], const uint4 (&k)[2]) {
   float acc = 0.f;
-  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
+  if constexpr (Elem<T>::kBytes == 2) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      acc = dot2_bf16(q[c].x, k[c].x, acc);
-      acc = dot2_bf16(q[c].y, k[c].y, acc);
-      acc = dot2_bf16(q[c].z, k[c].z, acc);
-      acc = dot2_bf16(q[c].w, k[c].w, acc);
+      acc = dot2_half<T>(q[c].x, k[c].x, acc);
+      acc = dot2_half<T>(q[c].y, k[c].y, acc);
+      acc = dot2_half<T>(q[c].z, k[c].z, acc);
+      acc = dot2_half<T>(q[c].w, k[c].w, acc);
     }
   } else {
 #pragma unroll
@@ -233,14 +229,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   constexpr int PE = S::kPe;
   constexpr int R = S::kR;
   constexpr int ROWS = S::kRows;
-  constexpr bool BF16 = S::kBf16;
-  // p staging per wave: bf16 pairs [16 pairs][G] or fp32 [32 tokens][G]
+  constexpr bool HALF = S::kHalf;  // 16-bit elements (bf16 or fp16)
+  // p staging per wave: 16-bit pairs [16 pairs][G] or fp32 [32 tokens][G]
   constexpr int kTile = S::kTile;
-  constexpr int PWORDS = BF16 ? (kTile / 2) * G : kTile * G;
+  constexpr int PWORDS = HALF ? (kTile / 2) * G : kTile * G;
   constexpr int GA = PAIR ? G / 2 : G;    // heads a lane accumulates
   constexpr int OUT_D = PAIR ? D / 2 : D;  // output elements per query head
-  static_assert(!PAIR || (BF16 && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
-                "pairs: bf16, an even head count, one V row per wave load");
+  static_assert(!PAIR || (HALF && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
+                "pairs: 16-bit elements, an even head count, one V row per wave load");
 
   __shared__ int s_blk[kMaxPartition + 2];
   __shared__ uint4 s_q[G * D * S::kE / 16];
@@ -335,7 +331,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // scores: lane lig owns "combos" k = lig % LS + LS*r, each one (token pair,
   // head) for bf16 or (token, head) for fp32, and computes, sums and stages
   // only those.
-  constexpr int NC = (BF16 ? TPG / 2 : TPG) * NS;  // combos per lane group
+  constexpr int NC = (HALF ? TPG / 2 : TPG) * NS;  // combos per lane group
   constexpr int CPL = (NC + LS - 1) / LS;          // combos per lane
   float lsum[NS];  // this lane's share of the softmax denominators of its NS heads
 #pragma unroll
@@ -526,7 +522,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
         const bool mine = c == cc;
-        if constexpr (BF16) {
+        if constexpr (HALF) {
           sa = mine ? s[2 * (cc / NS)][cc % NS] : sa;
           sb = mine ? s[2 * (cc / NS) + 1][cc % NS] : sb;
         } else {
@@ -537,12 +533,12 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       const int jl = SPLIT ? c % NS : g;  // its slot in lsum
 #pragma unroll
       for (int gg = 0; gg < G; ++gg) mc = g == gg ? mneg[gg] : mc;
-      if constexpr (BF16) {
+      if constexpr (HALF) {
         const float pa = fast_exp2(fmaf(sa, scale, mc));
         const float pb = fast_exp2(fmaf(sb, scale, mc));
 #pragma unroll
         for (int gg = 0; gg < NS; ++gg) lsum[gg] += jl == gg ? pa + pb : 0.f;
-        sp[((c / NS) * GPW + gi) * G + g] = pack_bf16x2(pa, pb);
+        sp[((c / NS) * GPW + gi) * G + g] = pack_half2<T>(pa, pb);
       } else {
         const float pa = fast_exp2(fmaf(sa, scale, mc));
 #pragma unroll
@@ -556,7 +552,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // Accumulate P x V of the loaded V tile.
   auto pv = [&]() {
     const uint32_t* sp = s_p[wave];
-    if constexpr (BF16) {
+    if constexpr (HALF) {
       constexpr int PARTNER = GPW / R;  // V load holding token t + GPW
 #pragma unroll
       for (int u = 0; u < ROWS; ++u) {
@@ -574,8 +570,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
           const uint32_t hi = __builtin_amdgcn_perm(vbb, va, 0x07060302u);
 #pragma unroll
           for (int j = 0; j < GA; ++j) {
-            acc[j][2 * w] = dot2_bf16(pw[j], lo, acc[j][2 * w]);
-            acc[j][2 * w + 1] = dot2_bf16(pw[j], hi, acc[j][2 * w + 1]);
+            acc[j][2 * w] = dot2_half<T>(pw[j], lo, acc[j][2 * w]);
+            acc[j][2 * w + 1] = dot2_half<T>(pw[j], hi, acc[j][2 * w + 1]);
           }
         }
       }
@@ -827,9 +823,14 @@ static hipError_t visit_group(int G, const Op& op) {
 template <typename Op>
 static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, const Op& op) {
   if (pair) {
-    if (dtype != PA_DTYPE_BF16 || group < 1 || group > 4) return hipErrorNotSupported;
-    if (head_dim == 64) return visit_group<bf16_t, 128, true>(2 * group, op);
-    if (head_dim == 128) return visit_group<bf16_t, 256, true>(2 * group, op);
+    if (group < 1 || group > 4) return hipErrorNotSupported;
+    if (dtype == PA_DTYPE_BF16) {
+      if (head_dim == 64) return visit_group<bf16_t, 128, true>(2 * group, op);
+      if (head_dim == 128) return visit_group<bf16_t, 256, true>(2 * group, op);
+    } else if (dtype == PA_DTYPE_F16) {
+      if (head_dim == 64) return visit_group<f16_t, 128, true>(2 * group, op);
+      if (head_dim == 128) return visit_group<f16_t, 256, true>(2 * group, op);
+    }
     return hipErrorNotSupported;
   }
   if (group < 1) return hipErrorNotSupported;
@@ -837,6 +838,9 @@ static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, co
   if (dtype == PA_DTYPE_BF16) {
     if (head_dim == 128) return visit_group<bf16_t, 128, false>(g, op);
     if (head_dim == 64) return visit_group<bf16_t, 64, false>(g, op);
+  } else if (dtype == PA_DTYPE_F16) {
+    if (head_dim == 128) return visit_group<f16_t, 128, false>(g, op);
+    if (head_dim == 64) return visit_group<f16_t, 64, false>(g, op);
   } else if (dtype == PA_DTYPE_F32) {
     if (head_dim == 128) return visit_group<float, 128, false>(g, op);
     if (head_dim == 64) return visit_group<float, 64, false>(g, op);
@@ -844,7 +848,7 @@ static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, co
   return hipErrorNotSupported;
 }
 
-// Largest real group run as pairs, per real head dim (bf16; 0 = never).
+// Largest real group run as pairs, per real head dim (bf16 and fp16; 0 = never).
 // Kernel time on 256 lognormal contexts (median 1024) with 8 KV heads,
 // unpaired -> paired, each at its best partition:
 //   D 64:  G 1 0.180 -> 0.141 ms, G 2 0.181 -> 0.140, G 3 0.183 -> 0.147,
@@ -860,7 +864,8 @@ static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, co
 #endif
 
 bool decode_pairs_heads(int dtype, int head_dim, int num_kv_heads, int group) {
-  if (dtype != PA_DTYPE_BF16 || num_kv_heads % 2 != 0 || group < 1) return false;
+  if ((dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) || num_kv_heads % 2 != 0 || group < 1)
+    return false;
   if (head_dim == 64) return group <= PA_DECODE_PAIR_MAX_GROUP_D64;
   if (head_dim == 128) return group <= PA_DECODE_PAIR_MAX_GROUP_D128;
   return false;
@@ -875,7 +880,7 @@ int decode_sub_groups(int group) {
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition) {
-  if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16) return false;
+  if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;

@@ -17,23 +17,6 @@
 
 namespace pa {
 
-struct f16_t {
-  _Float16 v;
-};
-template <>
-struct Elem<f16_t> {
-  static constexpr int kBytes = 2;
-  static constexpr int kDtype = PA_DTYPE_F16;
-};
-template <>
-__device__ __forceinline__ float load_scalar<f16_t>(const f16_t* p) {
-  return static_cast<float>(p->v);
-}
-template <>
-__device__ __forceinline__ void store_scalar<f16_t>(f16_t* p, float v) {
-  p->v = static_cast<_Float16>(v);
-}
-
 template <typename T, int EPL, bool kMasked>
 __global__ __launch_bounds__(kWave) void generic_attention_kernel(GenericArgs a) {
   const int lane = threadIdx.x;

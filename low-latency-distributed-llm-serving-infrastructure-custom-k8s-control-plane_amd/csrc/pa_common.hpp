@@ -28,6 +28,9 @@ constexpr float kScoreFloor = -1e30f;
 struct bf16_t {
   uint16_t bits;
 };
+struct f16_t {
+  _Float16 v;
+};
 
 template <typename T>
 struct Elem;
@@ -40,6 +43,11 @@ template <>
 struct Elem<bf16_t> {
   static constexpr int kBytes = 2;
   static constexpr int kDtype = PA_DTYPE_BF16;
+};
+template <>
+struct Elem<f16_t> {
+  static constexpr int kBytes = 2;
+  static constexpr int kDtype = PA_DTYPE_F16;
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) {
@@ -66,6 +74,37 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(pack_bf16x2(f, 0.f) & 0xffffu);
 }
 
+typedef _Float16 f16x2cv __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2dv __attribute__((ext_vector_type(2)));
+
+// fp32 pair -> packed pair of a 16-bit element type (round to nearest even).
+template <typename T>
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack_half2<bf16_t>(float lo, float hi) {
+  return pack_bf16x2(lo, hi);
+}
+template <>
+__device__ __forceinline__ uint32_t pack_half2<f16_t>(float lo, float hi) {
+  const f32x2v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2cv));
+}
+
+// Dot product of two packed pairs of a 16-bit element type, accumulated in
+// fp32 (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <typename T>
+__device__ __forceinline__ float dot2_half(uint32_t a, uint32_t b, float c);
+template <>
+__device__ __forceinline__ float dot2_half<bf16_t>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2dv, a),
+                                         __builtin_bit_cast(bf16x2dv, b), c, false);
+}
+template <>
+__device__ __forceinline__ float dot2_half<f16_t>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2cv, a), __builtin_bit_cast(f16x2cv, b), c,
+                                false);
+}
+
 template <typename T>
 __device__ __forceinline__ float load_scalar(const T* p);
 template <>
@@ -75,6 +114,10 @@ __device__ __forceinline__ float load_scalar<float>(const float* p) {
 template <>
 __device__ __forceinline__ float load_scalar<bf16_t>(const bf16_t* p) {
   return bf16_to_f32(p->bits);
+}
+template <>
+__device__ __forceinline__ float load_scalar<f16_t>(const f16_t* p) {
+  return static_cast<float>(p->v);
 }
 
 template <typename T>
@@ -86,6 +129,10 @@ __device__ __forceinline__ void store_scalar<float>(float* p, float v) {
 template <>
 __device__ __forceinline__ void store_scalar<bf16_t>(bf16_t* p, float v) {
   p->bits = f32_to_bf16(v);
+}
+template <>
+__device__ __forceinline__ void store_scalar<f16_t>(f16_t* p, float v) {
+  p->v = static_cast<_Float16>(v);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) {

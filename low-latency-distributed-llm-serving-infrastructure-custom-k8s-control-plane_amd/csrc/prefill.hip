@@ -11,7 +11,8 @@
 // Both products are computed transposed so that a lane owns one query row:
 //   S^T[kv][row] = sum_d K[kv][d] Q[row][d]       (A = K from LDS, B = Q regs)
 //   O^T[d][row] += sum_kv V^T[d][kv] P^T[kv][row]  (A = V^T, B = P^T regs)
-// with v_mfma_f32_32x32x16_bf16.  In the 32x32 accumulator lane l holds
+// with v_mfma_f32_32x32x16_bf16 (or _f16 for fp16 caches).  In the 32x32
+// accumulator lane l holds
 // column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4), i = 0..15, so the
 // softmax max/sum of a query row needs only its own 16 values plus the
 // partner lane l ^ 32, and the probabilities a lane holds are the B operand
@@ -50,6 +51,7 @@
 namespace pa {
 
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4v __attribute__((ext_vector_type(4)));
 
@@ -63,9 +65,15 @@ constexpr int kPrefillWaves = kPrefillThreads / 64;
 constexpr int kIdRing = 8;          // block-id slots (one per stage in flight)
 constexpr int kIdSlotBytes = 256;   // up to 64 table entries per stage
 
+template <typename T>
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
-                                                 __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
+  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
+                                                   __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a),
+                                                  __builtin_bit_cast(f16x8v, b), c, 0, 0, 0);
+  }
 }
 
 // ds_read_b64_tr_b16 at an LDS address (see the header comment).
@@ -104,8 +112,9 @@ __device__ __forceinline__ int chunk_swizzle(int r) {
   else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-template <int D, int G>
+template <typename T, int D, int G>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
+  static_assert(Elem<T>::kBytes == 2, "16-bit caches (bf16 or fp16)");
   constexpr int MTOK = kPrefillRows / G;  // query tokens per workgroup
   constexpr int KS = D / 16;              // MFMA k-steps of QK^T
   constexpr int DB = D / 32;              // 32-wide d blocks of the output
@@ -307,7 +316,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     uint4 ka[KS];
     read_k(0, ka);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s_cur = mfma32(ka[ks], qreg[ks], s_cur);
+    for (int ks = 0; ks < KS; ++ks) s_cur = mfma32<T>(ka[ks], qreg[ks], s_cur);
   }
   int off_cur = 0, off_next = kStageBytes, off_land = 2 * kStageBytes, off_copy = 3 * kStageBytes;
 
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       uint4 pb[2];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s_next = mfma32(ka[ks], qreg[ks], s_next);
+        s_next = mfma32<T>(ka[ks], qreg[ks], s_next);
         // two (D = 128) or four (D = 64) probabilities per QK step
 #pragma unroll
         for (int j = ks * 16 / KS; j < (ks + 1) * 16 / KS; ++j) {
@@ -370,16 +379,16 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         }
         if ((ks + 1) * 16 / KS % 8 == 0) {
           const int c = (ks + 1) * 16 / KS / 8 - 1;
-          pb[c].x = pack_bf16x2(s[8 * c + 0], s[8 * c + 1]);
-          pb[c].y = pack_bf16x2(s[8 * c + 2], s[8 * c + 3]);
-          pb[c].z = pack_bf16x2(s[8 * c + 4], s[8 * c + 5]);
-          pb[c].w = pack_bf16x2(s[8 * c + 6], s[8 * c + 7]);
+          pb[c].x = pack_half2<T>(s[8 * c + 0], s[8 * c + 1]);
+          pb[c].y = pack_half2<T>(s[8 * c + 2], s[8 * c + 3]);
+          pb[c].z = pack_half2<T>(s[8 * c + 4], s[8 * c + 5]);
+          pb[c].w = pack_half2<T>(s[8 * c + 6], s[8 * c + 7]);
         }
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] = mfma32(va[ks][db], pb[ks], acc[db]);
+        for (int db = 0; db < DB; ++db) acc[db] = mfma32<T>(va[ks][db], pb[ks], acc[db]);
       rsum = sum_halves(rsum);
       l += rsum;
     }  // t < ntiles
@@ -442,14 +451,14 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = db * 32 + 8 * q4 + 4 * half;
       uint2 w;
-      w.x = pack_bf16x2(acc[db][4 * q4 + 0] * inv, acc[db][4 * q4 + 1] * inv);
-      w.y = pack_bf16x2(acc[db][4 * q4 + 2] * inv, acc[db][4 * q4 + 3] * inv);
+      w.x = pack_half2<T>(acc[db][4 * q4 + 0] * inv, acc[db][4 * q4 + 1] * inv);
+      w.y = pack_half2<T>(acc[db][4 * q4 + 2] * inv, acc[db][4 * q4 + 3] * inv);
       *reinterpret_cast<uint2*>(orow + d) = w;
     }
 }
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
-  if (dtype != PA_DTYPE_BF16) return false;
+  if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
   if (head_dim != 64 && head_dim != 128) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
@@ -462,19 +471,19 @@ int prefill_tile_for(int group) {
   return group > 0 ? kPrefillRows / (group / decode_sub_groups(group)) : kPrefillRows;
 }
 
-template <int D>
+template <typename T, int D>
 static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items,
                                    hipStream_t s) {
   const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
   switch (group / a.sub_groups) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((prefill_kernel<D, 3>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((prefill_kernel<D, 5>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((prefill_kernel<D, 6>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((prefill_kernel<D, 7>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<T, D, 1>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<T, D, 2>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((prefill_kernel<T, D, 3>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<T, D, 4>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((prefill_kernel<T, D, 5>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((prefill_kernel<T, D, 6>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((prefill_kernel<T, D, 7>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((prefill_kernel<T, D, 8>), grid, dim3(kPrefillThreads), 0, s, a); break;
     default: return hipErrorNotSupported;
   }
   return hipGetLastError();
@@ -483,9 +492,13 @@ static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
-  if (dtype != PA_DTYPE_BF16) return hipErrorNotSupported;
-  if (head_dim == 128) return launch_prefill_d<128>(a, group, num_items, stream);
-  if (head_dim == 64) return launch_prefill_d<64>(a, group, num_items, stream);
+  if (dtype == PA_DTYPE_BF16) {
+    if (head_dim == 128) return launch_prefill_d<bf16_t, 128>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_d<bf16_t, 64>(a, group, num_items, stream);
+  } else if (dtype == PA_DTYPE_F16) {
+    if (head_dim == 128) return launch_prefill_d<f16_t, 128>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_d<f16_t, 64>(a, group, num_items, stream);
+  }
   return hipErrorNotSupported;
 }
 

@@ -118,8 +118,10 @@ def test_workgroups_per_item():
         # groups above 8: the fewest equal sub-groups of at most 8 heads
         (bf16, 128, 8, 128): 16, (bf16, 128, 4, 48): 8, (f32, 64, 2, 22): 22, (bf16, 128, 1, 64): 8,
         (bf16, 64, 2, 18): 6,
+        # fp16 pairs like bf16
+        (native.PA_DTYPE_F16, 64, 8, 8): 4, (native.PA_DTYPE_F16, 128, 2, 8): 1,
         # no tuned kernel (the generic one runs a workgroup per KV head's rows)
-        (native.PA_DTYPE_F16, 64, 8, 8): 8, (bf16, 96, 8, 8): 8, (bf16, 128, 1, 72): 1,
+        (bf16, 96, 8, 8): 8, (bf16, 128, 1, 72): 1,
         # rejected head counts
         (bf16, 64, 0, 8): 0, (bf16, 64, 8, 12): 0, (bf16, 64, 8, 0): 0,
     }

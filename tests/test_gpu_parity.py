@@ -275,7 +275,10 @@ def test_decode_fp32_matches_oracle(device):
     # heads of 128 with a group of 2
     (24, 8, 64, torch.bfloat16), (16, 8, 128, torch.bfloat16),
     # groups above 8 as sub-groups of at most 8 (16 = 2 x 8, 12 = 2 x 6, 11 = 11 x 1)
-    (32, 2, 128, torch.bfloat16), (24, 2, 64, torch.bfloat16), (11, 1, 64, torch.float32)])
+    (32, 2, 128, torch.bfloat16), (24, 2, 64, torch.bfloat16), (11, 1, 64, torch.float32),
+    # fp16 caches (the reference's LLM_DTYPE=fp16): unpaired, paired, sub-groups
+    (32, 8, 128, torch.float16), (40, 8, 128, torch.float16), (16, 8, 64, torch.float16),
+    (8, 8, 128, torch.float16), (32, 2, 128, torch.float16), (9, 3, 64, torch.float16)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
@@ -472,6 +475,17 @@ def test_device_strategy_copy_blocks(device):
                                      # groups above 8: sub-groups of 8 and of 6 query heads
                                      (32, 2, 128), (24, 2, 64)])
 def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
+    _prefill_case(device, hq, hkv, d, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64), (32, 2, 128)])
+def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
+    """fp16 caches run the same MFMA kernel with the f16 MFMA (the reference's
+    LLM_DTYPE=fp16, app/memory/strategies.py:14-33)."""
+    _prefill_case(device, hq, hkv, d, torch.float16)
+
+
+def _prefill_case(device, hq, hkv, d, dtype):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]
     rng = np.random.Generator(np.random.PCG64(hq + d))
@@ -482,10 +496,10 @@ def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
     for n in need:
         lists.append([int(x) for x in perm[off : off + n]])
         off += n
-    w = wl.StepWorkload("prefill_edges", hq, hkv, d, 16, torch.bfloat16, 1.0, starts, counts, lists, sum(need) + 3)
+    w = wl.StepWorkload("prefill_edges", hq, hkv, d, 16, dtype, 1.0, starts, counts, lists, sum(need) + 3)
     t = wl.make_tensors(w, device, seed=9)
     step = pack_workload(w, device)
-    log(f"prefill hq={hq} hkv={hkv} d={d} items={step.num_prefill_items} tile={step.prefill_tile}")
+    log(f"prefill {dtype} hq={hq} hkv={hkv} d={d} items={step.num_prefill_items} tile={step.prefill_tile}")
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
     check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
