@@ -693,6 +693,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 // global round trips are the entry and then the partials.  (With several
 // outputs per thread their round trips queued one behind the other: eight
 // heads of 128 at partition 2048 took 19 us.)
+constexpr int kMergeBatch = 8;  // partitions whose partials one round trip loads
+
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
   const int hkv = a.num_kv_heads;
@@ -716,31 +718,32 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
     const float* ml = a.part_ml + 2 * h;
     const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
     float mx = kScoreFloor, sum = 0.f, o = 0.f;
-    // Four partitions per round trip; slots past the last one read the
-    // first partition again and are given no weight.
-    for (int p = 0; p < nparts; p += 4) {
-      float mp[4], lp[4], xp[4];
+    // kMergeBatch partitions per round trip; slots past the last one read
+    // the first partition again and are given no weight.
+    for (int p = 0; p < nparts; p += kMergeBatch) {
+      float mp[kMergeBatch], lp[kMergeBatch], xp[kMergeBatch];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
         const int64_t it = item_of(p + u < nparts ? p + u : 0);
         mp[u] = ml[it * ml_stride];
         lp[u] = ml[it * ml_stride + 1];
         xp[u] = acc[it * stride];
       }
+      float mn = mx;
 #pragma unroll
-      for (int u = 1; u < 4; ++u) {
-        if (p + u >= nparts) {
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (u > 0 && p + u >= nparts) {
           mp[u] = kScoreFloor;
           lp[u] = 0.f;
           xp[u] = 0.f;
         }
+        mn = fmaxf(mn, mp[u]);
       }
-      const float mn = fmaxf(fmaxf(mx, mp[0]), fmaxf(fmaxf(mp[1], mp[2]), mp[3]));
       const float r = fast_exp2(mx - mn);
       sum *= r;
       o *= r;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
         const float w = fast_exp2(mp[u] - mn);
         sum = fmaf(lp[u], w, sum);
         o = fmaf(xp[u], w, o);

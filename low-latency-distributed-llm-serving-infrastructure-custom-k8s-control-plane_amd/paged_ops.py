@@ -210,25 +210,39 @@ def choose_partition(
     fastest partition of every measured shape: 4096 for 32/8 heads of 128,
     2048 for the same heads paired (three workgroups per CU), 1024 for 8/8.
 
-    A step too small for that rule at any size keeps 256, unless every
-    context fits one partition of at most 512 tokens: then that size is
-    taken, since skipping the merge launch saves more than the longer
-    workgroups cost.  Measured with graph replay on 8 fp32 MHA sequences of
-    16-512 tokens: 256 -> 24.9 us with merges, 512 -> 15.8 us without.
+    A step too small for that rule (a latency-bound step) takes the largest
+    partition that still gives two thirds of the slots a workgroup with at
+    most 64 partials per sequence, or, when none does, the smallest of 64,
+    128, ... that keeps every sequence to 64 partials: short walks per
+    workgroup, few partials to merge.
+    Measured with graph replay, 32/8 heads of 128 paired: 1 sequence of 1024
+    tokens 16.6 us at 256 -> 11.3 at 64; 16 of 4096 55.9 -> 50.7 at 512.
     """
     hkv = max(int(num_kv_heads), 1)
     group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
     per_cu = int(workgroups_per_cu or 0) or (5 if group == 1 else 4)
-    need = 3 * int(compute_units) * per_cu // 2
+    slots = int(compute_units) * per_cu
     width = max(int(workgroups_per_item or hkv), 1)  # workgroups per item
     ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
+
+    def workgroups(p: int) -> int:
+        return sum(-(-x // p) for x in ctx) * width
+
     p = PA_DECODE_MAX_PARTITION
     while p > 256:
-        if sum(-(-x // p) for x in ctx) * width >= need:
+        if workgroups(p) >= 3 * slots // 2:
             return p
         p //= 2
     longest = max(ctx, default=0)
-    return 512 if 256 < longest <= 512 else 256
+    p = PA_DECODE_MAX_PARTITION
+    while p >= 64:
+        if workgroups(p) >= 2 * slots // 3 and -(-longest // p) <= 64:
+            return p
+        p //= 2
+    p = 64
+    while p < PA_DECODE_MAX_PARTITION and -(-longest // p) > 64:
+        p *= 2
+    return p
 
 
 def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Tensor]:

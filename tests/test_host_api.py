@@ -299,16 +299,21 @@ def test_choose_partition_fills_the_chip():
     # the single-head kernel has more resident slots, so it splits more
     assert ops.choose_partition([3000] * 896, [1] * 896, 2, 2) == 2048
     assert ops.choose_partition([3000] * 896, [1] * 896, 2, 8) == 4096
-    # fewer sequences get smaller partitions, never below 256
+    # fewer sequences get smaller partitions
     assert ops.choose_partition([4095] * 32, [1] * 32, 8, 32) == 512
-    assert ops.choose_partition([3000] * 4, [1] * 4, 8, 32) == 256
+    # a latency-bound step: the largest partition still giving two thirds of
+    # the slots a workgroup (4 x 24 x 8 = 768 >= 682 at 128) ...
+    assert ops.choose_partition([3000] * 4, [1] * 4, 8, 32) == 128
+    # ... with at most 64 partials per sequence
+    assert ops.choose_partition([16383] * 4, [1] * 4, 8, 32) == 512
+    # ... else the smallest partition keeping a sequence to 64 partials
+    assert ops.choose_partition([3000], [1], 8, 32) == 64
+    assert ops.choose_partition([16383], [1], 8, 32) == 256
+    assert ops.choose_partition([15, 300, 511], [1, 1, 1], 8, 8) == 64
     # prefill rows do not count as decode work
-    assert ops.choose_partition([0, 3000], [500, 1], 8, 32) == 256
-    assert ops.choose_partition([], [], 8) == 256
-    # a small step whose contexts all fit 512 tokens skips the merge launch
-    assert ops.choose_partition([15, 300, 511], [1, 1, 1], 8, 8) == 512
-    assert ops.choose_partition([15, 300, 512], [1, 1, 1], 8, 8) == 256
-    assert ops.choose_partition([15, 200, 255], [1, 1, 1], 8, 8) == 256
+    assert ops.choose_partition([0, 3000], [500, 1], 8, 32) == 64
+    assert ops.choose_partition([0, 16383], [500, 1], 8, 32) == 256
+    assert ops.choose_partition([], [], 8) == 64
     # paired KV heads halve the launch width: the same step splits further
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, workgroups_per_item=4) == 2048
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, workgroups_per_item=4) == 2048
