@@ -339,10 +339,15 @@ def pack_step(
         raise ValueError("partition_size must be positive")
     t, c, ditems, mitems, pitems, ndec, npre = work_counts(
         start_positions, new_token_counts, partition_size, prefill_tile)
+    # Host lists go up from pinned buffers (torch's caching host allocator), so
+    # the copies are asynchronous: a pageable source would make the host wait
+    # for the stream to drain the previous step before the copy.
     if start_positions_dev is None:
-        start_positions_dev = torch.tensor(list(start_positions), dtype=torch.int64).to(device, non_blocking=True)
+        start_positions_dev = torch.tensor(list(start_positions), dtype=torch.int64,
+                                           pin_memory=True).to(device, non_blocking=True)
     if new_token_counts_dev is None:
-        new_token_counts_dev = torch.tensor(list(new_token_counts), dtype=torch.int64).to(device, non_blocking=True)
+        new_token_counts_dev = torch.tensor(list(new_token_counts), dtype=torch.int64,
+                                            pin_memory=True).to(device, non_blocking=True)
     step = PackedStep(
         block_tables=block_tables,
         start_positions=start_positions_dev,
