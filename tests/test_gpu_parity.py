@@ -379,6 +379,23 @@ def test_decode_occupancy_query(device):
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 1, 72) == 0
 
 
+def test_pack_step_partition_uses_the_kernel_queries(device):
+    """pack_step's automatic partition is choose_partition fed with the
+    library's launch-shape queries and the device's compute units."""
+    for hq, hkv, d, dtype in ((32, 8, 128, torch.bfloat16), (8, 8, 128, torch.float32),
+                              (128, 8, 128, torch.bfloat16), (16, 8, 64, torch.float16)):
+        w = wl.llama3_8b_gqa_decode(seed=0)
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                             num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+        want = ops.choose_partition(
+            w.start_positions, w.new_token_counts, hkv, hq,
+            ops.decode_workgroups_per_item(dtype, d, hkv, hq), ops.decode_workgroups_per_cu(dtype, d, hkv, hq),
+            torch.cuda.get_device_properties(device).multi_processor_count)
+        log(f"partition {hq}/{hkv}/{d} {dtype}: {step.partition_size}")
+        assert step.partition_size == want
+
+
 def test_decode_phases_equal_one_call(device):
     """Partition phase then merge phase (two launches) gives pa_decode's bits."""
     w = wl.llama3_8b_gqa_decode(seed=2)
