@@ -181,5 +181,8 @@ bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_s
 int prefill_tile_for(int group);
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream);
+// fp32 caches: the VALU kernel of prefill_f32.hip (same items and tile).
+hipError_t launch_prefill_f32(const PrefillArgs& a, int head_dim, int group, int64_t num_items,
+                              hipStream_t stream);
 
 }  // namespace pa

@@ -458,7 +458,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 }
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
-  if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
+  // bf16 / fp16: the MFMA kernel below; fp32: prefill_f32_kernel (VALU).
+  if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16 && dtype != PA_DTYPE_F32) return false;
   if (head_dim != 64 && head_dim != 128) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
@@ -492,6 +493,7 @@ static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
+  if (dtype == PA_DTYPE_F32) return launch_prefill_f32(a, head_dim, group, num_items, stream);
   if (dtype == PA_DTYPE_BF16) {
     if (head_dim == 128) return launch_prefill_d<bf16_t, 128>(a, group, num_items, stream);
     if (head_dim == 64) return launch_prefill_d<bf16_t, 64>(a, group, num_items, stream);

@@ -502,6 +502,12 @@ def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
     _prefill_case(device, hq, hkv, d, torch.float16)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 64), (32, 2, 128), (9, 3, 64)])
+def test_prefill_fp32_matches_oracle(device, hq, hkv, d):
+    """fp32 caches prefill on the VALU kernel (fp32 throughout), to 1e-4."""
+    _prefill_case(device, hq, hkv, d, torch.float32)
+
+
 def _prefill_case(device, hq, hkv, d, dtype):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]
@@ -519,7 +525,7 @@ def _prefill_case(device, hq, hkv, d, dtype):
     log(f"prefill {dtype} hq={hq} hkv={hkv} d={d} items={step.num_prefill_items} tile={step.prefill_tile}")
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
-    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=dtype == torch.float32)
 
 
 # ---------------------------------------------------------------------------
