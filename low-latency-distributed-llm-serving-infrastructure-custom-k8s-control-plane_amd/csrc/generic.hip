@@ -1,7 +1,8 @@
 // Generic paged attention: one wavefront per (query token, query head).
 //
-// Covers every shape the tuned kernels do not (any head_dim up to 256, any
-// GQA ratio, any block size, fp16) and implements the reference C ABI
+// Covers every shape the tuned kernels do not (head dims other than 64 and
+// 128 up to 256, groups above 64, block sizes that are not powers of two)
+// and implements the reference C ABI
 // (csrc/include/paged_kernels.h:22-34) over a flat gather list plus a dense
 // uint8 mask.  Semantics follow csrc/src/paged_kernels.cpp:30-104: masked
 // context tokens are skipped, a row with no attended token and an empty
