@@ -78,36 +78,36 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
-// Streaming K/V loads (read once, never reused by this kernel).
-template <typename V>
+// K/V loads.  NT: streaming (non-temporal) loads, for rows no other
+// workgroup reads; plain cached loads where sibling workgroups re-read them.
+template <typename V, bool NT>
 __device__ __forceinline__ V kv_load(const void* p);
 template <>
-__device__ __forceinline__ uint4 kv_load<uint4>(const void* p) {
-#if PA_DECODE_NT
+__device__ __forceinline__ uint4 kv_load<uint4, true>(const void* p) {
   const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *reinterpret_cast<const uint4*>(p);
-#endif
 }
 template <>
-__device__ __forceinline__ uint2 kv_load<uint2>(const void* p) {
-#if PA_DECODE_NT
+__device__ __forceinline__ uint2 kv_load<uint2, true>(const void* p) {
   const u32x2v v = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(p));
   return make_uint2(v.x, v.y);
-#else
-  return *reinterpret_cast<const uint2*>(p);
-#endif
 }
 template <>
-__device__ __forceinline__ uint32_t kv_load<uint32_t>(const void* p) {
-#if PA_DECODE_NT
+__device__ __forceinline__ uint32_t kv_load<uint32_t, true>(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-#else
-  return *reinterpret_cast<const uint32_t*>(p);
-#endif
 }
-
+template <>
+__device__ __forceinline__ uint4 kv_load<uint4, false>(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+template <>
+__device__ __forceinline__ uint2 kv_load<uint2, false>(const void* p) {
+  return *reinterpret_cast<const uint2*>(p);
+}
+template <>
+__device__ __forceinline__ uint32_t kv_load<uint32_t, false>(const void* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
 
 template <typename T, int D, int TILE>
 struct DecodeShape {
@@ -215,13 +215,16 @@ __device__ __forceinline__ float across_groups_max(float x) {
 //    reads 128-byte runs); each head dots its own piece, summed over L lanes.
 // PV layout: lanes [0, 32) hold the first half of the row, and each lane
 // accumulates only the G/2 heads of its half.
-template <typename T, int D, int G, bool PAIR>
+// SHARED: the workgroup is one of several sub-groups of a KV head's query
+// heads, whose siblings read the same K/V rows (cached loads).
+template <typename T, int D, int G, bool PAIR, bool SHARED>
 __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G / 2 : G), PAIR) void decode_partition_kernel(DecodeArgs a) {
   // Tiles of 16 tokens for wide groups and for paired rows of 512 bytes (the
   // same bytes per tile as 32 tokens of 256-byte rows).
   using S = DecodeShape<T, D, ((G > 4 || (PAIR && D * sizeof(T) > 256)) ? PA_DECODE_TILE_WIDE
                                                                           : PA_DECODE_TILE)>;
   using VR = typename VRaw<S::kPvBytes>::type;
+  constexpr bool kNt = PA_DECODE_NT && !SHARED;
   constexpr int L = S::kL;
   constexpr int GPW = S::kGpw;
   constexpr int TPG = S::kTpg;
@@ -251,11 +254,28 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int hkv = a.num_kv_heads;
   // Workgroup -> (item, KV head, sub-group of G of the head's a.group query
   // heads; one sub-group unless a.group exceeds the largest kernel group).
-  const int units = hkv * a.sub_groups;
-  const int64_t item = blockIdx.x / units;
-  const int unit = static_cast<int>(blockIdx.x - item * units);
-  const int kvh = unit / a.sub_groups;
-  const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
+  int64_t item;
+  int kvh, sg = 0;
+  if (a.sub_groups == 1) {
+    item = blockIdx.x / hkv;
+    kvh = static_cast<int>(blockIdx.x - item * hkv);
+  } else {
+    // Sibling sub-groups read the same K/V rows.  Workgroup ids are dealt to
+    // the XCDs round-robin, so siblings get ids that are equal modulo the XCD
+    // count and close together: the later reads hit that XCD's L2.  Runs of
+    // kXcds (item, KV head) units, each run repeated once per sub-group; the
+    // last run may be shorter.
+    const int64_t span = static_cast<int64_t>(kXcds) * a.sub_groups;
+    const int64_t run = blockIdx.x / span;
+    const int64_t base = run * kXcds;
+    const int width = static_cast<int>(min<int64_t>(kXcds, gridDim.x / a.sub_groups - base));
+    const int r = static_cast<int>(blockIdx.x - run * span);
+    sg = r / width;
+    const int64_t u = base + (r - sg * width);
+    item = u / hkv;
+    kvh = static_cast<int>(u - item * hkv);
+  }
+  const int h0 = kvh * a.group + sg * G;  // first query head
   const int seq = a.items[2 * item];
   const int part = a.items[2 * item + 1];
   const int ctx = a.context_lens[seq];
@@ -364,8 +384,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
           const int64_t slot0 =
               (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + GPW * i) & bs_mask);
           const T* row = kbase + slot0 * row_stride + koff;
-          kb[i][0] = kv_load<uint4>(row);
-          kb[i][1] = kv_load<uint4>(row + KP1 * CE);
+          kb[i][0] = kv_load<uint4, kNt>(row);
+          kb[i][1] = kv_load<uint4, kNt>(row + KP1 * CE);
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -377,8 +397,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         if (kok[i]) {
           const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
           const T* row = kbase + slot * row_stride;
-          kb[i][0] = kv_load<uint4>(row + kp0 * CE);
-          kb[i][1] = kv_load<uint4>(row + (kp0 + KP1) * CE);
+          kb[i][0] = kv_load<uint4, kNt>(row + kp0 * CE);
+          kb[i][1] = kv_load<uint4, kNt>(row + (kp0 + KP1) * CE);
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -407,14 +427,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
           if (full) {
 #pragma unroll
             for (int r = 0; r < kRun; ++r) {
-              vb[run * kRun + r] = kv_load<VR>(rowp);
+              vb[run * kRun + r] = kv_load<VR, kNt>(rowp);
               rowp += row_stride;
             }
           } else {
 #pragma unroll
             for (int r = 0; r < kRun; ++r) {
               const int u = run * kRun + r;
-              vb[u] = t0 + u < n ? kv_load<VR>(rowp) : VR{};
+              vb[u] = t0 + u < n ? kv_load<VR, kNt>(rowp) : VR{};
               rowp += row_stride;
             }
           }
@@ -437,7 +457,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         }
         if (b >= 0) {
           const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
-          vb[u] = kv_load<VR>(vbase + slot * row_stride + lp * PE);
+          vb[u] = kv_load<VR, kNt>(vbase + slot * row_stride + lp * PE);
         } else {
           vb[u] = VR{};
         }
@@ -764,12 +784,12 @@ struct LaunchOp {
   int64_t num_items;
   int phases;
   hipStream_t stream;
-  template <typename T, int D, int G, bool PAIR>
+  template <typename T, int D, int G, bool PAIR, bool SHARED>
   hipError_t run() const {
     const int64_t grid = num_items * a.num_kv_heads * a.sub_groups;
     const int64_t merge_grid = a.num_merge * a.num_kv_heads;
     if (phases & PA_DECODE_PHASE_PARTITIONS) {
-      hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR>), dim3(static_cast<uint32_t>(grid)),
+      hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR, SHARED>), dim3(static_cast<uint32_t>(grid)),
                          dim3(kDecodeThreads), 0, stream, a);
       const hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
@@ -789,40 +809,56 @@ struct LaunchOp {
 // Resident partition workgroups per CU of one kernel instance.
 struct OccupancyOp {
   int* per_cu;
-  template <typename T, int D, int G, bool PAIR>
+  template <typename T, int D, int G, bool PAIR, bool SHARED>
   hipError_t run() const {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_partition_kernel<T, D, G, PAIR>,
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_partition_kernel<T, D, G, PAIR, SHARED>,
                                                         kDecodeThreads, 0);
   }
 };
 
-template <typename T, int D, int G, bool PAIR, typename Op>
+template <typename T, int D, int G, bool PAIR, bool SHARED, typename Op>
 static hipError_t visit_one(const Op& op) {
   if constexpr (PAIR && G % 2 != 0) {
     return hipErrorNotSupported;  // a pair's group is even
   } else {
-    return op.template run<T, D, G, PAIR>();
+    return op.template run<T, D, G, PAIR, SHARED>();
   }
 }
 
-template <typename T, int D, bool PAIR, typename Op>
+template <typename T, int D, bool PAIR, bool SHARED = false, typename Op>
 static hipError_t visit_group(int G, const Op& op) {
   switch (G) {
-    case 1: return visit_one<T, D, 1, PAIR>(op);
-    case 2: return visit_one<T, D, 2, PAIR>(op);
-    case 3: return visit_one<T, D, 3, PAIR>(op);
-    case 4: return visit_one<T, D, 4, PAIR>(op);
-    case 5: return visit_one<T, D, 5, PAIR>(op);
-    case 6: return visit_one<T, D, 6, PAIR>(op);
-    case 7: return visit_one<T, D, 7, PAIR>(op);
-    case 8: return visit_one<T, D, 8, PAIR>(op);
+    case 1: return visit_one<T, D, 1, PAIR, SHARED>(op);
+    case 2: return visit_one<T, D, 2, PAIR, SHARED>(op);
+    case 3: return visit_one<T, D, 3, PAIR, SHARED>(op);
+    case 4: return visit_one<T, D, 4, PAIR, SHARED>(op);
+    case 5: return visit_one<T, D, 5, PAIR, SHARED>(op);
+    case 6: return visit_one<T, D, 6, PAIR, SHARED>(op);
+    case 7: return visit_one<T, D, 7, PAIR, SHARED>(op);
+    case 8: return visit_one<T, D, 8, PAIR, SHARED>(op);
     default: return hipErrorNotSupported;
   }
 }
 
+template <bool SHARED, typename Op>
+static hipError_t visit_unpaired(int dtype, int head_dim, int g, const Op& op) {
+  if (dtype == PA_DTYPE_BF16) {
+    if (head_dim == 128) return visit_group<bf16_t, 128, false, SHARED>(g, op);
+    if (head_dim == 64) return visit_group<bf16_t, 64, false, SHARED>(g, op);
+  } else if (dtype == PA_DTYPE_F16) {
+    if (head_dim == 128) return visit_group<f16_t, 128, false, SHARED>(g, op);
+    if (head_dim == 64) return visit_group<f16_t, 64, false, SHARED>(g, op);
+  } else if (dtype == PA_DTYPE_F32) {
+    if (head_dim == 128) return visit_group<float, 128, false, SHARED>(g, op);
+    if (head_dim == 64) return visit_group<float, 64, false, SHARED>(g, op);
+  }
+  return hipErrorNotSupported;
+}
+
 // The kernel instance of a real shape: paired heads of D run as the
 // instance of head dim 2D and group 2G; a group above the largest kernel
-// group runs as decode_sub_groups(group) workgroups per KV head.
+// group runs as decode_sub_groups(group) workgroups per KV head, on the
+// SHARED instances (cached K/V loads: the siblings' re-reads hit L2).
 template <typename Op>
 static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, const Op& op) {
   if (pair) {
@@ -837,18 +873,9 @@ static hipError_t visit_decode(int dtype, int head_dim, int group, bool pair, co
     return hipErrorNotSupported;
   }
   if (group < 1) return hipErrorNotSupported;
-  const int g = group / decode_sub_groups(group);
-  if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return visit_group<bf16_t, 128, false>(g, op);
-    if (head_dim == 64) return visit_group<bf16_t, 64, false>(g, op);
-  } else if (dtype == PA_DTYPE_F16) {
-    if (head_dim == 128) return visit_group<f16_t, 128, false>(g, op);
-    if (head_dim == 64) return visit_group<f16_t, 64, false>(g, op);
-  } else if (dtype == PA_DTYPE_F32) {
-    if (head_dim == 128) return visit_group<float, 128, false>(g, op);
-    if (head_dim == 64) return visit_group<float, 64, false>(g, op);
-  }
-  return hipErrorNotSupported;
+  const int nsub = decode_sub_groups(group);
+  return nsub > 1 ? visit_unpaired<true>(dtype, head_dim, group / nsub, op)
+                  : visit_unpaired<false>(dtype, head_dim, group, op);
 }
 
 // Largest real group run as pairs, per real head dim (bf16 and fp16; 0 = never).

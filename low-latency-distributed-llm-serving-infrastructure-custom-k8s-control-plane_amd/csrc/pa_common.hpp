@@ -18,6 +18,9 @@
 namespace pa {
 
 constexpr int kWave = 64;
+// XCDs of an MI355X: workgroup ids of one launch are dealt to them round-robin,
+// and each XCD has its own L2.
+constexpr int kXcds = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 // Finite floor used as the initial running maximum: exp2 of a masked score
 // (-inf) minus the floor is exactly 0 and no (-inf) - (-inf) NaN can appear.
