@@ -192,15 +192,17 @@ __device__ __forceinline__ float max_row_pairs(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Every step pairs lanes of equal (lane % L) only (rotations by multiples of
+// L within a row of 16, then the row and half swaps), so the lanes of one
+// row group may hold different values (the reduce-scatter score layout).
 template <int L>
 __device__ __forceinline__ float across_groups_max(float x) {
+  if constexpr (L <= 1) x = fmaxf(x, dpp<kDppRowRor1>(x));
+  if constexpr (L <= 2) x = fmaxf(x, dpp<kDppRowRor2>(x));
+  if constexpr (L <= 4) x = fmaxf(x, dpp<kDppRowRor4>(x));
   if constexpr (L <= 8) x = fmaxf(x, dpp<kDppRowRor8>(x));
   if constexpr (L <= 16) x = max_row_pairs(x);
-  x = max_halves(x);
-  if constexpr (L <= 4) x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
-  if constexpr (L <= 2) x = fmaxf(x, dpp<kDppQuadXor2>(x));
-  if constexpr (L <= 1) x = fmaxf(x, dpp<kDppQuadXor1>(x));
-  return x;
+  return max_halves(x);
 }
 
 // PAIR: two adjacent real KV heads of D/2 run as one head of D with the G
@@ -240,9 +242,13 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   constexpr int OUT_D = PAIR ? D / 2 : D;  // output elements per query head
   static_assert(!PAIR || (HALF && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
                 "pairs: 16-bit elements, an even head count, one V row per wave load");
+  // RS: reduce-scatter scores, for unpaired groups of more than half a row
+  // group of lanes (L of 4 or 8): lane lig of every row group ends with the
+  // scores of query head lig alone (see qk_softmax).
+  constexpr bool RS = !PAIR && (L == 4 || L == 8) && G > L / 2 && G <= L;
 
   __shared__ int s_blk[kMaxPartition + 2];
-  __shared__ uint4 s_q[G * D * S::kE / 16];
+  __shared__ uint4 s_q[(RS ? L : G) * D * S::kE / 16];
   __shared__ uint32_t s_p[kDecodeWaves][PWORDS];
   __shared__ float s_m[kDecodeWaves][G];
   __shared__ float s_l[kDecodeWaves][G];
@@ -307,7 +313,20 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int gi = lane / L;   // row group within the wave
   constexpr int QCHUNKS = G * D / CE;  // 16-byte pieces of the G query rows
   constexpr int HC = D / CE / 2;  // 16-byte pieces of a real head when paired
-  for (int i = tid; i < QCHUNKS; i += kDecodeThreads) {
+  if constexpr (RS) {
+    // Per (position p, lane l) of a row group, the two pieces (l and l + L)
+    // lane l dots at position p: those of query head p ^ l, zero past G.  A
+    // lane's reads for p = 0 .. L-1 are then one base address plus constants.
+    for (int i = tid; i < 2 * L * L; i += kDecodeThreads) {
+      const int piece = i & 1;
+      const int ln = (i >> 1) % L;
+      const int g = ((i >> 1) / L) ^ ln;
+      const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
+                      static_cast<int64_t>(h0 + min(g, G - 1)) * a.q_head_stride;
+      s_q[i] = g < G ? ld16(qrow + (ln + piece * L) * CE) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  for (int i = tid; i < (RS ? 0 : QCHUNKS); i += kDecodeThreads) {
     const int g = i / (D / CE);
     const int c = i - g * (D / CE);
     const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
@@ -356,6 +375,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   float lsum[NS];  // this lane's share of the softmax denominators of its NS heads
 #pragma unroll
   for (int j = 0; j < NS; ++j) lsum[j] = 0.f;
+  float ml = kScoreFloor;  // RS: running maximum of the lane's own head (lsum[0])
 
   uint4 kb[TPG][2];
   bool kok[TPG];
@@ -468,6 +488,88 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // Scores of the loaded K tile, online-softmax update, p -> LDS.
   // Scores stay unscaled (the max commutes with the positive scale); the
   // scale is applied inside the exponent: p = exp2(s * scale - max * scale).
+  //
+  // RS layout: position p of lane lig dots the query head p ^ lig, so after
+  // the L partial dots every lane holds one partial of each head.  Halving
+  // steps over the row group (lane partners lig ^ 7 or ^ 3 (mirror), ^ 2,
+  // ^ 1) each add the partner's partial of the head the lane keeps, and after
+  // log2(L) steps (L - 1 adds instead of L per head) lane lig holds the
+  // score of head lig.  The tile maximum is then one reduction over the row
+  // groups, and the lane computes, sums and stages its own head's
+  // exponentials with no selection among heads.
+  auto qk_softmax_rs = [&](bool full) {
+    float s[TPG];
+    {
+      float x[TPG][L];
+      const uint4* sq = s_q + 2 * lig;
+#pragma unroll
+      for (int p = 0; p < L; ++p) {
+        const uint4 qg[2] = {sq[2 * L * p], sq[2 * L * p + 1]};
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) x[i][p] = slice_dot<T>(qg, kb[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < TPG; ++i) {
+        if constexpr (L == 8) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[i][q] += dpp<kDppRowHalfMirror>(x[i][7 - q]);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) x[i][q] += dpp<kDppQuadXor2>(x[i][q ^ 2]);
+        x[i][0] += dpp<kDppQuadXor1>(x[i][1]);
+        s[i] = (full || kok[i]) ? x[i][0] : -INFINITY;
+      }
+    }
+    float tm = s[0];
+#pragma unroll
+    for (int i = 1; i < TPG; ++i) tm = fmaxf(tm, s[i]);
+    tm = across_groups_max<L>(tm);  // head lig's tile maximum, in every row group
+    // Head g's maximum is read from lane g (row group 0).
+    bool moved = false;
+    float m_new[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m_new[g] = fmaxf(m[g], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tm), g)));
+      moved |= m_new[g] != m[g];
+    }
+    const float ml_new = fmaxf(ml, tm);  // m_new[lig] for lig < G
+    if (moved) {  // wave-uniform
+      float alpha[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        alpha[g] = fast_exp2((m[g] - m_new[g]) * scale);
+        m[g] = m_new[g];
+      }
+      lsum[0] *= fast_exp2((ml - ml_new) * scale);
+#pragma unroll
+      for (int j = 0; j < GA; ++j)
+#pragma unroll
+        for (int e = 0; e < PE; ++e) acc[j][e] *= alpha[j];
+    }
+    ml = ml_new;
+    const float mc = -ml * scale;
+    uint32_t* sp = s_p[wave];
+    if (lig < G) {
+      if constexpr (HALF) {
+#pragma unroll
+        for (int k = 0; k < TPG / 2; ++k) {
+          const float pa = fast_exp2(fmaf(s[2 * k], scale, mc));
+          const float pb = fast_exp2(fmaf(s[2 * k + 1], scale, mc));
+          lsum[0] += pa + pb;
+          sp[(k * GPW + gi) * G + lig] = pack_half2<T>(pa, pb);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) {
+          const float pa = fast_exp2(fmaf(s[i], scale, mc));
+          lsum[0] += pa;
+          sp[(gi + GPW * i) * G + lig] = __float_as_uint(pa);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
   auto qk_softmax = [&](bool full) {
     float s[TPG][NS];
     float tmax[NS];
@@ -628,7 +730,11 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     const bool full = (tile + 1) * kTile <= n && __ballot(lane < kTile && blk_lane < 0) == 0;
     issue_k(tile, blk_lane);
     issue_v(tile, blk_lane, full);
-    qk_softmax(full);
+    if constexpr (RS) {
+      qk_softmax_rs(full);
+    } else {
+      qk_softmax(full);
+    }
     pv();
   }
 
@@ -637,7 +743,9 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   float ltot[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float l = SPLIT ? (khalf == g / GA ? lsum[g % NS] : 0.f) : lsum[g % NS];
+    float l = SPLIT ? (khalf == g / GA ? lsum[g % NS] : 0.f)
+              : RS  ? (lig == g ? lsum[0] : 0.f)
+                    : lsum[g % NS];
 #pragma unroll
     for (int o = kWave / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
     ltot[g] = l;

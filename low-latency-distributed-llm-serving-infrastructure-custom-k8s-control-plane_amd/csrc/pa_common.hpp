@@ -148,6 +148,9 @@ constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7-i within 8
 constexpr int kDppRowMirror = 0x140;      // lane i <- lane 15-i within 16
+constexpr int kDppRowRor1 = 0x121;        // lane i <- lane (i+1)%16 within 16
+constexpr int kDppRowRor2 = 0x122;        // lane i <- lane (i+2)%16 within 16
+constexpr int kDppRowRor4 = 0x124;        // lane i <- lane (i+4)%16 within 16
 constexpr int kDppRowRor8 = 0x128;        // lane i <- lane (i+8)%16 within 16
 
 template <int Ctrl>

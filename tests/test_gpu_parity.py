@@ -278,7 +278,10 @@ def test_decode_fp32_matches_oracle(device):
     (32, 2, 128, torch.bfloat16), (24, 2, 64, torch.bfloat16), (11, 1, 64, torch.float32),
     # fp16 caches (the reference's LLM_DTYPE=fp16): unpaired, paired, sub-groups
     (32, 8, 128, torch.float16), (40, 8, 128, torch.float16), (16, 8, 64, torch.float16),
-    (8, 8, 128, torch.float16), (32, 2, 128, torch.float16), (9, 3, 64, torch.float16)])
+    (8, 8, 128, torch.float16), (32, 2, 128, torch.float16), (9, 3, 64, torch.float16),
+    # reduce-scatter scores (unpaired groups of more than half a row group):
+    # rows of 4 lanes with groups of 3 and 4, rows of 8 with groups of 5-8
+    (12, 3, 64, torch.bfloat16), (21, 3, 128, torch.float16), (15, 3, 64, torch.float32)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
