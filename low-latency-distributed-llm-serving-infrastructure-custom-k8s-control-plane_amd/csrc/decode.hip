@@ -15,7 +15,9 @@
 //                 contiguously); a wave covers 64 / kL tokens per load.
 //                 Dots with the G query slices use v_dot2_f32_bf16 /
 //                 v_dot2_f32_f16 (16-bit types) and a DPP butterfly sums
-//                 each group.
+//                 each group; groups of more than half a row group use a
+//                 reduce-scatter instead, after which each lane holds one
+//                 head's scores (qk_softmax_rs).
 //  V (PV layout)  one wave load covers whole V rows (one 256-byte row for
 //                 bf16 D=128, 4 bytes per lane), so the row address of a
 //                 load is wave-uniform and is formed in scalar registers
