@@ -67,13 +67,14 @@ constexpr int kMaxPartition = PA_DECODE_MAX_PARTITION;
 #define PA_DECODE_MIN_WAVES_WIDE 2  // the same for wider groups or rows
 #endif
 #ifndef PA_DECODE_MIN_WAVES_PAIR512
-#define PA_DECODE_MIN_WAVES_PAIR512 3  // the same for paired rows of 512 bytes
+#define PA_DECODE_MIN_WAVES_PAIR512 3  // the same for 16-bit rows of 512 bytes (pairs, D 256)
 #endif
 // GA: query heads whose accumulators one lane holds (G, or G/2 when paired,
 // whose rows of up to 512 bytes come in half-length tiles).
 #define PA_DECODE_OCCUPANCY(T, D, GA, PAIR)                                                  \
   __attribute__((amdgpu_waves_per_eu(                                                        \
-      ((GA) <= 4 && (PAIR) && (D) * sizeof(T) > 256) ? PA_DECODE_MIN_WAVES_PAIR512           \
+      ((GA) <= 4 && ((PAIR) || sizeof(T) == 2) && (D) * sizeof(T) > 256)                     \
+          ? PA_DECODE_MIN_WAVES_PAIR512                                                      \
       : ((GA) <= 4 && ((D) * sizeof(T) <= 256 || (PAIR))) ? PA_DECODE_MIN_WAVES              \
                                                           : PA_DECODE_MIN_WAVES_WIDE)))
 
@@ -223,10 +224,12 @@ __device__ __forceinline__ float across_groups_max(float x) {
 // heads, whose siblings read the same K/V rows (cached loads).
 template <typename T, int D, int G, bool PAIR, bool SHARED>
 __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G / 2 : G), PAIR) void decode_partition_kernel(DecodeArgs a) {
-  // Tiles of 16 tokens for wide groups and for paired rows of 512 bytes (the
-  // same bytes per tile as 32 tokens of 256-byte rows).
-  using S = DecodeShape<T, D, ((G > 4 || (PAIR && D * sizeof(T) > 256)) ? PA_DECODE_TILE_WIDE
-                                                                          : PA_DECODE_TILE)>;
+  // Tiles of 16 tokens for wide groups and for 16-bit rows of 512 bytes
+  // (pairs of heads of 128, heads of 256: the same bytes per tile as 32
+  // tokens of 256-byte rows).
+  using S = DecodeShape<T, D,
+                        ((G > 4 || (Elem<T>::kBytes == 2 && D * sizeof(T) > 256)) ? PA_DECODE_TILE_WIDE
+                                                                                   : PA_DECODE_TILE)>;
   using VR = typename VRaw<S::kPvBytes>::type;
   constexpr bool kNt = PA_DECODE_NT && !SHARED;
   constexpr int L = S::kL;
@@ -955,9 +958,11 @@ static hipError_t visit_unpaired(int dtype, int head_dim, int g, const Op& op) {
   if (dtype == PA_DTYPE_BF16) {
     if (head_dim == 128) return visit_group<bf16_t, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<bf16_t, 64, false, SHARED>(g, op);
+    if (head_dim == 256) return visit_group<bf16_t, 256, false, SHARED>(g, op);
   } else if (dtype == PA_DTYPE_F16) {
     if (head_dim == 128) return visit_group<f16_t, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<f16_t, 64, false, SHARED>(g, op);
+    if (head_dim == 256) return visit_group<f16_t, 256, false, SHARED>(g, op);
   } else if (dtype == PA_DTYPE_F32) {
     if (head_dim == 128) return visit_group<float, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<float, 64, false, SHARED>(g, op);
@@ -1021,7 +1026,8 @@ int decode_sub_groups(int group) {
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition) {
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
-  if (head_dim != 64 && head_dim != 128) return false;
+  // Rows of up to 512 bytes: heads of 64 and 128, and of 256 in 16-bit types.
+  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PA_DTYPE_F32)) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;

@@ -281,7 +281,11 @@ def test_decode_fp32_matches_oracle(device):
     (8, 8, 128, torch.float16), (32, 2, 128, torch.float16), (9, 3, 64, torch.float16),
     # reduce-scatter scores (unpaired groups of more than half a row group):
     # rows of 4 lanes with groups of 3 and 4, rows of 8 with groups of 5-8
-    (12, 3, 64, torch.bfloat16), (21, 3, 128, torch.float16), (15, 3, 64, torch.float32)])
+    (12, 3, 64, torch.bfloat16), (21, 3, 128, torch.float16), (15, 3, 64, torch.float32),
+    # heads of 256 (Gemma's; 16-bit rows of 512 bytes): MHA, groups of 2 and 8,
+    # a group of 16 as two sub-groups; fp32 heads of 256 run the generic kernel
+    (4, 4, 256, torch.bfloat16), (16, 8, 256, torch.bfloat16), (16, 2, 256, torch.float16),
+    (32, 2, 256, torch.bfloat16), (4, 2, 256, torch.float32)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
