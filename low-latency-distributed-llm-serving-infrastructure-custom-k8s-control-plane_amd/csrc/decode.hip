@@ -248,12 +248,16 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   static_assert(!PAIR || (HALF && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
                 "pairs: 16-bit elements, an even head count, one V row per wave load");
   // RS: reduce-scatter scores, for unpaired groups of more than half a row
-  // group of lanes (L of 4 or 8): lane lig of every row group ends with the
-  // scores of query head lig alone (see qk_softmax).
-  constexpr bool RS = !PAIR && (L == 4 || L == 8) && G > L / 2 && G <= L;
+  // group of lanes (L of 4 or 8): NP score positions (G rounded up to a power
+  // of two, at least L), and lane lig of every row group ends with the
+  // scores of its HPL query heads lig*HPL .. lig*HPL + HPL-1 alone (see
+  // qk_softmax_rs).
+  constexpr bool RS = !PAIR && (L == 4 || L == 8) && G > L / 2;
+  constexpr int NP = !RS ? 1 : (G <= L ? L : 8);
+  constexpr int HPL = RS ? NP / L : 1;
 
   __shared__ int s_blk[kMaxPartition + 2];
-  __shared__ uint4 s_q[(RS ? L : G) * D * S::kE / 16];
+  __shared__ uint4 s_q[(RS ? NP : G) * D * S::kE / 16];
   __shared__ uint32_t s_p[kDecodeWaves][PWORDS];
   __shared__ float s_m[kDecodeWaves][G];
   __shared__ float s_l[kDecodeWaves][G];
@@ -320,12 +324,13 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   constexpr int HC = D / CE / 2;  // 16-byte pieces of a real head when paired
   if constexpr (RS) {
     // Per (position p, lane l) of a row group, the two pieces (l and l + L)
-    // lane l dots at position p: those of query head p ^ l, zero past G.  A
-    // lane's reads for p = 0 .. L-1 are then one base address plus constants.
-    for (int i = tid; i < 2 * L * L; i += kDecodeThreads) {
+    // lane l dots at position p: those of query head p ^ (l * HPL), zero past
+    // G.  A lane's reads for p = 0 .. NP-1 are then one base address plus
+    // constants.
+    for (int i = tid; i < 2 * L * NP; i += kDecodeThreads) {
       const int piece = i & 1;
       const int ln = (i >> 1) % L;
-      const int g = ((i >> 1) / L) ^ ln;
+      const int g = ((i >> 1) / L) ^ (ln * HPL);
       const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                       static_cast<int64_t>(h0 + min(g, G - 1)) * a.q_head_stride;
       s_q[i] = g < G ? ld16(qrow + (ln + piece * L) * CE) : make_uint4(0, 0, 0, 0);
@@ -380,7 +385,9 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   float lsum[NS];  // this lane's share of the softmax denominators of its NS heads
 #pragma unroll
   for (int j = 0; j < NS; ++j) lsum[j] = 0.f;
-  float ml = kScoreFloor;  // RS: running maximum of the lane's own head (lsum[0])
+  float ml[HPL];  // RS: running maxima of the lane's own heads (sums in lsum[0 .. HPL-1])
+#pragma unroll
+  for (int h = 0; h < HPL; ++h) ml[h] = kScoreFloor;
 
   uint4 kb[TPG][2];
   bool kok[TPG];
@@ -494,21 +501,24 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // Scores stay unscaled (the max commutes with the positive scale); the
   // scale is applied inside the exponent: p = exp2(s * scale - max * scale).
   //
-  // RS layout: position p of lane lig dots the query head p ^ lig, so after
-  // the L partial dots every lane holds one partial of each head.  Halving
-  // steps over the row group (lane partners lig ^ 7 or ^ 3 (mirror), ^ 2,
-  // ^ 1) each add the partner's partial of the head the lane keeps, and after
-  // log2(L) steps (L - 1 adds instead of L per head) lane lig holds the
-  // score of head lig.  The tile maximum is then one reduction over the row
-  // groups, and the lane computes, sums and stages its own head's
-  // exponentials with no selection among heads.
+  // RS layout: position p of lane lig dots the query head p ^ (lig * HPL),
+  // so after the NP partial dots every lane holds one partial of each head.
+  // Halving steps over the row group each add the partner lane's partial of
+  // the heads the lane keeps: partners lig ^ 7 (row half-mirror), ^ 2, ^ 1
+  // for rows of 8 lanes; lig ^ 2, ^ 1 for rows of 4.  The partner holds head
+  // h at position h ^ ((lig ^ c) * HPL), so for a kept position p it is
+  // p ^ (c * HPL), in the discarded half.  After the steps (NP - HPL adds
+  // instead of log2(L) per head) positions 0 .. HPL-1 of lane lig hold the
+  // scores of heads lig*HPL + h.  The tile maxima are then HPL reductions
+  // over the row groups, and the lane computes, sums and stages its own
+  // heads' exponentials with no selection among heads.
   auto qk_softmax_rs = [&](bool full) {
-    float s[TPG];
+    float s[TPG][HPL];
     {
-      float x[TPG][L];
+      float x[TPG][NP];
       const uint4* sq = s_q + 2 * lig;
 #pragma unroll
-      for (int p = 0; p < L; ++p) {
+      for (int p = 0; p < NP; ++p) {
         const uint4 qg[2] = {sq[2 * L * p], sq[2 * L * p + 1]};
 #pragma unroll
         for (int i = 0; i < TPG; ++i) x[i][p] = slice_dot<T>(qg, kb[i]);
@@ -517,27 +527,44 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       for (int i = 0; i < TPG; ++i) {
         if constexpr (L == 8) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) x[i][q] += dpp<kDppRowHalfMirror>(x[i][7 - q]);
+          for (int q = 0; q < 4; ++q) x[i][q] += dpp<kDppRowHalfMirror>(x[i][q ^ 7]);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) x[i][q] += dpp<kDppQuadXor2>(x[i][q ^ 2]);
+          x[i][0] += dpp<kDppQuadXor1>(x[i][1]);
+        } else if constexpr (NP == 4) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) x[i][q] += dpp<kDppQuadXor2>(x[i][q ^ 2]);
+          x[i][0] += dpp<kDppQuadXor1>(x[i][1]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[i][q] += dpp<kDppQuadXor2>(x[i][q ^ 4]);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) x[i][q] += dpp<kDppQuadXor1>(x[i][q ^ 2]);
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) x[i][q] += dpp<kDppQuadXor2>(x[i][q ^ 2]);
-        x[i][0] += dpp<kDppQuadXor1>(x[i][1]);
-        s[i] = (full || kok[i]) ? x[i][0] : -INFINITY;
+        for (int h = 0; h < HPL; ++h) s[i][h] = (full || kok[i]) ? x[i][h] : -INFINITY;
       }
     }
-    float tm = s[0];
+    // Head lig*HPL + h's tile maximum, in every row group; head g's is read
+    // from lane g / HPL (row group 0).
+    float tm[HPL];
 #pragma unroll
-    for (int i = 1; i < TPG; ++i) tm = fmaxf(tm, s[i]);
-    tm = across_groups_max<L>(tm);  // head lig's tile maximum, in every row group
-    // Head g's maximum is read from lane g (row group 0).
+    for (int h = 0; h < HPL; ++h) {
+      tm[h] = s[0][h];
+#pragma unroll
+      for (int i = 1; i < TPG; ++i) tm[h] = fmaxf(tm[h], s[i][h]);
+      tm[h] = across_groups_max<L>(tm[h]);
+    }
     bool moved = false;
     float m_new[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      m_new[g] = fmaxf(m[g], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tm), g)));
+      m_new[g] = fmaxf(m[g], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tm[g % HPL]), g / HPL)));
       moved |= m_new[g] != m[g];
     }
-    const float ml_new = fmaxf(ml, tm);  // m_new[lig] for lig < G
+    float ml_new[HPL];  // m_new of the lane's heads (those below G)
+#pragma unroll
+    for (int h = 0; h < HPL; ++h) ml_new[h] = fmaxf(ml[h], tm[h]);
     if (moved) {  // wave-uniform
       float alpha[G];
 #pragma unroll
@@ -545,30 +572,35 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         alpha[g] = fast_exp2((m[g] - m_new[g]) * scale);
         m[g] = m_new[g];
       }
-      lsum[0] *= fast_exp2((ml - ml_new) * scale);
+#pragma unroll
+      for (int h = 0; h < HPL; ++h) lsum[h] *= fast_exp2((ml[h] - ml_new[h]) * scale);
 #pragma unroll
       for (int j = 0; j < GA; ++j)
 #pragma unroll
         for (int e = 0; e < PE; ++e) acc[j][e] *= alpha[j];
     }
-    ml = ml_new;
-    const float mc = -ml * scale;
     uint32_t* sp = s_p[wave];
-    if (lig < G) {
-      if constexpr (HALF) {
 #pragma unroll
-        for (int k = 0; k < TPG / 2; ++k) {
-          const float pa = fast_exp2(fmaf(s[2 * k], scale, mc));
-          const float pb = fast_exp2(fmaf(s[2 * k + 1], scale, mc));
-          lsum[0] += pa + pb;
-          sp[(k * GPW + gi) * G + lig] = pack_half2<T>(pa, pb);
-        }
-      } else {
+    for (int h = 0; h < HPL; ++h) {
+      ml[h] = ml_new[h];
+      const float mc = -ml[h] * scale;
+      const int head = lig * HPL + h;
+      if (head < G) {
+        if constexpr (HALF) {
 #pragma unroll
-        for (int i = 0; i < TPG; ++i) {
-          const float pa = fast_exp2(fmaf(s[i], scale, mc));
-          lsum[0] += pa;
-          sp[(gi + GPW * i) * G + lig] = __float_as_uint(pa);
+          for (int k = 0; k < TPG / 2; ++k) {
+            const float pa = fast_exp2(fmaf(s[2 * k][h], scale, mc));
+            const float pb = fast_exp2(fmaf(s[2 * k + 1][h], scale, mc));
+            lsum[h] += pa + pb;
+            sp[(k * GPW + gi) * G + head] = pack_half2<T>(pa, pb);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < TPG; ++i) {
+            const float pa = fast_exp2(fmaf(s[i][h], scale, mc));
+            lsum[h] += pa;
+            sp[(gi + GPW * i) * G + head] = __float_as_uint(pa);
+          }
         }
       }
     }
@@ -749,7 +781,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float l = SPLIT ? (khalf == g / GA ? lsum[g % NS] : 0.f)
-              : RS  ? (lig == g ? lsum[0] : 0.f)
+              : RS  ? (lig == g / HPL ? lsum[g % HPL] : 0.f)
                     : lsum[g % NS];
 #pragma unroll
     for (int o = kWave / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
