@@ -222,7 +222,12 @@ __device__ __forceinline__ float across_groups_max(float x) {
 // accumulates only the G/2 heads of its half.
 // SHARED: the workgroup is one of several sub-groups of a KV head's query
 // heads, whose siblings read the same K/V rows (cached loads).
-template <typename T, int D, int G, bool PAIR, bool SHARED>
+// DM: the head dim in memory, when smaller than the lane layout's D (heads
+// of 80 and 96 on the layout of 128).  Lanes whose K pieces or V slice lie
+// past DM read the row's first piece or slice instead (always in bounds);
+// their q pieces are zero, so those K pieces add nothing to the scores, and
+// their accumulators are never stored.
+template <typename T, int D, int G, bool PAIR, bool SHARED, int DM>
 __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G / 2 : G), PAIR) void decode_partition_kernel(DecodeArgs a) {
   // Tiles of 16 tokens for wide groups and for 16-bit rows of 512 bytes
   // (pairs of heads of 128, heads of 256: the same bytes per tile as 32
@@ -231,7 +236,10 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
                         ((G > 4 || (Elem<T>::kBytes == 2 && D * sizeof(T) > 256)) ? PA_DECODE_TILE_WIDE
                                                                                    : PA_DECODE_TILE)>;
   using VR = typename VRaw<S::kPvBytes>::type;
-  constexpr bool kNt = PA_DECODE_NT && !SHARED;
+  // Nontemporal K/V loads, except where other workgroups re-read the same
+  // lines: sibling sub-groups (SHARED), and the rows of heads of 80 and 96,
+  // whose 128-byte lines straddle two KV heads.
+  constexpr bool kNt = PA_DECODE_NT && !SHARED && DM == D;
   constexpr int L = S::kL;
   constexpr int GPW = S::kGpw;
   constexpr int TPG = S::kTpg;
@@ -244,7 +252,12 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   constexpr int kTile = S::kTile;
   constexpr int PWORDS = HALF ? (kTile / 2) * G : kTile * G;
   constexpr int GA = PAIR ? G / 2 : G;    // heads a lane accumulates
-  constexpr int OUT_D = PAIR ? D / 2 : D;  // output elements per query head
+  constexpr int OUT_D = PAIR ? D / 2 : D;  // s_acc elements per query head
+  constexpr bool MASKD = DM < D;
+  constexpr int ODM = PAIR ? D / 2 : DM;  // output elements per query head in memory
+  constexpr int KPM = DM / S::kChunkElems;  // 16-byte pieces of a row in memory
+  static_assert(!MASKD || (!PAIR && DM % S::kChunkElems == 0 && KPM >= S::kL && DM % S::kPe == 0),
+                "masked head dims: unpaired, whole 16-byte pieces, at least one piece per lane");
   static_assert(!PAIR || (HALF && G % 2 == 0 && S::kR == 1 && S::kTpg >= 1),
                 "pairs: 16-bit elements, an even head count, one V row per wave load");
   // RS: reduce-scatter scores, for unpaired groups of more than half a row
@@ -299,9 +312,9 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int64_t qtok = a.cu_seqlens[seq];
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
-  const int64_t row_stride = static_cast<int64_t>(hkv) * D;
-  const T* kbase = reinterpret_cast<const T*>(a.key_cache) + kvh * D;
-  const T* vbase = reinterpret_cast<const T*>(a.value_cache) + kvh * D;
+  const int64_t row_stride = static_cast<int64_t>(hkv) * DM;
+  const T* kbase = reinterpret_cast<const T*>(a.key_cache) + kvh * DM;
+  const T* vbase = reinterpret_cast<const T*>(a.value_cache) + kvh * DM;
 
   // Block ids covering this partition -> LDS (invalid ids become -1).
   const int first_blk = p0 >> log2_bs;
@@ -333,7 +346,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       const int g = ((i >> 1) / L) ^ (ln * HPL);
       const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                       static_cast<int64_t>(h0 + min(g, G - 1)) * a.q_head_stride;
-      s_q[i] = g < G ? ld16(qrow + (ln + piece * L) * CE) : make_uint4(0, 0, 0, 0);
+      s_q[i] = (g < G && (!MASKD || ln + piece * L < KPM)) ? ld16(qrow + (ln + piece * L) * CE)
+                                                          : make_uint4(0, 0, 0, 0);
     }
   }
   for (int i = tid; i < (RS ? 0 : QCHUNKS); i += kDecodeThreads) {
@@ -346,7 +360,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       // elements go into that half of the row (the other half is never read).
       s_q[i] = (c / HC) == (g / GA) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
     } else {
-      s_q[i] = ld16(qrow + c * CE);
+      s_q[i] = (!MASKD || c < KPM) ? ld16(qrow + c * CE) : make_uint4(0, 0, 0, 0);
     }
   }
   __syncthreads();
@@ -400,6 +414,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // Per-lane element offset of its K slice within a wave load: row group gi
   // reads row gi of the load (GPW consecutive tokens).
   const int64_t koff = static_cast<int64_t>(gi) * row_stride + kp0 * CE;
+  // Second K piece of the lane (its first piece again past DM).
+  const int kp1 = (!MASKD || kp0 + KP1 < KPM) ? kp0 + KP1 : kp0;
   const bool k_uniform = log2_bs >= S::kLog2Gpw;  // a load's GPW tokens share a block
   auto issue_k = [&](int tile, int blk_lane) {
     const int t0 = tile * kTile;
@@ -417,7 +433,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
               (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + GPW * i) & bs_mask);
           const T* row = kbase + slot0 * row_stride + koff;
           kb[i][0] = kv_load<uint4, kNt>(row);
-          kb[i][1] = kv_load<uint4, kNt>(row + KP1 * CE);
+          kb[i][1] = kv_load<uint4, kNt>(row + (MASKD ? (kp1 - kp0) * CE : KP1 * CE));
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -430,7 +446,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
           const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
           const T* row = kbase + slot * row_stride;
           kb[i][0] = kv_load<uint4, kNt>(row + kp0 * CE);
-          kb[i][1] = kv_load<uint4, kNt>(row + (kp0 + KP1) * CE);
+          kb[i][1] = kv_load<uint4, kNt>(row + (MASKD ? kp1 : kp0 + KP1) * CE);
         } else {
           kb[i][0] = make_uint4(0, 0, 0, 0);
           kb[i][1] = make_uint4(0, 0, 0, 0);
@@ -446,6 +462,15 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // uninitialised cache contents).
   constexpr int kRun = 16;
   const bool v_runs = R == 1 && log2_bs >= 4;
+  // Element offset of the lane's V slice (formed at each use: a value kept
+  // across the loop costs registers).
+  auto v_slice = [&]() -> int {
+    if constexpr (MASKD) {
+      return lp * PE < DM ? lp * PE : 0;
+    } else {
+      return lp * PE;
+    }
+  };
   auto issue_v = [&](int tile, int blk_lane, bool full) {
     const int t0 = tile * kTile;
     if (v_runs) {
@@ -455,7 +480,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         if (b >= 0) {
           const int64_t slot0 =
               (static_cast<int64_t>(b) << log2_bs) | ((p0 + t0 + run * kRun) & bs_mask);
-          const T* rowp = vbase + slot0 * row_stride + lp * PE;
+          const T* rowp = vbase + slot0 * row_stride + v_slice();
           if (full) {
 #pragma unroll
             for (int r = 0; r < kRun; ++r) {
@@ -489,7 +514,7 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         }
         if (b >= 0) {
           const int64_t slot = (static_cast<int64_t>(b) << log2_bs) | ((p0 + t) & bs_mask);
-          vb[u] = kv_load<VR, kNt>(vbase + slot * row_stride + lp * PE);
+          vb[u] = kv_load<VR, kNt>(vbase + slot * row_stride + v_slice());
         } else {
           vb[u] = VR{};
         }
@@ -819,10 +844,11 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // those of both of its KV heads).
   const int hq = hkv * a.group;
   const int nparts = (ctx + a.partition - 1) / a.partition;
-  float* pacc = a.part_acc + (item * hq + h0) * OUT_D;
-  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + h0) * OUT_D;
-  for (int i = tid; i < G * OUT_D; i += kDecodeThreads) {
-    const int g = i / OUT_D;
+  float* pacc = a.part_acc + (item * hq + h0) * ODM;
+  T* out = reinterpret_cast<T*>(a.output) + (qtok * hq + h0) * ODM;
+  for (int i = tid; i < G * ODM; i += kDecodeThreads) {
+    const int g = i / ODM;
+    const int si = MASKD ? g * OUT_D + (i - g * ODM) : i;  // its s_acc element
     float mx = s_m[0][g];
 #pragma unroll
     for (int w = 1; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
@@ -830,14 +856,14 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 #pragma unroll
     for (int w = 0; w < kDecodeWaves; ++w) {
       const float f = fast_exp2(s_m[w][g] - mx);
-      o = fmaf(s_acc[w][i], f, o);
+      o = fmaf(s_acc[w][si], f, o);
       l = fmaf(s_l[w][g], f, l);
     }
     if (nparts <= 1) {
       store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
     } else {
       pacc[i] = o;
-      if (i % OUT_D == 0) {
+      if (i % ODM == 0) {
         float* pml = a.part_ml + (item * hq + h0 + g) * 2;
         pml[0] = mx;
         pml[1] = l;
@@ -929,12 +955,12 @@ struct LaunchOp {
   int64_t num_items;
   int phases;
   hipStream_t stream;
-  template <typename T, int D, int G, bool PAIR, bool SHARED>
+  template <typename T, int D, int G, bool PAIR, bool SHARED, int DM>
   hipError_t run() const {
     const int64_t grid = num_items * a.num_kv_heads * a.sub_groups;
     const int64_t merge_grid = a.num_merge * a.num_kv_heads;
     if (phases & PA_DECODE_PHASE_PARTITIONS) {
-      hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR, SHARED>), dim3(static_cast<uint32_t>(grid)),
+      hipLaunchKernelGGL((decode_partition_kernel<T, D, G, PAIR, SHARED, DM>), dim3(static_cast<uint32_t>(grid)),
                          dim3(kDecodeThreads), 0, stream, a);
       const hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
@@ -942,7 +968,7 @@ struct LaunchOp {
     if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
     // Partials are in the real layout: rows of D/2 when paired; all a.group
     // query heads of a KV head (or pair) merge in one workgroup row.
-    constexpr int kOutD = PAIR ? D / 2 : D;
+    constexpr int kOutD = PAIR ? D / 2 : DM;
     const int chunks = (a.group * kOutD + kDecodeThreads - 1) / kDecodeThreads;
     hipLaunchKernelGGL((decode_merge_kernel<T>),
                        dim3(static_cast<uint32_t>(merge_grid), static_cast<uint32_t>(chunks)),
@@ -954,33 +980,33 @@ struct LaunchOp {
 // Resident partition workgroups per CU of one kernel instance.
 struct OccupancyOp {
   int* per_cu;
-  template <typename T, int D, int G, bool PAIR, bool SHARED>
+  template <typename T, int D, int G, bool PAIR, bool SHARED, int DM>
   hipError_t run() const {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_partition_kernel<T, D, G, PAIR, SHARED>,
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_partition_kernel<T, D, G, PAIR, SHARED, DM>,
                                                         kDecodeThreads, 0);
   }
 };
 
-template <typename T, int D, int G, bool PAIR, bool SHARED, typename Op>
+template <typename T, int D, int G, bool PAIR, bool SHARED, int DM, typename Op>
 static hipError_t visit_one(const Op& op) {
   if constexpr (PAIR && G % 2 != 0) {
     return hipErrorNotSupported;  // a pair's group is even
   } else {
-    return op.template run<T, D, G, PAIR, SHARED>();
+    return op.template run<T, D, G, PAIR, SHARED, DM>();
   }
 }
 
-template <typename T, int D, bool PAIR, bool SHARED = false, typename Op>
+template <typename T, int D, bool PAIR, bool SHARED = false, int DM = D, typename Op>
 static hipError_t visit_group(int G, const Op& op) {
   switch (G) {
-    case 1: return visit_one<T, D, 1, PAIR, SHARED>(op);
-    case 2: return visit_one<T, D, 2, PAIR, SHARED>(op);
-    case 3: return visit_one<T, D, 3, PAIR, SHARED>(op);
-    case 4: return visit_one<T, D, 4, PAIR, SHARED>(op);
-    case 5: return visit_one<T, D, 5, PAIR, SHARED>(op);
-    case 6: return visit_one<T, D, 6, PAIR, SHARED>(op);
-    case 7: return visit_one<T, D, 7, PAIR, SHARED>(op);
-    case 8: return visit_one<T, D, 8, PAIR, SHARED>(op);
+    case 1: return visit_one<T, D, 1, PAIR, SHARED, DM>(op);
+    case 2: return visit_one<T, D, 2, PAIR, SHARED, DM>(op);
+    case 3: return visit_one<T, D, 3, PAIR, SHARED, DM>(op);
+    case 4: return visit_one<T, D, 4, PAIR, SHARED, DM>(op);
+    case 5: return visit_one<T, D, 5, PAIR, SHARED, DM>(op);
+    case 6: return visit_one<T, D, 6, PAIR, SHARED, DM>(op);
+    case 7: return visit_one<T, D, 7, PAIR, SHARED, DM>(op);
+    case 8: return visit_one<T, D, 8, PAIR, SHARED, DM>(op);
     default: return hipErrorNotSupported;
   }
 }
@@ -991,10 +1017,14 @@ static hipError_t visit_unpaired(int dtype, int head_dim, int g, const Op& op) {
     if (head_dim == 128) return visit_group<bf16_t, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<bf16_t, 64, false, SHARED>(g, op);
     if (head_dim == 256) return visit_group<bf16_t, 256, false, SHARED>(g, op);
+    if (head_dim == 96) return visit_group<bf16_t, 128, false, SHARED, 96>(g, op);
+    if (head_dim == 80) return visit_group<bf16_t, 128, false, SHARED, 80>(g, op);
   } else if (dtype == PA_DTYPE_F16) {
     if (head_dim == 128) return visit_group<f16_t, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<f16_t, 64, false, SHARED>(g, op);
     if (head_dim == 256) return visit_group<f16_t, 256, false, SHARED>(g, op);
+    if (head_dim == 96) return visit_group<f16_t, 128, false, SHARED, 96>(g, op);
+    if (head_dim == 80) return visit_group<f16_t, 128, false, SHARED, 80>(g, op);
   } else if (dtype == PA_DTYPE_F32) {
     if (head_dim == 128) return visit_group<float, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<float, 64, false, SHARED>(g, op);
@@ -1058,8 +1088,10 @@ int decode_sub_groups(int group) {
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
                                 int partition) {
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
-  // Rows of up to 512 bytes: heads of 64 and 128, and of 256 in 16-bit types.
-  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PA_DTYPE_F32)) return false;
+  // Rows of up to 512 bytes: heads of 64 and 128, and of 256 in 16-bit types;
+  // 16-bit heads of 80 and 96 on the lane layout of 128.
+  const bool wide16 = dtype != PA_DTYPE_F32 && (head_dim == 256 || head_dim == 96 || head_dim == 80);
+  if (head_dim != 64 && head_dim != 128 && !wide16) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;

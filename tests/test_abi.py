@@ -120,8 +120,10 @@ def test_workgroups_per_item():
         (bf16, 64, 2, 18): 6,
         # fp16 pairs like bf16
         (native.PA_DTYPE_F16, 64, 8, 8): 4, (native.PA_DTYPE_F16, 128, 2, 8): 1,
+        # heads of 96 and 256 are never paired
+        (bf16, 96, 8, 8): 8, (bf16, 256, 8, 16): 8,
         # no tuned kernel (the generic one runs a workgroup per KV head's rows)
-        (bf16, 96, 8, 8): 8, (bf16, 128, 1, 72): 1,
+        (bf16, 112, 8, 8): 8, (bf16, 128, 1, 72): 1,
         # rejected head counts
         (bf16, 64, 0, 8): 0, (bf16, 64, 8, 12): 0, (bf16, 64, 8, 0): 0,
     }

@@ -285,7 +285,12 @@ def test_decode_fp32_matches_oracle(device):
     # heads of 256 (Gemma's; 16-bit rows of 512 bytes): MHA, groups of 2 and 8,
     # a group of 16 as two sub-groups; fp32 heads of 256 run the generic kernel
     (4, 4, 256, torch.bfloat16), (16, 8, 256, torch.bfloat16), (16, 2, 256, torch.float16),
-    (32, 2, 256, torch.bfloat16), (4, 2, 256, torch.float32)])
+    (32, 2, 256, torch.bfloat16), (4, 2, 256, torch.float32),
+    # heads of 96 (Phi-3-mini) and 80 (Phi-2) on the lane layout of 128 with
+    # the pieces past the head masked: MHA, a group of 6 (reduce-scatter
+    # scores), fp16, and a group of 12 as two sub-groups
+    (8, 8, 96, torch.bfloat16), (24, 4, 96, torch.bfloat16), (8, 8, 80, torch.float16),
+    (12, 2, 80, torch.bfloat16), (24, 2, 96, torch.float16)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
@@ -382,7 +387,10 @@ def test_decode_occupancy_query(device):
                     f"{ops.decode_workgroups_per_item(dtype, d, 8, 8 * g)} workgroups per item")
                 assert 1 <= per_cu <= 8
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 2, 32) >= 1  # group 16: two sub-groups
-    assert ops.decode_workgroups_per_cu(torch.bfloat16, 96, 8, 8) == 0
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 256, 8, 16) >= 1  # heads of 256
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 96, 8, 8) >= 1  # masked heads of 96
+    assert ops.decode_workgroups_per_cu(torch.float32, 96, 8, 8) == 0  # fp32 96: generic kernel
+    assert ops.decode_workgroups_per_cu(torch.bfloat16, 112, 8, 8) == 0
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 1, 72) == 0
 
 
