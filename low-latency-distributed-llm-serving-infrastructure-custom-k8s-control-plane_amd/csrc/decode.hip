@@ -223,7 +223,7 @@ __device__ __forceinline__ float across_groups_max(float x) {
 // SHARED: the workgroup is one of several sub-groups of a KV head's query
 // heads, whose siblings read the same K/V rows (cached loads).
 // DM: the head dim in memory, when smaller than the lane layout's D (heads
-// of 80 and 96 on the layout of 128).  Lanes whose K pieces or V slice lie
+// of 80 and 96 on the layout of 128, in every dtype).  Lanes whose K pieces or V slice lie
 // past DM read the row's first piece or slice instead (always in bounds);
 // their q pieces are zero, so those K pieces add nothing to the scores, and
 // their accumulators are never stored.
@@ -1028,6 +1028,8 @@ static hipError_t visit_unpaired(int dtype, int head_dim, int g, const Op& op) {
   } else if (dtype == PA_DTYPE_F32) {
     if (head_dim == 128) return visit_group<float, 128, false, SHARED>(g, op);
     if (head_dim == 64) return visit_group<float, 64, false, SHARED>(g, op);
+    if (head_dim == 96) return visit_group<float, 128, false, SHARED, 96>(g, op);
+    if (head_dim == 80) return visit_group<float, 128, false, SHARED, 80>(g, op);
   }
   return hipErrorNotSupported;
 }
@@ -1089,9 +1091,9 @@ bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_si
                                 int partition) {
   if (dtype != PA_DTYPE_F32 && dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16) return false;
   // Rows of up to 512 bytes: heads of 64 and 128, and of 256 in 16-bit types;
-  // 16-bit heads of 80 and 96 on the lane layout of 128.
-  const bool wide16 = dtype != PA_DTYPE_F32 && (head_dim == 256 || head_dim == 96 || head_dim == 80);
-  if (head_dim != 64 && head_dim != 128 && !wide16) return false;
+  // heads of 80 and 96 on the lane layout of 128.
+  const bool wide16 = dtype != PA_DTYPE_F32 && head_dim == 256;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 80 && head_dim != 96 && !wide16) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (partition <= 0 || partition > kMaxPartition || partition % 32 != 0) return false;

@@ -290,7 +290,8 @@ def test_decode_fp32_matches_oracle(device):
     # the pieces past the head masked: MHA, a group of 6 (reduce-scatter
     # scores), fp16, and a group of 12 as two sub-groups
     (8, 8, 96, torch.bfloat16), (24, 4, 96, torch.bfloat16), (8, 8, 80, torch.float16),
-    (12, 2, 80, torch.bfloat16), (24, 2, 96, torch.float16)])
+    (12, 2, 80, torch.bfloat16), (24, 2, 96, torch.float16), (8, 8, 96, torch.float32),
+    (12, 2, 80, torch.float32)])
 def test_decode_shapes_and_long_contexts(device, hq, hkv, d, dtype):
     rng = np.random.Generator(np.random.PCG64(hq * 1000 + d))
     ctx = [1, 2, 15, 16, 17, 511, 512, 513, 1024, 3000, 9000]
@@ -389,7 +390,8 @@ def test_decode_occupancy_query(device):
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 2, 32) >= 1  # group 16: two sub-groups
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 256, 8, 16) >= 1  # heads of 256
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 96, 8, 8) >= 1  # masked heads of 96
-    assert ops.decode_workgroups_per_cu(torch.float32, 96, 8, 8) == 0  # fp32 96: generic kernel
+    assert ops.decode_workgroups_per_cu(torch.float32, 96, 8, 8) >= 1  # fp32 heads of 96
+    assert ops.decode_workgroups_per_cu(torch.float32, 256, 8, 8) == 0  # fp32 256: generic kernel
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 112, 8, 8) == 0
     assert ops.decode_workgroups_per_cu(torch.bfloat16, 128, 1, 72) == 0
 
