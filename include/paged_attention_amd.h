@@ -212,7 +212,8 @@ size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
  *    query heads: each token's rows of the two heads are read as one row of
  *    twice the length);
  *  - num_kv_heads x the sub-groups of a group of more than 8 query heads
- *    (the fewest equal sub-groups of at most 8; each re-reads the K/V);
+ *    (the fewest equal sub-groups of at most 8; each reads the K/V again,
+ *    ordered so that the re-reads of one KV head's rows meet one L2);
  *  - num_kv_heads otherwise; 0 for head counts pa_decode rejects.
  * A host choosing the split-K partition size from the launch width uses it.
  * (No counterpart in the reference, whose CPU kernel has no workgroups.) */
@@ -247,7 +248,11 @@ int32_t pa_decode_workgroups_per_cu(int32_t dtype, int32_t head_dim,
  * of decode sequence i is flat token cu_seqlens[i]; it attends positions
  * [0, context_lens[i]).  query: [T, H_q, D] through PaStepDims strides;
  * output: [T, H_q, D] contiguous, dtype of the caches; rows of tokens that
- * are not decode tokens are not written.
+ * are not decode tokens are not written.  Tuned kernels serve head_dim 64,
+ * 80, 96 and 128 (every dtype) and 256 (bf16, fp16) with groups of up to
+ * 64 query heads, power-of-two block sizes and partitions that are
+ * multiples of 32 up to 4096; other shapes run a generic kernel with the
+ * same results.
  */
 int pa_decode(const void *query, const void *key_cache,
               const void *value_cache, int32_t layer_idx, PaStepDims dims,
