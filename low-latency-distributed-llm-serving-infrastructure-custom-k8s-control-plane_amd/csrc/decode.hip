@@ -5,8 +5,13 @@
 // rows of both heads as one row of twice the length (see PAIR below).
 //
 // The workgroup (4 waves) serves the G = H_q / H_kv query heads that share
-// one KV head, so every K/V row of the partition is read from HBM once.
-// The partition is cut into 32-token tiles dealt round-robin to the waves;
+// one KV head, so every K/V row of the partition is read from HBM once
+// (groups above 8 run as sub-groups of at most 8 on SHARED instances, whose
+// re-reads are ordered to meet in one XCD's L2).  Heads of 64, 128 and 256
+// have their own instances; heads of 80 and 96 run those of 128 with the
+// pieces past the head masked (DM below).
+// The partition is cut into 32-token tiles (16 for groups above 4 and for
+// 512-byte rows) dealt round-robin to the waves;
 // each wave runs flash-style online softmax over its tiles with no
 // workgroup barrier inside the loop:
 //
