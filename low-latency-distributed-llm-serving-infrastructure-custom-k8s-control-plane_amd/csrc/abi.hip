@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <initializer_list>
+
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
 
@@ -56,6 +58,17 @@ int check_step(const PaStepDims& d, const char* who) {
     return fail(PA_ERR_INVALID_ARGUMENT, "%s: cache geometry must be positive", who);
   if (d.max_blocks_per_seq < 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "%s: negative block-table stride", who);
+  return PA_OK;
+}
+
+// PA_ERR_INVALID_ARGUMENT naming the first pointer of `list` that is NULL.
+struct Required {
+  const void* ptr;
+  const char* name;
+};
+int require(const char* who, std::initializer_list<Required> list) {
+  for (const Required& r : list)
+    if (r.ptr == nullptr) return fail(PA_ERR_INVALID_ARGUMENT, "%s: %s must not be NULL", who, r.name);
   return PA_OK;
 }
 
@@ -339,6 +352,11 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
   if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) *
           pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
+  rc = require("pa_decode", {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
+                              {output, "output"}, {block_tables, "block_tables"},
+                              {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
+                              {decode_items, "decode_items"}});
+  if (rc != PA_OK) return rc;
   if (num_merge_items < 0 || (num_merge_items > 0 && merge_items == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items is required when num_merge_items > 0");
   if (!aligned16(merge_items))
@@ -428,6 +446,11 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
     return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
                 dims.num_layers);
   if (num_prefill_items <= 0 || dims.num_seqs == 0) return PA_OK;
+  rc = require("pa_prefill", {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
+                               {output, "output"}, {block_tables, "block_tables"},
+                               {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
+                               {prefill_items, "prefill_items"}});
+  if (rc != PA_OK) return rc;
   if (num_prefill_items * static_cast<int64_t>(dims.num_kv_heads) *
           pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill: too many work items");

@@ -535,6 +535,24 @@ def _check_attention_inputs(q: torch.Tensor, key_cache: torch.Tensor, value_cach
         raise ValueError(f"query has {q.shape[0]} tokens, the step has {step.num_query_tokens}")
 
 
+def _output_for(q: torch.Tensor, key_cache: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+    """``out`` checked against what the kernels write ([T, H_q, D] contiguous rows
+    of the cache dtype on the query's device; a [1, T, H_q, D] tensor is taken
+    as the same rows), or a new such tensor when ``out`` is None."""
+    if out is None:
+        return torch.empty(q.shape, dtype=key_cache.dtype, device=q.device)
+    rows = out[0] if out.dim() == 4 and out.shape[0] == 1 else out
+    if tuple(rows.shape) != tuple(q.shape):
+        raise ValueError(f"out must have shape {tuple(q.shape)} (or (1, *that)), got {tuple(out.shape)}")
+    if out.dtype != key_cache.dtype:
+        raise ValueError(f"out dtype {out.dtype} differs from the cache dtype {key_cache.dtype}")
+    if out.device != q.device:
+        raise ValueError(f"out is on {out.device}, the query on {q.device}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    return rows
+
+
 def decode(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -554,8 +572,7 @@ def decode(
     q = _query_view(query)
     device = _require_device(q, key_cache, value_cache, step.block_tables)
     _check_attention_inputs(q, key_cache, value_cache, step)
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    out = _output_for(q, key_cache, out)
     dims = _step_dims(q, key_cache, step)
     ws = step.workspace(int(q.shape[1]), int(q.shape[2]), device)
     lib = _native.load_library()
@@ -596,8 +613,7 @@ def prefill(
     q = _query_view(query)
     device = _require_device(q, key_cache, value_cache, step.block_tables)
     _check_attention_inputs(q, key_cache, value_cache, step)
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    out = _output_for(q, key_cache, out)
     dims = _step_dims(q, key_cache, step)
     lib = _native.load_library()
     status = lib.pa_prefill(
@@ -631,9 +647,9 @@ def attention(
 ) -> torch.Tensor:
     """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D]."""
     q = _query_view(query)
-    device = _require_device(q)
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    _require_device(q, key_cache, value_cache)
+    _check_attention_inputs(q, key_cache, value_cache, step)
+    out = _output_for(q, key_cache, out)
     if step.num_prefill_items > 0:
         prefill(q, key_cache, value_cache, layer_idx, step, scaling, out=out)
     if step.num_decode_items > 0:

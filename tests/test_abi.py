@@ -78,6 +78,34 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == native.PA_ERR_INVALID_ARGUMENT
 
 
+DECODE_POINTERS = ["query", "key_cache", "value_cache", "output", "block_tables", "context_lens", "cu_seqlens",
+                   "decode_items"]
+
+
+@pytest.mark.parametrize("missing", DECODE_POINTERS)
+def test_decode_and_prefill_reject_null_pointers(missing):
+    """With work to do, every required device pointer is checked before any
+    launch: a NULL gives PA_ERR_INVALID_ARGUMENT and a message naming it."""
+    native = pkg("_native")
+    lib = native.load_library()
+    dims = native.PaStepDims(num_seqs=1, num_query_tokens=1, num_query_heads=8, num_kv_heads=4, head_dim=64,
+                             block_size=16, total_blocks=8, num_layers=1, max_blocks_per_seq=1,
+                             partition_size=512, dtype=native.PA_DTYPE_BF16, q_token_stride=512, q_head_stride=64)
+    fake = {name: 0x1000 * (i + 1) for i, name in enumerate(DECODE_POINTERS)}
+    fake[missing] = None
+    p = fake
+    rc = lib.pa_decode(p["query"], p["key_cache"], p["value_cache"], 0, dims, p["block_tables"],
+                       p["context_lens"], p["cu_seqlens"], p["decode_items"], 1, None, 0, 1.0, p["output"],
+                       None, 0, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_last_error_message() == f"pa_decode: {missing} must not be NULL".encode()
+    name = "prefill_items" if missing == "decode_items" else missing
+    rc = lib.pa_prefill(p["query"], p["key_cache"], p["value_cache"], 0, dims, p["block_tables"],
+                        p["context_lens"], p["cu_seqlens"], p["decode_items"], 1, 16, 1.0, p["output"], None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_last_error_message() == f"pa_prefill: {name} must not be NULL".encode()
+
+
 def test_reference_abi_latches_errors():
     native = pkg("_native")
     lib = native.load_library()

@@ -4,9 +4,9 @@ Integer work (packing, cache write) must be bit-exact.  Attention: fp32
 max-abs-err <= 1e-4 against the reference kernel; bf16 inputs against the
 reference kernel run on exact fp32 up-casts of the same values, with
 max|g - r| / max|r| <= 2e-2 and |g - r| <= 2e-2 |r| + 2e-2 rms(r)
-elementwise (helpers.bf16_close).  Full-size workloads are checked on a
-subset of sequences (the oracle runs per sequence on the CPU) plus
-size-independent properties on the whole batch.
+elementwise (helpers.bf16_close).  Full-size workloads are checked on every
+sequence (the oracle runs per sequence on the CPU) plus size-independent
+properties on the whole batch.
 """
 
 import sys
@@ -238,20 +238,20 @@ def test_block_table_path_matches_golden(device, name):
 # (c) decode at full size
 
 
-@pytest.mark.parametrize("seed,name,subset", [(3, "llama7b_mha_decode", [0, 1, 17, 33, 63]),
-                                              (4, "llama3_8b_gqa_decode", [0, 5, 100, 200, 255])])
-def test_decode_bf16_full_size(device, seed, name, subset):
+@pytest.mark.parametrize("seed,name", [(3, "llama7b_mha_decode"), (4, "llama3_8b_gqa_decode")])
+def test_decode_bf16_full_size(device, seed, name):
+    """Every sequence of the full-size workload (64 MHA and 256 GQA decodes)
+    against the oracle."""
     w = wl.WORKLOADS[name](seed=seed)
-    longest = int(np.argmax(w.context_lens))
-    shortest = int(np.argmin(w.context_lens))
-    seqs = sorted(set(subset + [longest, shortest]))
-    log(f"decode {name}: B={w.num_seqs} C={w.num_context_tokens} checking seqs {seqs}")
+    log(f"decode {name}: B={w.num_seqs} C={w.num_context_tokens} checking all {w.num_seqs} sequences")
     t = wl.make_tensors(w, device, seed=seed)
     step = pack_workload(w, device)
     out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    check_rows(w, out, oracle_rows(w, t, seqs), fp32=False)
+    rows = oracle_rows(w, t, range(w.num_seqs))
+    assert len(rows) == w.num_seqs
+    check_rows(w, out, rows, fp32=False)
 
 
 def test_decode_fp32_matches_oracle(device):
@@ -551,8 +551,8 @@ def _prefill_case(device, hq, hkv, d, dtype):
 
 def test_mixed_step_end_to_end(device):
     """4 x 512-token prefill chunks + 128 long-context decodes: pack, write the
-    step's K/V, attend -- all on the GPU -- then check the cache bytes and a
-    subset of rows against the oracle."""
+    step's K/V, attend -- all on the GPU -- then check the K and V cache bytes
+    and the output rows of all 132 sequences against the oracle."""
     w = wl.mixed_step(seed=5)
     t = wl.make_tensors(w, device, seed=5)
     step = pack_workload(w, device)
@@ -562,7 +562,10 @@ def test_mixed_step_end_to_end(device):
     slots = torch.from_numpy(op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size,
                                                    w.start_positions, w.new_token_counts)).to(device)
     got_k = t.key_cache[0].view(-1, w.num_kv_heads, w.head_dim)[slots]
+    got_v = t.value_cache[0].view(-1, w.num_kv_heads, w.head_dim)[slots]
     assert torch.equal(got_k.view(torch.int16), t.new_keys.view(torch.int16))
-    seqs = [0, 3, 4, 50, 131]
-    log(f"mixed step: checking rows of seqs {seqs}")
-    check_rows(w, out, oracle_rows(w, t, seqs), fp32=False)
+    assert torch.equal(got_v.view(torch.int16), t.new_values.view(torch.int16))
+    log(f"mixed step: checking rows of all {w.num_seqs} sequences")
+    rows = oracle_rows(w, t, range(w.num_seqs))
+    assert len(rows) == w.num_seqs and sum(c > 1 for c in w.new_token_counts) == 4
+    check_rows(w, out, rows, fp32=False)

@@ -325,3 +325,26 @@ def test_choose_partition_fills_the_chip():
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 32, 4, workgroups_per_cu=8) == 1024
     # a chip with fewer compute units fills at longer partitions
     assert ops.choose_partition([3000] * 256, [1] * 256, 8, 8, 4, compute_units=128) == 4096
+
+
+# ---- caller-supplied outputs ------------------------------------------------
+
+
+def test_output_checked_against_what_the_kernels_write():
+    """decode / prefill / attention write [T, H_q, D] contiguous rows of the
+    cache dtype: any other `out` is refused before a launch."""
+    q = torch.zeros(5, 4, 64, dtype=torch.bfloat16)
+    cache = torch.zeros(1, 2, 16, 2, 64, dtype=torch.bfloat16)
+    ok = torch.empty(5, 4, 64, dtype=torch.bfloat16)
+    assert ops._output_for(q, cache, ok) is ok
+    alias = torch.empty(1, 5, 4, 64, dtype=torch.bfloat16)
+    assert ops._output_for(q, cache, alias).data_ptr() == alias.data_ptr()
+    assert ops._output_for(q, cache, None).shape == (5, 4, 64)
+    with pytest.raises(ValueError, match="shape"):
+        ops._output_for(q, cache, torch.empty(4, 4, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="dtype"):
+        ops._output_for(q, cache, torch.empty(5, 4, 64, dtype=torch.float32))
+    with pytest.raises(ValueError, match="contiguous"):
+        ops._output_for(q, cache, torch.empty(4, 5, 64, dtype=torch.bfloat16).transpose(0, 1))
+    with pytest.raises(ValueError, match="is on"):
+        ops._output_for(q, cache, torch.empty(5, 4, 64, dtype=torch.bfloat16, device="meta"))
