@@ -5,7 +5,8 @@
  * `stream` is a hipStream_t passed as void* (NULL = the null stream).  No
  * entry point allocates, frees or synchronises: outputs and workspaces are
  * caller-owned, every launch is asynchronous on `stream`, and the library
- * keeps no device-side state between calls (reentrant).
+ * keeps no device-side state between calls (reentrant), apart from the
+ * scratch array of pa_decode_no_alloc (see there).
  *
  * Entry points returning int return 0 (PA_OK) on success or a PA_ERR_* code;
  * pa_error_string() turns a code into text and pa_last_error_message()
@@ -282,6 +283,35 @@ int pa_decode_phases(int32_t phases, const void *query, const void *key_cache,
                      int64_t num_decode_items, const int32_t *merge_items,
                      int64_t num_merge_items, float scaling, void *output,
                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Bytes of the file-scope device array behind pa_decode_no_alloc (64 MiB:
+ * the split-K partials of about 4000 decode work items of 32 query heads of
+ * 128; pa_decode_workspace_size gives the need of a step). */
+#define PA_DECODE_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * No counterpart in the reference: pa_decode for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * pa_decode without the workspace: the split-K partials go into a
+ * file-scope device array of PA_DECODE_SCRATCH_BYTES that each device the
+ * library runs on holds from its first use until the process ends.  The
+ * first call on a device (with that device current) looks up the array's
+ * address with hipGetSymbolAddress; no call allocates or frees anything.
+ * A step whose partials exceed the array (pa_decode_workspace_size) is
+ * rejected with PA_ERR_WORKSPACE and nothing is launched.  The array keeps
+ * the last call's contents and nothing in it needs to start at zero: the
+ * partition phase writes every partial the merge reads.  Every call on one
+ * device shares that device's array, so calls that overlap in time on one
+ * device (two streams, two threads) race; serialise them on one stream.
+ */
+int pa_decode_no_alloc(const void *query, const void *key_cache,
+                       const void *value_cache, int32_t layer_idx,
+                       PaStepDims dims, const int32_t *block_tables,
+                       const int32_t *context_lens, const int64_t *cu_seqlens,
+                       const int32_t *decode_items, int64_t num_decode_items,
+                       const int32_t *merge_items, int64_t num_merge_items,
+                       float scaling, void *output, void *stream);
 
 /* ---- (d) causal chunked prefill ----------------------------------------- */
 

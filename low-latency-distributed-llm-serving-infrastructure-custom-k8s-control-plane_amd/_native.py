@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -30,6 +30,7 @@ PA_DECODE_PARTITION = 2048
 PA_DECODE_MAX_PARTITION = 4096
 PA_DECODE_PHASE_PARTITIONS = 1
 PA_DECODE_PHASE_MERGE = 2
+PA_DECODE_SCRATCH_BYTES = 64 << 20
 
 #: Every symbol the header declares; tests check the library exports them all.
 EXPORTED_SYMBOLS = (
@@ -44,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "pa_prefill_tile",
     "pa_decode",
     "pa_decode_phases",
+    "pa_decode_no_alloc",
     "pa_prefill",
     "pa_error_string",
     "pa_last_error_message",
@@ -127,6 +129,10 @@ _SIGNATURES = {
     "pa_decode_phases": (
         ctypes.c_int,
         [_i32, _vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz, _vp],
+    ),
+    "pa_decode_no_alloc": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp],
     ),
     "pa_prefill": (
         ctypes.c_int,

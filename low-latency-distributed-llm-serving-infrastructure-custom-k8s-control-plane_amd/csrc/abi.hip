@@ -4,7 +4,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <initializer_list>
+#include <mutex>
 
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
@@ -80,9 +82,48 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 }  // namespace
 
+// Split-K partials of pa_decode_no_alloc: a file-scope array every device
+// the library runs on holds once, from the load of this code object until
+// the process ends.  In host code `scratch` is only a stand-in for the
+// symbol; kernels get the device address that hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[PA_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up with
+// hipGetSymbolAddress on the first call per device and kept.
+int scratch_address(void** out, const char* who) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PA_ERR_LAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(PA_ERR_UNSUPPORTED, "%s: device %d is beyond the %d the scratch table holds", who, dev,
+                kMaxScratchDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return fail(PA_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return PA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
-int pa_abi_version(void) { return 5; }
+int pa_abi_version(void) { return 6; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -333,17 +374,23 @@ int pa_decode(const void* query, const void* key_cache, const void* value_cache,
                           output, workspace, workspace_bytes, stream);
 }
 
-int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
-                     const void* value_cache, int32_t layer_idx, PaStepDims dims,
-                     const int32_t* block_tables, const int32_t* context_lens,
-                     const int64_t* cu_seqlens, const int32_t* decode_items,
-                     int64_t num_decode_items, const int32_t* merge_items,
-                     int64_t num_merge_items, float scaling, void* output, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// pa_decode_phases with the split-K partials in `workspace`, or, when
+// `use_scratch`, in this device's `scratch` array (workspace ignored).
+int decode_phases(const char* who, bool use_scratch, int32_t phases, const void* query,
+                  const void* key_cache, const void* value_cache, int32_t layer_idx,
+                  PaStepDims dims, const int32_t* block_tables, const int32_t* context_lens,
+                  const int64_t* cu_seqlens, const int32_t* decode_items,
+                  int64_t num_decode_items, const int32_t* merge_items, int64_t num_merge_items,
+                  float scaling, void* output, void* workspace, size_t workspace_bytes,
+                  void* stream) {
   if (phases <= 0 || (phases & ~(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE)) != 0)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: phases must be a non-empty mask of "
-                "PA_DECODE_PHASE_PARTITIONS and PA_DECODE_PHASE_MERGE, got %d", phases);
-  int rc = check_step(dims, "pa_decode");
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: phases must be a non-empty mask of "
+                "PA_DECODE_PHASE_PARTITIONS and PA_DECODE_PHASE_MERGE, got %d", who, phases);
+  int rc = check_step(dims, who);
   if (rc != PA_OK) return rc;
   if (layer_idx < 0 || layer_idx >= dims.num_layers)
     return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
@@ -351,16 +398,16 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
   if (num_decode_items <= 0 || dims.num_seqs == 0) return PA_OK;
   if (num_decode_items * static_cast<int64_t>(dims.num_kv_heads) *
           pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: too many work items");
-  rc = require("pa_decode", {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
-                              {output, "output"}, {block_tables, "block_tables"},
-                              {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
-                              {decode_items, "decode_items"}});
+    return fail(PA_ERR_UNSUPPORTED, "%s: too many work items", who);
+  rc = require(who, {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
+                    {output, "output"}, {block_tables, "block_tables"},
+                    {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
+                    {decode_items, "decode_items"}});
   if (rc != PA_OK) return rc;
   if (num_merge_items < 0 || (num_merge_items > 0 && merge_items == nullptr))
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items is required when num_merge_items > 0");
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: merge_items is required when num_merge_items > 0", who);
   if (!aligned16(merge_items))
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: merge_items must be 16-byte aligned");
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: merge_items must be 16-byte aligned", who);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = dims.num_query_heads / dims.num_kv_heads;
   const int eb = elem_bytes(dims.dtype);
@@ -373,8 +420,19 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
       (dims.q_token_stride * eb) % 16 == 0 && (dims.q_head_stride * eb) % 16 == 0;
   if (fast) {
     const size_t need = pa_decode_workspace_size(dims, num_decode_items);
+    if (use_scratch) {
+      if (need > PA_DECODE_SCRATCH_BYTES)
+        return fail(PA_ERR_WORKSPACE,
+                    "%s: %lld decode items need %zu bytes of split-K partials, more than the %zu "
+                    "bytes of scratch; use pa_decode with a workspace",
+                    who, static_cast<long long>(num_decode_items), need,
+                    static_cast<size_t>(PA_DECODE_SCRATCH_BYTES));
+      rc = scratch_address(&workspace, who);
+      if (rc != PA_OK) return rc;
+      workspace_bytes = PA_DECODE_SCRATCH_BYTES;
+    }
     if (workspace == nullptr || workspace_bytes < need)
-      return fail(PA_ERR_WORKSPACE, "pa_decode: workspace of %zu bytes needed, %zu given", need,
+      return fail(PA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need,
                   workspace_bytes);
     const DecodeWorkspaceLayout wl = decode_workspace_layout(dims, num_decode_items);
     pa::DecodeArgs a{};
@@ -403,11 +461,10 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
     a.group = pair ? 2 * group : group;
     a.sub_groups = pair ? 1 : pa::decode_sub_groups(group);
     return from_hip(
-        pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s),
-        "pa_decode");
+        pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s), who);
   }
   if (!pa::generic_supported(dims.dtype, dims.head_dim))
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: head_dim %d / dtype %d not supported",
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d / dtype %d not supported", who,
                 dims.head_dim, dims.dtype);
   // The generic kernel finishes every row in one pass: it is the partition
   // phase, and the merge phase has nothing to do.
@@ -432,7 +489,37 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
   a.num_kv_heads = dims.num_kv_heads;
   a.head_dim = dims.head_dim;
   a.scale_log2e = scaling * pa::kLog2e;
-  return from_hip(pa::launch_generic(a, dims.dtype, false, s), "pa_decode");
+  return from_hip(pa::launch_generic(a, dims.dtype, false, s), who);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
+                     const void* value_cache, int32_t layer_idx, PaStepDims dims,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const int64_t* cu_seqlens, const int32_t* decode_items,
+                     int64_t num_decode_items, const int32_t* merge_items,
+                     int64_t num_merge_items, float scaling, void* output, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  return decode_phases("pa_decode", false, phases, query, key_cache, value_cache, layer_idx, dims,
+                       block_tables, context_lens, cu_seqlens, decode_items, num_decode_items,
+                       merge_items, num_merge_items, scaling, output, workspace, workspace_bytes,
+                       stream);
+}
+
+int pa_decode_no_alloc(const void* query, const void* key_cache, const void* value_cache,
+                       int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
+                       const int32_t* context_lens, const int64_t* cu_seqlens,
+                       const int32_t* decode_items, int64_t num_decode_items,
+                       const int32_t* merge_items, int64_t num_merge_items, float scaling,
+                       void* output, void* stream) {
+  return decode_phases("pa_decode_no_alloc", true,
+                       PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE, query, key_cache,
+                       value_cache, layer_idx, dims, block_tables, context_lens, cu_seqlens,
+                       decode_items, num_decode_items, merge_items, num_merge_items, scaling,
+                       output, nullptr, 0, stream);
 }
 
 int pa_prefill(const void* query, const void* key_cache, const void* value_cache,
