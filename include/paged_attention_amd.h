@@ -118,7 +118,9 @@ typedef struct {
     int32_t max_blocks_per_seq; /* row stride of block_tables               */
     int32_t partition_size;     /* decode split-K partition, tokens         */
     int32_t prefill_tile;       /* query tokens per prefill work item       */
-    int32_t reserved;
+    int32_t num_table_rows;     /* rows of block_tables (0 = num_seqs)      */
+    int32_t num_updates;        /* (row, col, block) triples in `updates`   */
+    int32_t step_table_width;   /* columns of step_block_tables             */
     int64_t max_query_tokens;   /* capacity of scatter_slots / position_ids */
     int64_t max_context_tokens; /* capacity of gather_slots                 */
     int64_t max_decode_items;   /* capacity of decode_items (pairs)         */
@@ -126,22 +128,37 @@ typedef struct {
     int64_t max_prefill_items;  /* capacity of prefill_items (pairs)        */
 } PaPackDims;
 
+/* Bytes of workspace pa_pack needs for `num_seqs` sequences (a 512-byte
+ * header + 16 bytes per sequence).  No counterpart in the reference. */
+size_t pa_pack_workspace_size(int32_t num_seqs);
+
 /*
  * Replaces, on the GPU: _cumulative_offsets (app/model/paged_attention.py:
  * 121-125), PagedKVCacheManager.build_slot_mapping / _sequence_slots
  * (app/memory/manager.py:104-128, 301-333) for both the scatter slots and
- * the gather slots (paged_attention.py:64-69), and PagedStepContext.
- * position_ids (paged_attention.py:81-90).
+ * the gather slots (paged_attention.py:64-69), PagedStepContext.
+ * position_ids (paged_attention.py:81-90), and build_block_tables
+ * (manager.py:236-271) from a device-resident pool of table rows.
  *
- * Inputs: block_tables int32 [B, max_blocks_per_seq] (-1 padded, the layout
- * of manager.py:236-271), start_positions / new_token_counts int64 [B].
+ * block_tables: int32 [num_table_rows, max_blocks_per_seq], -1 padded.
+ * With rows == NULL it is the step's own table (row i = sequence i); with
+ * rows (int32 [B]) it is a pool of rows kept on the device across steps and
+ * sequence i reads row rows[i] (a row outside the pool reads as all -1).
+ * updates (int32 [num_updates, 3], may be NULL when num_updates is 0):
+ * (row, col, block id) entries written into block_tables before anything
+ * reads it (entries outside the table are skipped) -- how a host appends
+ * the blocks it allocated since the last step.
+ * start_positions / new_token_counts: int64 [B].
  * Outputs (all int64 unless noted, bit-exact with the reference):
+ *   step_block_tables int32 [B, step_table_width] (may be NULL): the rows
+ *   of the step's sequences, -1 past max_blocks_per_seq;
  *   cu_seqlens [B+1], cu_context_offsets [B+1], context_lens int32 [B],
  *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
  *   decode_items int32 pairs (seq, partition) for every sequence with one
  *   new token: all full partitions first (by sequence, then partition),
- *   then the partial last partitions from longest to shortest (ties by
- *   sequence), so short work ends the launch (may be NULL),
+ *   then the partial last partitions by decreasing length bucket (bucket =
+ *   (length - 1) * 64 / partition_size; ties by sequence), so short work
+ *   ends the launch (may be NULL),
  *   merge_items int32 [., 4]: (index in decode_items of the sequence's first
  *   full partition, number of full partitions, sequence, index of its
  *   partial partition or -1) for every single-token sequence whose context
@@ -151,14 +168,67 @@ typedef struct {
  *   than one new token (may be NULL).
  * Writes past a capacity in PaPackDims are dropped, never performed.
  * A block-table entry that is negative or past its row yields slot -1.
+ * workspace: pa_pack_workspace_size(B) bytes, 16-byte aligned; calls that
+ * share one must not overlap in time.  Two launches, each linear in B.
  */
-int pa_pack(const int32_t *block_tables, const int64_t *start_positions,
-            const int64_t *new_token_counts, PaPackDims dims,
-            int64_t *cu_seqlens, int64_t *cu_context_offsets,
-            int32_t *context_lens, int64_t *scatter_slots,
-            int64_t *position_ids, int64_t *gather_slots,
-            int32_t *decode_items, int32_t *merge_items,
-            int32_t *prefill_items, void *stream);
+int pa_pack(int32_t *block_tables, const int32_t *rows, const int32_t *updates,
+            const int64_t *start_positions, const int64_t *new_token_counts,
+            PaPackDims dims, int32_t *step_block_tables, int64_t *cu_seqlens,
+            int64_t *cu_context_offsets, int32_t *context_lens,
+            int64_t *scatter_slots, int64_t *position_ids,
+            int64_t *gather_slots, int32_t *decode_items,
+            int32_t *merge_items, int32_t *prefill_items, void *workspace,
+            size_t workspace_bytes, void *stream);
+
+/* ---- host-side step planning ------------------------------------------- */
+
+typedef struct {
+    int32_t block_size;          /* bs                                       */
+    int32_t prefill_tile;        /* query tokens per prefill work item       */
+    int32_t partition_size;      /* > 0: use it; 0: choose (see below)       */
+    int32_t num_kv_heads;        /* H_kv                                     */
+    int32_t num_query_heads;     /* H_q (0: 4 x H_kv)                        */
+    int32_t workgroups_per_item; /* decode launch width per item (0: H_kv)   */
+    int32_t workgroups_per_cu;   /* resident decode workgroups per CU (0:
+                                    5 for one query head per KV head, else 4) */
+    int32_t compute_units;       /* CUs of the device (0: 256)               */
+} PaPlanParams;
+
+typedef struct {
+    int64_t num_query_tokens;    /* T                                        */
+    int64_t num_context_tokens;  /* C                                        */
+    int64_t num_decode_items;    /* sizes of pa_pack's work lists            */
+    int64_t num_merge_items;
+    int64_t num_prefill_items;
+    int64_t max_context;         /* longest context of the step              */
+    int32_t num_decode_seqs;     /* sequences with one new token             */
+    int32_t num_prefill_seqs;    /* sequences with more than one             */
+    int32_t partition_size;      /* the split-K partition of the step        */
+    int32_t max_blocks;          /* max over sequences of ceil(ctx / bs)     */
+    int32_t bad_seq;             /* first sequence failing a check, or -1    */
+    int32_t reserved;
+} PaStepPlan;
+
+/*
+ * Host code, no GPU call: sizes a step from the HOST arrays of its start
+ * positions and new-token counts (int64 [num_seqs]) -- what pa_pack will
+ * emit, so buffers are sized without reading the device -- and chooses the
+ * decode split-K partition when params.partition_size is 0: the largest of
+ * 4096 ... 256 tokens whose decode launch (items x workgroups_per_item)
+ * gives every resident workgroup slot (compute_units x workgroups_per_cu)
+ * one and a half workgroups; failing that (a latency-bound step) the
+ * largest partition still giving two thirds of the slots a workgroup with
+ * at most 64 partials per sequence, else the smallest of 64, 128, ... that
+ * keeps every sequence to 64 partials.
+ * allocated_tokens (int64 [num_seqs], may be NULL): tokens each sequence has
+ * slots for; a sequence with start + count above it, or a negative start or
+ * count, fails the call with PA_ERR_INVALID_ARGUMENT and plan->bad_seq set
+ * (the checks of app/memory/manager.py:104-128, 301-315).
+ * No counterpart in the reference (whose step has no work lists).
+ */
+int pa_plan_step(const int64_t *start_positions, const int64_t *new_token_counts,
+                 const int64_t *allocated_tokens, int32_t num_seqs,
+                 PaPlanParams params, PaStepPlan *plan);
 
 /* ---- (b) K/V cache write ------------------------------------------------ */
 
@@ -200,6 +270,33 @@ int pa_copy_blocks(const void *src_cache, void *dst_cache,
                    int32_t num_layers, int64_t src_total_blocks,
                    int64_t dst_total_blocks, int64_t block_bytes,
                    void *stream);
+
+/* Directions of pa_swap_blocks. */
+enum { PA_SWAP_OUT = 0, PA_SWAP_IN = 1 };
+
+/*
+ * Replaces: the data movement behind PageAllocator::swap_out / swap_in
+ * (csrc/include/page_allocator.hpp:179-247), which only keeps the
+ * bookkeeping, and KVCacheMemoryStrategy.copy_blocks (app/memory/
+ * strategies.py:50-56, 117-122).  Copies blocks between a device cache
+ * (L, device_total_blocks, bs, H_kv, D) in HBM and a host pool of the same
+ * block shape (L, host_total_blocks, bs, H_kv, D) in pinned host memory
+ * (hipHostMalloc'd, e.g. a torch pin_memory tensor), every layer, in one
+ * launch: PA_SWAP_OUT copies device block -> host block for each (device
+ * block, host block) pair of block_mapping, PA_SWAP_IN host block -> device
+ * block for each (host block, device block) pair.  block_mapping: int64
+ * [num_pairs, 2] in device memory; pairs outside a cache are skipped.
+ * host_cache is a HOST pointer: the library maps it with
+ * hipHostGetDevicePointer and refuses memory that is not pinned host
+ * memory (PA_ERR_INVALID_ARGUMENT).  Call once for the keys and once for
+ * the values; the copy is asynchronous on `stream` (the host pool is only
+ * complete, or free to reuse, once the stream reaches that point).
+ */
+int pa_swap_blocks(void *device_cache, void *host_cache,
+                   const int64_t *block_mapping, int64_t num_pairs,
+                   int32_t num_layers, int64_t device_total_blocks,
+                   int64_t host_total_blocks, int64_t block_bytes,
+                   int32_t direction, void *stream);
 
 /* ---- (c) paged-attention decode (split-K) ------------------------------ */
 

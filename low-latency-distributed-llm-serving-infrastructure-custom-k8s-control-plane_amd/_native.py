@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -31,14 +31,19 @@ PA_DECODE_MAX_PARTITION = 4096
 PA_DECODE_PHASE_PARTITIONS = 1
 PA_DECODE_PHASE_MERGE = 2
 PA_DECODE_SCRATCH_BYTES = 64 << 20
+PA_SWAP_OUT = 0
+PA_SWAP_IN = 1
 
 #: Every symbol the header declares; tests check the library exports them all.
 EXPORTED_SYMBOLS = (
     "paged_attention",
     "pa_last_error",
+    "pa_pack_workspace_size",
     "pa_pack",
+    "pa_plan_step",
     "pa_reshape_and_cache",
     "pa_copy_blocks",
+    "pa_swap_blocks",
     "pa_decode_workspace_size",
     "pa_decode_workgroups_per_item",
     "pa_decode_workgroups_per_cu",
@@ -94,12 +99,44 @@ class PaPackDims(ctypes.Structure):
         ("max_blocks_per_seq", ctypes.c_int32),
         ("partition_size", ctypes.c_int32),
         ("prefill_tile", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("num_table_rows", ctypes.c_int32),
+        ("num_updates", ctypes.c_int32),
+        ("step_table_width", ctypes.c_int32),
         ("max_query_tokens", ctypes.c_int64),
         ("max_context_tokens", ctypes.c_int64),
         ("max_decode_items", ctypes.c_int64),
         ("max_merge_items", ctypes.c_int64),
         ("max_prefill_items", ctypes.c_int64),
+    ]
+
+
+class PaPlanParams(ctypes.Structure):
+    _fields_ = [
+        ("block_size", ctypes.c_int32),
+        ("prefill_tile", ctypes.c_int32),
+        ("partition_size", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("num_query_heads", ctypes.c_int32),
+        ("workgroups_per_item", ctypes.c_int32),
+        ("workgroups_per_cu", ctypes.c_int32),
+        ("compute_units", ctypes.c_int32),
+    ]
+
+
+class PaStepPlan(ctypes.Structure):
+    _fields_ = [
+        ("num_query_tokens", ctypes.c_int64),
+        ("num_context_tokens", ctypes.c_int64),
+        ("num_decode_items", ctypes.c_int64),
+        ("num_merge_items", ctypes.c_int64),
+        ("num_prefill_items", ctypes.c_int64),
+        ("max_context", ctypes.c_int64),
+        ("num_decode_seqs", ctypes.c_int32),
+        ("num_prefill_seqs", ctypes.c_int32),
+        ("partition_size", ctypes.c_int32),
+        ("max_blocks", ctypes.c_int32),
+        ("bad_seq", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -112,12 +149,18 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "paged_attention": (None, [_vp, _vp, _vp, _i32, PagedAttentionDims, _vp, _vp, _f32, _vp, _vp, _vp]),
     "pa_last_error": (ctypes.c_int, []),
-    "pa_pack": (ctypes.c_int, [_vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pa_pack_workspace_size": (_sz, [_i32]),
+    "pa_pack": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "pa_plan_step": (ctypes.c_int, [_vp, _vp, _vp, _i32, PaPlanParams, ctypes.POINTER(PaStepPlan)]),
     "pa_reshape_and_cache": (
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "pa_copy_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _vp]),
+    "pa_swap_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _vp]),
     "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
     "pa_decode_workgroups_per_item": (_i32, [_i32, _i32, _i32, _i32]),
     "pa_decode_workgroups_per_cu": (_i32, [_i32, _i32, _i32, _i32]),

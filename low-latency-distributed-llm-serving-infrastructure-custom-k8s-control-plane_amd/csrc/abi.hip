@@ -9,6 +9,7 @@
 #include <mutex>
 
 #include "pa_common.hpp"
+#include "pa_error.hpp"
 #include "pa_launch.hpp"
 
 namespace {
@@ -16,10 +17,15 @@ namespace {
 thread_local char g_msg[512] = "";
 thread_local int g_ref_abi_status = PA_OK;
 
-int fail(int code, const char* fmt, ...) {
+int vfail(int code, const char* fmt, va_list ap) {
+  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  return code;
+}
+
+__attribute__((format(printf, 2, 3))) int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  vfail(code, fmt, ap);
   va_end(ap);
   return code;
 }
@@ -82,6 +88,16 @@ const char* layer_base(const void* cache, const PaStepDims& d, int32_t layer_idx
 
 }  // namespace
 
+int pa::set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vfail(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+const char* pa::last_error_message() { return g_msg; }
+
 // Split-K partials of pa_decode_no_alloc: a file-scope array every device
 // the library runs on holds once, from the load of this code object until
 // the process ends.  In host code `scratch` is only a stand-in for the
@@ -109,9 +125,11 @@ int scratch_address(void** out, const char* who) {
     p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
     if (p == nullptr) {
       e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-      if (e != hipSuccess || p == nullptr)
+      if (e != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();  // leave no stale error for the next launch check
         return fail(PA_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
                     hipGetErrorString(e));
+      }
       g_scratch_ptr[dev].store(p, std::memory_order_release);
     }
   }
@@ -123,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 6; }
+int pa_abi_version(void) { return 7; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -188,30 +206,52 @@ void paged_attention(const float* query, const float* key_cache, const float* va
       pa::launch_generic(a, PA_DTYPE_F32, true, static_cast<hipStream_t>(stream)), "paged_attention");
 }
 
-int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
-            const int64_t* new_token_counts, PaPackDims dims, int64_t* cu_seqlens,
-            int64_t* cu_context_offsets, int32_t* context_lens, int64_t* scatter_slots,
-            int64_t* position_ids, int64_t* gather_slots, int32_t* decode_items,
-            int32_t* merge_items, int32_t* prefill_items, void* stream) {
+size_t pa_pack_workspace_size(int32_t num_seqs) { return pa::pack_workspace_size(num_seqs); }
+
+int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
+            const int64_t* start_positions, const int64_t* new_token_counts, PaPackDims dims,
+            int32_t* step_block_tables, int64_t* cu_seqlens, int64_t* cu_context_offsets,
+            int32_t* context_lens, int64_t* scatter_slots, int64_t* position_ids,
+            int64_t* gather_slots, int32_t* decode_items, int32_t* merge_items,
+            int32_t* prefill_items, void* workspace, size_t workspace_bytes, void* stream) {
   if (dims.num_seqs < 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative num_seqs");
   if (dims.block_size <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: block_size must be positive");
-  if (dims.max_blocks_per_seq < 0)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative block-table stride");
+  if (dims.max_blocks_per_seq < 0 || dims.num_table_rows < 0 || dims.num_updates < 0 ||
+      dims.step_table_width < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative table geometry or update count");
   if (dims.partition_size <= 0 || dims.prefill_tile <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: partition and prefill tile must be positive");
   if (cu_seqlens == nullptr || cu_context_offsets == nullptr)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: cu_seqlens and cu_context_offsets are required");
-  if (dims.num_seqs > 0 &&
-      (start_positions == nullptr || new_token_counts == nullptr || context_lens == nullptr ||
-       scatter_slots == nullptr || position_ids == nullptr ||
-       (block_tables == nullptr && dims.max_blocks_per_seq > 0)))
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: missing input or output buffer");
+  const int32_t table_rows = rows != nullptr ? dims.num_table_rows : dims.num_seqs;
+  if (dims.num_seqs > 0) {
+    int rc = require("pa_pack", {{start_positions, "start_positions"},
+                                 {new_token_counts, "new_token_counts"},
+                                 {context_lens, "context_lens"},
+                                 {scatter_slots, "scatter_slots"},
+                                 {position_ids, "position_ids"}});
+    if (rc != PA_OK) return rc;
+  }
+  if (block_tables == nullptr && dims.max_blocks_per_seq > 0 && table_rows > 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: block_tables must not be NULL");
+  if (dims.num_updates > 0 && (updates == nullptr || block_tables == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: %d updates given without updates or block_tables",
+                dims.num_updates);
+  if (step_block_tables != nullptr && dims.step_table_width == 0 && dims.num_seqs > 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: step_block_tables given with step_table_width 0");
   if (!aligned16(merge_items))
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: merge_items must be 16-byte aligned");
+  const size_t need = pa::pack_workspace_size(dims.num_seqs);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(PA_ERR_WORKSPACE, "pa_pack: a 16-byte aligned workspace of %zu bytes is needed, %zu given",
+                need, workspace == nullptr ? size_t(0) : workspace_bytes);
   pa::PackArgs a{};
   a.block_tables = block_tables;
+  a.rows = rows;
+  a.updates = updates;
   a.start_positions = start_positions;
   a.new_token_counts = new_token_counts;
+  a.step_block_tables = step_block_tables;
   a.cu_seqlens = cu_seqlens;
   a.cu_context_offsets = cu_context_offsets;
   a.context_lens = context_lens;
@@ -221,7 +261,12 @@ int pa_pack(const int32_t* block_tables, const int64_t* start_positions,
   a.decode_items = decode_items;
   a.merge_items = merge_items;
   a.prefill_items = prefill_items;
+  a.ws_header = reinterpret_cast<int32_t*>(workspace);
+  a.ws_seq = reinterpret_cast<int4*>(reinterpret_cast<char*>(workspace) + pa::kPackHeaderBytes);
   a.num_seqs = dims.num_seqs;
+  a.num_table_rows = block_tables != nullptr ? table_rows : 0;
+  a.num_updates = dims.num_updates;
+  a.step_table_width = step_block_tables != nullptr ? dims.step_table_width : 0;
   a.block_size = dims.block_size;
   a.block_table_stride = dims.max_blocks_per_seq;
   a.partition = dims.partition_size;
@@ -296,6 +341,33 @@ int pa_copy_blocks(const void* src_cache, void* dst_cache, const int64_t* block_
   const bool vec16 = block_bytes % 16 == 0 && aligned16(src_cache) && aligned16(dst_cache);
   return from_hip(pa::launch_copy_blocks(a, vec16, static_cast<hipStream_t>(stream)),
                   "pa_copy_blocks");
+}
+
+int pa_swap_blocks(void* device_cache, void* host_cache, const int64_t* block_mapping,
+                   int64_t num_pairs, int32_t num_layers, int64_t device_total_blocks,
+                   int64_t host_total_blocks, int64_t block_bytes, int32_t direction,
+                   void* stream) {
+  if (direction != PA_SWAP_OUT && direction != PA_SWAP_IN)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_swap_blocks: direction must be PA_SWAP_OUT or PA_SWAP_IN, got %d",
+                direction);
+  if (num_pairs < 0 || num_layers < 0 || device_total_blocks < 0 || host_total_blocks < 0 ||
+      block_bytes < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_swap_blocks: negative size");
+  if (num_pairs == 0 || num_layers == 0 || block_bytes == 0) return PA_OK;
+  int rc = require("pa_swap_blocks", {{device_cache, "device_cache"}, {host_cache, "host_cache"},
+                                      {block_mapping, "block_mapping"}});
+  if (rc != PA_OK) return rc;
+  void* host_view = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&host_view, host_cache, 0);
+  if (e != hipSuccess || host_view == nullptr) {
+    (void)hipGetLastError();  // leave no stale error for the next launch check
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_swap_blocks: host_cache is not pinned host memory (%s)",
+                hipGetErrorString(e));
+  }
+  const bool out = direction == PA_SWAP_OUT;
+  return pa_copy_blocks(out ? device_cache : host_view, out ? host_view : device_cache, block_mapping,
+                        num_pairs, num_layers, out ? device_total_blocks : host_total_blocks,
+                        out ? host_total_blocks : device_total_blocks, block_bytes, stream);
 }
 
 namespace {

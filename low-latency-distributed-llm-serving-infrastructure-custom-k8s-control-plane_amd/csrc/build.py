@@ -24,7 +24,7 @@ LIBRARY_NAME = "libpaged_attention_amd.so"
 LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "pack.hip", "cache_write.hip", "decode.hip", "generic.hip", "prefill.hip",
+SOURCES = ["abi.hip", "plan.cpp", "pack.hip", "cache_write.hip", "decode.hip", "generic.hip", "prefill.hip",
            "prefill_f32.hip", "copy_blocks.hip"]
 
 HIP_FLAGS = [

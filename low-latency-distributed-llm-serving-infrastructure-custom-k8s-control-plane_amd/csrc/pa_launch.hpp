@@ -73,10 +73,18 @@ struct GenericArgs {
   float scale_log2e;
 };
 
+// Packing of one step (pack.hip): two launches, a one-workgroup scan and a
+// per-sequence fill, sharing a small workspace.
+constexpr int kPackBuckets = 64;          // length buckets of the partial partitions
+constexpr size_t kPackHeaderBytes = 512;  // workspace header: full count + bucket bases
+
 struct PackArgs {
-  const int32_t* block_tables;
+  int32_t* block_tables;          // the step's table, or a pool of rows
+  const int32_t* rows;            // row of each sequence in block_tables, or null (row = seq)
+  const int32_t* updates;         // (row, col, block) triples applied first
   const int64_t* start_positions;
   const int64_t* new_token_counts;
+  int32_t* step_block_tables;     // [B, step_table_width] copy of the rows, or null
   int64_t* cu_seqlens;
   int64_t* cu_context_offsets;
   int32_t* context_lens;
@@ -86,7 +94,12 @@ struct PackArgs {
   int32_t* decode_items;
   int32_t* merge_items;
   int32_t* prefill_items;
+  int32_t* ws_header;             // [0] full partitions, [1 + b] base of bucket b
+  int4* ws_seq;                   // per sequence: full, merge and prefill offsets, partial rank
   int32_t num_seqs;
+  int32_t num_table_rows;
+  int32_t num_updates;
+  int32_t step_table_width;
   int32_t block_size;
   int32_t block_table_stride;
   int32_t partition;
@@ -172,6 +185,7 @@ hipError_t decode_workgroups_per_cu(int dtype, int head_dim, int group, bool pai
 bool generic_supported(int dtype, int head_dim);
 hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStream_t stream);
 
+size_t pack_workspace_size(int64_t num_seqs);
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
 hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t stream);

@@ -1,31 +1,37 @@
-"""PagedKVCacheManager: the paged KV pool and its slot bookkeeping.
+"""PagedKVCacheManager: the paged KV pool, its block tables and slot mapping.
 
-Same constructor, attributes, methods and error messages as the reference's
-app/memory/manager.py:12-333, so the engine and the reference's tests drive
-it unchanged.  On a ROCm device the caches live in HBM
-(memory/strategies.py) and the per-step integer and copy work runs in the
-HIP kernels:
+Same constructor, attributes, method names and error messages as the
+reference's manager (app/memory/manager.py:12-333), so an engine and the
+reference's tests drive it unchanged.  Its organisation is the MI355X
+path's own:
 
-  * build_slot_mapping    -> pa_pack (GPU), after the same host-side checks
-  * scatter_layer_kv      -> pa_reshape_and_cache (GPU)
-  * build_block_tables    -> host table, one non-blocking upload
-
-On a CPU store the reference's torch code path is kept as is (it is the
-reference's own CPU behaviour, not a fallback of the GPU path: a GPU store
-never takes it).
+  * every sequence's block list is also a row of one :class:`BlockTablePool`
+    (memory/block_allocator.py), mirrored in HBM on a GPU store; a step
+    uploads only the entries allocated since the last step and the packing
+    kernel gathers the step's block table on the device (:meth:`pack_step`);
+  * on a GPU store the slot mapping, positions and work lists come from the
+    packing kernel (pa_pack) and K/V writes from pa_reshape_and_cache; the
+    host checks a step once, vectorised, from the pool's token counts;
+  * on a CPU store (the reference's CPU path) the same slot formula runs
+    vectorised in NumPy over the pool's host rows;
+  * preempted sequences swap their blocks to a pinned host pool and back in
+    one launch per cache (:meth:`swap_out` / :meth:`swap_in`).
 """
 
 from __future__ import annotations
 
-from typing import List, Optional, Tuple, Union
+from typing import List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
 
 from .. import paged_ops
-from ..scheduler.sequence import Sequence
-from .block_allocator import PageAllocator, SequenceBlockTable
+from .block_allocator import BlockTablePool, PageAllocator, SequenceBlockTable
 from .strategies import KVCacheMemoryStrategy, detect_strategy, strategy_from_device
+
+
+def _no_table(seq) -> ValueError:
+    return ValueError(f"Sequence {seq.seq_id} has no block table")
 
 
 class PagedKVCacheManager:
@@ -40,24 +46,15 @@ class PagedKVCacheManager:
         device: Optional[Union[str, torch.device]] = None,
         strategy: Optional[KVCacheMemoryStrategy] = None,
     ) -> "PagedKVCacheManager":
-        """manager.py:13-39: KV heads and head_dim from an HF-style config."""
-        num_attention_heads = config.num_attention_heads
-        num_kv_heads = getattr(config, "num_key_value_heads", num_attention_heads)
-        head_dim = getattr(config, "head_dim", None)
-        if head_dim is None:
-            head_dim = config.hidden_size // num_attention_heads
-        manager = cls(
-            total_blocks=total_blocks,
-            block_size=block_size,
-            num_heads=num_kv_heads,
-            head_dim=head_dim,
-            total_cpu_blocks=total_cpu_blocks,
-            dtype=dtype,
-            num_layers=config.num_hidden_layers,
-            device=device,
-            strategy=strategy,
-        )
-        manager.num_query_heads = num_attention_heads
+        """A pool for an HF-style model config (manager.py:13-39): its KV heads
+        (``num_key_value_heads``, else the attention heads), its head dim
+        (``head_dim``, else hidden_size / heads) and its layer count."""
+        query_heads = int(config.num_attention_heads)
+        kv_heads = int(getattr(config, "num_key_value_heads", None) or query_heads)
+        head_dim = getattr(config, "head_dim", None) or config.hidden_size // query_heads
+        manager = cls(total_blocks, block_size, kv_heads, int(head_dim), total_cpu_blocks=total_cpu_blocks,
+                      dtype=dtype, num_layers=int(config.num_hidden_layers), device=device, strategy=strategy)
+        manager.num_query_heads = query_heads
         return manager
 
     def __init__(
@@ -72,27 +69,26 @@ class PagedKVCacheManager:
         device: Optional[Union[str, torch.device]] = None,
         strategy: Optional[KVCacheMemoryStrategy] = None,
     ) -> None:
-        self.block_size = block_size
-        self.num_heads = num_heads
-        self.head_dim = head_dim
-        self.num_layers = num_layers
+        self.block_size = int(block_size)
+        self.num_heads = int(num_heads)
+        self.head_dim = int(head_dim)
+        self.num_layers = int(num_layers)
         self.dtype = dtype
-        # Query heads of the model using the pool, when known (sizes the
-        # prefill work items of a step); None until a model config says.
+        # Query heads of the model served from this pool, when a model config
+        # gave them (they size the prefill work items and decode workspace).
         self.num_query_heads: Optional[int] = None
-        if strategy is not None:
-            self.strategy = strategy
-        elif device is not None:
-            self.strategy = strategy_from_device(device)
-        else:
-            self.strategy = detect_strategy()
-        bytes_per_token = num_layers * num_heads * head_dim * dtype.itemsize * 2
-        self.allocator = PageAllocator(total_blocks, block_size, bytes_per_token, total_cpu_blocks)
-        self.key_cache, self.value_cache = self.strategy.allocate_cache(
-            total_blocks, block_size, num_layers, num_heads, head_dim, dtype
-        )
+        if strategy is None:
+            strategy = strategy_from_device(device) if device is not None else detect_strategy()
+        self.strategy = strategy
+        token_bytes = 2 * self.num_layers * self.num_heads * self.head_dim * dtype.itemsize
+        self.allocator = PageAllocator(total_blocks, self.block_size, token_bytes, total_cpu_blocks)
+        self.key_cache, self.value_cache = strategy.allocate_cache(
+            total_blocks, self.block_size, self.num_layers, self.num_heads, self.head_dim, dtype)
+        self.tables = BlockTablePool(width=max(1, min(int(total_blocks), 64)))
+        self._device_table: Optional[torch.Tensor] = None
+        self._host_pool: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
 
-    # -- bookkeeping (manager.py:75-102) -----------------------------------
+    # -- pool bookkeeping ---------------------------------------------------------
     @property
     def device(self) -> str:
         return str(self.strategy.device)
@@ -108,110 +104,159 @@ class PagedKVCacheManager:
     def get_allocator(self) -> PageAllocator:
         return self.allocator
 
-    def init_sequence_table(self, seq: Sequence) -> None:
+    def init_sequence_table(self, seq) -> None:
         if seq.block_table is None:
-            seq.block_table = SequenceBlockTable(self.allocator)
+            seq.block_table = SequenceBlockTable(self.allocator, self.tables)
 
-    def allocate_prefix_blocks(self, seq: Sequence) -> None:
+    def allocate_prefix_blocks(self, seq) -> None:
+        """Slots for every token the sequence holds (prompt + outputs)."""
         self.init_sequence_table(seq)
-        needed = seq.total_len - seq.block_table.get_tokens_count()
-        for _ in range(needed):
-            seq.block_table.append_token()
+        table = seq.block_table
+        for _ in range(seq.total_len - table.get_tokens_count()):
+            table.append_token()
 
-    def allocate_slot_for_next_token(self, seq: Sequence) -> None:
+    def allocate_slot_for_next_token(self, seq) -> None:
         assert seq.block_table is not None
         seq.block_table.append_token()
 
-    def free_sequence(self, seq: Sequence) -> None:
+    def free_sequence(self, seq) -> None:
         if seq.block_table is not None:
             seq.block_table.release()
             seq.block_table = None
 
-    # -- slot mapping (manager.py:104-128, 301-333) ------------------------
-    def check_slot_ranges(self, sequences: List[Sequence], start_tokens: List[int], token_counts: List[int]) -> None:
-        """The host-side checks of build_slot_mapping / _sequence_slots."""
+    # -- one step: checks, rows, packing --------------------------------------------
+    def step_rows(self, sequences: Sequence, start_tokens, token_counts) -> Tuple[np.ndarray, np.ndarray,
+                                                                                   np.ndarray]:
+        """(rows, starts, counts) of a step after the slot-range checks of
+        build_slot_mapping / _sequence_slots (manager.py:104-128, 301-315),
+        each raising the reference's ValueError."""
         if not (len(sequences) == len(start_tokens) == len(token_counts)):
             raise ValueError(
                 f"sequences ({len(sequences)}), start_tokens ({len(start_tokens)}) "
-                f"and token_counts ({len(token_counts)}) must have the same length"
-            )
-        for seq, start, count in zip(sequences, start_tokens, token_counts):
-            if seq.block_table is None:
-                raise ValueError(f"Sequence {seq.seq_id} has no block table")
-            if start < 0 or count < 0:
-                raise ValueError(
-                    f"Sequence {seq.seq_id}: start_token ({start}) and "
-                    f"token_count ({count}) must be non-negative"
-                )
-            tokens_count = seq.block_table.get_tokens_count()
-            if start + count > tokens_count:
-                raise ValueError(
-                    f"Sequence {seq.seq_id}: tokens [{start}, {start + count}) "
-                    f"exceed allocated tokens ({tokens_count})"
-                )
+                f"and token_counts ({len(token_counts)}) must have the same length")
+        try:
+            rows = np.fromiter((seq.block_table.row for seq in sequences), dtype=np.int32, count=len(sequences))
+        except AttributeError:
+            raise _no_table(next(seq for seq in sequences if seq.block_table is None)) from None
+        starts = np.asarray(start_tokens, dtype=np.int64).reshape(-1)
+        counts = np.asarray(token_counts, dtype=np.int64).reshape(-1)
+        if rows.size and rows.min() < 0:
+            seq = sequences[int(np.argmin(rows))]
+            raise ValueError(f"Sequence {seq.seq_id}: its block table does not belong to this store")
+        if rows.size:
+            negative = (starts < 0) | (counts < 0)
+            beyond = starts + counts > self.tables.tokens[rows]
+            if negative.any() or beyond.any():
+                i = int(np.argmax(negative | beyond))
+                seq, s, c = sequences[i], int(starts[i]), int(counts[i])
+                if negative[i]:
+                    raise ValueError(f"Sequence {seq.seq_id}: start_token ({s}) and "
+                                     f"token_count ({c}) must be non-negative")
+                raise ValueError(f"Sequence {seq.seq_id}: tokens [{s}, {s + c}) "
+                                 f"exceed allocated tokens ({int(self.tables.tokens[rows[i]])})")
+        return rows, starts, counts
 
-    def block_table_tensor(self, sequences: List[Sequence]) -> torch.Tensor:
-        """int32 [B, max_blocks] (-1 padded) on the store's device."""
-        lists = [seq.block_table.get_physical_blocks() if seq.block_table else [] for seq in sequences]
-        width = max((len(b) for b in lists), default=0)
-        host = np.full((len(lists), max(width, 1)), -1, dtype=np.int32)
-        for i, blocks in enumerate(lists):
-            if blocks:
-                host[i, : len(blocks)] = blocks
-        t = torch.from_numpy(host)
-        if self.on_gpu:
-            t = t.pin_memory().to(self.key_cache.device, non_blocking=True)
-        return t
+    def device_block_table(self) -> Tuple[torch.Tensor, Optional[np.ndarray]]:
+        """(HBM copy of the row pool, updates it still needs or None): the
+        copy is rebuilt from the host rows when the pool grew, else the
+        queued (row, col, block) entries are returned for pa_pack to apply."""
+        rebuild, updates = self.tables.take_updates()
+        host = self.tables.host
+        dev = self._device_table
+        if rebuild or dev is None or tuple(dev.shape) != host.shape:
+            dev = torch.from_numpy(host.copy()).pin_memory().to(self.key_cache.device, non_blocking=True)
+            self._device_table = dev
+            return dev, None
+        return dev, updates if updates.shape[0] else None
 
-    def build_slot_mapping(
-        self,
-        sequences: List[Sequence],
-        start_tokens: List[int],
-        token_counts: List[int],
-    ) -> torch.Tensor:
-        self.check_slot_ranges(sequences, start_tokens, token_counts)
-        if not sequences:
-            return torch.empty((0,), dtype=torch.long, device=self.device)
-        if self.on_gpu:
-            step = paged_ops.pack_step(
-                self.block_table_tensor(sequences), list(start_tokens), list(token_counts), self.block_size
-            )
-            return step.scatter_slots
-        chunks = []
-        for seq, start, count in zip(sequences, start_tokens, token_counts):
-            chunk = self._sequence_slots(seq, start, count)
-            if chunk.numel() > 0:
-                chunks.append(chunk)
-        if not chunks:
-            return torch.empty((0,), dtype=torch.long, device=self.device)
-        return torch.cat(chunks)
+    def pack_step(self, sequences: Sequence, start_tokens, token_counts, *, num_query_heads: Optional[int] = None,
+                  with_gather: bool = False, partition_size: Optional[int] = None) -> paged_ops.PackedStep:
+        """Check, plan and pack one step on the GPU (one upload, two launches)."""
+        rows, starts, counts = self.step_rows(sequences, start_tokens, token_counts)
+        table, updates = self.device_block_table()
+        hq = int(num_query_heads or self.num_query_heads or self.num_heads)
+        return paged_ops.pack_step(
+            table, starts, counts, self.block_size, rows=rows, updates=updates,
+            num_kv_heads=self.num_heads, num_query_heads=hq, head_dim=self.head_dim, dtype=self.dtype,
+            with_gather=with_gather, partition_size=partition_size)
 
-    # -- KV writes (manager.py:130-168) ---------------------------------------
+    def _host_slots(self, rows: np.ndarray, starts: np.ndarray, counts: np.ndarray) -> np.ndarray:
+        """Slots of positions [start, start + count) of every sequence, in
+        order: block[p // bs] * bs + p % bs, from the pool's host rows."""
+        total = int(counts.sum()) if counts.size else 0
+        if total == 0:
+            return np.zeros(0, dtype=np.int64)
+        owner = np.repeat(np.arange(rows.shape[0]), counts)
+        first = np.cumsum(counts) - counts
+        pos = np.arange(total, dtype=np.int64) - first[owner] + starts[owner]
+        blocks = self.tables.host[rows[owner], pos // self.block_size].astype(np.int64)
+        return blocks * self.block_size + pos % self.block_size
+
+    def build_slot_mapping(self, sequences: List, start_tokens: List[int], token_counts: List[int]) -> torch.Tensor:
+        """int64 slots of the given token ranges, concatenated in sequence
+        order, on the store's device (manager.py:104-128)."""
+        rows, starts, counts = self.step_rows(sequences, start_tokens, token_counts)
+        if self.on_gpu and rows.size:
+            return self.pack_step(sequences, starts, counts).scatter_slots
+        return torch.from_numpy(self._host_slots(rows, starts, counts)).to(self.device)
+
+    def build_block_tables(self, sequences: List) -> Tuple[torch.Tensor, torch.Tensor]:
+        """int32 [B, max_blocks] block table padded with -1, and int32 token
+        counts, on the store's device (manager.py:236-271)."""
+        tables = [seq.block_table for seq in sequences]
+        rows = [t.row if t is not None else -1 for t in tables]
+        width = max((int(self.tables.blocks[r]) for r in rows if r >= 0), default=0)
+        out = np.full((len(rows), width), -1, dtype=np.int32)
+        lens = np.zeros(len(rows), dtype=np.int32)
+        for i, r in enumerate(rows):
+            if r >= 0:
+                out[i] = self.tables.host[r, :width]
+                lens[i] = self.tables.tokens[r]
+        return (torch.from_numpy(out).to(self.device, non_blocking=True),
+                torch.from_numpy(lens).to(self.device, non_blocking=True))
+
+    # -- K/V writes and reads (manager.py:130-234) -------------------------------------
+    def _validate_layer_idx(self, layer_idx: int) -> None:
+        if not 0 <= layer_idx < self.num_layers:
+            raise ValueError(f"Layer index {layer_idx} out of range (num_layers={self.num_layers})")
+
+    @staticmethod
+    def _validate_token_tensors(keys: torch.Tensor, values: torch.Tensor, expected_shape) -> None:
+        if keys.shape != values.shape:
+            raise ValueError(f"Keys shape {keys.shape} != Values shape {values.shape}")
+        if tuple(keys.shape) != tuple(expected_shape):
+            raise ValueError(f"Expected keys shape {tuple(expected_shape)}, got {tuple(keys.shape)}")
+
     def scatter_kv(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
-        self._validate_token_tensors(
-            keys, values, (slot_mapping.numel(), self.num_layers, self.num_heads, self.head_dim)
-        )
+        """Every layer's K/V of the tokens ([T, L, H, D]) into their slots."""
+        self._validate_token_tensors(keys, values, (slot_mapping.numel(), self.num_layers, self.num_heads,
+                                                    self.head_dim))
         for layer_idx in range(self.num_layers):
             self.scatter_layer_kv(layer_idx, keys[:, layer_idx], values[:, layer_idx], slot_mapping)
 
     def scatter_layer_kv(self, layer_idx: int, keys: torch.Tensor, values: torch.Tensor,
                          slot_mapping: torch.Tensor) -> None:
+        """One layer's new K/V ([T, H, D], any token / head strides) into the
+        cache at ``slot_mapping`` (manager.py:150-168): pa_reshape_and_cache on
+        a GPU store, an index copy on a CPU one."""
         self._validate_layer_idx(layer_idx)
         self._validate_token_tensors(keys, values, (slot_mapping.numel(), self.num_heads, self.head_dim))
         if slot_mapping.numel() == 0:
             return
         if self.on_gpu:
-            paged_ops.reshape_and_cache(
-                keys.to(self.key_cache.device, self.dtype),
-                values.to(self.key_cache.device, self.dtype),
-                self.key_cache,
-                self.value_cache,
-                slot_mapping.to(self.key_cache.device, torch.int64),
-                layer_idx,
-            )
+            dev = self.key_cache.device
+            paged_ops.reshape_and_cache(keys.to(dev, self.dtype), values.to(dev, self.dtype), self.key_cache,
+                                        self.value_cache, slot_mapping.to(dev, torch.int64), layer_idx)
             return
-        self.key_cache[layer_idx].view(-1, self.num_heads, self.head_dim)[slot_mapping] = keys
-        self.value_cache[layer_idx].view(-1, self.num_heads, self.head_dim)[slot_mapping] = values
+        flat = (-1, self.num_heads, self.head_dim)
+        slots = slot_mapping.to(torch.int64)
+        self.key_cache[layer_idx].view(flat).index_copy_(0, slots, keys.to(self.dtype))
+        self.value_cache[layer_idx].view(flat).index_copy_(0, slots, values.to(self.dtype))
+
+    def _gather_layer(self, cache: torch.Tensor, layer_idx: int, slot_indices: torch.Tensor) -> torch.Tensor:
+        self._validate_layer_idx(layer_idx)
+        flat = cache[layer_idx].view(-1, self.num_heads, self.head_dim)
+        return flat.index_select(0, slot_indices.to(cache.device, torch.int64))
 
     def gather_layer_keys(self, layer_idx: int, slot_indices: torch.Tensor) -> torch.Tensor:
         return self._gather_layer(self.key_cache, layer_idx, slot_indices)
@@ -219,91 +264,83 @@ class PagedKVCacheManager:
     def gather_layer_values(self, layer_idx: int, slot_indices: torch.Tensor) -> torch.Tensor:
         return self._gather_layer(self.value_cache, layer_idx, slot_indices)
 
-    def write_prefix_kv(self, seq: Sequence, keys: torch.Tensor, values: torch.Tensor) -> torch.Tensor:
-        """manager.py:176-192."""
+    def write_prefix_kv(self, seq, keys: torch.Tensor, values: torch.Tensor) -> torch.Tensor:
+        """K/V of a whole prompt ([L, T, H, D]) into the sequence's first T
+        slots; returns the slots (manager.py:176-192)."""
         if keys.shape != values.shape:
             raise ValueError(f"Keys shape {keys.shape} != Values shape {values.shape}")
-        seq_len = keys.shape[1]
-        if seq_len == 0 or seq.block_table is None:
+        length = int(keys.shape[1])
+        if length == 0 or seq.block_table is None:
             return torch.empty((0,), dtype=torch.long, device=self.device)
-        slot_mapping = self.build_slot_mapping([seq], [0], [seq_len])
-        self.scatter_kv(keys.transpose(0, 1), values.transpose(0, 1), slot_mapping)
-        return slot_mapping
+        slots = self.build_slot_mapping([seq], [0], [length])
+        self.scatter_kv(keys.transpose(0, 1), values.transpose(0, 1), slots)
+        return slots
 
-    def write_single_token_kv(self, seq: Sequence, key_token: torch.Tensor, value_token: torch.Tensor) -> None:
-        """manager.py:194-205."""
+    def write_single_token_kv(self, seq, key_token: torch.Tensor, value_token: torch.Tensor) -> None:
+        """K/V ([L, H, D]) of the sequence's last allocated token (manager.py:194-205)."""
         if seq.block_table is None:
-            raise ValueError(f"Sequence {seq.seq_id} has no block table")
-        token_index = seq.block_table.get_tokens_count() - 1
-        slot_mapping = self.build_slot_mapping([seq], [token_index], [1])
-        self.scatter_kv(key_token.unsqueeze(0), value_token.unsqueeze(0), slot_mapping)
+            raise _no_table(seq)
+        last = seq.block_table.get_tokens_count() - 1
+        slots = self.build_slot_mapping([seq], [last], [1])
+        self.scatter_kv(key_token.unsqueeze(0), value_token.unsqueeze(0), slots)
 
-    def gather_kv_cache(self, seq: Sequence, read_len: Optional[int] = None):
-        """manager.py:207-234: per-layer contiguous [1, H, len, D] K/V of one sequence."""
+    def gather_kv_cache(self, seq, read_len: Optional[int] = None):
+        """Per layer, the sequence's first ``read_len`` tokens of K and V as
+        [1, H, len, D] (manager.py:207-234); None without a table or tokens."""
         if seq.block_table is None:
             return None
-        physical_blocks = seq.block_table.get_physical_blocks()
-        tokens_count = seq.block_table.get_tokens_count()
-        if read_len is None:
-            read_len = tokens_count
-        if read_len <= 0:
+        n = seq.block_table.get_tokens_count() if read_len is None else int(read_len)
+        if n <= 0:
             return None
-        idx = torch.as_tensor(physical_blocks, dtype=torch.long, device=self.key_cache.device)
-        result = []
-        for layer_idx in range(self.num_layers):
-            k = self.key_cache[layer_idx].index_select(0, idx).reshape(-1, self.num_heads, self.head_dim)[:read_len]
-            v = self.value_cache[layer_idx].index_select(0, idx).reshape(-1, self.num_heads, self.head_dim)[:read_len]
-            result.append((k.unsqueeze(0).transpose(1, 2), v.unsqueeze(0).transpose(1, 2)))
-        return tuple(result)
+        slots = self.build_slot_mapping([seq], [0], [n])
+        return tuple(
+            (self.gather_layer_keys(layer, slots).permute(1, 0, 2).unsqueeze(0),
+             self.gather_layer_values(layer, slots).permute(1, 0, 2).unsqueeze(0))
+            for layer in range(self.num_layers))
 
-    def build_block_tables(self, sequences: List[Sequence]) -> Tuple[torch.Tensor, torch.Tensor]:
-        """manager.py:236-271: int32 [B, max_blocks] padded with -1 and int32 token counts."""
-        batch_size = len(sequences)
-        if batch_size == 0:
-            return (
-                torch.empty((0, 0), dtype=torch.int32, device=self.device),
-                torch.empty((0,), dtype=torch.int32, device=self.device),
-            )
-        raw = [seq.block_table.get_physical_blocks() if seq.block_table else [] for seq in sequences]
-        lens = [seq.block_table.get_tokens_count() if seq.block_table else 0 for seq in sequences]
-        max_blocks = max(len(b) for b in raw)
-        table = torch.full((batch_size, max_blocks), fill_value=-1, dtype=torch.int32)
-        for i, blocks in enumerate(raw):
-            if blocks:
-                table[i, : len(blocks)] = torch.tensor(blocks, dtype=torch.int32)
-        context_lens = torch.tensor(lens, dtype=torch.int32)
-        return (
-            table.to(self.device, non_blocking=True),
-            context_lens.to(self.device, non_blocking=True),
-        )
+    # -- swap to the host pool -------------------------------------------------------
+    def host_pool(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The pinned host swap space (allocated on first use): K and V of
+        ``total_cpu_blocks`` blocks in the cache's block layout."""
+        if self._host_pool is None:
+            self._host_pool = self.strategy.allocate_host_pool(
+                self.allocator.get_total_cpu_blocks(), self.block_size, self.num_layers, self.num_heads,
+                self.head_dim, self.dtype)
+        return self._host_pool
 
-    # -- validation (manager.py:273-299) --------------------------------------
-    def _validate_layer_idx(self, layer_idx: int) -> None:
-        if layer_idx < 0 or layer_idx >= self.num_layers:
-            raise ValueError(f"Layer index {layer_idx} out of range (num_layers={self.num_layers})")
+    def swap_out(self, seq) -> List[int]:
+        """Move a sequence's blocks to the host pool: host blocks are taken
+        (PageAllocator.swap_out), one launch per cache copies every layer's
+        blocks out (pa_swap_blocks), and the device blocks return to the free
+        list -- safe, since later writes to them follow on the same stream.
+        Returns the host block ids (also kept on the sequence's table)."""
+        if seq.block_table is None:
+            raise _no_table(seq)
+        if not self.on_gpu:
+            raise RuntimeError("swap needs a store in device memory")
+        table = seq.block_table
+        blocks = table.get_physical_blocks()
+        host_ids = [self.allocator.swap_out(b) for b in blocks]
+        hk, hv = self.host_pool()
+        mapping = list(zip(blocks, host_ids))
+        paged_ops.swap_blocks(self.key_cache, hk, mapping, out=True)
+        paged_ops.swap_blocks(self.value_cache, hv, mapping, out=True)
+        table.take_blocks()
+        table.swapped_blocks = host_ids
+        return host_ids
 
-    def _validate_token_tensors(self, keys: torch.Tensor, values: torch.Tensor, expected_shape) -> None:
-        if keys.shape != values.shape:
-            raise ValueError(f"Keys shape {keys.shape} != Values shape {values.shape}")
-        if tuple(keys.shape) != tuple(expected_shape):
-            raise ValueError(f"Expected keys shape {tuple(expected_shape)}, got {tuple(keys.shape)}")
-
-    def _gather_layer(self, cache: torch.Tensor, layer_idx: int, slot_indices: torch.Tensor) -> torch.Tensor:
-        self._validate_layer_idx(layer_idx)
-        return cache[layer_idx].view(-1, self.num_heads, self.head_dim).index_select(
-            0, slot_indices.to(cache.device)
-        )
-
-    def _sequence_slots(self, seq: Sequence, start_token: int, token_count: int) -> torch.Tensor:
-        """manager.py:301-333 (CPU store)."""
-        self.check_slot_ranges([seq], [start_token], [token_count])
-        if token_count == 0:
-            return torch.empty((0,), dtype=torch.long, device=self.device)
-        first_block = start_token // self.block_size
-        last_block = (start_token + token_count - 1) // self.block_size
-        physical_blocks = seq.block_table.get_physical_blocks()[first_block : last_block + 1]
-        block_offsets = torch.tensor(physical_blocks, dtype=torch.long, device=self.device) * self.block_size
-        slot_offsets = torch.arange(self.block_size, dtype=torch.long, device=self.device)
-        all_slots = (block_offsets.unsqueeze(1) + slot_offsets.unsqueeze(0)).flatten()
-        offset = start_token - first_block * self.block_size
-        return all_slots[offset : offset + token_count]
+    def swap_in(self, seq) -> List[int]:
+        """Bring a swapped-out sequence's blocks back into fresh device blocks
+        (PageAllocator.swap_in + one copy launch per cache); returns them."""
+        table = seq.block_table
+        host_ids = getattr(table, "swapped_blocks", None) if table is not None else None
+        if not host_ids:
+            raise RuntimeError(f"Sequence {seq.seq_id} is not swapped out")
+        blocks = [self.allocator.swap_in(h) for h in host_ids]
+        hk, hv = self.host_pool()
+        mapping = list(zip(host_ids, blocks))
+        paged_ops.swap_blocks(self.key_cache, hk, mapping, out=False)
+        paged_ops.swap_blocks(self.value_cache, hv, mapping, out=False)
+        table.put_blocks(blocks)
+        table.swapped_blocks = None
+        return blocks

@@ -1,11 +1,13 @@
 """Where the paged KV cache lives.
 
-Same interface as the reference's app/memory/strategies.py:35-70 and the
-same 5-D layout (num_layers, total_blocks, block_size, num_kv_heads,
-head_dim).  The difference is the ROCm branch: the reference's
-HipZeroCopyStrategy (strategies.py:132-155) keeps the cache in pinned HOST
-memory; here a ROCm device gets :class:`DeviceKVCacheStrategy`, which places
-both caches in HBM where the HIP kernels read them.
+The interface is the reference's (app/memory/strategies.py:35-70): a
+strategy allocates the two caches in the fixed 5-D layout (num_layers,
+total_blocks, block_size, num_kv_heads, head_dim) and copies blocks.  The
+difference is the ROCm branch: the reference's HipZeroCopyStrategy
+(strategies.py:132-155) keeps the cache in pinned HOST memory; here a ROCm
+device gets :class:`DeviceKVCacheStrategy`, which places both caches in HBM
+where the HIP kernels read them, and pinned host memory is only the swap
+space that preempted sequences' blocks move to (:meth:`allocate_host_pool`).
 """
 
 from __future__ import annotations
@@ -16,35 +18,41 @@ from typing import Tuple, Union
 
 import torch
 
+# Names accepted for LLM_DTYPE / a dtype argument (strategies.py:14-32).
+_DTYPE_NAMES = {
+    torch.float16: ("fp16", "float16"),
+    torch.bfloat16: ("bf16", "bfloat16"),
+    torch.float32: ("fp32", "float32"),
+}
+_DTYPE_BY_NAME = {name: dtype for dtype, names in _DTYPE_NAMES.items() for name in names}
+
 
 def resolve_device(device: Union[str, torch.device, None] = None) -> torch.device:
-    """strategies.py:7-11: "auto" -> cuda when available, else cpu."""
-    requested = device or os.getenv("LLM_DEVICE", "auto")
-    if requested == "auto":
-        requested = "cuda" if torch.cuda.is_available() else "cpu"
-    return torch.device(requested)
+    """The store's device: the argument, else $LLM_DEVICE, where "auto" (the
+    default) is the GPU when one is visible (strategies.py:7-11)."""
+    name = device if device is not None and device != "" else os.getenv("LLM_DEVICE", "auto")
+    if name == "auto":
+        return torch.device("cuda" if torch.cuda.is_available() else "cpu")
+    return torch.device(name)
 
 
 def resolve_dtype(dtype: Union[str, torch.dtype, None] = None) -> torch.dtype:
-    """strategies.py:14-32: "auto" -> bf16 on a GPU, else fp32."""
-    requested = dtype or os.getenv("LLM_DTYPE", "auto")
-    if isinstance(requested, torch.dtype):
-        return requested
-    requested = requested.lower()
-    if requested == "auto":
+    """The cache dtype: a torch dtype as is, else a name from the argument or
+    $LLM_DTYPE; "auto" (the default) is bf16 with a GPU and fp32 without
+    (strategies.py:14-32).  An unknown name is a ValueError."""
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    name = (dtype or os.getenv("LLM_DTYPE", "auto")).lower()
+    if name == "auto":
         return torch.bfloat16 if torch.cuda.is_available() else torch.float32
-    aliases = {
-        "fp16": torch.float16,
-        "float16": torch.float16,
-        "bf16": torch.bfloat16,
-        "bfloat16": torch.bfloat16,
-        "fp32": torch.float32,
-        "float32": torch.float32,
-    }
-    try:
-        return aliases[requested]
-    except KeyError as exc:
-        raise ValueError(f"Unsupported dtype: {requested}") from exc
+    if name not in _DTYPE_BY_NAME:
+        raise ValueError(f"Unsupported dtype: {name}")
+    return _DTYPE_BY_NAME[name]
+
+
+def cache_shape(total_blocks: int, block_size: int, num_layers: int, num_heads: int, head_dim: int):
+    """(num_layers, total_blocks, block_size, num_kv_heads, head_dim)."""
+    return (int(num_layers), int(total_blocks), int(block_size), int(num_heads), int(head_dim))
 
 
 class KVCacheMemoryStrategy(ABC):
@@ -71,31 +79,33 @@ class KVCacheMemoryStrategy(ABC):
     def requires_copy_on_swap(self) -> bool:
         ...
 
-
-def _cache_shape(total_blocks, block_size, num_layers, num_heads, head_dim):
-    return (num_layers, total_blocks, block_size, num_heads, head_dim)
+    def allocate_host_pool(self, total_cpu_blocks: int, block_size: int, num_layers: int, num_heads: int,
+                           head_dim: int, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Swap space for preempted sequences' blocks, same block shape as the
+        caches.  Only a store whose caches are not host memory has one."""
+        raise RuntimeError(f"{type(self).__name__} has no host swap pool")
 
 
 class CpuKVCacheStrategy(KVCacheMemoryStrategy):
-    """Host cache (strategies.py:73-97)."""
-
-    def __init__(self) -> None:
-        self._device = torch.device("cpu")
+    """Both caches in host memory (strategies.py:73-97): the reference's CPU
+    path, kept for CPU runs of the operator API."""
 
     @property
     def device(self) -> torch.device:
-        return self._device
+        return torch.device("cpu")
 
     def allocate_cache(self, total_blocks, block_size, num_layers, num_heads, head_dim, dtype):
-        shape = _cache_shape(total_blocks, block_size, num_layers, num_heads, head_dim)
-        return torch.empty(shape, dtype=dtype), torch.empty(shape, dtype=dtype)
+        shape = cache_shape(total_blocks, block_size, num_layers, num_heads, head_dim)
+        return torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype)
 
     def copy_blocks(self, src_cache, dst_cache, physical_blocks):
-        for bid in physical_blocks:
-            dst_cache[:, bid].copy_(src_cache[:, bid])
+        """The named physical blocks of every layer, src -> dst."""
+        if len(physical_blocks):
+            ids = torch.as_tensor(list(physical_blocks), dtype=torch.long)
+            dst_cache.index_copy_(1, ids, src_cache.index_select(1, ids))
 
     def sync(self) -> None:
-        pass
+        return None
 
     @property
     def requires_copy_on_swap(self) -> bool:
@@ -105,10 +115,11 @@ class CpuKVCacheStrategy(KVCacheMemoryStrategy):
 class DeviceKVCacheStrategy(KVCacheMemoryStrategy):
     """Both caches in HBM of one ROCm device.
 
-    Allocated once, zero-filled, through torch's caching allocator on the
-    device's current stream; the HIP kernels address them directly.  At
-    288 GB of HBM per MI355X the pool is sized by the caller's budget, not
-    by host RAM.
+    Allocated once, zero-filled, through torch's caching allocator; the HIP
+    kernels address them directly.  At 288 GB of HBM per MI355X the pool is
+    sized by the caller's budget, not by host RAM.  Preempted sequences swap
+    to a pinned host pool (:meth:`allocate_host_pool`) through the HIP swap
+    kernel (pa_swap_blocks).
     """
 
     def __init__(self, device_id: int = 0) -> None:
@@ -119,20 +130,25 @@ class DeviceKVCacheStrategy(KVCacheMemoryStrategy):
         return self._device
 
     def allocate_cache(self, total_blocks, block_size, num_layers, num_heads, head_dim, dtype):
-        shape = _cache_shape(total_blocks, block_size, num_layers, num_heads, head_dim)
-        key_cache = torch.zeros(shape, dtype=dtype, device=self._device)
-        value_cache = torch.zeros(shape, dtype=dtype, device=self._device)
-        return key_cache, value_cache
+        shape = cache_shape(total_blocks, block_size, num_layers, num_heads, head_dim)
+        return (torch.zeros(shape, dtype=dtype, device=self._device),
+                torch.zeros(shape, dtype=dtype, device=self._device))
+
+    def allocate_host_pool(self, total_cpu_blocks, block_size, num_layers, num_heads, head_dim, dtype):
+        """Pinned (hipHostMalloc'd) host tensors the swap kernel maps into the
+        device's address space."""
+        shape = cache_shape(total_cpu_blocks, block_size, num_layers, num_heads, head_dim)
+        return (torch.zeros(shape, dtype=dtype, pin_memory=True),
+                torch.zeros(shape, dtype=dtype, pin_memory=True))
 
     def copy_blocks(self, src_cache, dst_cache, physical_blocks):
         """Copy the named physical blocks (every layer) from src_cache into
         dst_cache with the HIP block-copy kernel, on the current stream."""
-        if not physical_blocks:
+        if not len(physical_blocks):
             return
         from .. import paged_ops
 
-        ids = [int(b) for b in physical_blocks]
-        paged_ops.copy_blocks(src_cache, dst_cache, [(b, b) for b in ids])
+        paged_ops.copy_blocks(src_cache, dst_cache, [(int(b), int(b)) for b in physical_blocks])
 
     def sync(self) -> None:
         torch.cuda.current_stream(self._device).synchronize()
@@ -143,14 +159,13 @@ class DeviceKVCacheStrategy(KVCacheMemoryStrategy):
 
 
 def strategy_from_device(device: Union[str, torch.device]) -> KVCacheMemoryStrategy:
-    """strategies.py:162-168, with the ROCm device mapped to HBM."""
+    """CPU -> host caches; a ROCm device -> HBM caches on that device
+    (strategies.py:162-168 maps ROCm to pinned host memory instead)."""
     dev = torch.device(device)
-    if dev.type != "cuda":
-        return CpuKVCacheStrategy()
-    return DeviceKVCacheStrategy(device_id=dev.index or 0)
+    if dev.type == "cuda":
+        return DeviceKVCacheStrategy(device_id=dev.index if dev.index is not None else 0)
+    return CpuKVCacheStrategy()
 
 
 def detect_strategy() -> KVCacheMemoryStrategy:
-    if not torch.cuda.is_available():
-        return CpuKVCacheStrategy()
-    return strategy_from_device("cuda")
+    return strategy_from_device("cuda" if torch.cuda.is_available() else "cpu")

@@ -1,28 +1,36 @@
-"""Paged attention on top of the paged KV cache (the per-step and per-layer glue).
+"""Paged attention on top of the paged KV cache: the per-step and per-layer glue.
 
-Same operator API as the reference's app/model/paged_attention.py:
-``PagedStepContext`` (same constructor and attributes), the per-layer hook
-``paged_attention_forward`` registered in transformers'
+The operator API is the reference's (app/model/paged_attention.py):
+``PagedStepContext`` with the same constructor and attributes, the per-layer
+hook ``paged_attention_forward`` registered in transformers'
 ALL_ATTENTION_FUNCTIONS, ``register_paged_attention`` and
-``run_paged_forward``.  On a GPU store the context is packed once per step
-by the HIP packing kernel (``self.packed``: device cu_seqlens, slots,
-positions and the attention work lists), and every layer then runs
-reshape_and_cache + the installed backend on the device without host syncs.
+``run_paged_forward``.  The step runs flat: all sequences of a step are one
+``[1, T]`` batch.
+
+On a GPU store the context is packed once per step (``self.packed``: the
+step's block table gathered from the device-resident row pool, cu_seqlens,
+slots, positions and the attention work lists, from one upload and the
+packing kernels), and every layer then runs pa_reshape_and_cache + the HIP
+attention kernels on the device without host syncs.  A GPU store always
+takes the HIP path: with no backend installed the hook installs it, and the
+reference's dense SDPA path is refused there (it would gather the whole
+context and build a T x C mask on the device).
 """
 
 from __future__ import annotations
 
-from typing import List, Optional, Sequence as SequenceABC
+from itertools import accumulate
+from typing import List, Optional
 
+import numpy as np
 import torch
 
 from .. import paged_ops
-from ..memory.manager import PagedKVCacheManager
-from ..scheduler.sequence import Sequence
 
 PAGED_ATTENTION_NAME = "paged"
 
-# Pluggable backend (paged_attention.py:22-25); None -> inline SDPA path.
+# The backend every layer dispatches to (paged_attention.py:22-25).  None on a
+# CPU store means the inline SDPA path; a GPU store installs the HIP backend.
 _BACKEND = None
 _FALLBACK_BACKEND = None
 
@@ -37,23 +45,29 @@ def _get_fallback_backend():
 
 
 def set_backend(backend) -> None:
-    """Install the backend every layer dispatches to (None = inline SDPA)."""
+    """Install the backend every layer dispatches to (None = the default)."""
     global _BACKEND
     _BACKEND = backend
 
 
-class PagedStepContext:
-    """Slot bookkeeping and attention mask for a single engine step
-    (paged_attention.py:37-118)."""
+def _offsets(counts) -> torch.Tensor:
+    """int64 [n + 1]: 0 followed by the running totals of ``counts``."""
+    return torch.tensor([0, *accumulate(counts)], dtype=torch.long)
 
-    def __init__(
-        self,
-        store: PagedKVCacheManager,
-        sequences: List[Sequence],
-        start_positions: List[int],
-        new_token_counts: List[int],
-        prefill_tile: Optional[int] = None,
-    ) -> None:
+
+class PagedStepContext:
+    """Slot bookkeeping and attention layout of one engine step
+    (paged_attention.py:37-118).
+
+    Attributes (the reference's): store, sequences, start_positions,
+    new_token_counts, context_lens (lists), cu_seqlens, cu_context_offsets
+    (CPU int64 tensors), scatter_slots, gather_slots (int64 on the store's
+    device), num_query_tokens, num_context_tokens.  ``packed`` is the GPU
+    description of the step (None on a CPU store).
+    """
+
+    def __init__(self, store, sequences: List, start_positions: List[int], new_token_counts: List[int],
+                 prefill_tile: Optional[int] = None) -> None:
         if not (len(sequences) == len(start_positions) == len(new_token_counts)):
             raise ValueError(
                 f"sequences ({len(sequences)}), start_positions ({len(start_positions)}) "
@@ -61,63 +75,37 @@ class PagedStepContext:
             )
         self.store = store
         self.sequences = list(sequences)
-        self.start_positions = list(start_positions)
-        self.new_token_counts = list(new_token_counts)
-        self.context_lens = [start + count for start, count in zip(start_positions, new_token_counts)]
-        self.cu_seqlens = _cumulative_offsets(new_token_counts)
-        self.cu_context_offsets = _cumulative_offsets(self.context_lens)
+        self.start_positions = [int(s) for s in start_positions]
+        self.new_token_counts = [int(c) for c in new_token_counts]
+        self.context_lens = [s + c for s, c in zip(self.start_positions, self.new_token_counts)]
+        self.cu_seqlens = _offsets(self.new_token_counts)
+        self.cu_context_offsets = _offsets(self.context_lens)
         self.packed: Optional[paged_ops.PackedStep] = None
-        self._mask: Optional[torch.Tensor] = None
         self._gather_slots: Optional[torch.Tensor] = None
-
+        self._mask: Optional[torch.Tensor] = None
         if store.on_gpu:
-            # Same checks as the two build_slot_mapping calls of the
-            # reference (scatter range, then the whole context).
-            store.check_slot_ranges(self.sequences, self.start_positions, self.new_token_counts)
-            store.check_slot_ranges(self.sequences, [0] * len(self.sequences), self.context_lens)
-            hq = getattr(store, "num_query_heads", None) or store.num_heads
-            if prefill_tile is None:
-                prefill_tile = paged_ops.prefill_tile_for(hq, store.num_heads)
             if self.sequences:
-                self.packed = paged_ops.pack_step(
-                    store.block_table_tensor(self.sequences),
-                    self.start_positions,
-                    self.new_token_counts,
-                    store.block_size,
-                    prefill_tile=prefill_tile,
-                    num_kv_heads=store.num_heads,
-                    num_query_heads=hq,
-                    head_dim=store.head_dim,
-                    dtype=store.dtype,
-                )
+                self.packed = store.pack_step(self.sequences, self.start_positions, self.new_token_counts)
                 self.scatter_slots = self.packed.scatter_slots
             else:
                 self.scatter_slots = torch.empty((0,), dtype=torch.long, device=store.device)
         else:
-            self.scatter_slots = store.build_slot_mapping(
-                self.sequences, self.start_positions, self.new_token_counts
-            )
-            self._gather_slots = store.build_slot_mapping(
-                self.sequences, [0] * len(self.sequences), self.context_lens
-            )
+            rows, starts, counts = store.step_rows(self.sequences, self.start_positions, self.new_token_counts)
+            self.scatter_slots = torch.from_numpy(store._host_slots(rows, starts, counts))
+            self._gather_slots = torch.from_numpy(
+                store._host_slots(rows, np.zeros_like(starts), starts + counts))
 
     def packed_for(self, num_query_heads: int) -> paged_ops.PackedStep:
-        """The packed step with prefill work items sized for ``num_query_heads``
-        (re-packs once if the context was built for another head count)."""
+        """The packed step with prefill work items and decode workspace sized
+        for ``num_query_heads`` (re-packs once if the store did not know the
+        model's head count)."""
         if self.packed is None:
             raise RuntimeError("this step is not on a GPU store")
         tile = paged_ops.prefill_tile_for(num_query_heads, self.store.num_heads)
         if self.packed.prefill_tile != tile:
-            self.packed = paged_ops.pack_step(
-                self.packed.block_tables,
-                self.start_positions,
-                self.new_token_counts,
-                self.store.block_size,
-                prefill_tile=tile,
-                partition_size=self.packed.partition_size,
-                start_positions_dev=self.packed.start_positions,
-                new_token_counts_dev=self.packed.new_token_counts,
-            )
+            self.packed = self.store.pack_step(self.sequences, self.start_positions, self.new_token_counts,
+                                               num_query_heads=num_query_heads,
+                                               partition_size=self.packed.partition_size)
         return self.packed
 
     @property
@@ -139,53 +127,48 @@ class PagedStepContext:
         return int(self.cu_context_offsets[-1])
 
     def position_ids(self, device: torch.device) -> torch.Tensor:
-        """Flat per-token positions, restarting at every sequence boundary."""
-        if self.packed is not None and torch.device(device) == self.packed.position_ids.device:
+        """[1, T] positions, restarting at every sequence boundary."""
+        if self.packed is not None and torch.device(device) == self.packed.buffer.device:
             return self.packed.position_ids.unsqueeze(0)
-        positions = [
-            torch.arange(start, start + count, dtype=torch.long, device=device)
-            for start, count in zip(self.start_positions, self.new_token_counts)
-        ]
-        if not positions:
-            return torch.empty((1, 0), dtype=torch.long, device=device)
-        return torch.cat(positions).unsqueeze(0)
+        counts = np.asarray(self.new_token_counts, dtype=np.int64)
+        total = int(counts.sum()) if counts.size else 0
+        owner = np.repeat(np.arange(counts.size), counts)
+        first = self.cu_seqlens.numpy()[:-1]
+        pos = np.arange(total, dtype=np.int64) - first[owner] + np.asarray(self.start_positions, np.int64)[owner]
+        return torch.from_numpy(pos).to(device).unsqueeze(0)
 
     def attention_mask(self, device: torch.device) -> torch.Tensor:
-        """Block-diagonal causal mask bool (1, 1, T, C), True = attended.
+        """Block-diagonal causal mask, bool (1, 1, T, C), True = attended:
+        query token i of sequence s (position start_s + i) sees context
+        position j of the same sequence when j <= start_s + i.
 
-        Only the SDPA backend materialises it; the HIP kernels evaluate the
-        same rule from cu_seqlens / context_lens."""
-        if self._mask is not None and self._mask.device == torch.device(device):
+        Only the SDPA path materialises it; the HIP kernels evaluate the same
+        rule from cu_seqlens and context_lens."""
+        device = torch.device(device)
+        if self._mask is not None and self._mask.device == device:
             return self._mask
-        query_index = _sequence_index(self.new_token_counts, device)
-        context_index = _sequence_index(self.context_lens, device)
-        cu_seqlens = self.cu_seqlens.to(device)
-        cu_context_offsets = self.cu_context_offsets.to(device)
-        starts = torch.tensor(self.start_positions, dtype=torch.long, device=device)
-        query_position = torch.arange(self.num_query_tokens, device=device)
-        query_position = query_position - cu_seqlens[query_index] + starts[query_index]
-        context_position = torch.arange(self.num_context_tokens, device=device)
-        context_position = context_position - cu_context_offsets[context_index]
-        same_sequence = context_index.unsqueeze(0) == query_index.unsqueeze(1)
-        within_causal_window = context_position.unsqueeze(0) <= query_position.unsqueeze(1)
-        self._mask = (same_sequence & within_causal_window).unsqueeze(0).unsqueeze(0)
+        q_seq = torch.repeat_interleave(torch.arange(len(self.new_token_counts)),
+                                        torch.tensor(self.new_token_counts, dtype=torch.long))
+        c_seq = torch.repeat_interleave(torch.arange(len(self.context_lens)),
+                                        torch.tensor(self.context_lens, dtype=torch.long))
+        q_pos = self.position_ids(torch.device("cpu"))[0]
+        c_pos = torch.arange(self.num_context_tokens) - self.cu_context_offsets[c_seq]
+        mask = (q_seq[:, None] == c_seq[None, :]) & (c_pos[None, :] <= q_pos[:, None])
+        self._mask = mask[None, None].to(device)
         return self._mask
 
 
-def _cumulative_offsets(counts: List[int]) -> torch.Tensor:
-    offsets = [0]
-    for count in counts:
-        offsets.append(offsets[-1] + count)
-    return torch.tensor(offsets, dtype=torch.long)
+def _default_backend(store):
+    """The backend a layer uses when none is installed: the HIP backend for a
+    GPU store (installed for every later layer; raises when the library is
+    missing), none (inline SDPA) for a CPU store."""
+    global _BACKEND
+    if not store.on_gpu:
+        return None
+    from .attention_backends import select_backend
 
-
-def _sequence_index(counts: List[int], device: torch.device) -> torch.Tensor:
-    if not counts:
-        return torch.empty((0,), dtype=torch.long, device=device)
-    return torch.repeat_interleave(
-        torch.arange(len(counts), dtype=torch.long, device=device),
-        torch.tensor(counts, dtype=torch.long, device=device),
-    )
+    _BACKEND = select_backend("native")
+    return _BACKEND
 
 
 def paged_attention_forward(
@@ -198,55 +181,78 @@ def paged_attention_forward(
     scaling: Optional[float] = None,
     **kwargs,
 ) -> tuple[torch.Tensor, None]:
-    """Per-layer hook (paged_attention.py:138-180): scatter the new K/V into the
-    paged blocks, then attend through the installed backend (falling back to
-    SDPA for shapes it refuses) or the inline SDPA path."""
+    """Per-layer hook (paged_attention.py:138-180): write the layer's new K/V
+    into the paged blocks, then attend through the installed backend.  A CPU
+    store falls back to SDPA for shapes the backend refuses, or runs the
+    inline SDPA path with none installed; a GPU store runs the HIP kernels."""
     context: PagedStepContext = module.paged_context
-    store: PagedKVCacheManager = context.store
+    store = context.store
     layer_idx = module.layer_idx
+    # [1, H_kv, T, D] projections -> [T, H_kv, D] views (no copy)
+    store.scatter_layer_kv(layer_idx, key[0].transpose(0, 1), value[0].transpose(0, 1), context.scatter_slots)
+    scale = module.scaling if scaling is None else scaling
+    backend = _BACKEND if _BACKEND is not None else _default_backend(store)
+    if store.on_gpu:
+        from .attention_backends import NativePagedBackend
 
-    new_keys = key.squeeze(0).transpose(0, 1)
-    new_values = value.squeeze(0).transpose(0, 1)
-    store.scatter_layer_kv(layer_idx, new_keys, new_values, context.scatter_slots)
-
-    scale = scaling if scaling is not None else module.scaling
-    backend = _BACKEND
-    if backend is not None and not backend.supports(context, query.shape[2]):
-        backend = _get_fallback_backend()
+        if not isinstance(backend, NativePagedBackend):
+            raise RuntimeError(
+                f"a GPU store runs the HIP paged-attention backend, not {type(backend).__name__} "
+                "(dense SDPA would gather every context and build a T x C mask on the device)")
+        if query.shape[2] == 0:
+            return query.new_empty((1, 0, query.shape[1], query.shape[3])), None
+        return backend.attend(query, store, layer_idx, context, scale, dropout), None
     if backend is not None:
+        if not backend.supports(context, query.shape[2]):
+            backend = _get_fallback_backend()
         return backend.attend(query, store, layer_idx, context, scale, dropout), None
     from .attention_backends import dense_sdpa
 
     return dense_sdpa(query, store, layer_idx, context, scale, dropout), None
 
 
-def register_paged_attention(model) -> None:
-    """Route every decoder layer of ``model`` through the paged attention."""
-    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
-
-    ALL_ATTENTION_FUNCTIONS.register(PAGED_ATTENTION_NAME, paged_attention_forward)
-    for layer in _decoder_layers(model):
-        layer.self_attn.paged_context = None
-    model.config._attn_implementation = PAGED_ATTENTION_NAME
-
-
-def run_paged_forward(model, context: PagedStepContext, input_ids: torch.Tensor) -> torch.Tensor:
-    """Run one flat forward pass whose KV lands in the paged blocks."""
-    decoder = _decoder(model)
-    for layer in decoder.layers:
-        layer.self_attn.paged_context = context
-    position_ids = context.position_ids(input_ids.device)
-    outputs = model(input_ids, position_ids=position_ids, use_cache=False)
-    return outputs.logits
-
-
 def _decoder(model) -> torch.nn.Module:
-    for attribute in ("model", "transformer", "base_model"):
-        candidate = getattr(model, attribute, None)
-        if candidate is not None and hasattr(candidate, "layers"):
-            return candidate
+    """The module holding the decoder layers: the model's own decoder when it
+    exposes one, else the first of its usual attributes that has ``layers``."""
+    getter = getattr(model, "get_decoder", None)
+    if callable(getter):
+        try:
+            decoder = getter()
+        except (AttributeError, NotImplementedError):
+            decoder = None
+        if decoder is not None and hasattr(decoder, "layers"):
+            return decoder
+    for name in ("model", "transformer", "base_model"):
+        inner = getattr(model, name, None)
+        if inner is not None and hasattr(inner, "layers"):
+            return inner
     return model
 
 
-def _decoder_layers(model) -> SequenceABC[torch.nn.Module]:
-    return _decoder(model).layers
+def register_paged_attention(model, backend=None) -> None:
+    """Route every decoder layer of ``model`` through the paged hook
+    (paged_attention.py:183-188) and install ``backend`` (by default the one
+    select_backend names: the HIP backend when the library and a ROCm device
+    are there)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    from .attention_backends import select_backend
+
+    ALL_ATTENTION_FUNCTIONS.register(PAGED_ATTENTION_NAME, paged_attention_forward)
+    for layer in _decoder(model).layers:
+        layer.self_attn.paged_context = None
+    model.config._attn_implementation = PAGED_ATTENTION_NAME
+    set_backend(backend if backend is not None else select_backend())
+
+
+def run_paged_forward(model, context: PagedStepContext, input_ids: torch.Tensor, logits_to_keep=None
+                      ) -> torch.Tensor:
+    """One flat forward pass whose K/V lands in the paged blocks
+    (paged_attention.py:191-207).  ``logits_to_keep`` (a device index tensor
+    or a count) restricts the LM head to those rows, e.g. each sequence's
+    last token."""
+    for layer in _decoder(model).layers:
+        layer.self_attn.paged_context = context
+    extra = {} if logits_to_keep is None else {"logits_to_keep": logits_to_keep}
+    out = model(input_ids, position_ids=context.position_ids(input_ids.device), use_cache=False, **extra)
+    return out.logits

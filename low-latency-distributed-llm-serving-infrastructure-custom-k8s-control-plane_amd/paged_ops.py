@@ -16,9 +16,10 @@ plus :func:`attention` (decode + prefill of one flattened step) and
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
-from typing import List, Optional, Sequence
+import ctypes
+from typing import Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import _native
@@ -75,60 +76,206 @@ def prefill_tile_for(num_query_heads: int, num_kv_heads: int) -> int:
 # (a) packing
 
 
-@dataclass
-class PackedStep:
-    """Device-side description of one flattened ragged step (output of pa_pack).
+def _align(n: int, a: int = 256) -> int:
+    return (n + a - 1) // a * a
 
-    Host-side counts are derived from the host lists the scheduler already
-    holds, so no device->host synchronisation is needed to size the grids.
+
+class _Layout:
+    """Byte offsets of named arrays inside one buffer (256-byte aligned)."""
+
+    def __init__(self) -> None:
+        self.fields = {}
+        self.nbytes = 0
+
+    def add(self, name: str, dtype: torch.dtype, shape) -> None:
+        count = 1
+        for d in shape:
+            count *= int(d)
+        self.fields[name] = (self.nbytes, dtype, tuple(int(d) for d in shape))
+        self.nbytes += _align(count * torch.empty((), dtype=dtype).element_size())
+
+
+_ELEM = {torch.int64: 8, torch.int32: 4, torch.uint8: 1}
+
+
+class _HostStaging:
+    """A ring of pinned host buffers for the per-step uploads.
+
+    A slot is reused only after the copy that last read it has run (an event
+    recorded behind that copy), so the host never overwrites bytes a pending
+    copy still reads, and never waits in the steady state."""
+
+    SLOTS = 8
+
+    def __init__(self) -> None:
+        self._bufs = [None] * self.SLOTS
+        self._arrays = [None] * self.SLOTS
+        self._events = [None] * self.SLOTS
+        self._next = 0
+
+    def take(self, nbytes: int):
+        slot = self._next
+        self._next = (slot + 1) % self.SLOTS
+        if self._events[slot] is not None:
+            self._events[slot].synchronize()
+        buf = self._bufs[slot]
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(_align(nbytes, 1 << 16), 1 << 16), dtype=torch.uint8, pin_memory=True)
+            self._bufs[slot] = buf
+            self._arrays[slot] = buf.numpy()
+        return slot, buf, self._arrays[slot]
+
+    def done(self, slot: int, stream) -> None:
+        ev = self._events[slot]
+        if ev is None:
+            ev = self._events[slot] = torch.cuda.Event()
+        ev.record(stream)
+
+
+_STAGING: dict = {}  # device -> _HostStaging
+_CUS: dict = {}  # device index -> compute units
+
+
+def _staging(device: torch.device) -> _HostStaging:
+    key = device.index
+    st = _STAGING.get(key)
+    if st is None:
+        st = _STAGING[key] = _HostStaging()
+    return st
+
+
+def _compute_units(device: torch.device) -> int:
+    n = _CUS.get(device.index)
+    if n is None:
+        n = _CUS[device.index] = int(torch.cuda.get_device_properties(device).multi_processor_count)
+    return n
+
+
+class PackedStep:
+    """Device-side description of one flattened ragged step (what pa_pack
+    writes), in one device allocation.
+
+    Every array is a view of ``buffer``, materialised on first access; the
+    kernels are launched from the raw addresses (:meth:`ptr`), so a step
+    costs one allocation and no per-array tensor objects on the hot path.
+    Host-side counts come from the host planner (pa_plan_step), so no
+    device-to-host synchronisation sizes the grids.
+
+    Arrays: block_tables int32 [B, width] (the step's table), start_positions
+    / new_token_counts int64 [B], cu_seqlens / cu_context_offsets int64
+    [B+1], context_lens int32 [B], scatter_slots / position_ids int64 [T],
+    decode_items int32 [n, 2], merge_items int32 [n, 4], prefill_items int32
+    [n, 2]; gather_slots int64 [C] is built on first use.
     """
 
-    block_tables: torch.Tensor  # int32 [B, max_blocks]
-    start_positions: torch.Tensor  # int64 [B]
-    new_token_counts: torch.Tensor  # int64 [B]
-    cu_seqlens: torch.Tensor  # int64 [B+1]
-    cu_context_offsets: torch.Tensor  # int64 [B+1]
-    context_lens: torch.Tensor  # int32 [B]
-    scatter_slots: torch.Tensor  # int64 [T]
-    position_ids: torch.Tensor  # int64 [T]
-    decode_items: torch.Tensor  # int32 [num_decode_items, 2]
-    # int32 [num_merge_items, 4]: (first full-partition item, full partitions,
-    # seq, remainder item or -1)
-    merge_items: torch.Tensor
-    prefill_items: torch.Tensor  # int32 [num_prefill_items, 2]
-    block_size: int
-    partition_size: int
-    prefill_tile: int
-    num_query_tokens: int
-    num_context_tokens: int
-    num_decode_items: int
-    num_merge_items: int
-    num_prefill_items: int
-    num_decode_seqs: int
-    num_prefill_seqs: int
-    _gather_slots: Optional[torch.Tensor] = field(default=None, repr=False)
-    _workspace: Optional[torch.Tensor] = field(default=None, repr=False)
+    def __init__(self, buffer, layout, plan, block_size, prefill_tile, table, table_rows, rows_name,
+                 head_shape):
+        self.buffer = buffer
+        self._layout = layout
+        self._base = buffer.data_ptr()
+        self.block_size = int(block_size)
+        self.partition_size = int(plan.partition_size)
+        self.prefill_tile = int(prefill_tile)
+        self.num_seqs = int(layout.fields["start_positions"][2][0])
+        self.num_query_tokens = int(plan.num_query_tokens)
+        self.num_context_tokens = int(plan.num_context_tokens)
+        self.num_decode_items = int(plan.num_decode_items)
+        self.num_merge_items = int(plan.num_merge_items)
+        self.num_prefill_items = int(plan.num_prefill_items)
+        self.num_decode_seqs = int(plan.num_decode_seqs)
+        self.num_prefill_seqs = int(plan.num_prefill_seqs)
+        self.max_context = int(plan.max_context)
+        self._source_table = table  # the table pa_pack reads (the step's own, or a pool)
+        self._source_rows = table_rows
+        self._rows_name = rows_name  # None when block_tables is the step's own table
+        self._head_shape = head_shape  # (H_q, D) the workspace was sized for, or None
+        self._gather = None
+        self._extra_ws = None
+
+    # -- addresses and views ---------------------------------------------------
+    def ptr(self, name: str) -> int:
+        if name == "block_tables" and self._rows_name is None:
+            return self._source_table.data_ptr()
+        return self._base + self._layout.fields[name][0]
+
+    def _view(self, name: str) -> torch.Tensor:
+        off, dtype, shape = self._layout.fields[name]
+        count = 1
+        for d in shape:
+            count *= d
+        t = self.buffer[off : off + count * _ELEM[dtype]].view(dtype).view(shape)
+        self.__dict__[name] = t
+        return t
+
+    def __getattr__(self, name: str):
+        layout = self.__dict__.get("_layout")
+        if layout is None:
+            raise AttributeError(name)
+        if name == "block_tables" and self.__dict__["_rows_name"] is None:
+            return self.__dict__["_source_table"]
+        if name in layout.fields:
+            return self._view(name)
+        raise AttributeError(name)
 
     @property
-    def num_seqs(self) -> int:
-        return int(self.block_tables.shape[0])
+    def table_width(self) -> int:
+        if self._rows_name is None:
+            return int(self._source_table.shape[1])
+        return int(self._layout.fields["block_tables"][2][1])
 
     @property
     def gather_slots(self) -> torch.Tensor:
         """int64 [C] slots of every context token (built on first use)."""
-        if self._gather_slots is None:
-            self._gather_slots = _run_pack(self, with_gather=True)
-        return self._gather_slots
+        if self._gather is None:
+            self._gather = _run_pack(self, with_gather=True)
+        return self._gather
 
     def workspace(self, num_query_heads: int, head_dim: int, device: torch.device) -> torch.Tensor:
         """Decode workspace (split-K partials), reused across the layers of the
         step; calls that share it must not overlap in time."""
         need = decode_workspace_bytes(self.num_decode_items, num_query_heads, head_dim)
-        ws = self._workspace
+        if self._head_shape == (int(num_query_heads), int(head_dim)):
+            return self._view("decode_workspace") if "decode_workspace" not in self.__dict__ \
+                else self.__dict__["decode_workspace"]
+        ws = self._extra_ws
         if ws is None or ws.numel() < need or ws.device != device:
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
-            self._workspace = ws
+            self._extra_ws = ws
         return ws
+
+    def workspace_ptr(self, num_query_heads: int, head_dim: int) -> Tuple[int, int]:
+        """(address, bytes) of the decode workspace for these head counts."""
+        if self._head_shape == (int(num_query_heads), int(head_dim)):
+            off, _, shape = self._layout.fields["decode_workspace"]
+            return self._base + off, shape[0]
+        ws = self.workspace(num_query_heads, head_dim, self.buffer.device)
+        return ws.data_ptr(), ws.numel()
+
+
+def _plan(starts: np.ndarray, counts: np.ndarray, block_size: int, prefill_tile: int, partition_size: int,
+          num_kv_heads: int, num_query_heads: int, workgroups_per_item: int, workgroups_per_cu: int,
+          compute_units: int, allocated: Optional[np.ndarray] = None):
+    lib = _native.load_library()
+    params = _native.PaPlanParams(block_size=int(block_size), prefill_tile=int(prefill_tile),
+                                  partition_size=int(partition_size), num_kv_heads=int(num_kv_heads),
+                                  num_query_heads=int(num_query_heads),
+                                  workgroups_per_item=int(workgroups_per_item),
+                                  workgroups_per_cu=int(workgroups_per_cu), compute_units=int(compute_units))
+    plan = _native.PaStepPlan()
+    status = lib.pa_plan_step(starts.ctypes.data, counts.ctypes.data,
+                              None if allocated is None else allocated.ctypes.data,
+                              int(starts.shape[0]), params, ctypes.byref(plan))
+    if status != _native.PA_OK:
+        if plan.bad_seq >= 0:
+            raise ValueError(lib.pa_last_error_message().decode(errors="replace"))
+        _native.check(status, "pa_plan_step")
+    return plan
+
+
+def _int64_array(values) -> np.ndarray:
+    if isinstance(values, np.ndarray) and values.dtype == np.int64 and values.flags.c_contiguous:
+        return values
+    return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
 
 
 def work_counts(
@@ -137,21 +284,12 @@ def work_counts(
     partition_size: int,
     prefill_tile: int,
 ):
-    """Host-side sizes of a step:
+    """Host-side sizes of a step (pa_plan_step):
     (T, C, decode items, merge items, prefill items, #decode seqs, #prefill seqs)."""
-    t = c = ditems = mitems = pitems = ndec = npre = 0
-    for start, count in zip(start_positions, new_token_counts):
-        ctx = start + count
-        t += count
-        c += ctx
-        if count == 1:
-            ditems += -(-ctx // partition_size)
-            mitems += ctx > partition_size
-            ndec += 1
-        elif count > 1:
-            pitems += -(-count // prefill_tile)
-            npre += 1
-    return t, c, ditems, mitems, pitems, ndec, npre
+    p = _plan(_int64_array(start_positions), _int64_array(new_token_counts), 1, prefill_tile, partition_size,
+              1, 1, 1, 1, 1)
+    return (int(p.num_query_tokens), int(p.num_context_tokens), int(p.num_decode_items), int(p.num_merge_items),
+            int(p.num_prefill_items), int(p.num_decode_seqs), int(p.num_prefill_seqs))
 
 
 # Compute units of an MI355X; pack_step uses the device's own count.
@@ -197,7 +335,8 @@ def choose_partition(
     workgroups_per_cu: Optional[int] = None,
     compute_units: int = _DECODE_CUS,
 ) -> int:
-    """Split-K partition for the decode sequences of a step.
+    """Split-K partition for the decode sequences of a step (the rule of
+    pa_plan_step, which runs it on the host in C++).
 
     The largest of 4096, 2048, 1024, 512 and 256 tokens whose decode launch
     (partitions x workgroups_per_item, by default the KV heads) still gives every
@@ -218,65 +357,57 @@ def choose_partition(
     Measured with graph replay, 32/8 heads of 128 paired: 1 sequence of 1024
     tokens 16.6 us at 256 -> 11.3 at 64; 16 of 4096 55.9 -> 50.7 at 512.
     """
-    hkv = max(int(num_kv_heads), 1)
-    group = max(int(num_query_heads or 4 * hkv) // hkv, 1)
-    per_cu = int(workgroups_per_cu or 0) or (5 if group == 1 else 4)
-    slots = int(compute_units) * per_cu
-    width = max(int(workgroups_per_item or hkv), 1)  # workgroups per item
-    ctx = [s + c for s, c in zip(start_positions, new_token_counts) if c == 1]
-
-    def workgroups(p: int) -> int:
-        return sum(-(-x // p) for x in ctx) * width
-
-    p = PA_DECODE_MAX_PARTITION
-    while p > 256:
-        if workgroups(p) >= 3 * slots // 2:
-            return p
-        p //= 2
-    longest = max(ctx, default=0)
-    p = PA_DECODE_MAX_PARTITION
-    while p >= 64:
-        if workgroups(p) >= 2 * slots // 3 and -(-longest // p) <= 64:
-            return p
-        p //= 2
-    p = 64
-    while p < PA_DECODE_MAX_PARTITION and -(-longest // p) > 64:
-        p *= 2
-    return p
+    p = _plan(_int64_array(start_positions), _int64_array(new_token_counts), 1, 1, 0, num_kv_heads,
+              num_query_heads or 0, workgroups_per_item or 0, workgroups_per_cu or 0, compute_units)
+    return int(p.partition_size)
 
 
-def _run_pack(step: PackedStep, with_gather: bool = False) -> Optional[torch.Tensor]:
+def _run_pack(step: PackedStep, with_gather: bool = False, updates_ptr: int = 0, num_updates: int = 0
+              ) -> Optional[torch.Tensor]:
+    """Launch pa_pack for ``step`` (again): all outputs are rewritten, plus the
+    gather slots when asked for (returned)."""
     lib = _native.load_library()
-    device = _require_device(step.block_tables)
+    device = step.buffer.device
     gather = None
     if with_gather:
         gather = torch.empty(step.num_context_tokens, dtype=torch.int64, device=device)
+    pooled = step._rows_name is not None
+    table = step._source_table
     dims = _native.PaPackDims(
         num_seqs=step.num_seqs,
         block_size=step.block_size,
-        max_blocks_per_seq=int(step.block_tables.shape[1]) if step.block_tables.dim() == 2 else 0,
+        max_blocks_per_seq=int(table.shape[1]) if table.dim() == 2 else 0,
         partition_size=step.partition_size,
         prefill_tile=step.prefill_tile,
+        num_table_rows=step._source_rows,
+        num_updates=int(num_updates),
+        step_table_width=step.table_width if pooled else 0,
         max_query_tokens=step.num_query_tokens,
         max_context_tokens=step.num_context_tokens,
         max_decode_items=step.num_decode_items,
         max_merge_items=step.num_merge_items,
         max_prefill_items=step.num_prefill_items,
     )
+    ws_off, _, ws_shape = step._layout.fields["pack_workspace"]
     status = lib.pa_pack(
-        _ptr(step.block_tables),
-        _ptr(step.start_positions),
-        _ptr(step.new_token_counts),
+        table.data_ptr() if table.numel() else None,
+        step.ptr("rows") if pooled else None,
+        updates_ptr or None,
+        step.ptr("start_positions"),
+        step.ptr("new_token_counts"),
         dims,
-        _ptr(step.cu_seqlens),
-        _ptr(step.cu_context_offsets),
-        _ptr(step.context_lens),
-        _ptr(step.scatter_slots),
-        _ptr(step.position_ids),
+        step.ptr("block_tables") if pooled else None,
+        step.ptr("cu_seqlens"),
+        step.ptr("cu_context_offsets"),
+        step.ptr("context_lens"),
+        step.ptr("scatter_slots"),
+        step.ptr("position_ids"),
         _ptr(gather),
-        _ptr(step.decode_items),
-        _ptr(step.merge_items),
-        _ptr(step.prefill_items),
+        step.ptr("decode_items"),
+        step.ptr("merge_items"),
+        step.ptr("prefill_items"),
+        step._base + ws_off,
+        ws_shape[0],
         _stream(device),
     )
     _native.check(status, "pa_pack")
@@ -296,82 +427,116 @@ def pack_step(
     head_dim: Optional[int] = None,
     dtype: Optional[torch.dtype] = None,
     with_gather: bool = False,
-    start_positions_dev: Optional[torch.Tensor] = None,
-    new_token_counts_dev: Optional[torch.Tensor] = None,
+    rows=None,
+    updates: Optional[np.ndarray] = None,
+    allocated_tokens=None,
 ) -> PackedStep:
-    """Run the GPU packing kernel for one step.
+    """Plan a step on the host, upload its description once, and run the GPU
+    packing kernels.
 
-    ``block_tables``: int32 [B, max_blocks] device tensor (-1 padded).
-    ``start_positions`` / ``new_token_counts``: the host lists of the step
-    (also uploaded unless device copies are passed in).
-    ``partition_size``: decode split-K partition in tokens; by default
-    :func:`choose_partition` picks it from the step and the head counts
-    (and, when ``head_dim`` and the cache ``dtype`` are given, from how many
-    KV heads one decode workgroup reads).
+    ``block_tables``: int32 [B, max_blocks] device tensor (-1 padded), the
+    step's own table; or, with ``rows`` (one row index per sequence), a
+    device-resident pool of table rows from which pa_pack gathers the step's
+    table (``PackedStep.block_tables``), after applying ``updates`` (int32
+    [n, 3] (row, col, block) triples, host array) to it.
+    ``start_positions`` / ``new_token_counts``: the host lists of the step.
+    ``allocated_tokens``: per sequence, the tokens it has slots for; a step
+    reaching past them is a ValueError (as the reference's slot mapping).
+    ``partition_size``: decode split-K partition in tokens; by default the
+    planner picks it from the step and the head counts (and, when
+    ``head_dim`` and the cache ``dtype`` are given, from how many KV heads
+    one decode workgroup reads and the kernel's occupancy).
     ``prefill_tile``: query tokens per prefill work item; by default the
     MFMA kernel's tile for the head counts (:func:`prefill_tile_for`).
+    With ``head_dim`` given, the decode workspace for the query heads is
+    part of the step's one allocation.
     """
     device = _require_device(block_tables)
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
         raise ValueError("block_tables must be an int32 [B, max_blocks] tensor")
     if not block_tables.is_contiguous():
-        block_tables = block_tables.contiguous()
-    b = int(block_tables.shape[0])
-    if len(start_positions) != b or len(new_token_counts) != b:
+        raise ValueError("block_tables must be contiguous")
+    starts = _int64_array(start_positions)
+    counts = _int64_array(new_token_counts)
+    b = int(starts.shape[0])
+    if counts.shape[0] != b:
+        raise ValueError("start_positions / new_token_counts must have one entry per sequence")
+    if rows is None and b != int(block_tables.shape[0]):
         raise ValueError("start_positions / new_token_counts must have one entry per block-table row")
-    if any(s < 0 for s in start_positions) or any(c < 0 for c in new_token_counts):
-        raise ValueError("start positions and token counts must be non-negative")
+    hq = int(num_query_heads or 4 * num_kv_heads)
     if prefill_tile is None:
-        prefill_tile = prefill_tile_for(int(num_query_heads or 4 * num_kv_heads), int(num_kv_heads))
+        prefill_tile = prefill_tile_for(hq, int(num_kv_heads))
     if prefill_tile <= 0:
         raise ValueError("prefill_tile must be positive")
-    if partition_size is None:
-        per_item, per_cu = None, None
-        if head_dim is not None and dtype is not None:
-            hq = int(num_query_heads or 4 * num_kv_heads)
-            per_item = decode_workgroups_per_item(dtype, head_dim, num_kv_heads, hq) or None
-            with torch.cuda.device(device):  # the occupancy of the step's own device
-                per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq) or None
-        partition_size = choose_partition(
-            start_positions, new_token_counts, num_kv_heads, num_query_heads, per_item, per_cu,
-            torch.cuda.get_device_properties(device).multi_processor_count)
-    if partition_size <= 0:
+    if partition_size is not None and partition_size <= 0:
         raise ValueError("partition_size must be positive")
-    t, c, ditems, mitems, pitems, ndec, npre = work_counts(
-        start_positions, new_token_counts, partition_size, prefill_tile)
-    # Host lists go up from pinned buffers (torch's caching host allocator), so
-    # the copies are asynchronous: a pageable source would make the host wait
-    # for the stream to drain the previous step before the copy.
-    if start_positions_dev is None:
-        start_positions_dev = torch.tensor(list(start_positions), dtype=torch.int64,
-                                           pin_memory=True).to(device, non_blocking=True)
-    if new_token_counts_dev is None:
-        new_token_counts_dev = torch.tensor(list(new_token_counts), dtype=torch.int64,
-                                            pin_memory=True).to(device, non_blocking=True)
-    step = PackedStep(
-        block_tables=block_tables,
-        start_positions=start_positions_dev,
-        new_token_counts=new_token_counts_dev,
-        cu_seqlens=torch.empty(b + 1, dtype=torch.int64, device=device),
-        cu_context_offsets=torch.empty(b + 1, dtype=torch.int64, device=device),
-        context_lens=torch.empty(b, dtype=torch.int32, device=device),
-        scatter_slots=torch.empty(t, dtype=torch.int64, device=device),
-        position_ids=torch.empty(t, dtype=torch.int64, device=device),
-        decode_items=torch.empty((ditems, 2), dtype=torch.int32, device=device),
-        merge_items=torch.empty((mitems, 4), dtype=torch.int32, device=device),
-        prefill_items=torch.empty((pitems, 2), dtype=torch.int32, device=device),
-        block_size=int(block_size),
-        partition_size=int(partition_size),
-        prefill_tile=int(prefill_tile),
-        num_query_tokens=t,
-        num_context_tokens=c,
-        num_decode_items=ditems,
-        num_merge_items=mitems,
-        num_prefill_items=pitems,
-        num_decode_seqs=ndec,
-        num_prefill_seqs=npre,
-    )
-    step._gather_slots = _run_pack(step, with_gather=with_gather)
+    per_item = per_cu = 0
+    if partition_size is None and head_dim is not None and dtype is not None:
+        per_item = decode_workgroups_per_item(dtype, head_dim, num_kv_heads, hq)
+        with torch.cuda.device(device):  # the occupancy of the step's own device
+            per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq)
+    allocated = None if allocated_tokens is None else _int64_array(allocated_tokens)
+    plan = _plan(starts, counts, block_size, prefill_tile, partition_size or 0, num_kv_heads, hq, per_item,
+                 per_cu, _compute_units(device), allocated)
+    pooled = rows is not None
+    n_upd = 0 if updates is None else int(updates.shape[0])
+
+    # One host staging area and one device buffer per step.
+    inputs = _Layout()
+    inputs.add("start_positions", torch.int64, (b,))
+    inputs.add("new_token_counts", torch.int64, (b,))
+    if pooled:
+        inputs.add("rows", torch.int32, (b,))
+    if n_upd:
+        inputs.add("updates", torch.int32, (n_upd, 3))
+    layout = _Layout()
+    for name, (_, dt, shape) in inputs.fields.items():
+        layout.add(name, dt, shape)
+    assert layout.nbytes == inputs.nbytes
+    t, c = int(plan.num_query_tokens), int(plan.num_context_tokens)
+    if pooled:
+        layout.add("block_tables", torch.int32, (b, max(int(plan.max_blocks), 1)))
+    layout.add("cu_seqlens", torch.int64, (b + 1,))
+    layout.add("cu_context_offsets", torch.int64, (b + 1,))
+    layout.add("context_lens", torch.int32, (b,))
+    layout.add("scatter_slots", torch.int64, (t,))
+    layout.add("position_ids", torch.int64, (t,))
+    layout.add("decode_items", torch.int32, (int(plan.num_decode_items), 2))
+    layout.add("merge_items", torch.int32, (int(plan.num_merge_items), 4))
+    layout.add("prefill_items", torch.int32, (int(plan.num_prefill_items), 2))
+    lib = _native.load_library()
+    layout.add("pack_workspace", torch.uint8, (int(lib.pa_pack_workspace_size(b)),))
+    head_shape = None
+    if head_dim is not None:
+        head_shape = (hq, int(head_dim))
+        layout.add("decode_workspace", torch.uint8,
+                   (max(decode_workspace_bytes(int(plan.num_decode_items), hq, int(head_dim)), 1),))
+    buffer = torch.empty(layout.nbytes, dtype=torch.uint8, device=device)
+
+    stream = torch.cuda.current_stream(device)
+    staging = _staging(device)
+    slot, host, host_np = staging.take(inputs.nbytes)
+    host_np[inputs.fields["start_positions"][0] : inputs.fields["start_positions"][0] + 8 * b].view(
+        np.int64)[:] = starts
+    host_np[inputs.fields["new_token_counts"][0] : inputs.fields["new_token_counts"][0] + 8 * b].view(
+        np.int64)[:] = counts
+    if pooled:
+        off = inputs.fields["rows"][0]
+        host_np[off : off + 4 * b].view(np.int32)[:] = np.asarray(rows, dtype=np.int32).reshape(-1)
+    if n_upd:
+        off = inputs.fields["updates"][0]
+        host_np[off : off + 12 * n_upd].view(np.int32)[:] = np.ascontiguousarray(updates, dtype=np.int32).reshape(-1)
+    if inputs.nbytes:
+        buffer[: inputs.nbytes].copy_(host[: inputs.nbytes], non_blocking=True)
+    staging.done(slot, stream)
+
+    table_rows = int(block_tables.shape[0]) if block_tables.numel() else 0
+    step = PackedStep(buffer, layout, plan, block_size, prefill_tile, block_tables, table_rows,
+                      "rows" if pooled else None, head_shape)
+    upd_ptr = step.ptr("updates") if n_upd else 0
+    gather = _run_pack(step, with_gather=with_gather, updates_ptr=upd_ptr, num_updates=n_upd)
+    if with_gather:
+        step._gather = gather
     return step
 
 
@@ -473,6 +638,43 @@ def copy_blocks(src_cache: torch.Tensor, dst_cache: torch.Tensor, block_mapping)
     _native.check(status, "pa_copy_blocks")
 
 
+def swap_blocks(device_cache: torch.Tensor, host_cache: torch.Tensor, block_mapping, out: bool) -> None:
+    """Copy blocks between a device cache and a pinned host pool of the same
+    block shape, every layer in one launch (pa_swap_blocks): ``out`` copies
+    device -> host for (device block, host block) pairs, else host -> device
+    for (host block, device block) pairs.  Asynchronous on the current stream."""
+    if device_cache.dim() != 5 or host_cache.dim() != 5:
+        raise ValueError("caches must be 5-D (layers, blocks, block_size, heads, dim)")
+    if device_cache.dtype != host_cache.dtype or device_cache.shape[0] != host_cache.shape[0] or \
+            device_cache.shape[2:] != host_cache.shape[2:]:
+        raise ValueError("device cache and host pool differ in dtype, layer count or block shape")
+    if not (device_cache.is_contiguous() and host_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if host_cache.device.type != "cpu" or not host_cache.is_pinned():
+        raise ValueError("the host pool must be pinned host memory")
+    device = _require_device(device_cache)
+    mapping = torch.as_tensor(block_mapping, dtype=torch.int64).reshape(-1, 2)
+    if mapping.shape[0] == 0:
+        return
+    mapping = mapping.pin_memory().to(device, non_blocking=True)
+    block_bytes = device_cache[0, 0].numel() * device_cache.element_size()
+    lib = _native.load_library()
+    with torch.cuda.device(device):
+        status = lib.pa_swap_blocks(
+            device_cache.data_ptr(),
+            host_cache.data_ptr(),
+            mapping.data_ptr(),
+            int(mapping.shape[0]),
+            int(device_cache.shape[0]),
+            int(device_cache.shape[1]),
+            int(host_cache.shape[1]),
+            int(block_bytes),
+            _native.PA_SWAP_OUT if out else _native.PA_SWAP_IN,
+            _stream(device),
+        )
+    _native.check(status, "pa_swap_blocks")
+
+
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
     """Bytes pa_decode needs for its split-K partials: fp32 acc[items, H_q, D]
     and (max, sum)[items, H_q], each rounded up to 256 bytes."""
@@ -496,7 +698,7 @@ def _step_dims(query_t: torch.Tensor, key_cache: torch.Tensor, step: PackedStep)
         block_size=int(block_size),
         total_blocks=int(total_blocks),
         num_layers=int(num_layers),
-        max_blocks_per_seq=int(step.block_tables.shape[1]),
+        max_blocks_per_seq=step.table_width,
         partition_size=step.partition_size,
         dtype=dtype_code(key_cache.dtype),
         q_token_stride=query_t.stride(0),
@@ -524,7 +726,7 @@ def _check_attention_inputs(q: torch.Tensor, key_cache: torch.Tensor, value_cach
         raise ValueError("caches must be 5-D (layers, blocks, block_size, heads, dim) and alike")
     if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
         raise ValueError("caches must be contiguous")
-    if q.dtype != key_cache.dtype:
+    if q.dtype != key_cache.dtype or value_cache.dtype != key_cache.dtype:
         raise ValueError(f"query dtype {q.dtype} differs from cache dtype {key_cache.dtype}")
     num_kv_heads, head_dim = key_cache.shape[3], key_cache.shape[4]
     if q.shape[2] != head_dim:
@@ -553,6 +755,71 @@ def _output_for(q: torch.Tensor, key_cache: torch.Tensor, out: Optional[torch.Te
     return rows
 
 
+def _checked(query, key_cache, value_cache, step: PackedStep):
+    """([T, H_q, D] query view, launch dims) after the input checks.  The
+    checks and dims of the last call on ``step`` are kept, keyed by
+    everything they depend on, so the layers of a step after the first skip
+    them."""
+    q = _query_view(query)
+    key = (tuple(q.shape), q.stride(), q.dtype, q.device, key_cache.data_ptr(), value_cache.data_ptr(),
+           tuple(key_cache.shape), key_cache.dtype, value_cache.dtype)
+    cached = step.__dict__.get("_launch_key")
+    if cached is not None and cached[0] == key:
+        return q, cached[1]
+    _require_device(q, key_cache, value_cache, step.buffer)
+    _check_attention_inputs(q, key_cache, value_cache, step)
+    dims = _step_dims(q, key_cache, step)
+    step.__dict__["_launch_key"] = (key, dims)
+    return q, dims
+
+
+def _launch_decode(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, phases) -> None:
+    ws_ptr, ws_bytes = step.workspace_ptr(int(q.shape[1]), int(q.shape[2]))
+    lib = _native.load_library()
+    status = lib.pa_decode_phases(
+        int(phases),
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        step.ptr("block_tables"),
+        step.ptr("context_lens"),
+        step.ptr("cu_seqlens"),
+        step.ptr("decode_items") if step.num_decode_items else None,
+        step.num_decode_items,
+        step.ptr("merge_items") if step.num_merge_items else None,
+        step.num_merge_items,
+        float(scaling),
+        out.data_ptr(),
+        ws_ptr,
+        ws_bytes,
+        _stream(q.device),
+    )
+    _native.check(status, "pa_decode")
+
+
+def _launch_prefill(q, key_cache, value_cache, layer_idx, step, scaling, out, dims) -> None:
+    lib = _native.load_library()
+    status = lib.pa_prefill(
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        step.ptr("block_tables"),
+        step.ptr("context_lens"),
+        step.ptr("cu_seqlens"),
+        step.ptr("prefill_items") if step.num_prefill_items else None,
+        step.num_prefill_items,
+        step.prefill_tile,
+        float(scaling),
+        out.data_ptr(),
+        _stream(q.device),
+    )
+    _native.check(status, "pa_prefill")
+
+
 def decode(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -569,34 +836,9 @@ def decode(
     ``phases`` launches only the partition and/or the merge phase (a merge
     call must follow a partition call of the same step and workspace).
     """
-    q = _query_view(query)
-    device = _require_device(q, key_cache, value_cache, step.block_tables)
-    _check_attention_inputs(q, key_cache, value_cache, step)
+    q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
-    dims = _step_dims(q, key_cache, step)
-    ws = step.workspace(int(q.shape[1]), int(q.shape[2]), device)
-    lib = _native.load_library()
-    status = lib.pa_decode_phases(
-        int(phases),
-        q.data_ptr(),
-        key_cache.data_ptr(),
-        value_cache.data_ptr(),
-        int(layer_idx),
-        dims,
-        step.block_tables.data_ptr(),
-        step.context_lens.data_ptr(),
-        step.cu_seqlens.data_ptr(),
-        _ptr(step.decode_items),
-        step.num_decode_items,
-        _ptr(step.merge_items),
-        step.num_merge_items,
-        float(scaling),
-        out.data_ptr(),
-        ws.data_ptr(),
-        ws.numel(),
-        _stream(device),
-    )
-    _native.check(status, "pa_decode")
+    _launch_decode(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, phases)
     return out
 
 
@@ -610,29 +852,9 @@ def prefill(
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Causal chunked prefill for the multi-token sequences of ``step``."""
-    q = _query_view(query)
-    device = _require_device(q, key_cache, value_cache, step.block_tables)
-    _check_attention_inputs(q, key_cache, value_cache, step)
+    q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
-    dims = _step_dims(q, key_cache, step)
-    lib = _native.load_library()
-    status = lib.pa_prefill(
-        q.data_ptr(),
-        key_cache.data_ptr(),
-        value_cache.data_ptr(),
-        int(layer_idx),
-        dims,
-        step.block_tables.data_ptr(),
-        step.context_lens.data_ptr(),
-        step.cu_seqlens.data_ptr(),
-        _ptr(step.prefill_items),
-        step.num_prefill_items,
-        step.prefill_tile,
-        float(scaling),
-        out.data_ptr(),
-        _stream(device),
-    )
-    _native.check(status, "pa_prefill")
+    _launch_prefill(q, key_cache, value_cache, layer_idx, step, scaling, out, dims)
     return out
 
 
@@ -646,14 +868,13 @@ def attention(
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D]."""
-    q = _query_view(query)
-    _require_device(q, key_cache, value_cache)
-    _check_attention_inputs(q, key_cache, value_cache, step)
+    q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
     if step.num_prefill_items > 0:
-        prefill(q, key_cache, value_cache, layer_idx, step, scaling, out=out)
+        _launch_prefill(q, key_cache, value_cache, layer_idx, step, scaling, out, dims)
     if step.num_decode_items > 0:
-        decode(q, key_cache, value_cache, layer_idx, step, scaling, out=out)
+        _launch_decode(q, key_cache, value_cache, layer_idx, step, scaling, out, dims,
+                       _native.PA_DECODE_PHASE_PARTITIONS | _native.PA_DECODE_PHASE_MERGE)
     if step.num_query_tokens > 0 and step.num_decode_items == 0 and step.num_prefill_items == 0:
         out.zero_()
     return out

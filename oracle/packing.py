@@ -131,6 +131,10 @@ def copy_blocks(src: np.ndarray, dst: np.ndarray, mapping: Sequence[Tuple[int, i
             dst[:, d_blk] = src[:, s_blk]
 
 
+#: Length buckets that order the partial decode partitions.
+PARTIAL_BUCKETS = 64
+
+
 def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, prefill_tile: int
                ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Attention work lists the GPU packing kernel emits alongside the
@@ -138,7 +142,8 @@ def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, pre
 
     decode: (seq, partition) of single-token sequences -- every full
     partition first, by sequence then partition, then the partial last
-    partitions by decreasing length (ties by sequence);
+    partitions by decreasing length bucket, bucket = (length - 1) * 64 //
+    partition (ties by sequence);
     merge: (first full item, number of full partitions, seq, item of the
     partial partition or -1) of every sequence with more than one
     partition, by sequence;
@@ -154,7 +159,7 @@ def work_items(starts: Sequence[int], counts: Sequence[int], partition: int, pre
             full += [(i, p) for p in range(ctx // partition)]
             if ctx % partition:
                 rems.append((ctx % partition, i, ctx // partition))
-    rems.sort(key=lambda r: (-r[0], r[1]))
+    rems.sort(key=lambda r: (-(((r[0] - 1) * PARTIAL_BUCKETS) // partition), r[1]))
     rem_index = {seq: len(full) + k for k, (_, seq, _) in enumerate(rems)}
     dec = full + [(seq, p) for _, seq, p in rems]
     merge: List[Tuple[int, int, int, int]] = []

@@ -5,6 +5,7 @@ version and argument checks that return before any HIP call."""
 
 import ctypes
 import re
+import subprocess
 from pathlib import Path
 
 import pytest
@@ -35,11 +36,28 @@ def test_library_exports_every_declared_symbol():
     assert lib.pa_abi_version() == native.ABI_VERSION
 
 
-def test_struct_layouts():
+def test_struct_layouts(tmp_path):
+    """The ctypes mirrors match the header's structs field by field: a C
+    program built against the header prints every offset and size."""
     native = pkg("_native")
-    assert ctypes.sizeof(native.PagedAttentionDims) == 32
-    assert ctypes.sizeof(native.PaStepDims) == 12 * 4 + 2 * 8
-    assert ctypes.sizeof(native.PaPackDims) == 6 * 4 + 5 * 8
+    structs = {name: getattr(native, name) for name in
+               ("PagedAttentionDims", "PaStepDims", "PaPackDims", "PaPlanParams", "PaStepPlan")}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "paged_attention_amd.h"', "int main(void) {"]
+    for name, st in structs.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for field, _ in st._fields_:
+            lines.append(f'printf("{name}.{field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for name, st in structs.items():
+        assert int(got[name]) == ctypes.sizeof(st), name
+        for field, _ in st._fields_:
+            assert int(got[f"{name}.{field}"]) == getattr(st, field).offset, f"{name}.{field}"
 
 
 def test_error_strings():
@@ -74,8 +92,25 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == native.PA_ERR_INVALID_ARGUMENT and b"missing" in lib.pa_last_error_message()
     assert lib.pa_copy_blocks(None, None, None, 0, 1, 1, 1, 16, None) == native.PA_OK
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
-    rc = lib.pa_pack(None, None, None, pdims, None, None, None, None, None, None, None, None, None, None)
-    assert rc == native.PA_ERR_INVALID_ARGUMENT
+    args = [None] * 5 + [pdims] + [None] * 10 + [None, 0, None]
+    assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
+    pdims.block_size = 16
+    pdims.step_table_width = 4
+    fake = [0x1000 * (i + 1) for i in range(16)]
+    args = fake[:5] + [pdims] + fake[5:15] + [None, 0, None]
+    rc = lib.pa_pack(*args)
+    assert rc == native.PA_ERR_WORKSPACE and b"workspace of 528 bytes" in lib.pa_last_error_message()
+    assert lib.pa_pack_workspace_size(1) == 528 and lib.pa_pack_workspace_size(0) == 512
+    pdims.num_updates = 2
+    args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:15] + [fake[15], 4096, None]
+    assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
+    assert b"2 updates" in lib.pa_last_error_message()
+    for direction in (-1, 2):
+        rc = lib.pa_swap_blocks(None, None, None, 1, 1, 1, 1, 16, direction, None)
+        assert rc == native.PA_ERR_INVALID_ARGUMENT and b"direction" in lib.pa_last_error_message()
+    rc = lib.pa_swap_blocks(None, None, None, 1, 1, 1, 1, 16, native.PA_SWAP_OUT, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT and b"device_cache must not be NULL" in lib.pa_last_error_message()
+    assert lib.pa_swap_blocks(None, None, None, 0, 1, 1, 1, 16, native.PA_SWAP_IN, None) == native.PA_OK
 
 
 DECODE_POINTERS = ["query", "key_cache", "value_cache", "output", "block_tables", "context_lens", "cu_seqlens",

@@ -19,7 +19,7 @@ from oracle import packing as op
 paged_attention = pkg("model.paged_attention")
 backends = pkg("model.attention_backends")
 manager_mod = pkg("memory.manager")
-sequence_mod = pkg("scheduler.sequence")
+sequence_mod = pkg("engine.request")
 ops = pkg("paged_ops")
 
 NUM_LAYERS = 4
@@ -38,7 +38,7 @@ def store():
 def _prefill_step(store, prompt_lens):
     seqs = []
     for i, n in enumerate(prompt_lens):
-        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        seq = sequence_mod.Request(seq_id=i + 1, prompt_token_ids=list(range(n)))
         store.allocate_prefix_blocks(seq)
         seqs.append(seq)
     return seqs, paged_attention.PagedStepContext(store, seqs, [0] * len(seqs), list(prompt_lens))
@@ -185,7 +185,7 @@ def test_position_ids_prefill_and_decode(store):
     other = manager_mod.PagedKVCacheManager(total_blocks=8, block_size=BLOCK_SIZE, num_heads=NUM_KV_HEADS,
                                             head_dim=HEAD_DIM, num_layers=NUM_LAYERS, device="cpu")
     for i, n in enumerate([4, 2]):
-        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        seq = sequence_mod.Request(seq_id=i + 1, prompt_token_ids=list(range(n)))
         other.allocate_prefix_blocks(seq)
         other.allocate_slot_for_next_token(seq)
         seqs.append(seq)
@@ -241,18 +241,18 @@ def _kv_manager():
 
 def test_slot_mapping_requires_block_table():
     with pytest.raises(ValueError, match="no block table"):
-        _kv_manager().build_slot_mapping([sequence_mod.Sequence(seq_id=5, prompt_token_ids=[1])], [0], [1])
+        _kv_manager().build_slot_mapping([sequence_mod.Request(seq_id=5, prompt_token_ids=[1])], [0], [1])
 
 
 def test_single_token_write_requires_block_table():
     token = torch.zeros(1, 2, 8)
     with pytest.raises(ValueError, match="no block table"):
-        _kv_manager().write_single_token_kv(sequence_mod.Sequence(seq_id=4, prompt_token_ids=[1]), token, token)
+        _kv_manager().write_single_token_kv(sequence_mod.Request(seq_id=4, prompt_token_ids=[1]), token, token)
 
 
 def test_slot_mapping_range_and_length_errors():
     m = _kv_manager()
-    seq = sequence_mod.Sequence(seq_id=1, prompt_token_ids=[1, 2, 3, 4])
+    seq = sequence_mod.Request(seq_id=1, prompt_token_ids=[1, 2, 3, 4])
     m.allocate_prefix_blocks(seq)
     with pytest.raises(ValueError):
         m.build_slot_mapping([seq], [0], [5])
@@ -267,7 +267,7 @@ def test_manager_slots_and_tables_match_oracle():
     m = _kv_manager()
     seqs = []
     for i, n in enumerate([3, 7, 1]):
-        seq = sequence_mod.Sequence(seq_id=i + 1, prompt_token_ids=list(range(n)))
+        seq = sequence_mod.Request(seq_id=i + 1, prompt_token_ids=list(range(n)))
         m.allocate_prefix_blocks(seq)
         seqs.append(seq)
     lists = [s.block_table.get_physical_blocks() for s in seqs]
@@ -348,3 +348,86 @@ def test_output_checked_against_what_the_kernels_write():
         ops._output_for(q, cache, torch.empty(4, 5, 64, dtype=torch.bfloat16).transpose(0, 1))
     with pytest.raises(ValueError, match="is on"):
         ops._output_for(q, cache, torch.empty(5, 4, 64, dtype=torch.bfloat16, device="meta"))
+
+
+# ---- block-table pool and host swap bookkeeping -----------------------------
+
+alloc_mod = pkg("memory.block_allocator")
+
+
+def test_pool_rows_track_block_lists_and_queue_updates():
+    alloc = alloc_mod.PageAllocator(64, 4, 8, total_cpu_blocks=4)
+    pool = alloc_mod.BlockTablePool(rows=2, width=2)
+    a, b = alloc_mod.SequenceBlockTable(alloc, pool), alloc_mod.SequenceBlockTable(alloc, pool)
+    assert pool.take_updates()[0] is True  # a fresh pool is uploaded whole once
+    for _ in range(9):  # 3 blocks: the row grows past width 2
+        a.append_token()
+    b.append_token()
+    rebuild, upd = pool.take_updates()
+    assert rebuild and upd.shape == (0, 3)  # growth: rebuilt from the host rows
+    assert pool.host[a.row, :3].tolist() == a.get_physical_blocks()
+    assert pool.tokens[a.row] == 9 and pool.blocks[a.row] == 3
+    for _ in range(4):
+        a.append_token()  # tokens 10-13: block 4 at token 13
+    rebuild, upd = pool.take_updates()
+    assert not rebuild and upd.tolist() == [[a.row, 3, a.get_physical_blocks()[3]]]
+    c = alloc_mod.SequenceBlockTable(alloc, pool)  # a third row: the pool doubles its rows
+    assert pool.num_rows == 4 and c.row not in (a.row, b.row)
+    pool.take_updates()
+    row = a.row
+    a.release()
+    rebuild, upd = pool.take_updates()
+    assert not rebuild and sorted(upd.tolist()) == [[row, col, -1] for col in range(4)]
+    assert (pool.host[row] == -1).all() and pool.tokens[row] == 0
+    assert alloc.get_num_free_blocks() == 64 - 1  # b's block only
+
+
+def test_swap_bookkeeping_matches_reference_messages():
+    alloc = alloc_mod.PageAllocator(4, 4, 8, total_cpu_blocks=2)
+    blocks = alloc.allocate_blocks(3)
+    cpu = alloc.swap_out(blocks[0])
+    assert alloc.get_num_free_blocks() == 2 and alloc.get_num_free_cpu_blocks() == 1
+    assert alloc.get_cpu_block_id(blocks[0]) == cpu
+    alloc.share_block(blocks[1])
+    with pytest.raises(RuntimeError, match="ref_count != 1"):
+        alloc.swap_out(blocks[1])
+    alloc.swap_out(blocks[2])
+    alloc.allocate_block()
+    with pytest.raises(RuntimeError, match="Host RAM Block Pool exhausted"):
+        alloc.swap_out(alloc.allocate_block())
+    gpu = alloc.swap_in(cpu)
+    assert alloc.get_num_free_cpu_blocks() == 1 and 0 <= gpu < 4
+    with pytest.raises(RuntimeError, match="not currently swapped out"):
+        alloc.swap_in(cpu)
+    with pytest.raises(IndexError, match="CPU block ID out of range"):
+        alloc.release_swapped_block(7)
+    none = alloc_mod.PageAllocator(4, 4, 8, total_cpu_blocks=0)
+    with pytest.raises(RuntimeError, match="no host pool configured"):
+        none.swap_out(none.allocate_block())
+
+
+def test_swap_needs_a_device_store(store):
+    seqs, _ = _prefill_step(store, [4])
+    with pytest.raises(RuntimeError, match="device memory"):
+        store.swap_out(seqs[0])
+
+
+def test_cpu_store_slots_match_oracle_after_growth():
+    """Slots from the pool's host rows equal the oracle's per-sequence
+    formula, also after rows and columns grew."""
+    m = manager_mod.PagedKVCacheManager(total_blocks=400, block_size=4, num_heads=2, head_dim=8, device="cpu")
+    rng = __import__("numpy").random.default_rng(5)
+    seqs = []
+    for i in range(70):  # more rows than the pool starts with
+        seq = sequence_mod.Request(seq_id=i + 1, prompt_token_ids=list(range(int(rng.integers(1, 30)))))
+        m.allocate_prefix_blocks(seq)
+        seqs.append(seq)
+    lists = [s.block_table.get_physical_blocks() for s in seqs]
+    toks = [s.block_table.get_tokens_count() for s in seqs]
+    starts = [int(rng.integers(0, t)) for t in toks]
+    counts = [t - s for s, t in zip(starts, toks)]
+    got = m.build_slot_mapping(seqs, starts, counts)
+    assert got.tolist() == op.build_slot_mapping(lists, toks, 4, starts, counts).tolist()
+    table, lens = m.build_block_tables(seqs)
+    want_table, want_lens = op.build_block_tables(lists, toks)
+    assert table.tolist() == want_table.tolist() and lens.tolist() == want_lens.tolist()

@@ -8,7 +8,7 @@ from helpers import pkg
 
 metrics = pkg("metrics")
 manager_mod = pkg("memory.manager")
-sequence_mod = pkg("scheduler.sequence")
+sequence_mod = pkg("engine.request")
 
 
 class FakeEvent:
@@ -54,7 +54,7 @@ def test_metrics_text_has_the_reference_lines(monkeypatch):
     monkeypatch.delenv("LLM_PAGED_METRICS", raising=False)
     metrics.disable()
     mgr = manager_mod.PagedKVCacheManager(total_blocks=10, block_size=4, num_heads=2, head_dim=8, device="cpu")
-    seq = sequence_mod.Sequence(seq_id=1, prompt_token_ids=[1, 2, 3, 4, 5])
+    seq = sequence_mod.Request(seq_id=1, prompt_token_ids=[1, 2, 3, 4, 5])
     mgr.allocate_prefix_blocks(seq)
     text = metrics.metrics_text(mgr)
     lines = dict(line.split() for line in text.strip().splitlines())
@@ -82,7 +82,7 @@ def test_native_backend_records_attention(device):
     paged_attention._BACKEND = backends.NativePagedBackend()
     rec = metrics.enable()
     try:
-        seq = sequence_mod.Sequence(seq_id=1, prompt_token_ids=list(range(40)))
+        seq = sequence_mod.Request(seq_id=1, prompt_token_ids=list(range(40)))
         store.allocate_prefix_blocks(seq)
         ctx = paged_attention.PagedStepContext(store, [seq], [0], [40])
         with torch.inference_mode():

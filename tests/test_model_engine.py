@@ -33,7 +33,7 @@ transformers = pytest.importorskip("transformers")
 paged_attention = pkg("model.paged_attention")
 backends = pkg("model.attention_backends")
 manager_mod = pkg("memory.manager")
-sequence_mod = pkg("scheduler.sequence")
+sequence_mod = pkg("engine.request")
 
 BLOCK_SIZE = 16
 
@@ -86,21 +86,22 @@ class Reference:
         return exact, (own - exact).abs()
 
 
-class Engine:
-    """The reference engine's step loop (app/engine/llm_engine.py:175-204),
-    reduced to what the attention path needs: one flat forward per step over
-    any mix of prefill chunks and decodes."""
+class Stepper:
+    """Teacher-forced steps through the paged hook: one flat forward per step
+    over any mix of prefill chunks and decodes, on token streams fixed in
+    advance (the product engine, which feeds back its own tokens, is tested
+    below)."""
 
     def __init__(self, model, device, total_blocks=256):
         self.model = model
         self.device = device
         self.store = manager_mod.PagedKVCacheManager.from_model_config(
             model.config, total_blocks=total_blocks, block_size=BLOCK_SIZE, dtype=model.dtype, device=device)
-        paged_attention.register_paged_attention(model)
+        paged_attention.register_paged_attention(model, backend=paged_attention._BACKEND)
         self.next_id = 1
 
     def add(self, prompt):
-        seq = sequence_mod.Sequence(seq_id=self.next_id, prompt_token_ids=list(prompt))
+        seq = sequence_mod.Request(seq_id=self.next_id, prompt_token_ids=list(prompt))
         self.next_id += 1
         self.store.allocate_prefix_blocks(seq)
         return seq
@@ -150,7 +151,7 @@ def run_scenario(model, device, tol, prompts, decode_steps, late_prompt=None):
     torch.manual_seed(123)
     vocab = model.config.vocab_size
     streams = [list(p) + torch.randint(0, vocab, (decode_steps,)).tolist() for p in prompts]
-    eng = Engine(model, device)
+    eng = Stepper(model, device)
     reference = Reference(model, device, tol)
     seqs = [eng.add(p) for p in prompts]
     # step 0: all prompts prefilled together (ragged)
@@ -189,7 +190,7 @@ def test_cpu_cache_holds_history_for_every_layer(monkeypatch):
     # tests/correctness/test_paged_attention.py:87-119
     monkeypatch.setattr(paged_attention, "_BACKEND", None)
     model = tiny_llama(torch.float32, "cpu", layers=3)
-    eng = Engine(model, "cpu", total_blocks=32)
+    eng = Stepper(model, "cpu", total_blocks=32)
     prompt = list(range(1, 20))
     seq = eng.add(prompt)
     eng.step([(seq, 0, prompt)])
@@ -247,3 +248,113 @@ def test_gpu_engine_smollm_head_shape(native, monkeypatch):
     model = tiny_llama(torch.bfloat16, "cuda", heads=9, kv_heads=3)
     prompts = [list(range(3, 60)), [7, 1, 4], list(range(100, 230))]
     run_scenario(model, "cuda", None, prompts, decode_steps=4, late_prompt=list(range(50, 90)))
+
+
+# ---------------------------------------------------------------------------
+# The product engine: one forward per step, GPU argmax, HIP backend installed
+
+
+engine_mod = pkg("engine.llm_engine")
+
+
+def _generate(model, prompt, n, device):
+    """Greedy continuation by the model's own generate() (SDPA, its own cache)."""
+    impl = model.config._attn_implementation
+    model.config._attn_implementation = "sdpa"
+    try:
+        with torch.inference_mode():
+            ids = torch.tensor([prompt], device=device)
+            out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=n, do_sample=False,
+                                 pad_token_id=0)
+    finally:
+        model.config._attn_implementation = impl
+    return out[0, len(prompt):].tolist()
+
+
+def run_engine(model, device, prompts, late_prompt, max_tokens, total_blocks=256):
+    """Serve ``prompts`` (and ``late_prompt``, added after the second step so
+    that a prefill shares a step with decodes) through LLMEngine.step()."""
+    from fcfs import FcfsScheduler
+
+    store = manager_mod.PagedKVCacheManager.from_model_config(
+        model.config, total_blocks=total_blocks, block_size=BLOCK_SIZE, dtype=model.dtype, device=device)
+    engine = engine_mod.LLMEngine(store, FcfsScheduler(store), model=model)
+    calls = {"n": 0}
+    forward = model.forward
+
+    def counted(*args, **kwargs):
+        calls["n"] += 1
+        return forward(*args, **kwargs)
+
+    model.forward = counted
+    try:
+        eos = model.config.eos_token_id  # generate() stops there too
+        reqs = [engine.add_request(p, max_tokens=max_tokens, eos_token_id=eos) for p in prompts]
+        steps = mixed = 0
+        late = None
+        while engine.has_unfinished_requests():
+            if steps == 2 and late_prompt is not None:
+                late = engine.add_request(late_prompt, max_tokens=max_tokens, eos_token_id=eos)
+            before = calls["n"]
+            result = engine.step()
+            steps += 1
+            assert calls["n"] == before + 1, "one forward per step"
+            if late is not None and late in result["running"] and len(late.output_token_ids) == 1:
+                mixed += 1
+    finally:
+        model.forward = forward
+    assert engine.forward_passes == steps
+    if late_prompt is not None:
+        assert mixed == 1, "the late prompt was prefilled in a step with decodes"
+        reqs.append(late)
+    assert store.get_allocator().get_num_free_blocks() == total_blocks
+    return reqs, steps
+
+
+def test_cpu_engine_greedy_matches_generate(monkeypatch):
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    model = tiny_llama(torch.float32, "cpu")
+    prompts = [[5, 9, 2, 7, 1], [3, 3, 8], list(range(40, 75))]
+    late = [11, 12, 13, 14]
+    reqs, steps = run_engine(model, "cpu", prompts, late, max_tokens=6)
+    # the first prompts finish at step 6; the late one, prefilled at step 3, at step 8
+    assert steps == 8
+    for req, prompt in zip(reqs, prompts + [late]):
+        assert req.output_token_ids == _generate(model, prompt, 6, "cpu"), req.seq_id
+
+
+@pytest.mark.gpu
+def test_gpu_engine_greedy_matches_generate(monkeypatch):
+    """The product engine on an HBM store with no backend installed beforehand:
+    it installs the HIP backend itself, never runs dense SDPA, makes one
+    forward per step, and its greedy tokens equal the model's own generate()
+    (fp32 model: HIP decode and fp32 prefill kernels)."""
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+
+    def no_dense(*args, **kwargs):
+        raise AssertionError("dense SDPA ran on a GPU store")
+
+    monkeypatch.setattr(backends, "dense_sdpa", no_dense)
+    monkeypatch.setattr(backends.TorchSdpBackend, "attend", no_dense)
+    model = tiny_llama(torch.float32, "cuda")
+    prompts = [list(range(3, 40)), [7, 1, 4], list(range(100, 300)), [11] * 70]
+    late = list(range(50, 95))
+    reqs, _ = run_engine(model, "cuda", prompts, late, max_tokens=12)
+    assert isinstance(paged_attention._BACKEND, backends.NativePagedBackend)
+    for req, prompt in zip(reqs, prompts + [late]):
+        assert req.output_token_ids == _generate(model, prompt, 12, "cuda"), req.seq_id
+
+
+@pytest.mark.gpu
+def test_gpu_engine_bf16_long_context(monkeypatch):
+    """bf16 GQA heads of 128 with a 2500-token prompt (split-K decode): the
+    engine's first token equals generate()'s, and every step is one forward."""
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    monkeypatch.setattr(backends, "dense_sdpa", lambda *a, **k: (_ for _ in ()).throw(AssertionError("dense")))
+    model = tiny_llama(torch.bfloat16, "cuda", head_dim=128)
+    torch.manual_seed(7)
+    prompt = torch.randint(0, 512, (2500,)).tolist()
+    reqs, _ = run_engine(model, "cuda", [prompt, prompt[:300]], None, max_tokens=4, total_blocks=512)
+    for req, p in zip(reqs, [prompt, prompt[:300]]):
+        assert 1 <= len(req.output_token_ids) <= 4
+        assert req.output_token_ids[0] == _generate(model, p, 1, "cuda")[0]

@@ -148,6 +148,15 @@ def test_work_items():
     assert dec.tolist() == [[1, 0], [2, 0], [2, 1], [5, 0], [5, 1], [1, 1], [2, 2], [4, 0]]
     assert merge.tolist() == [[0, 1, 1, 5], [1, 2, 2, 6], [3, 2, 5, -1]]
     assert pre.tolist() == [[0, q] for q in range(10)] + [[3, 0]]
+    # partials of 73 and 79 tokens share a bucket ((r - 1) * 64 // 512 = 9):
+    # the earlier sequence goes first although it is shorter; 89 (bucket 11)
+    # and 88 (bucket 10) lead, 8 (bucket 0) ends the launch
+    dec, merge, _ = op.work_items([72, 78, 7, 87, 600], [1, 1, 1, 1, 1], 512, 32)
+    assert dec.tolist() == [[4, 0], [4, 1], [3, 0], [0, 0], [1, 0], [2, 0]]
+    assert merge.tolist() == [[0, 1, 4, 1]]
+    # with partitions of 64 tokens every length is its own bucket
+    dec, _, _ = op.work_items([40, 62, 9], [1, 1, 1], 64, 32)
+    assert dec.tolist() == [[1, 0], [0, 0], [2, 0]]
 
 
 @pytest.mark.parametrize("seed", range(3))
@@ -162,7 +171,12 @@ def test_work_items_cover_every_partition_once(seed):
                   for p in range(-(-(s + c) // part)))
     assert sorted(map(tuple, dec.tolist())) == want
     length = [min(part, starts[s] + 1 - p * part) for s, p in dec.tolist()]
-    assert length == sorted(length, reverse=True)
+    bucket = [64 if n == part else (n - 1) * 64 // part for n in length]
+    assert bucket == sorted(bucket, reverse=True)
+    # ties within a bucket keep sequence order
+    for k in range(len(dec) - 1):
+        if bucket[k] == bucket[k + 1] and bucket[k] < 64:
+            assert dec[k][0] < dec[k + 1][0]
     for first, nfull, seq, rem in merge.tolist():
         items = [tuple(x) for x in dec[first : first + nfull].tolist()] + ([tuple(dec[rem])] if rem >= 0 else [])
         assert items == [(seq, p) for p in range(-(-(starts[seq] + 1) // part))]
