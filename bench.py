@@ -1,27 +1,40 @@
-"""Paged-attention decode benchmark on one MI355X.
+"""Paged-attention benchmark on one MI355X.
 
-Workload (default): Llama-3-8B-shaped GQA decode, bf16 -- 256 sequences,
-32 query / 8 KV heads, head_dim 128, block size 16, contexts
+Headline workload: Llama-3-8B-shaped GQA decode, bf16 -- 256 sequences, 32
+query / 8 KV heads, head_dim 128, block size 16, contexts
 clip(round(lognormal(ln 1024, 1.0)), 32, 8192), random non-contiguous block
 tables, N(0,1) synthetic values.  A "step" is one decode pass of one layer
 over the batch (the HIP split-K partition kernel + its merge kernel), with
 the batch already packed and resident in HBM.
 
-value   = algorithmic KV-read GB/s = decode bytes / mean step time, where
-          decode bytes = sum_i ctx_i * 2 * H_kv * D * 2 (K+V read once per
-          KV head) + q and out rows + block-table entries + context lengths;
+value    = algorithmic KV-read GB/s = decode bytes / mean step time, where
+           decode bytes = sum_i ctx_i * 2 * H_kv * D * 2 (K+V read once per
+           KV head) + q and out rows + block-table entries + context lengths;
 tokens/s = sequences / mean step time (one token per sequence per layer).
-roofline = the dominant kernel (the split-K partition kernel), its
-          algorithmic bytes over its own launch time, measured with HIP
-          events around each partition launch on its stream; traffic = its
-          HBM bytes per launch from the committed rocprofv3 PMC summary.
-Also reported: the full step time (GPU packing + K/V write of the step's
-tokens + attention), the reference CPU kernel timed on a bounded sample of
-the same workload on this host's cores, and for --workload mixed_step (prefill +
-decode step) the prefill kernel's TFLOP/s against the bf16 MFMA peak.
+roofline = the dominant kernel (the split-K partition kernel): its
+           algorithmic bytes over its own launch time, measured with HIP
+           events around each partition launch on its stream; traffic = its
+           HBM bytes per launch from the committed rocprofv3 PMC summary.
+Also on the line:
+  full_step_ms   a whole step through the product path, host included: the
+                 step context built on an HBM store (checks, plan, one
+                 upload, the two packing launches), the K/V write of the
+                 step's tokens, and the attention;
+  host_step_us   the host time of building that step context (median), for
+                 this workload and the mixed step;
+  graph_step_ms  the decode step replayed from a HIP graph, timed in
+                 alternation with the eager loop (graph_vs_eager);
+  configs        the other workloads' lines: fp32 MHA decode and the K/V
+                 write + packing step timed over rotated pool copies (their
+                 data would otherwise sit in the 256 MB MALL), Llama-7B MHA
+                 decode, and the mixed prefill + decode step (decode GB/s,
+                 tokens/s, the prefill kernel's TFLOP/s against the bf16 MFMA
+                 peak), each with its CPU baseline on a bounded sample;
+  cpu_baseline   the reference CPU kernel on a bounded sample of the same
+                 workload on this host's cores.
 
-python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
-                [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step]
+python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs]
+                [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack]
 """
 
 from __future__ import annotations
@@ -41,6 +54,7 @@ PACKAGE = "low-latency-distributed-llm-serving-infrastructure-custom-k8s-control
 METRIC = "paged-attn decode KV-read GB/s (% HBM peak) + decode tokens/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
 
 
 def pkg(sub):
@@ -58,11 +72,38 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(w, t, budget_s: float):
-    """Reference kernel (oracle/_ref) per sequence on fp32 up-casts of the
-    same values.  Sequences are taken in order until ~budget_s/6 seconds of
-    kernel time (a bounded sample), then that sample is timed once more as a
-    warm-up plus five times; the median pass is reported."""
+def host_desc() -> str:
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return f"host {cpu_model()}, nproc {os.cpu_count()}, OMP_NUM_THREADS {threads}"
+
+
+def median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+# ---------------------------------------------------------------------------
+# CPU baselines (the reference kernel, or the oracle where it is not built)
+
+
+def _kv_of(w, t, i):
+    import numpy as np
+    import torch
+
+    blocks = torch.tensor(w.block_lists[i], dtype=torch.long, device=t.key_cache.device)
+    k = t.key_cache[:, blocks].float().cpu().numpy()
+    v = t.value_cache[:, blocks].float().cpu().numpy()
+    slots = np.arange(len(w.block_lists[i]) * w.block_size, dtype=np.int64)[: w.context_lens[i]]
+    return k, v, slots
+
+
+def cpu_baseline_per_sequence(w, t, budget_s: float, which: str = "decode"):
+    """The reference kernel, one call per sequence (decode: T=1, all-ones
+    mask; prefill chunk: causal-offset mask), on fp32 up-casts of the same
+    values.  Sequences of the kind asked for are taken in order until about
+    budget_s / 6 seconds of kernel time (a bounded sample), then the sample
+    is timed once more as a warm-up plus five times; the median pass is
+    reported, with GB/s over the same algorithmic bytes as the GPU's."""
     import numpy as np
     import torch
 
@@ -70,58 +111,178 @@ def cpu_baseline(w, t, budget_s: float):
 
     kind = "reference" if oa.reference_available() else "port"
     q_all = t.query[0].transpose(0, 1)
-    e = 2 if w.dtype == torch.bfloat16 else 4
-    qbase = np.concatenate([[0], np.cumsum(w.new_token_counts)])  # first query token of each sequence
+    e = 2 if w.dtype != torch.float32 else 4
+    qbase = np.concatenate([[0], np.cumsum(w.new_token_counts)])
     sample, spent = [], 0.0
     for i in range(w.num_seqs):
-        if w.new_token_counts[i] != 1:
-            continue  # decode sequences only (a mixed step's prefill chunks are not decode work)
-        blocks = torch.tensor(w.block_lists[i], dtype=torch.long, device=t.key_cache.device)
-        k = t.key_cache[:, blocks].float().cpu().numpy()
-        v = t.value_cache[:, blocks].float().cpu().numpy()
-        ctx = w.context_lens[i]
-        slots = np.arange(len(w.block_lists[i]) * w.block_size, dtype=np.int64)[:ctx]
-        q = q_all[qbase[i] : qbase[i] + 1].float().cpu().numpy().transpose(1, 0, 2)
-        _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [w.start_positions[i]], [1], slots, w.scaling,
+        n = w.new_token_counts[i]
+        if (which == "decode") != (n == 1) or n == 0:
+            continue
+        k, v, slots = _kv_of(w, t, i)
+        q = q_all[qbase[i] : qbase[i] + n].float().cpu().numpy().transpose(1, 0, 2)
+        _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [w.start_positions[i]], [n], slots, w.scaling,
                                                   kind=kind)
-        sample.append((q, k, v, slots, w.start_positions[i], ctx))
+        sample.append((q, k, v, slots, w.start_positions[i], n))
         spent += secs
         if spent >= budget_s / 6:
             break
     passes = []
     for _ in range(5):
         total = 0.0
-        for q, k, v, slots, start, _ in sample:
-            _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [start], [1], slots, w.scaling, kind=kind)
+        for q, k, v, slots, start, n in sample:
+            _, secs = oa.paged_attention_per_sequence(q, k, v, 0, [start], [n], slots, w.scaling, kind=kind)
             total += secs
         passes.append(total)
-    med = sorted(passes)[len(passes) // 2]
-    nbytes = sum(c * 2 * w.num_kv_heads * w.head_dim * e + w.num_query_heads * w.head_dim * 2 * e
-                 for *_, c in sample)
+    med = median(passes)
+    ctx_tokens = sum(s + n for *_, s, n in sample)
+    nbytes = sum((s + n) * 2 * w.num_kv_heads * w.head_dim * e + n * w.num_query_heads * w.head_dim * 2 * e
+                 for *_, s, n in sample)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    total_kind = sum(1 for c in w.new_token_counts if (which == "decode") == (c == 1) and c > 0)
+    return {
+        "value": round(nbytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "tokens_per_s": round(sum(n for *_, n in sample) / med, 2),
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"first {len(sample)} of {total_kind} {which} sequences ({ctx_tokens} context tokens), one call "
+                   f"per sequence ({'T=1, all-ones mask' if which == 'decode' else 'causal-offset mask'}; OpenMP "
+                   f"parallelism capped at T*H_q rows), "
+                   f"{'fp32 up-casts of the 16-bit' if e == 2 else 'the fp32'} values, median of 5 passes after a "
+                   f"warm-up ({med:.3f} s/pass kernel time, steady_clock around the C call); {host_desc()}"),
+    }
+
+
+def cpu_baseline_flat(w, t):
+    """The reference's native-backend call for the whole step: one flat call
+    with the T x C uint8 mask (app/model/attention_backends.py:97-117)."""
+    import numpy as np
+
+    from oracle import attention as oa
+    from oracle import packing as op
+
+    kind = "reference" if oa.reference_available() else "port"
+    q = t.query.float().cpu().numpy()
+    k = t.key_cache.float().cpu().numpy()
+    v = t.value_cache.float().cpu().numpy()
+    slots = op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size, [0] * w.num_seqs,
+                                  w.context_lens).astype(np.int32)
+    mask = op.attention_mask(w.start_positions, w.new_token_counts).astype(np.uint8)
+    times = []
+    for _ in range(6):
+        t0 = time.perf_counter()
+        oa.paged_attention(q, k, v, 0, slots, mask, w.scaling, kind=kind)
+        times.append(time.perf_counter() - t0)
+    med = median(times[1:])
+    wl = pkg("workloads")
+    nbytes = wl.decode_bytes(w)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {
         "value": round(nbytes / med / 1e9, 4),
         "unit": "GB/s",
-        "tokens_per_s": round(len(sample) / med, 2),
+        "tokens_per_s": round(w.num_query_tokens / med, 2),
         "cores": threads,
         "kind": kind,
-        "sample": (f"first {len(sample)} of {sum(1 for c in w.new_token_counts if c == 1)} decode sequences "
-                   f"({sum(c for *_, c in sample)} context tokens), "
-                   f"one call per sequence (T=1, all-ones mask; OpenMP parallelism capped at T*H_q="
-                   f"{w.num_query_heads} rows), {'fp32 up-casts of the bf16' if e == 2 else 'the fp32'} values, "
-                   f"median of 5 passes after a "
-                   f"warm-up ({med:.2f} s/pass kernel time, steady_clock around the C call); "
-                   f"host {cpu_model()}, nproc {os.cpu_count()}, OMP_NUM_THREADS {threads}"),
+        "sample": (f"the whole step ({w.num_seqs} sequences, {w.num_context_tokens} context tokens): one flat call "
+                   f"with the T x C mask, as the reference's native backend makes it; median of 5 after a warm-up "
+                   f"({med * 1e3:.3f} ms, wall clock around the call); {host_desc()}"),
     }
+
+
+# ---------------------------------------------------------------------------
+# GPU timing helpers
+
+
+def graph_ms(fn, reps, warmup, stream):
+    """Per-call time of `reps` back-to-back calls captured in one HIP graph
+    and replayed between two events: microsecond launches are timed without
+    host launch gaps."""
+    import torch
+
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(reps):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def graph_vs_eager_ms(fn, steps, stream, rounds=3):
+    """(eager ms, graph ms) per call: `steps` eager calls and a replay of the
+    same `steps` calls captured in one HIP graph, alternated `rounds` times;
+    medians.  Alternating matters: the GPU's clock drifts over a run, so a
+    graph timed after the eager loop reads slower for reasons of its own."""
+    import torch
+
+    fn(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    eager, replay = [], []
+    for _ in range(rounds):
+        eager.append(timed_ms(lambda: fn(0), steps, 0, stream))
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        replay.append(a.elapsed_time(b) / steps)
+    return median(eager), median(replay)
+
+
+def timed_ms(fn, steps, warmup, stream):
+    """Mean time of `steps` eager calls between two events after `warmup`."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def events_ms(launch, timed, steps, warmup, stream):
+    """Average duration of the launches `timed()` issues, bracketed by HIP
+    events on the launch stream, with `launch()` issued around them."""
+    import torch
+
+    pairs = []
+    for i in range(warmup + steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        timed()
+        b.record(stream)
+        launch()
+        if i >= warmup:
+            pairs.append((a, b))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
 
 
 def measured_traffic(workload: str):
     """HBM bytes per launch of the dominant kernel on `workload`, from the
     committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled
     by what the counter reads for a copy of known size); None if absent."""
-    path = REPO / "profiles" / "pmc_traffic.json"
     try:
-        table = json.loads(path.read_text())
+        table = json.loads((REPO / "profiles" / "pmc_traffic.json").read_text())
     except (OSError, ValueError):
         return None
     entry = table.get(workload)
@@ -143,123 +304,6 @@ def workload_config(w, **extra):
     return cfg
 
 
-def bench_kv_write_pack(args, w, t, device):
-    """The integer side of a step: the GPU packing kernel over the step's
-    block tables plus the K/V write of its new tokens (32 sequences: 24
-    decodes and 8 prompts of 64-256 tokens, 32 KV heads, D 128, bf16).
-
-    value   = algorithmic GB/s of the step: new K and V rows read + cache
-              rows written (4 * T * H_kv * D * 2 bytes) + the int64 slots
-              read by the write and the packing outputs written;
-    roofline = the K/V write kernel alone, timed with HIP events;
-    cpu_baseline = the NumPy restatement (slot mapping + scatter) on the same
-              step, one host thread."""
-    import time
-
-    import numpy as np
-    import torch
-
-    from oracle import packing as op
-
-    ops = pkg("paged_ops")
-    table = torch.from_numpy(w.block_table_array()).to(device)
-    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
-                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
-    stream = torch.cuda.current_stream(device)
-    e = t.new_keys.element_size()
-    T, B = w.num_query_tokens, w.num_seqs
-    write_bytes = 4 * T * w.num_kv_heads * w.head_dim * e + 8 * T
-    pack_bytes = (8 * 2 + 8 * 2) * B + 16 * T + 4 * B + 4 * table.numel()
-    total = write_bytes + pack_bytes
-
-    def write():
-        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
-
-    def step_fn():
-        ops._run_pack(step)
-        write()
-
-    ms = graph_ms(step_fn, args.steps, args.warmup, stream)
-    kms = graph_ms(write, args.steps, args.warmup, stream)
-    result = {
-        "metric": "paged KV write + ragged packing GB/s (% HBM peak), 1 GPU",
-        "value": round(total / (ms * 1e-3) / 1e9, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) K/V, random non-contiguous block tables)",
-        "config": workload_config(w),
-        "timing": "HIP graph of back-to-back steps replayed between two events",
-        "tokens_per_s": round(T / (ms * 1e-3), 1),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "cache_write_vec_kernel",
-            "achieved": round(write_bytes / (kms * 1e-3) / 1e9, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(write_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel_ms": round(kms, 5),
-            "algorithmic_bytes": write_bytes,
-        },
-    }
-    if not args.no_cpu_baseline:
-        ctx = [s + c for s, c in zip(w.start_positions, w.new_token_counts)]
-        shape = (1, w.total_blocks, w.block_size, w.num_kv_heads, w.head_dim)
-        kcache, vcache = np.zeros(shape, dtype=np.uint16), np.zeros(shape, dtype=np.uint16)
-        krows = t.new_keys.view(torch.int16).cpu().numpy().view(np.uint16)
-        vrows = t.new_values.view(torch.int16).cpu().numpy().view(np.uint16)
-        passes = []
-        for _ in range(6):
-            t0 = time.perf_counter()
-            slots = op.build_slot_mapping(w.block_lists, ctx, w.block_size, w.start_positions, w.new_token_counts)
-            op.cumulative_offsets(w.new_token_counts)
-            op.scatter_layer_kv(kcache, 0, krows, slots)
-            op.scatter_layer_kv(vcache, 0, vrows, slots)
-            passes.append(time.perf_counter() - t0)
-        med = sorted(passes[1:])[2]
-        result["cpu_baseline"] = {
-            "value": round(total / med / 1e9, 4),
-            "unit": "GB/s",
-            "tokens_per_s": round(T / med, 1),
-            "cores": 1,
-            "kind": "port",
-            "sample": (f"the whole step ({T} new tokens of {B} sequences): NumPy slot mapping + cu_seqlens + "
-                       f"K and V scatter into a host cache, median of 5 passes after a warm-up "
-                       f"({med * 1e3:.2f} ms/pass); host {cpu_model()}"),
-        }
-    return result
-
-
-def graph_ms(fn, reps, warmup, stream):
-    """Per-call time of `reps` back-to-back calls captured in one HIP graph
-    and replayed between two events: microsecond launches are timed without
-    host launch gaps."""
-    import torch
-
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(reps):
-            fn()
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    graph.replay()
-    b.record(stream)
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps
-
-
 def calibrate_copy(device, nbytes: int = 1 << 30, reps: int = 5) -> None:
     """A plain device-to-device copy of known size (for scaling the PMC
     FETCH_SIZE / WRITE_SIZE counters of the profiled kernels)."""
@@ -274,6 +318,347 @@ def calibrate_copy(device, nbytes: int = 1 << 30, reps: int = 5) -> None:
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# the product path's step: an HBM store, its row pool and the step context
+
+
+def build_store(w, device, seed=0):
+    """An HBM store holding the workload's sequences (blocks from the pool's
+    own allocator), random cache contents, and the step's new K/V rows."""
+    import torch
+
+    mm = pkg("memory.manager")
+    rq = pkg("engine.request")
+    store = mm.PagedKVCacheManager(total_blocks=w.total_blocks, block_size=w.block_size, num_heads=w.num_kv_heads,
+                                   head_dim=w.head_dim, dtype=w.dtype, num_layers=1, device=device)
+    store.num_query_heads = w.num_query_heads
+    seqs = []
+    for i, ctx in enumerate(w.context_lens):
+        seq = rq.Request(i + 1, [0] * ctx)
+        store.allocate_prefix_blocks(seq)
+        seqs.append(seq)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    for cache in (store.key_cache, store.value_cache):
+        cache.copy_(torch.randn(cache.shape, generator=gen, device=device).to(w.dtype))
+    return store, seqs
+
+
+def host_step_us(store, seqs, w, reps=200):
+    """Median host time of building the step context (no device sync inside)."""
+    import torch
+
+    pa = pkg("model.paged_attention")
+    starts, counts = list(w.start_positions), list(w.new_token_counts)
+    for _ in range(5):
+        pa.PagedStepContext(store, seqs, starts, counts)
+    torch.cuda.synchronize()
+    times = []
+    for i in range(reps):
+        t0 = time.perf_counter()
+        pa.PagedStepContext(store, seqs, starts, counts)
+        times.append(time.perf_counter() - t0)
+        if i % 50 == 49:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return round(median(times) * 1e6, 1)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+
+
+def decode_main(args, w, t, device):
+    """The headline decode line (cfg 4 by default; cfg 3 with --workload)."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    pa = pkg("model.paged_attention")
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                         dtype=w.dtype)
+    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def decode_step():
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+
+    # The per-launch kernel timing runs first, after 500 untimed launches
+    # (about 0.15 s): they bring the GPU from idle to its steady clock, which
+    # a few warm-up steps alone do not.  The step is then timed after its W
+    # warm-ups.
+    kernel_ms = events_ms(
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
+        args.steps, max(args.warmup, 500), stream)
+    ms = timed_ms(decode_step, args.steps, args.warmup, stream)
+    eager_alt, graph_step = graph_vs_eager_ms(lambda i: decode_step(), args.steps, stream)
+
+    # The whole step through the product path on an HBM store.
+    store, seqs = build_store(w, device)
+    new_k = t.new_keys
+    new_v = t.new_values
+    sout = torch.empty_like(out)
+
+    def full_step():
+        ctx = pa.PagedStepContext(store, seqs, w.start_positions, w.new_token_counts)
+        store.scatter_layer_kv(0, new_k, new_v, ctx.scatter_slots)
+        ops.attention(t.query, store.key_cache, store.value_cache, 0, ctx.packed, w.scaling, out=sout)
+
+    full_ms = timed_ms(full_step, args.steps, args.warmup, stream)
+    host_us = host_step_us(store, seqs, w)
+    del store, seqs
+
+    kv_bytes = wl.decode_bytes(w)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else ("fp16" if w.dtype == torch.float16 else "fp32"),
+        "data": "synthetic (seeded N(0,1) K/V/Q, random non-contiguous block tables)",
+        "config": workload_config(w, partition=step.partition_size),
+        "tokens_per_s": round(w.num_query_tokens / (ms * 1e-3), 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "full_step_ms": round(full_ms, 5),
+        "full_step_gbs": round(kv_bytes / (full_ms * 1e-3) / 1e9, 2),
+        "host_step_us": {w.name: host_us},
+        "graph_step_ms": round(graph_step, 5),
+        "graph_vs_eager": {"graph_ms": round(graph_step, 5), "eager_ms": round(eager_alt, 5),
+                           "timing": "3 alternating rounds of the eager loop and a replay of it captured in a "
+                                     "HIP graph, medians"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_partition_kernel",
+            "achieved": round(kernel_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(w.name),
+            "kernel_ms": round(kernel_ms, 5),
+            "algorithmic_bytes": kv_bytes,
+        },
+    }
+
+
+def rotated_copies(nbytes_per_copy: int) -> int:
+    """Copies of a working set that together exceed the MALL twice over."""
+    return max(4, -(-2 * MALL_BYTES // max(nbytes_per_copy, 1)))
+
+
+def decode_rotated(args, w, device):
+    """A launch-bound decode (cfg 1) timed from a HIP graph over R copies of
+    the pool, one per launch, so no launch finds its K/V in the MALL."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    kv_bytes = wl.decode_bytes(w)
+    copies = rotated_copies(kv_bytes)
+    tensors = [wl.make_tensors(w, device, seed=s) for s in range(copies)]
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, num_kv_heads=w.num_kv_heads,
+                         num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
+    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def call(i):
+        t = tensors[i % copies]
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+
+    reps = copies * max(1, args.steps // copies + 1)
+    ms = graph_ms(call, reps, 3, stream)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "ms_per_step": round(ms, 5), "tokens_per_s": round(w.num_query_tokens / (ms * 1e-3), 1),
+        "dtype": "fp32", "partition": step.partition_size,
+        "timing": f"HIP graph of {reps} decode steps over {copies} rotated pool copies (MALL 256 MB)",
+        "config": workload_config(w),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_flat(w, tensors[0])
+    return line
+
+
+def kv_write_pack_line(args, w, device):
+    """cfg 2: the packing kernels over the step's block tables plus the K/V
+    write of its new tokens, timed from a HIP graph over R rotated copies of
+    the new rows and the cache."""
+    import numpy as np
+    import torch
+
+    from oracle import packing as op
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads)
+    e = 2
+    T, B = w.num_query_tokens, w.num_seqs
+    write_bytes = 4 * T * w.num_kv_heads * w.head_dim * e + 8 * T
+    pack_bytes = (8 * 2 + 8 * 2) * B + 16 * T + 4 * B + 4 * table.numel()
+    total = write_bytes + pack_bytes
+    copies = rotated_copies(write_bytes)
+    tensors = [wl.make_tensors(w, device, seed=s) for s in range(copies)]
+    stream = torch.cuda.current_stream(device)
+
+    def write(i):
+        t = tensors[i % copies]
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+
+    def step_fn(i):
+        ops._run_pack(step)
+        write(i)
+
+    reps = copies * max(1, args.steps // copies + 1)
+    ms = graph_ms(step_fn, reps, 3, stream)
+    kms = graph_ms(write, reps, 3, stream)
+    line = {
+        "metric": "paged KV write + ragged packing GB/s (% HBM peak), 1 GPU",
+        "value": round(total / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+        "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "ms_per_step": round(ms, 5), "tokens_per_s": round(T / (ms * 1e-3), 1), "dtype": "bf16",
+        "timing": f"HIP graph of {reps} steps over {copies} rotated copies of the new K/V rows and the cache "
+                  f"(MALL 256 MB)",
+        "config": workload_config(w),
+        "roofline": {
+            "bound": "hbm", "kernel": "cache_write_vec_kernel",
+            "achieved": round(write_bytes / (kms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(write_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel_ms": round(kms, 5),
+            "algorithmic_bytes": write_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        t = tensors[0]
+        ctx = w.context_lens
+        shape = (1, w.total_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+        kcache, vcache = np.zeros(shape, dtype=np.uint16), np.zeros(shape, dtype=np.uint16)
+        krows = t.new_keys.view(torch.int16).cpu().numpy().view(np.uint16)
+        vrows = t.new_values.view(torch.int16).cpu().numpy().view(np.uint16)
+        passes = []
+        for _ in range(6):
+            t0 = time.perf_counter()
+            slots = op.build_slot_mapping(w.block_lists, ctx, w.block_size, w.start_positions, w.new_token_counts)
+            op.cumulative_offsets(w.new_token_counts)
+            op.scatter_layer_kv(kcache, 0, krows, slots)
+            op.scatter_layer_kv(vcache, 0, vrows, slots)
+            passes.append(time.perf_counter() - t0)
+        med = median(passes[1:])
+        line["cpu_baseline"] = {
+            "value": round(total / med / 1e9, 4), "unit": "GB/s", "tokens_per_s": round(T / med, 1),
+            "cores": 1, "kind": "port",
+            "sample": (f"the whole step ({T} new tokens of {B} sequences): NumPy slot mapping + cu_seqlens + K and V "
+                       f"scatter into a host cache, median of 5 passes after a warm-up ({med * 1e3:.2f} ms/pass); "
+                       f"{host_desc()}"),
+        }
+    return line
+
+
+def decode_config_line(args, w, t, device):
+    """cfg 3 inside `configs`: the decode step, its partition kernel and the
+    CPU baseline (the pool, 2.2 GB, is far larger than the MALL)."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, num_kv_heads=w.num_kv_heads,
+                         num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
+    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+    kernel_ms = events_ms(
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
+        args.steps, 100, stream)
+    ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                  args.steps, args.warmup, stream)
+    kv_bytes = wl.decode_bytes(w)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "ms_per_step": round(ms, 5), "tokens_per_s": round(w.num_query_tokens / (ms * 1e-3), 1), "dtype": "bf16",
+        "partition": step.partition_size, "config": workload_config(w),
+        "roofline": {"bound": "hbm", "kernel": "decode_partition_kernel",
+                     "achieved": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kv_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "kernel_ms": round(kernel_ms, 5), "algorithmic_bytes": kv_bytes},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2)
+    return line
+
+
+def mixed_line(args, w, t, device):
+    """cfg 5: four 512-token prefill chunks + 128 long-context decodes in one
+    flattened step: the attention step (prefill + split-K decode), the whole
+    step with packing and the K/V write, the decode kernel's GB/s, and the
+    prefill kernel's TFLOP/s against the bf16 MFMA peak."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                         dtype=w.dtype)
+    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+    ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                  args.steps, args.warmup, stream)
+    decode_kernel_ms = events_ms(
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
+        args.steps, 20, stream)
+    prefill_ms = events_ms(lambda: None,
+                           lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                           args.steps, 20, stream)
+
+    def whole():
+        s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
+                          num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                          dtype=w.dtype)
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
+
+    full_ms = timed_ms(whole, max(5, args.steps // 2), 2, stream)
+    kv_bytes = wl.decode_bytes(w)
+    pf = wl.prefill_flops(w)
+    line = {
+        "value": round(w.num_query_tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+        "ms_per_step": round(ms, 5), "full_step_ms": round(full_ms, 5),
+        "full_step_tokens_per_s": round(w.num_query_tokens / (full_ms * 1e-3), 1), "dtype": "bf16",
+        "partition": step.partition_size, "config": workload_config(w),
+        "decode": {"kernel": "decode_partition_kernel", "kernel_ms": round(decode_kernel_ms, 5),
+                   "gbs": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9, 2),
+                   "hbm_frac": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "algorithmic_bytes": kv_bytes},
+        "prefill": {"kernel": "prefill_kernel", "gflop": round(pf / 1e9, 2), "kernel_ms": round(prefill_ms, 5),
+                    "tflops": round(pf / (prefill_ms * 1e-3) / 1e12, 1),
+                    "mfma_frac": round(pf / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+    }
+    if not args.no_cpu_baseline:
+        dec = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "decode")
+        pre = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "prefill")
+        line["cpu_baseline"] = {"decode": dec, "prefill": pre, "value": dec["value"], "unit": "GB/s",
+                                "cores": dec["cores"], "kind": dec["kind"],
+                                "sample": "decode: " + dec["sample"] + " | prefill: " + pre["sample"]}
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,6 +669,7 @@ def main() -> int:
                              "kv_write_pack"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="only the headline line, without `configs`")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
@@ -295,7 +681,6 @@ def main() -> int:
 
     import torch
 
-    ops = pkg("paged_ops")
     wl = pkg("workloads")
     pkg("_native").load_library()
     device = torch.device("cuda", 0)
@@ -305,131 +690,42 @@ def main() -> int:
         return 0
 
     w = wl.WORKLOADS[args.workload](seed=args.seed)
-    mixed = args.workload == "mixed_step"
-    t = wl.make_tensors(w, device, seed=args.seed)
     if args.workload == "kv_write_pack":
-        result = bench_kv_write_pack(args, w, t, device)
-        print(json.dumps(result), flush=True)
+        print(json.dumps(kv_write_pack_line(args, w, device)), flush=True)
         return 0
-    table = torch.from_numpy(w.block_table_array()).to(device)
-    tile = ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads)
-    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
-                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
-                         head_dim=w.head_dim, dtype=w.dtype)
-    out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
-    stream = torch.cuda.current_stream(device)
+    if args.workload == "fp32_mha_decode":
+        print(json.dumps(decode_rotated(args, w, device)), flush=True)
+        return 0
+    t = wl.make_tensors(w, device, seed=args.seed)
+    if args.workload == "mixed_step":
+        print(json.dumps(mixed_line(args, w, t, device)), flush=True)
+        return 0
 
-    def decode_step():
-        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
-
-    def partition_kernel_ms(steps, warmup):
-        """Average duration of the dominant kernel (the split-K partition
-        kernel): the step is issued as pa_decode's two phases and HIP events
-        on the launch stream bracket every partition launch."""
-        pairs = []
-        for i in range(warmup + steps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1)
-            b.record(stream)
-            ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2)
-            if i >= warmup:
-                pairs.append((a, b))
-        torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
-
-    def prefill_kernel_ms(steps, warmup):
-        """Average duration of the prefill kernel alone (HIP events on its stream)."""
-        pairs = []
-        for i in range(warmup + steps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
-            b.record(stream)
-            if i >= warmup:
-                pairs.append((a, b))
-        torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
-
-    def full_step():
-        s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
-                          num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
-                          head_dim=w.head_dim, dtype=w.dtype)
-        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
-        ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
-
-    def timed(fn, steps, warmup):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(steps):
-            fn()
-        stop.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(stop) / steps  # ms
-
-    # The per-launch kernel timing runs first, after 500 untimed launches
-    # (about 0.15 s): they bring the GPU from idle to its steady clock, which
-    # a few warm-up steps alone do not (the first timed loop after start-up
-    # ran about 5 % slow).  The step is then timed after its W warm-ups.
-    kernel_ms = partition_kernel_ms(args.steps, max(args.warmup, 500))
-    ms = timed(decode_step, args.steps, args.warmup)
-    full_ms = timed(full_step, max(5, args.steps // 5), 2)
-    # The same step replayed from a HIP graph: for small steps the eager loop
-    # above is bound by the host's launch rate, the graph shows the GPU's time.
-    graph_step_ms = graph_ms(decode_step, args.steps, 2, stream)
-
-    kv_bytes = wl.decode_bytes(w)
-    gbs = kv_bytes / (ms * 1e-3) / 1e9
-    kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
-    traffic = measured_traffic(w.name)
-    tokens_per_s = w.num_query_tokens / (ms * 1e-3)
-    result = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
-        "data": "synthetic (seeded N(0,1) K/V/Q, random non-contiguous block tables)",
-        "config": workload_config(w, partition=step.partition_size),
-        "tokens_per_s": round(tokens_per_s, 1),
-        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "full_step_ms": round(full_ms, 5),
-        "graph_step_ms": round(graph_step_ms, 5),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "decode_partition_kernel",
-            "achieved": round(kernel_gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel_ms": round(kernel_ms, 5),
-            "algorithmic_bytes": kv_bytes,
-        },
-    }
-    if mixed:
-        pf = wl.prefill_flops(w)
-        pms = prefill_kernel_ms(args.steps, args.warmup)
-        result["prefill"] = {
-            "kernel": "prefill_kernel",
-            "gflop": round(pf / 1e9, 2),
-            "kernel_ms": round(pms, 5),
-            "tflops": round(pf / (pms * 1e-3) / 1e12, 1),
-            "mfma_frac": round(pf / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        }
-        result["mixed_tokens_per_s"] = round(w.num_query_tokens / (ms * 1e-3), 1)
+    result = decode_main(args, w, t, device)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, t, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline_per_sequence(w, t, args.cpu_budget)
+    del t
+    if not args.no_configs and args.workload == "llama3_8b_gqa_decode":
+        configs = {}
+        w1 = wl.fp32_mha_decode(seed=args.seed)
+        configs["fp32_mha_decode"] = decode_rotated(args, w1, device)
+        w2 = wl.kv_write_pack(seed=args.seed)
+        configs["kv_write_pack"] = kv_write_pack_line(args, w2, device)
+        torch.cuda.empty_cache()
+        w3 = wl.llama7b_mha_decode(seed=args.seed)
+        t3 = wl.make_tensors(w3, device, seed=args.seed)
+        configs["llama7b_mha_decode"] = decode_config_line(args, w3, t3, device)
+        del t3
+        torch.cuda.empty_cache()
+        w5 = wl.mixed_step(seed=args.seed)
+        t5 = wl.make_tensors(w5, device, seed=args.seed)
+        configs["mixed_step"] = mixed_line(args, w5, t5, device)
+        del t5
+        torch.cuda.empty_cache()
+        store, seqs = build_store(w5, device)
+        result["host_step_us"][w5.name] = host_step_us(store, seqs, w5)
+        del store, seqs
+        result["configs"] = configs
     print(json.dumps(result), flush=True)
     return 0
 

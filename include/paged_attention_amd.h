@@ -129,7 +129,7 @@ typedef struct {
 } PaPackDims;
 
 /* Bytes of workspace pa_pack needs for `num_seqs` sequences (a 512-byte
- * header + 16 bytes per sequence).  No counterpart in the reference. */
+ * header + 32 bytes per sequence).  No counterpart in the reference. */
 size_t pa_pack_workspace_size(int32_t num_seqs);
 
 /*
@@ -149,6 +149,14 @@ size_t pa_pack_workspace_size(int32_t num_seqs);
  * reads it (entries outside the table are skipped) -- how a host appends
  * the blocks it allocated since the last step.
  * start_positions / new_token_counts: int64 [B].
+ * rows, updates, start_positions and new_token_counts are read once, by
+ * the first launch, and may sit in pinned host memory (the device address
+ * pa_map_host_memory gives): a host hands a step over without a copy.  The
+ * first launch keeps a copy of the starts, counts and rows in the workspace:
+ * with start_positions and new_token_counts both NULL, a call re-runs the
+ * step the last call on this workspace described (rows then ignored), e.g.
+ * from a captured HIP graph.
+ * Positions and counts must stay below 2^31 (context_lens is int32).
  * Outputs (all int64 unless noted, bit-exact with the reference):
  *   step_block_tables int32 [B, step_table_width] (may be NULL): the rows
  *   of the step's sequences, -1 past max_blocks_per_seq;
@@ -429,6 +437,12 @@ int pa_prefill(const void *query, const void *key_cache,
                void *output, void *stream);
 
 /* ---- utilities ------------------------------------------------------------ */
+
+/* The device address of pinned host memory (hipHostMalloc'd, e.g. a torch
+ * pin_memory tensor), for passing host-resident inputs to pa_pack, or
+ * PA_ERR_INVALID_ARGUMENT for memory that is not pinned.  No counterpart in
+ * the reference. */
+int pa_map_host_memory(const void *host_ptr, void **device_ptr);
 
 const char *pa_error_string(int code);
 const char *pa_last_error_message(void);

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode_phases",
     "pa_decode_no_alloc",
     "pa_prefill",
+    "pa_map_host_memory",
     "pa_error_string",
     "pa_last_error_message",
     "pa_abi_version",
@@ -181,6 +182,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
     ),
+    "pa_map_host_memory": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "pa_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "pa_last_error_message": (ctypes.c_char_p, []),
     "pa_abi_version": (ctypes.c_int, []),

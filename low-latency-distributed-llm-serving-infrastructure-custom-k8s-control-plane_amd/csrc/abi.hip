@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 7; }
+int pa_abi_version(void) { return 8; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -155,6 +155,20 @@ const char* pa_error_string(int code) {
 }
 
 const char* pa_last_error_message(void) { return g_msg; }
+
+int pa_map_host_memory(const void* host_ptr, void** device_ptr) {
+  if (host_ptr == nullptr || device_ptr == nullptr)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_map_host_memory: NULL pointer");
+  *device_ptr = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(device_ptr, const_cast<void*>(host_ptr), 0);
+  if (e != hipSuccess || *device_ptr == nullptr) {
+    (void)hipGetLastError();  // leave no stale error for the next launch check
+    *device_ptr = nullptr;
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_map_host_memory: not pinned host memory (%s)",
+                hipGetErrorString(e));
+  }
+  return PA_OK;
+}
 
 int pa_last_error(void) { return g_ref_abi_status; }
 
@@ -224,10 +238,11 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
   if (cu_seqlens == nullptr || cu_context_offsets == nullptr)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: cu_seqlens and cu_context_offsets are required");
   const int32_t table_rows = rows != nullptr ? dims.num_table_rows : dims.num_seqs;
+  if ((start_positions == nullptr) != (new_token_counts == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_pack: start_positions and new_token_counts are given together or both NULL (re-run)");
   if (dims.num_seqs > 0) {
-    int rc = require("pa_pack", {{start_positions, "start_positions"},
-                                 {new_token_counts, "new_token_counts"},
-                                 {context_lens, "context_lens"},
+    int rc = require("pa_pack", {{context_lens, "context_lens"},
                                  {scatter_slots, "scatter_slots"},
                                  {position_ids, "position_ids"}});
     if (rc != PA_OK) return rc;

@@ -95,7 +95,8 @@ struct PackArgs {
   int32_t* merge_items;
   int32_t* prefill_items;
   int32_t* ws_header;             // [0] full partitions, [1 + b] base of bucket b
-  int4* ws_seq;                   // per sequence: full, merge and prefill offsets, partial rank
+  int4* ws_seq;                   // per sequence: (full, merge and prefill offsets, partial
+                                  // rank), (start, count, table row, 0)
   int32_t num_seqs;
   int32_t num_table_rows;
   int32_t num_updates;

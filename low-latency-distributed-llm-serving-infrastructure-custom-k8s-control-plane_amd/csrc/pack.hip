@@ -6,8 +6,11 @@
 //                      chunks of 1024 with block-wide exclusive scans:
 //                      cu_seqlens, cu_context_offsets, context_lens, and per
 //                      sequence (into the workspace) the offsets of its
-//                      full decode partitions, merge entry and prefill tiles
-//                      and the rank of its partial partition.
+//                      full decode partitions, merge entry and prefill tiles,
+//                      the rank of its partial partition, and its start,
+//                      count and table row.  It is the only reader of the
+//                      step's host inputs, which may sit in pinned host
+//                      memory (read once, over PCIe, with no copy launch).
 //   pack_fill_kernel   one workgroup per sequence.  Copies the sequence's
 //                      block-table row into the step table, writes its
 //                      scatter slots, positions, gather slots and work items
@@ -34,10 +37,12 @@
 // items (seq, query tile) for the multi-token sequences, by sequence.
 //
 // The partial-partition rank is a stable counting sort over the 64 buckets:
-// within a chunk, a wave ranks its lanes of one bucket with a ballot, the 16
-// waves' counts are scanned per bucket, and a per-bucket carry crosses the
-// chunks; bucket bases (largest bucket first) follow once every chunk is
-// counted.
+// within a chunk, each wave finds every lane's bucket-mates with six ballots
+// (one per bucket bit), ranks it among them with mbcnt and counts each
+// bucket, the 16 waves' counts are scanned per bucket, and a per-bucket carry
+// crosses the chunks; bucket bases (largest bucket first) follow once every
+// chunk is counted.  In-chunk sums are 32-bit: a step's context tokens stay
+// below 2^31 (pa_plan_step checks it).
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
 
@@ -49,36 +54,67 @@ constexpr int kFillThreads = 256;
 
 __device__ __forceinline__ int64_t nonneg(int64_t v) { return v < 0 ? 0 : v; }
 
-// Inclusive scan over a wave (64 lanes) with shuffles.
-template <typename T>
-__device__ __forceinline__ T wave_inclusive_scan(T v, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const T n = __shfl_up(v, o, kWave);
-    if (lane >= o) v += n;
-  }
+// Five per-sequence counts scanned together (one shuffle chain, one pair of
+// barriers for all five).
+struct Counts {
+  int32_t tok, ctx, full, merge, tiles;
+};
+
+__device__ __forceinline__ Counts add(Counts x, Counts y) {
+  return {x.tok + y.tok, x.ctx + y.ctx, x.full + y.full, x.merge + y.merge, x.tiles + y.tiles};
+}
+
+// Inclusive scan over the 64 lanes of a wave with DPP moves, no LDS: sums
+// within rows of 16 lanes (row_shr 1, 2, 4, 8; lanes without a source add
+// 0), then the last lane of row 0 and of row 2 into rows 1 and 3
+// (row_bcast:15) and the last lane of row 1 into rows 2 and 3
+// (row_bcast:31).
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ int32_t dpp_in(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, Ctrl, RowMask, 0xF, false);
+}
+
+__device__ __forceinline__ int32_t wave_inclusive_sum(int32_t v) {
+  v += dpp_in<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_in<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_in<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_in<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_in<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_in<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 
-// Exclusive scan of one value per thread across the workgroup; `carry` is
-// added to every result and advanced by the workgroup total.  `s_tot` holds
-// one entry per wave.  Ends with a barrier, so `s_tot` can be reused.
-template <typename T>
-__device__ __forceinline__ T block_exclusive_scan(T v, T& carry, T* s_tot, int lane, int wave) {
-  const T inc = wave_inclusive_scan(v, lane);
-  if (lane == kWave - 1) s_tot[wave] = inc;
-  __syncthreads();
-  T before = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < kScanWaves; ++w) {
-    const T t = s_tot[w];
-    before += w < wave ? t : T(0);
-    total += t;
+__device__ __forceinline__ Counts wave_inclusive_sum(Counts v) {
+  return {wave_inclusive_sum(v.tok), wave_inclusive_sum(v.ctx), wave_inclusive_sum(v.full),
+          wave_inclusive_sum(v.merge), wave_inclusive_sum(v.tiles)};
+}
+
+// A workgroup barrier that orders LDS only: the scan kernel never reads back
+// its global stores, so they are not waited for at every chunk.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+struct SeqInput {
+  uint32_t start, count;
+  int32_t row;
+};
+
+// Sequence `seq`'s start, count and table row: from the caller's inputs, or
+// without them, from the copies the previous call left in the workspace.
+__device__ __forceinline__ SeqInput load_input(const PackArgs& a, int seq) {
+  SeqInput in{0u, 0u, -1};
+  if (seq >= a.num_seqs) return in;
+  if (a.start_positions != nullptr) {
+    // Positions and counts are below 2^31 (context_lens is int32).
+    in.start = static_cast<uint32_t>(nonneg(a.start_positions[seq]));
+    in.count = static_cast<uint32_t>(nonneg(a.new_token_counts[seq]));
+    in.row = a.rows != nullptr ? a.rows[seq] : seq;
+  } else {
+    const int4 w = a.ws_seq[2 * seq + 1];
+    in.start = static_cast<uint32_t>(w.x);
+    in.count = static_cast<uint32_t>(w.y);
+    in.row = w.z;
   }
-  const T out = carry + before + inc - v;
-  carry += total;
-  __syncthreads();
-  return out;
+  return in;
 }
 
 __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
@@ -95,8 +131,7 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
       a.block_tables[static_cast<int64_t>(row) * a.block_table_stride + col] = a.updates[3 * u + 2];
   }
 
-  __shared__ int64_t s_tot64[kScanWaves];
-  __shared__ int32_t s_tot32[kScanWaves];
+  __shared__ Counts s_wave[kScanWaves];
   __shared__ int32_t s_bucket_wave[kScanWaves][kPackBuckets];  // per-chunk counts, then offsets
   __shared__ int32_t s_bucket_carry[kPackBuckets];
   if (tid < kPackBuckets) s_bucket_carry[tid] = 0;
@@ -105,85 +140,130 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
     a.cu_context_offsets[0] = 0;
   }
 
-  const int64_t P = a.partition;
+  const uint32_t P = static_cast<uint32_t>(a.partition);
+  // Partitions are powers of two in practice: shifts instead of divisions.
+  const int log2_p = (P & (P - 1)) == 0 ? __builtin_ctz(P) : -1;
   int64_t tok_carry = 0, ctx_carry = 0;
-  int32_t full_carry = 0, merge_carry = 0, prefill_carry = 0;
+  int32_t full_carry = 0, merge_carry = 0, tiles_carry = 0;
+  SeqInput next = load_input(a, tid);
   for (int base = 0; base < a.num_seqs; base += kScanThreads) {
     const int seq = base + tid;
     const bool valid = seq < a.num_seqs;
-    const int64_t count = valid ? nonneg(a.new_token_counts[seq]) : 0;
-    const int64_t clen = valid ? nonneg(a.start_positions[seq]) + count : 0;
-    const int32_t nfull = count == 1 ? static_cast<int32_t>(clen / P) : 0;
-    const int64_t rlen = count == 1 ? clen % P : 0;
-    const int32_t merge = count == 1 && nfull + (rlen > 0 ? 1 : 0) > 1 ? 1 : 0;
-    const int32_t tiles = count > 1 ? static_cast<int32_t>((count + a.prefill_tile - 1) / a.prefill_tile) : 0;
-    const int bucket = rlen > 0 ? static_cast<int>(((rlen - 1) * kPackBuckets) / P) : -1;
+    const SeqInput cur = next;
+    // The next chunk's loads are in flight while this chunk is scanned.
+    next = load_input(a, seq + kScanThreads);
+    const uint32_t start = cur.start, count = cur.count;
+    const int32_t row = cur.row;
+    const uint32_t clen = start + count;
+    const uint32_t nfull = count == 1 ? (log2_p >= 0 ? clen >> log2_p : clen / P) : 0u;
+    const uint32_t rlen = count == 1 ? clen - nfull * P : 0u;
+    Counts v;
+    v.tok = static_cast<int32_t>(count);
+    v.ctx = static_cast<int32_t>(clen);
+    v.full = static_cast<int32_t>(nfull);
+    v.merge = count == 1 && nfull + (rlen > 0 ? 1u : 0u) > 1u ? 1 : 0;
+    v.tiles = count > 1 ? static_cast<int32_t>((count + a.prefill_tile - 1) / a.prefill_tile) : 0;
+    const int bucket = rlen == 0 ? -1
+                       : static_cast<int>(log2_p >= 0 ? ((rlen - 1) * kPackBuckets) >> log2_p
+                                                      : ((rlen - 1) * kPackBuckets) / P);
 
-    const int64_t tok = block_exclusive_scan<int64_t>(count, tok_carry, s_tot64, lane, wave);
-    const int64_t ctx = block_exclusive_scan<int64_t>(clen, ctx_carry, s_tot64, lane, wave);
-    const int32_t fulls = block_exclusive_scan<int32_t>(nfull, full_carry, s_tot32, lane, wave);
-    const int32_t mitems = block_exclusive_scan<int32_t>(merge, merge_carry, s_tot32, lane, wave);
-    const int32_t pitems = block_exclusive_scan<int32_t>(tiles, prefill_carry, s_tot32, lane, wave);
-
-    // Stable rank of this sequence's partial partition within its bucket.
-    for (int i = tid; i < kScanWaves * kPackBuckets; i += kScanThreads)
-      (&s_bucket_wave[0][0])[i] = 0;
-    __syncthreads();
-    int wave_rank = 0;
-    uint64_t todo = __ballot(bucket >= 0);
-    while (todo != 0) {
-      const int leader = __ffsll(static_cast<unsigned long long>(todo)) - 1;
-      const int b = __shfl(bucket, leader, kWave);
-      const uint64_t same = __ballot(bucket == b);
-      if (bucket == b) wave_rank = __popcll(same & ((uint64_t(1) << lane) - 1));
-      if (lane == 0) s_bucket_wave[wave][b] = __popcll(same);
-      todo &= ~same;
+    // Exclusive scan of the five counts across the chunk.
+    const Counts inc = wave_inclusive_sum(v);
+    if (lane == kWave - 1) s_wave[wave] = inc;
+    // Stable rank among this wave's lanes of the same bucket: the lanes
+    // sharing a lane's bucket are the AND, over the bucket's 6 bits, of the
+    // ballot of that bit (or of its complement where the lane's bit is 0);
+    // mbcnt counts the lower ones.  The first lane of each bucket records the
+    // wave's count of it.
+    const uint64_t with_rem = __ballot(bucket >= 0);
+    uint32_t same_lo = static_cast<uint32_t>(with_rem), same_hi = static_cast<uint32_t>(with_rem >> 32);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const bool bit = bucket >= 0 && ((bucket >> k) & 1);
+      const uint64_t ones = __ballot(bit);
+      same_lo &= bit ? static_cast<uint32_t>(ones) : ~static_cast<uint32_t>(ones);
+      same_hi &= bit ? static_cast<uint32_t>(ones >> 32) : ~static_cast<uint32_t>(ones >> 32);
     }
-    __syncthreads();
+    const int wave_rank = __builtin_amdgcn_mbcnt_hi(same_hi, __builtin_amdgcn_mbcnt_lo(same_lo, 0));
+    s_bucket_wave[wave][lane] = 0;  // LDS stores of one wave land in program order
+    if (bucket >= 0 && wave_rank == 0) s_bucket_wave[wave][bucket] = __popc(same_lo) + __popc(same_hi);
+    lds_barrier();
+    // Every wave scans the 16 wave totals in its first 16 lanes and picks
+    // its own prefix and the chunk total.
+    const Counts wt = wave_inclusive_sum(lane < kScanWaves ? s_wave[lane] : Counts{0, 0, 0, 0, 0});
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    const Counts total = {__builtin_amdgcn_readlane(wt.tok, kScanWaves - 1),
+                          __builtin_amdgcn_readlane(wt.ctx, kScanWaves - 1),
+                          __builtin_amdgcn_readlane(wt.full, kScanWaves - 1),
+                          __builtin_amdgcn_readlane(wt.merge, kScanWaves - 1),
+                          __builtin_amdgcn_readlane(wt.tiles, kScanWaves - 1)};
+    Counts before = {0, 0, 0, 0, 0};
+    if (wave_s > 0)
+      before = {__builtin_amdgcn_readlane(wt.tok, wave_s - 1), __builtin_amdgcn_readlane(wt.ctx, wave_s - 1),
+                __builtin_amdgcn_readlane(wt.full, wave_s - 1), __builtin_amdgcn_readlane(wt.merge, wave_s - 1),
+                __builtin_amdgcn_readlane(wt.tiles, wave_s - 1)};
     if (tid < kPackBuckets) {
+      int32_t c[kScanWaves];
+#pragma unroll
+      for (int w = 0; w < kScanWaves; ++w) c[w] = s_bucket_wave[w][tid];
       int32_t run = s_bucket_carry[tid];
+#pragma unroll
       for (int w = 0; w < kScanWaves; ++w) {
-        const int32_t c = s_bucket_wave[w][tid];
         s_bucket_wave[w][tid] = run;
-        run += c;
+        run += c[w];
       }
       s_bucket_carry[tid] = run;
     }
-    __syncthreads();
+    lds_barrier();
     if (valid) {
+      const Counts ex = add(before, {inc.tok - v.tok, inc.ctx - v.ctx, inc.full - v.full, inc.merge - v.merge,
+                                     inc.tiles - v.tiles});
+      const int64_t tok = tok_carry + ex.tok;
+      const int64_t ctx = ctx_carry + ex.ctx;
       a.cu_seqlens[seq + 1] = tok + count;
       a.cu_context_offsets[seq + 1] = ctx + clen;
       a.context_lens[seq] = static_cast<int32_t>(clen);
       int4 e;
-      e.x = fulls;
-      e.y = mitems;
-      e.z = pitems;
+      e.x = full_carry + ex.full;
+      e.y = merge_carry + ex.merge;
+      e.z = tiles_carry + ex.tiles;
       e.w = bucket >= 0 ? s_bucket_wave[wave][bucket] + wave_rank : -1;
-      a.ws_seq[seq] = e;
+      int4 in;
+      in.x = static_cast<int32_t>(start);
+      in.y = static_cast<int32_t>(count);
+      in.z = row;
+      in.w = 0;
+      a.ws_seq[2 * seq] = e;
+      a.ws_seq[2 * seq + 1] = in;
     }
-    __syncthreads();  // s_bucket_wave is cleared by the next chunk
+    tok_carry += total.tok;
+    ctx_carry += total.ctx;
+    full_carry += total.full;
+    merge_carry += total.merge;
+    tiles_carry += total.tiles;
+    lds_barrier();  // s_wave and s_bucket_wave are rewritten by the next chunk
   }
-  if (tid == 0) {
-    // Bucket bases, largest bucket first, after every full partition.
-    int32_t run = full_carry;
-    for (int b = kPackBuckets - 1; b >= 0; --b) {
-      a.ws_header[1 + b] = run;
-      run += s_bucket_carry[b];
-    }
-    a.ws_header[0] = full_carry;
+  if (wave == 0) {
+    // Bucket bases, largest bucket first, after every full partition: lane l
+    // scans bucket 63 - l.
+    const int32_t mine = s_bucket_carry[kPackBuckets - 1 - lane];
+    const int32_t incl = wave_inclusive_sum(mine);
+    a.ws_header[1 + kPackBuckets - 1 - lane] = full_carry + incl - mine;
+    if (lane == 0) a.ws_header[0] = full_carry;
   }
 }
 
 __global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(PackArgs a) {
   const int seq = blockIdx.x;
   const int tid = threadIdx.x;
-  const int64_t start = nonneg(a.start_positions[seq]);
-  const int64_t count = nonneg(a.new_token_counts[seq]);
+  const int4 e = a.ws_seq[2 * seq];
+  const int4 in = a.ws_seq[2 * seq + 1];
+  const int64_t start = in.x;
+  const int64_t count = in.y;
   const int64_t clen = start + count;
   const int64_t tok = a.cu_seqlens[seq];
   const int64_t ctx = a.cu_context_offsets[seq];
-  const int4 e = a.ws_seq[seq];
-  const int32_t row = a.rows != nullptr ? a.rows[seq] : seq;
+  const int32_t row = in.z;
   const int32_t* bt = row >= 0 && row < a.num_table_rows
                           ? a.block_tables + static_cast<int64_t>(row) * a.block_table_stride
                           : nullptr;
@@ -263,7 +343,7 @@ __global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(PackArgs a) {
 }
 
 size_t pack_workspace_size(int64_t num_seqs) {
-  return kPackHeaderBytes + static_cast<size_t>(num_seqs > 0 ? num_seqs : 0) * sizeof(int4);
+  return kPackHeaderBytes + static_cast<size_t>(num_seqs > 0 ? num_seqs : 0) * 2 * sizeof(int4);
 }
 
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream) {

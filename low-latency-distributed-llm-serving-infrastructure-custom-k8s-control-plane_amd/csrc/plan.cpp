@@ -98,6 +98,8 @@ int pa_plan_step(const int64_t* starts, const int64_t* counts, const int64_t* al
       plan->num_prefill_items += ceil_div(c, params.prefill_tile);
     }
   }
+  if (plan->num_context_tokens >= (int64_t(1) << 31))
+    return plan_fail(plan, -1, "a step's context tokens must stay below 2^31");
   const DecodeContexts d{starts, counts, num_seqs};
   const int64_t part = params.partition_size > 0 ? params.partition_size
                                                  : choose_partition(d, params, longest_decode);

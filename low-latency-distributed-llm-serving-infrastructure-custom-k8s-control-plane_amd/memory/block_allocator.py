@@ -279,6 +279,22 @@ class SequenceBlockTable:
         if self._pool is not None:
             self._pool.tokens[self.row] = self._tokens
 
+    def append_tokens(self, n: int) -> None:
+        """``n`` append_token calls, with the new blocks taken in one call."""
+        if n <= 0:
+            return
+        have = len(self._blocks) * self._block_size
+        need = max(0, -(-(self._tokens + n - have) // self._block_size))
+        if need:
+            first = len(self._blocks)
+            new = self._allocator.allocate_blocks(need)
+            self._blocks.extend(new)
+            for i, block in enumerate(new):
+                self._record(first + i, block)
+        self._tokens += n
+        if self._pool is not None:
+            self._pool.tokens[self.row] = self._tokens
+
     def append_block(self, block_id: int) -> None:
         self._allocator._validate(block_id)
         self._blocks.append(block_id)

@@ -112,8 +112,7 @@ class PagedKVCacheManager:
         """Slots for every token the sequence holds (prompt + outputs)."""
         self.init_sequence_table(seq)
         table = seq.block_table
-        for _ in range(seq.total_len - table.get_tokens_count()):
-            table.append_token()
+        table.append_tokens(seq.total_len - table.get_tokens_count())
 
     def allocate_slot_for_next_token(self, seq) -> None:
         assert seq.block_table is not None
@@ -173,6 +172,13 @@ class PagedKVCacheManager:
                   with_gather: bool = False, partition_size: Optional[int] = None) -> paged_ops.PackedStep:
         """Check, plan and pack one step on the GPU (one upload, two launches)."""
         rows, starts, counts = self.step_rows(sequences, start_tokens, token_counts)
+        return self.pack_rows(rows, starts, counts, num_query_heads=num_query_heads, with_gather=with_gather,
+                              partition_size=partition_size)
+
+    def pack_rows(self, rows: np.ndarray, starts: np.ndarray, counts: np.ndarray, *,
+                  num_query_heads: Optional[int] = None, with_gather: bool = False,
+                  partition_size: Optional[int] = None) -> paged_ops.PackedStep:
+        """:meth:`pack_step` for a step :meth:`step_rows` already checked."""
         table, updates = self.device_block_table()
         hq = int(num_query_heads or self.num_query_heads or self.num_heads)
         return paged_ops.pack_step(

@@ -19,7 +19,6 @@ context and build a T x C mask on the device).
 
 from __future__ import annotations
 
-from itertools import accumulate
 from typing import List, Optional
 
 import numpy as np
@@ -50,9 +49,11 @@ def set_backend(backend) -> None:
     _BACKEND = backend
 
 
-def _offsets(counts) -> torch.Tensor:
+def _offsets(counts: np.ndarray) -> torch.Tensor:
     """int64 [n + 1]: 0 followed by the running totals of ``counts``."""
-    return torch.tensor([0, *accumulate(counts)], dtype=torch.long)
+    out = np.zeros(counts.shape[0] + 1, dtype=np.int64)
+    np.cumsum(counts, out=out[1:])
+    return torch.from_numpy(out)
 
 
 class PagedStepContext:
@@ -63,7 +64,8 @@ class PagedStepContext:
     new_token_counts, context_lens (lists), cu_seqlens, cu_context_offsets
     (CPU int64 tensors), scatter_slots, gather_slots (int64 on the store's
     device), num_query_tokens, num_context_tokens.  ``packed`` is the GPU
-    description of the step (None on a CPU store).
+    description of the step (None on a CPU store).  The host-side lists and
+    offsets are built on first use: a GPU step needs none of them.
     """
 
     def __init__(self, store, sequences: List, start_positions: List[int], new_token_counts: List[int],
@@ -74,26 +76,48 @@ class PagedStepContext:
                 f"and new_token_counts ({len(new_token_counts)}) must have the same length"
             )
         self.store = store
-        self.sequences = list(sequences)
-        self.start_positions = [int(s) for s in start_positions]
-        self.new_token_counts = [int(c) for c in new_token_counts]
-        self.context_lens = [s + c for s, c in zip(self.start_positions, self.new_token_counts)]
-        self.cu_seqlens = _offsets(self.new_token_counts)
-        self.cu_context_offsets = _offsets(self.context_lens)
+        self.sequences = sequences if isinstance(sequences, list) else list(sequences)
         self.packed: Optional[paged_ops.PackedStep] = None
         self._gather_slots: Optional[torch.Tensor] = None
         self._mask: Optional[torch.Tensor] = None
+        self._rows, self._starts, self._counts = store.step_rows(self.sequences, start_positions, new_token_counts)
         if store.on_gpu:
             if self.sequences:
-                self.packed = store.pack_step(self.sequences, self.start_positions, self.new_token_counts)
+                self.packed = store.pack_rows(self._rows, self._starts, self._counts)
                 self.scatter_slots = self.packed.scatter_slots
             else:
                 self.scatter_slots = torch.empty((0,), dtype=torch.long, device=store.device)
         else:
-            rows, starts, counts = store.step_rows(self.sequences, self.start_positions, self.new_token_counts)
-            self.scatter_slots = torch.from_numpy(store._host_slots(rows, starts, counts))
+            self.scatter_slots = torch.from_numpy(store._host_slots(self._rows, self._starts, self._counts))
             self._gather_slots = torch.from_numpy(
-                store._host_slots(rows, np.zeros_like(starts), starts + counts))
+                store._host_slots(self._rows, np.zeros_like(self._starts), self._starts + self._counts))
+
+    # -- host-side views of the step (built on first use) ------------------------------
+    def _cached(self, name, build):
+        value = self.__dict__.get(name)
+        if value is None:
+            value = self.__dict__[name] = build()
+        return value
+
+    @property
+    def start_positions(self) -> List[int]:
+        return self._cached("_start_list", self._starts.tolist)
+
+    @property
+    def new_token_counts(self) -> List[int]:
+        return self._cached("_count_list", self._counts.tolist)
+
+    @property
+    def context_lens(self) -> List[int]:
+        return self._cached("_ctx_list", lambda: (self._starts + self._counts).tolist())
+
+    @property
+    def cu_seqlens(self) -> torch.Tensor:
+        return self._cached("_cu_q", lambda: _offsets(self._counts))
+
+    @property
+    def cu_context_offsets(self) -> torch.Tensor:
+        return self._cached("_cu_c", lambda: _offsets(self._starts + self._counts))
 
     def packed_for(self, num_query_heads: int) -> paged_ops.PackedStep:
         """The packed step with prefill work items and decode workspace sized
@@ -103,7 +127,7 @@ class PagedStepContext:
             raise RuntimeError("this step is not on a GPU store")
         tile = paged_ops.prefill_tile_for(num_query_heads, self.store.num_heads)
         if self.packed.prefill_tile != tile:
-            self.packed = self.store.pack_step(self.sequences, self.start_positions, self.new_token_counts,
+            self.packed = self.store.pack_rows(self._rows, self._starts, self._counts,
                                                num_query_heads=num_query_heads,
                                                partition_size=self.packed.partition_size)
         return self.packed
@@ -120,11 +144,11 @@ class PagedStepContext:
 
     @property
     def num_query_tokens(self) -> int:
-        return int(self.cu_seqlens[-1])
+        return int(self._counts.sum())
 
     @property
     def num_context_tokens(self) -> int:
-        return int(self.cu_context_offsets[-1])
+        return int((self._starts + self._counts).sum())
 
     def position_ids(self, device: torch.device) -> torch.Tensor:
         """[1, T] positions, restarting at every sequence boundary."""

@@ -80,6 +80,9 @@ def _align(n: int, a: int = 256) -> int:
     return (n + a - 1) // a * a
 
 
+_ELEM = {torch.int64: 8, torch.int32: 4, torch.uint8: 1}
+
+
 class _Layout:
     """Byte offsets of named arrays inside one buffer (256-byte aligned)."""
 
@@ -90,30 +93,31 @@ class _Layout:
     def add(self, name: str, dtype: torch.dtype, shape) -> None:
         count = 1
         for d in shape:
-            count *= int(d)
-        self.fields[name] = (self.nbytes, dtype, tuple(int(d) for d in shape))
-        self.nbytes += _align(count * torch.empty((), dtype=dtype).element_size())
-
-
-_ELEM = {torch.int64: 8, torch.int32: 4, torch.uint8: 1}
+            count *= d
+        self.fields[name] = (self.nbytes, dtype, shape)
+        self.nbytes += _align(count * _ELEM[dtype])
 
 
 class _HostStaging:
-    """A ring of pinned host buffers for the per-step uploads.
+    """A ring of pinned host buffers the packing kernel reads a step's inputs
+    from (through their device addresses, pa_map_host_memory), so no copy
+    launch precedes it.
 
-    A slot is reused only after the copy that last read it has run (an event
-    recorded behind that copy), so the host never overwrites bytes a pending
-    copy still reads, and never waits in the steady state."""
+    A slot is reused only after the launch that last read it has run (an
+    event recorded behind it), so the host never overwrites bytes a pending
+    launch still reads, and never waits in the steady state."""
 
     SLOTS = 8
 
     def __init__(self) -> None:
         self._bufs = [None] * self.SLOTS
         self._arrays = [None] * self.SLOTS
+        self._device = [0] * self.SLOTS
         self._events = [None] * self.SLOTS
         self._next = 0
 
     def take(self, nbytes: int):
+        """(slot, numpy view, device address) of a free buffer of >= nbytes."""
         slot = self._next
         self._next = (slot + 1) % self.SLOTS
         if self._events[slot] is not None:
@@ -121,9 +125,11 @@ class _HostStaging:
         buf = self._bufs[slot]
         if buf is None or buf.numel() < nbytes:
             buf = torch.empty(max(_align(nbytes, 1 << 16), 1 << 16), dtype=torch.uint8, pin_memory=True)
-            self._bufs[slot] = buf
-            self._arrays[slot] = buf.numpy()
-        return slot, buf, self._arrays[slot]
+            lib = _native.load_library()
+            dev = ctypes.c_void_p()
+            _native.check(lib.pa_map_host_memory(buf.data_ptr(), ctypes.byref(dev)), "pa_map_host_memory")
+            self._bufs[slot], self._arrays[slot], self._device[slot] = buf, buf.numpy(), int(dev.value)
+        return slot, self._arrays[slot], self._device[slot]
 
     def done(self, slot: int, stream) -> None:
         ev = self._events[slot]
@@ -169,14 +175,15 @@ class PackedStep:
     """
 
     def __init__(self, buffer, layout, plan, block_size, prefill_tile, table, table_rows, rows_name,
-                 head_shape):
+                 head_shape, inputs):
         self.buffer = buffer
         self._layout = layout
         self._base = buffer.data_ptr()
         self.block_size = int(block_size)
         self.partition_size = int(plan.partition_size)
         self.prefill_tile = int(prefill_tile)
-        self.num_seqs = int(layout.fields["start_positions"][2][0])
+        self._inputs = inputs  # host (starts int64, counts int64, rows int32 or None)
+        self.num_seqs = int(inputs[0].shape[0])
         self.num_query_tokens = int(plan.num_query_tokens)
         self.num_context_tokens = int(plan.num_context_tokens)
         self.num_decode_items = int(plan.num_decode_items)
@@ -216,6 +223,36 @@ class PackedStep:
         if name in layout.fields:
             return self._view(name)
         raise AttributeError(name)
+
+    @property
+    def start_positions(self) -> np.ndarray:
+        """int64 [B] (host) start position of every sequence."""
+        return self._inputs[0]
+
+    @property
+    def new_token_counts(self) -> np.ndarray:
+        """int64 [B] (host) new tokens of every sequence."""
+        return self._inputs[1]
+
+    def repack(self, start_positions=None, new_token_counts=None) -> None:
+        """Rerun the packing kernels in place with new positions / counts of
+        the same sequences (what a step captured in a graph re-reads): every
+        output keeps its address.  The new step must need the same buffer
+        sizes (tokens, contexts and work items)."""
+        starts = self._inputs[0] if start_positions is None else _int64_array(start_positions)
+        counts = self._inputs[1] if new_token_counts is None else _int64_array(new_token_counts)
+        plan = _plan(starts, counts, self.block_size, self.prefill_tile, self.partition_size, 1, 1, 1, 1, 1)
+        same = (plan.num_query_tokens, plan.num_decode_items, plan.num_merge_items, plan.num_prefill_items) == (
+            self.num_query_tokens, self.num_decode_items, self.num_merge_items, self.num_prefill_items)
+        if starts.shape[0] != self.num_seqs or not same:
+            raise ValueError("repack needs a step of the same sizes; pack a new step instead")
+        if self.table_width and plan.max_blocks > self.table_width:
+            raise ValueError("repack: a context grew past the step's block table")
+        self._inputs = (starts, counts, self._inputs[2])
+        self.num_context_tokens = int(plan.num_context_tokens)
+        self.max_context = int(plan.max_context)
+        self._gather = None
+        _run_pack(self, fresh=True)
 
     @property
     def table_width(self) -> int:
@@ -326,6 +363,16 @@ def decode_workgroups_per_cu(dtype: torch.dtype, head_dim: int, num_kv_heads: in
     return per_cu
 
 
+def _occupancy_on(device: torch.device, dtype, head_dim: int, num_kv_heads: int, num_query_heads: int) -> int:
+    """decode_workgroups_per_cu for ``device`` (made current only for a miss)."""
+    key = (id(_native.load_library()), device.index, dtype, int(head_dim), int(num_kv_heads), int(num_query_heads))
+    per_cu = _OCCUPANCY_CACHE.get(key)
+    if per_cu is None:
+        with torch.cuda.device(device):
+            per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, num_query_heads)
+    return per_cu
+
+
 def choose_partition(
     start_positions: Sequence[int],
     new_token_counts: Sequence[int],
@@ -362,25 +409,46 @@ def choose_partition(
     return int(p.partition_size)
 
 
-def _run_pack(step: PackedStep, with_gather: bool = False, updates_ptr: int = 0, num_updates: int = 0
-              ) -> Optional[torch.Tensor]:
-    """Launch pa_pack for ``step`` (again): all outputs are rewritten, plus the
-    gather slots when asked for (returned)."""
+def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.ndarray] = None,
+              fresh: bool = False) -> Optional[torch.Tensor]:
+    """Launch pa_pack for ``step``: all outputs are rewritten, plus the gather
+    slots when asked for (returned).  ``fresh``: the step's host inputs (and
+    ``updates``) are staged in pinned host memory the scan kernel reads;
+    otherwise the kernel re-reads its own copy of them in the step's
+    workspace (no host memory involved, so the call can be graph-captured)."""
     lib = _native.load_library()
     device = step.buffer.device
     gather = None
     if with_gather:
         gather = torch.empty(step.num_context_tokens, dtype=torch.int64, device=device)
-    pooled = step._rows_name is not None
+    starts, counts, rows = step._inputs
+    b = step.num_seqs
+    pooled = rows is not None
+    n_upd = 0 if updates is None else int(updates.shape[0])
+    staging = slot = None
+    dev = o_counts = o_rows = o_upd = 0
+    if fresh or n_upd:
+        o_counts = _align(8 * b, 64)
+        o_rows = o_counts + _align(8 * b, 64)
+        o_upd = o_rows + (_align(4 * b, 64) if pooled else 0)
+        nbytes = o_upd + 12 * n_upd
+        staging = _staging(device)
+        slot, host, dev = staging.take(max(nbytes, 1))
+        host[:o_counts].view(np.int64)[:b] = starts
+        host[o_counts:o_rows].view(np.int64)[:b] = counts
+        if pooled:
+            host[o_rows : o_rows + 4 * b].view(np.int32)[:] = rows
+        if n_upd:
+            host[o_upd:nbytes].view(np.int32)[:] = updates.reshape(-1)
     table = step._source_table
     dims = _native.PaPackDims(
-        num_seqs=step.num_seqs,
+        num_seqs=b,
         block_size=step.block_size,
         max_blocks_per_seq=int(table.shape[1]) if table.dim() == 2 else 0,
         partition_size=step.partition_size,
         prefill_tile=step.prefill_tile,
         num_table_rows=step._source_rows,
-        num_updates=int(num_updates),
+        num_updates=n_upd,
         step_table_width=step.table_width if pooled else 0,
         max_query_tokens=step.num_query_tokens,
         max_context_tokens=step.num_context_tokens,
@@ -391,10 +459,10 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates_ptr: int = 0,
     ws_off, _, ws_shape = step._layout.fields["pack_workspace"]
     status = lib.pa_pack(
         table.data_ptr() if table.numel() else None,
-        step.ptr("rows") if pooled else None,
-        updates_ptr or None,
-        step.ptr("start_positions"),
-        step.ptr("new_token_counts"),
+        dev + o_rows if pooled and dev else None,
+        dev + o_upd if n_upd else None,
+        dev or None,
+        dev + o_counts if dev else None,
         dims,
         step.ptr("block_tables") if pooled else None,
         step.ptr("cu_seqlens"),
@@ -410,6 +478,8 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates_ptr: int = 0,
         ws_shape[0],
         _stream(device),
     )
+    if staging is not None:
+        staging.done(slot, torch.cuda.current_stream(device))
     _native.check(status, "pa_pack")
     return gather
 
@@ -473,26 +543,15 @@ def pack_step(
     per_item = per_cu = 0
     if partition_size is None and head_dim is not None and dtype is not None:
         per_item = decode_workgroups_per_item(dtype, head_dim, num_kv_heads, hq)
-        with torch.cuda.device(device):  # the occupancy of the step's own device
-            per_cu = decode_workgroups_per_cu(dtype, head_dim, num_kv_heads, hq)
+        per_cu = _occupancy_on(device, dtype, head_dim, num_kv_heads, hq)
     allocated = None if allocated_tokens is None else _int64_array(allocated_tokens)
     plan = _plan(starts, counts, block_size, prefill_tile, partition_size or 0, num_kv_heads, hq, per_item,
                  per_cu, _compute_units(device), allocated)
     pooled = rows is not None
     n_upd = 0 if updates is None else int(updates.shape[0])
 
-    # One host staging area and one device buffer per step.
-    inputs = _Layout()
-    inputs.add("start_positions", torch.int64, (b,))
-    inputs.add("new_token_counts", torch.int64, (b,))
-    if pooled:
-        inputs.add("rows", torch.int32, (b,))
-    if n_upd:
-        inputs.add("updates", torch.int32, (n_upd, 3))
+    # One device buffer per step; the inputs go over in pinned host memory.
     layout = _Layout()
-    for name, (_, dt, shape) in inputs.fields.items():
-        layout.add(name, dt, shape)
-    assert layout.nbytes == inputs.nbytes
     t, c = int(plan.num_query_tokens), int(plan.num_context_tokens)
     if pooled:
         layout.add("block_tables", torch.int32, (b, max(int(plan.max_blocks), 1)))
@@ -512,29 +571,12 @@ def pack_step(
         layout.add("decode_workspace", torch.uint8,
                    (max(decode_workspace_bytes(int(plan.num_decode_items), hq, int(head_dim)), 1),))
     buffer = torch.empty(layout.nbytes, dtype=torch.uint8, device=device)
-
-    stream = torch.cuda.current_stream(device)
-    staging = _staging(device)
-    slot, host, host_np = staging.take(inputs.nbytes)
-    host_np[inputs.fields["start_positions"][0] : inputs.fields["start_positions"][0] + 8 * b].view(
-        np.int64)[:] = starts
-    host_np[inputs.fields["new_token_counts"][0] : inputs.fields["new_token_counts"][0] + 8 * b].view(
-        np.int64)[:] = counts
-    if pooled:
-        off = inputs.fields["rows"][0]
-        host_np[off : off + 4 * b].view(np.int32)[:] = np.asarray(rows, dtype=np.int32).reshape(-1)
-    if n_upd:
-        off = inputs.fields["updates"][0]
-        host_np[off : off + 12 * n_upd].view(np.int32)[:] = np.ascontiguousarray(updates, dtype=np.int32).reshape(-1)
-    if inputs.nbytes:
-        buffer[: inputs.nbytes].copy_(host[: inputs.nbytes], non_blocking=True)
-    staging.done(slot, stream)
-
+    rows_arr = None if rows is None else np.ascontiguousarray(np.asarray(rows, dtype=np.int32).reshape(-1))
     table_rows = int(block_tables.shape[0]) if block_tables.numel() else 0
     step = PackedStep(buffer, layout, plan, block_size, prefill_tile, block_tables, table_rows,
-                      "rows" if pooled else None, head_shape)
-    upd_ptr = step.ptr("updates") if n_upd else 0
-    gather = _run_pack(step, with_gather=with_gather, updates_ptr=upd_ptr, num_updates=n_upd)
+                      "rows" if pooled else None, head_shape, (starts, counts, rows_arr))
+    upd = None if not n_upd else np.ascontiguousarray(updates, dtype=np.int32)
+    gather = _run_pack(step, with_gather=with_gather, updates=upd, fresh=True)
     if with_gather:
         step._gather = gather
     return step

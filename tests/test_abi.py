@@ -99,8 +99,11 @@ def test_invalid_arguments_rejected_before_launch():
     fake = [0x1000 * (i + 1) for i in range(16)]
     args = fake[:5] + [pdims] + fake[5:15] + [None, 0, None]
     rc = lib.pa_pack(*args)
-    assert rc == native.PA_ERR_WORKSPACE and b"workspace of 528 bytes" in lib.pa_last_error_message()
-    assert lib.pa_pack_workspace_size(1) == 528 and lib.pa_pack_workspace_size(0) == 512
+    assert rc == native.PA_ERR_WORKSPACE and b"workspace of 544 bytes" in lib.pa_last_error_message()
+    assert lib.pa_pack_workspace_size(1) == 544 and lib.pa_pack_workspace_size(0) == 512
+    args = fake[:3] + [None, fake[4], pdims] + fake[5:15] + [fake[15], 4096, None]
+    assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
+    assert b"both NULL" in lib.pa_last_error_message()
     pdims.num_updates = 2
     args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:15] + [fake[15], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
@@ -214,3 +217,11 @@ def test_product_path_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(native, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         native.load_library()
+
+
+def test_map_host_memory_rejects_unpinned_and_null():
+    native = pkg("_native")
+    lib = native.load_library()
+    out = ctypes.c_void_p()
+    assert lib.pa_map_host_memory(None, ctypes.byref(out)) == native.PA_ERR_INVALID_ARGUMENT
+    assert b"NULL" in lib.pa_last_error_message()

@@ -76,8 +76,7 @@ def test_decode_layers_replay_bit_exact(device):
     for k in range(steps):
         # next step: every sequence one token further, new inputs
         starts = [s + 1 for s in starts]
-        step.start_positions.copy_(torch.tensor(starts, dtype=torch.int64))
-        ops._run_pack(step)
+        step.repack(starts)
         for l in range(layers):
             q[l].copy_(rand(1, hq, b, d))
             new_k[l].copy_(rand(b, hkv, d))

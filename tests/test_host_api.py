@@ -431,3 +431,23 @@ def test_cpu_store_slots_match_oracle_after_growth():
     table, lens = m.build_block_tables(seqs)
     want_table, want_lens = op.build_block_tables(lists, toks)
     assert table.tolist() == want_table.tolist() and lens.tolist() == want_lens.tolist()
+
+
+def test_append_tokens_equals_repeated_append_token():
+    for start in (0, 1, 3, 4, 9):
+        for n in (0, 1, 2, 4, 7, 16):
+            tables = []
+            for bulk in (True, False):
+                alloc = alloc_mod.PageAllocator(64, 4, 8)
+                pool = alloc_mod.BlockTablePool()
+                t = alloc_mod.SequenceBlockTable(alloc, pool)
+                for _ in range(start):
+                    t.append_token()
+                if bulk:
+                    t.append_tokens(n)
+                else:
+                    for _ in range(n):
+                        t.append_token()
+                tables.append((t.get_physical_blocks(), t.get_tokens_count(), pool.host.copy(), pool.tokens.copy()))
+            (b1, n1, h1, k1), (b2, n2, h2, k2) = tables
+            assert b1 == b2 and n1 == n2 and (h1 == h2).all() and (k1 == k2).all(), (start, n)
