@@ -17,9 +17,11 @@ roofline = the dominant kernel (the split-K partition kernel): its
            HBM bytes per launch from the committed rocprofv3 PMC summary.
 Also on the line:
   full_step_ms   a whole step through the product path, host included: the
-                 step context built on an HBM store (checks, plan, one
-                 upload, the two packing launches), the K/V write of the
-                 step's tokens, and the attention;
+                 step context built on an HBM store (checks, plan, the
+                 inputs handed over in pinned memory, the packing launch),
+                 the K/V write of the step's tokens, and the attention;
+                 full_vs_decode_step times it in alternation with the decode
+                 step alone (the gap is what the step's plumbing costs);
   host_step_us   the host time of building that step context (median), for
                  this workload and the mixed step;
   graph_step_ms  the decode step replayed from a HIP graph, timed in
@@ -243,6 +245,20 @@ def graph_vs_eager_ms(fn, steps, stream, rounds=3):
     return median(eager), median(replay)
 
 
+def paired_ms(fn_a, fn_b, steps, stream, rounds=5):
+    """(a ms, b ms) per call: `steps` eager calls of each, alternated `rounds`
+    times after one untimed pass of both; medians.  Two loops timed in
+    alternation see the same clock, so their difference is the cost of what
+    b adds, not clock drift."""
+    a, b = [], []
+    timed_ms(fn_a, steps, 0, stream)
+    timed_ms(fn_b, steps, 0, stream)
+    for _ in range(rounds):
+        a.append(timed_ms(fn_a, steps, 0, stream))
+        b.append(timed_ms(fn_b, steps, 0, stream))
+    return median(a), median(b)
+
+
 def timed_ms(fn, steps, warmup, stream):
     """Mean time of `steps` eager calls between two events after `warmup`."""
     import torch
@@ -409,6 +425,7 @@ def decode_main(args, w, t, device):
         ops.attention(t.query, store.key_cache, store.value_cache, 0, ctx.packed, w.scaling, out=sout)
 
     full_ms = timed_ms(full_step, args.steps, args.warmup, stream)
+    dec_alt, full_alt = paired_ms(decode_step, full_step, args.steps, stream)
     host_us = host_step_us(store, seqs, w)
     del store, seqs
 
@@ -433,6 +450,10 @@ def decode_main(args, w, t, device):
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "full_step_ms": round(full_ms, 5),
         "full_step_gbs": round(kv_bytes / (full_ms * 1e-3) / 1e9, 2),
+        "full_vs_decode_step": {"full_step_ms": round(full_alt, 5), "decode_step_ms": round(dec_alt, 5),
+                                "gap_us": round((full_alt - dec_alt) * 1e3, 2),
+                                "timing": "5 alternating rounds of the full-step loop and the decode-step loop, "
+                                          "medians"},
         "host_step_us": {w.name: host_us},
         "graph_step_ms": round(graph_step, 5),
         "graph_vs_eager": {"graph_ms": round(graph_step, 5), "eager_ms": round(eager_alt, 5),

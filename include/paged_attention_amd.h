@@ -105,9 +105,14 @@ typedef struct {
     int32_t max_blocks_per_seq; /* row stride of block_tables (elements)    */
     int32_t partition_size;     /* decode split-K partition, tokens         */
     int32_t dtype;              /* PA_DTYPE_* of query, caches and output   */
-    int32_t reserved;
+    int32_t num_table_rows;     /* rows of block_tables (0: num_seqs)       */
     int64_t q_token_stride;     /* query element stride between tokens      */
     int64_t q_head_stride;      /* query element stride between heads       */
+    /* Row of block_tables per sequence (int32 [num_seqs], device), or NULL:
+     * row i is sequence i.  With it, block_tables can be a pool of rows kept
+     * on the device across steps (pa_pack's table), read in place.  A row
+     * outside [0, num_table_rows) reads as a sequence without blocks. */
+    const int32_t *block_table_rows;
 } PaStepDims;
 
 /* ---- (a) ragged-batch packing ------------------------------------------ */
@@ -121,6 +126,8 @@ typedef struct {
     int32_t num_table_rows;     /* rows of block_tables (0 = num_seqs)      */
     int32_t num_updates;        /* (row, col, block) triples in `updates`   */
     int32_t step_table_width;   /* columns of step_block_tables             */
+    int32_t max_new_tokens;     /* hint: most new tokens of one sequence    */
+    int32_t max_context;        /* hint: longest context (0: no hints)      */
     int64_t max_query_tokens;   /* capacity of scatter_slots / position_ids */
     int64_t max_context_tokens; /* capacity of gather_slots                 */
     int64_t max_decode_items;   /* capacity of decode_items (pairs)         */
@@ -160,6 +167,9 @@ size_t pa_pack_workspace_size(int32_t num_seqs);
  * Outputs (all int64 unless noted, bit-exact with the reference):
  *   step_block_tables int32 [B, step_table_width] (may be NULL): the rows
  *   of the step's sequences, -1 past max_blocks_per_seq;
+ *   step_rows int32 [B] (may be NULL): the row of every sequence (rows[i],
+ *   or i without rows) -- with it, the attention entry points read the
+ *   pool in place (PaStepDims.block_table_rows) and no step table is built;
  *   cu_seqlens [B+1], cu_context_offsets [B+1], context_lens int32 [B],
  *   scatter_slots [T], position_ids [T], gather_slots [C] (may be NULL),
  *   decode_items int32 pairs (seq, partition) for every sequence with one
@@ -177,11 +187,15 @@ size_t pa_pack_workspace_size(int32_t num_seqs);
  * Writes past a capacity in PaPackDims are dropped, never performed.
  * A block-table entry that is negative or past its row yields slot -1.
  * workspace: pa_pack_workspace_size(B) bytes, 16-byte aligned; calls that
- * share one must not overlap in time.  Two launches, each linear in B.
+ * share one must not overlap in time.  Two launches, each linear in B; one
+ * launch when B <= 1024, neither gather_slots nor step_block_tables is
+ * asked for, and the hints bound every sequence's new tokens and full
+ * partitions by 32 (hints that understate only slow that launch down).
  */
 int pa_pack(int32_t *block_tables, const int32_t *rows, const int32_t *updates,
             const int64_t *start_positions, const int64_t *new_token_counts,
-            PaPackDims dims, int32_t *step_block_tables, int64_t *cu_seqlens,
+            PaPackDims dims, int32_t *step_block_tables, int32_t *step_rows,
+            int64_t *cu_seqlens,
             int64_t *cu_context_offsets, int32_t *context_lens,
             int64_t *scatter_slots, int64_t *position_ids,
             int64_t *gather_slots, int32_t *decode_items,
@@ -214,7 +228,7 @@ typedef struct {
     int32_t partition_size;      /* the split-K partition of the step        */
     int32_t max_blocks;          /* max over sequences of ceil(ctx / bs)     */
     int32_t bad_seq;             /* first sequence failing a check, or -1    */
-    int32_t reserved;
+    int32_t max_new_tokens;      /* most new tokens of one sequence          */
 } PaStepPlan;
 
 /*

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -87,9 +87,10 @@ class PaStepDims(ctypes.Structure):
         ("max_blocks_per_seq", ctypes.c_int32),
         ("partition_size", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("num_table_rows", ctypes.c_int32),
         ("q_token_stride", ctypes.c_int64),
         ("q_head_stride", ctypes.c_int64),
+        ("block_table_rows", ctypes.c_void_p),
     ]
 
 
@@ -103,6 +104,8 @@ class PaPackDims(ctypes.Structure):
         ("num_table_rows", ctypes.c_int32),
         ("num_updates", ctypes.c_int32),
         ("step_table_width", ctypes.c_int32),
+        ("max_new_tokens", ctypes.c_int32),
+        ("max_context", ctypes.c_int32),
         ("max_query_tokens", ctypes.c_int64),
         ("max_context_tokens", ctypes.c_int64),
         ("max_decode_items", ctypes.c_int64),
@@ -137,7 +140,7 @@ class PaStepPlan(ctypes.Structure):
         ("partition_size", ctypes.c_int32),
         ("max_blocks", ctypes.c_int32),
         ("bad_seq", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("max_new_tokens", ctypes.c_int32),
     ]
 
 
@@ -153,7 +156,7 @@ _SIGNATURES = {
     "pa_pack_workspace_size": (_sz, [_i32]),
     "pa_pack": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+        [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
     "pa_plan_step": (ctypes.c_int, [_vp, _vp, _vp, _i32, PaPlanParams, ctypes.POINTER(PaStepPlan)]),
     "pa_reshape_and_cache": (

@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 8; }
+int pa_abi_version(void) { return 9; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -224,7 +224,7 @@ size_t pa_pack_workspace_size(int32_t num_seqs) { return pa::pack_workspace_size
 
 int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
             const int64_t* start_positions, const int64_t* new_token_counts, PaPackDims dims,
-            int32_t* step_block_tables, int64_t* cu_seqlens, int64_t* cu_context_offsets,
+            int32_t* step_block_tables, int32_t* step_rows, int64_t* cu_seqlens, int64_t* cu_context_offsets,
             int32_t* context_lens, int64_t* scatter_slots, int64_t* position_ids,
             int64_t* gather_slots, int32_t* decode_items, int32_t* merge_items,
             int32_t* prefill_items, void* workspace, size_t workspace_bytes, void* stream) {
@@ -237,7 +237,9 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: partition and prefill tile must be positive");
   if (cu_seqlens == nullptr || cu_context_offsets == nullptr)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: cu_seqlens and cu_context_offsets are required");
-  const int32_t table_rows = rows != nullptr ? dims.num_table_rows : dims.num_seqs;
+  // A re-run reads each sequence's row from the workspace: the table's row
+  // count is the caller's in every mode.
+  const int32_t table_rows = dims.num_table_rows > 0 ? dims.num_table_rows : dims.num_seqs;
   if ((start_positions == nullptr) != (new_token_counts == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "pa_pack: start_positions and new_token_counts are given together or both NULL (re-run)");
@@ -267,6 +269,7 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
   a.start_positions = start_positions;
   a.new_token_counts = new_token_counts;
   a.step_block_tables = step_block_tables;
+  a.step_rows = step_rows;
   a.cu_seqlens = cu_seqlens;
   a.cu_context_offsets = cu_context_offsets;
   a.context_lens = context_lens;
@@ -291,6 +294,7 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
   a.max_decode_items = decode_items ? dims.max_decode_items : 0;
   a.max_merge_items = merge_items ? dims.max_merge_items : 0;
   a.max_prefill_items = prefill_items ? dims.max_prefill_items : 0;
+  a.fused = pa::pack_fusable(a, dims.max_new_tokens, dims.max_context) ? 1 : 0;
   return from_hip(pa::launch_pack(a, static_cast<hipStream_t>(stream)), "pa_pack");
 }
 
@@ -529,6 +533,8 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
     a.key_cache = layer_base(key_cache, dims, layer_idx);
     a.value_cache = layer_base(value_cache, dims, layer_idx);
     a.block_tables = block_tables;
+    a.rows = dims.block_table_rows;
+    a.num_table_rows = dims.num_table_rows > 0 ? dims.num_table_rows : dims.num_seqs;
     a.context_lens = context_lens;
     a.cu_seqlens = cu_seqlens;
     a.items = decode_items;
@@ -563,6 +569,8 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
   a.key_cache = layer_base(key_cache, dims, layer_idx);
   a.value_cache = layer_base(value_cache, dims, layer_idx);
   a.block_tables = block_tables;
+  a.rows = dims.block_table_rows;
+  a.num_table_rows = dims.num_table_rows > 0 ? dims.num_table_rows : dims.num_seqs;
   a.context_lens = context_lens;
   a.cu_seqlens = cu_seqlens;
   a.num_seqs = dims.num_seqs;
@@ -646,6 +654,8 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
     a.key_cache = layer_base(key_cache, dims, layer_idx);
     a.value_cache = layer_base(value_cache, dims, layer_idx);
     a.block_tables = block_tables;
+    a.rows = dims.block_table_rows;
+    a.num_table_rows = dims.num_table_rows > 0 ? dims.num_table_rows : dims.num_seqs;
     a.context_lens = context_lens;
     a.cu_seqlens = cu_seqlens;
     a.items = prefill_items;
@@ -671,6 +681,8 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
   a.key_cache = layer_base(key_cache, dims, layer_idx);
   a.value_cache = layer_base(value_cache, dims, layer_idx);
   a.block_tables = block_tables;
+  a.rows = dims.block_table_rows;
+  a.num_table_rows = dims.num_table_rows > 0 ? dims.num_table_rows : dims.num_seqs;
   a.context_lens = context_lens;
   a.cu_seqlens = cu_seqlens;
   a.num_seqs = dims.num_seqs;

@@ -311,6 +311,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int h0 = kvh * a.group + sg * G;  // first query head
   const int seq = a.items[2 * item];
   const int part = a.items[2 * item + 1];
+  const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
+  const bool row_ok = trow >= 0 && trow < a.num_table_rows;
   const int ctx = a.context_lens[seq];
   const int p0 = part * a.partition;
   const int n = max(0, min(a.partition, ctx - p0));
@@ -327,8 +329,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   for (int i = tid; i < nblk; i += kDecodeThreads) {
     const int col = first_blk + i;
     int b = -1;
-    if (col < a.block_table_stride) {
-      b = a.block_tables[static_cast<int64_t>(seq) * a.block_table_stride + col];
+    if (row_ok && col < a.block_table_stride) {
+      b = a.block_tables[trow * a.block_table_stride + col];
       if (b < 0 || b >= a.total_blocks) b = -1;
     }
     s_blk[i] = b;

@@ -31,6 +31,7 @@ __global__ __launch_bounds__(kWave) void generic_attention_kernel(GenericArgs a)
   const int64_t row_stride = static_cast<int64_t>(a.num_kv_heads) * D;
 
   int seq = 0;
+  int64_t trow = 0;
   int n_ctx;
   if constexpr (kMasked) {
     n_ctx = a.num_context_tokens;
@@ -42,6 +43,7 @@ __global__ __launch_bounds__(kWave) void generic_attention_kernel(GenericArgs a)
       if (a.cu_seqlens[mid] <= t) lo = mid; else hi = mid;
     }
     seq = lo;
+    trow = a.rows != nullptr ? a.rows[seq] : seq;
     const int64_t first = a.cu_seqlens[seq];
     const int64_t count = a.cu_seqlens[seq + 1] - first;
     if ((a.filter == 1 && count != 1) || (a.filter == 2 && count == 1)) return;
@@ -76,8 +78,8 @@ __global__ __launch_bounds__(kWave) void generic_attention_kernel(GenericArgs a)
         }
       } else {
         const int col = c / a.block_size;
-        if (col < a.block_table_stride) {
-          const int b = a.block_tables[static_cast<int64_t>(seq) * a.block_table_stride + col];
+        if (trow >= 0 && trow < a.num_table_rows && col < a.block_table_stride) {
+          const int b = a.block_tables[trow * a.block_table_stride + col];
           if (b >= 0 && b < a.total_blocks)
             slot = static_cast<int64_t>(b) * a.block_size + (c - col * a.block_size);
         }

@@ -18,6 +18,10 @@
 namespace pa {
 
 constexpr int kWave = 64;
+
+// The block-table row a sequence with an invalid table row reads: one -1
+// (no block), so no kernel reads outside a caller's table.
+static __device__ const int32_t kNoBlockRow[1] = {-1};
 // XCDs of an MI355X: workgroup ids of one launch are dealt to them round-robin,
 // and each XCD has its own L2.
 constexpr int kXcds = 8;

@@ -15,6 +15,8 @@ struct DecodeArgs {
   const void* key_cache;    // base of the layer
   const void* value_cache;  // base of the layer
   const int32_t* block_tables;
+  const int32_t* rows;      // row of block_tables per sequence, or null (row = seq)
+  int32_t num_table_rows;   // rows of block_tables (a row outside reads as no blocks)
   const int32_t* context_lens;
   const int64_t* cu_seqlens;
   const int32_t* items;     // (seq, partition) pairs
@@ -53,6 +55,8 @@ struct GenericArgs {
   const void* value_cache;
   // block-table source
   const int32_t* block_tables;
+  const int32_t* rows;  // row of block_tables per sequence, or null (row = seq)
+  int32_t num_table_rows;
   const int32_t* context_lens;
   const int64_t* cu_seqlens;
   int32_t num_seqs;
@@ -85,6 +89,7 @@ struct PackArgs {
   const int64_t* start_positions;
   const int64_t* new_token_counts;
   int32_t* step_block_tables;     // [B, step_table_width] copy of the rows, or null
+  int32_t* step_rows;             // [B] the sequences' rows, or null
   int64_t* cu_seqlens;
   int64_t* cu_context_offsets;
   int32_t* context_lens;
@@ -101,6 +106,7 @@ struct PackArgs {
   int32_t num_table_rows;
   int32_t num_updates;
   int32_t step_table_width;
+  int32_t fused;                  // the scan kernel writes every output (one launch)
   int32_t block_size;
   int32_t block_table_stride;
   int32_t partition;
@@ -148,6 +154,8 @@ struct PrefillArgs {
   const void* key_cache;
   const void* value_cache;
   const int32_t* block_tables;
+  const int32_t* rows;   // row of block_tables per sequence, or null (row = seq)
+  int32_t num_table_rows;
   const int32_t* context_lens;
   const int64_t* cu_seqlens;
   const int32_t* items;  // (seq, query tile) pairs
@@ -187,6 +195,10 @@ bool generic_supported(int dtype, int head_dim);
 hipError_t launch_generic(const GenericArgs& a, int dtype, bool masked, hipStream_t stream);
 
 size_t pack_workspace_size(int64_t num_seqs);
+// Whether one launch can pack the step: a single scan chunk, no gather or
+// step table, and per-sequence work (new tokens, full partitions) bounded
+// by the hints.
+bool pack_fusable(const PackArgs& a, int32_t max_new_tokens, int32_t max_context);
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
 hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t stream);

@@ -16,6 +16,12 @@
 //                      scatter slots, positions, gather slots and work items
 //                      at the offsets the scan left.
 //
+// A small step (one chunk of sequences, no gather slots or step table, and
+// little work per sequence: a decode batch) is packed in ONE launch: the
+// scan kernel keeps each thread's sequence in registers and, once the bucket
+// bases are known, every thread fills its own sequence.  The two launches
+// would cost a second dispatch on the step's critical path.
+//
 // Reference semantics (all int64, bit-exact):
 //   cu_seqlens / cu_context_offsets: exclusive prefix sums over the new-token
 //     counts and over context_len = start + count
@@ -51,6 +57,9 @@ namespace pa {
 constexpr int kScanThreads = 1024;
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kFillThreads = 256;
+// Per-sequence work (new tokens, full partitions) one thread of the fused
+// launch takes on.
+constexpr int kFusedMaxWork = 32;
 
 __device__ __forceinline__ int64_t nonneg(int64_t v) { return v < 0 ? 0 : v; }
 
@@ -117,6 +126,95 @@ __device__ __forceinline__ SeqInput load_input(const PackArgs& a, int seq) {
   return in;
 }
 
+// One sequence's scatter slots, positions, gather slots and work items, at
+// the offsets the scan found (e: full, merge and prefill offsets and the
+// partial partition's rank in its bucket; in: start, count, table row; tok,
+// ctx: its first query and context token; bases: the buckets' first item).
+// `stride` threads share the loops, thread `first` of them calling.
+__device__ __forceinline__ void fill_sequence(const PackArgs& a, int seq, int4 e, int4 in, int64_t tok,
+                                              int64_t ctx, const int32_t* bases, int first, int stride) {
+  const int64_t start = in.x;
+  const int64_t count = in.y;
+  const int64_t clen = start + count;
+  const int32_t row = in.z;
+  const int32_t* bt = row >= 0 && row < a.num_table_rows
+                          ? a.block_tables + static_cast<int64_t>(row) * a.block_table_stride
+                          : nullptr;
+  const int64_t stride_bt = bt != nullptr ? a.block_table_stride : 0;
+  const int64_t bs = a.block_size;
+
+  // The sequence's row of the step's own block table (-1 past its row).
+  if (a.step_block_tables != nullptr) {
+    int32_t* out = a.step_block_tables + static_cast<int64_t>(seq) * a.step_table_width;
+    for (int j = first; j < a.step_table_width; j += stride) out[j] = j < stride_bt ? bt[j] : -1;
+  }
+
+  // New tokens: scatter slots + positions.
+  for (int64_t j = first; j < count; j += stride) {
+    const int64_t idx = tok + j;
+    if (idx >= a.max_query_tokens) break;
+    const int64_t p = start + j;
+    const int64_t col = p / bs;
+    int64_t slot = -1;
+    if (col < stride_bt) {
+      const int32_t b = bt[col];
+      if (b >= 0) slot = static_cast<int64_t>(b) * bs + (p - col * bs);
+    }
+    a.scatter_slots[idx] = slot;
+    a.position_ids[idx] = p;
+  }
+
+  // Whole context: gather slots.
+  if (a.gather_slots != nullptr) {
+    for (int64_t c = first; c < clen; c += stride) {
+      const int64_t idx = ctx + c;
+      if (idx >= a.max_context_tokens) break;
+      const int64_t col = c / bs;
+      int64_t slot = -1;
+      if (col < stride_bt) {
+        const int32_t b = bt[col];
+        if (b >= 0) slot = static_cast<int64_t>(b) * bs + (c - col * bs);
+      }
+      a.gather_slots[idx] = slot;
+    }
+  }
+
+  // Attention work lists.
+  const int64_t P = a.partition;
+  const int64_t nfull = count == 1 ? clen / P : 0;
+  const int64_t rem_idx = e.w >= 0 ? static_cast<int64_t>(bases[((clen % P - 1) * kPackBuckets) / P]) + e.w : -1;
+  if (count == 1 && a.merge_items != nullptr && first == 0 && e.y < a.max_merge_items &&
+      nfull + (rem_idx >= 0 ? 1 : 0) > 1) {
+    int4 m;
+    m.x = e.x;
+    m.y = static_cast<int32_t>(nfull);
+    m.z = seq;
+    m.w = static_cast<int32_t>(rem_idx);
+    reinterpret_cast<int4*>(a.merge_items)[e.y] = m;
+  }
+  if (count == 1 && a.decode_items != nullptr) {
+    for (int64_t p = first; p < nfull; p += stride) {
+      const int64_t idx = e.x + p;
+      if (idx >= a.max_decode_items) break;
+      a.decode_items[2 * idx] = seq;
+      a.decode_items[2 * idx + 1] = static_cast<int32_t>(p);
+    }
+    if (first == 0 && rem_idx >= 0 && rem_idx < a.max_decode_items) {
+      a.decode_items[2 * rem_idx] = seq;
+      a.decode_items[2 * rem_idx + 1] = static_cast<int32_t>(nfull);
+    }
+  } else if (count > 1 && a.prefill_items != nullptr) {
+    const int64_t ntiles = (count + a.prefill_tile - 1) / a.prefill_tile;
+    for (int64_t q = first; q < ntiles; q += stride) {
+      const int64_t idx = e.z + q;
+      if (idx >= a.max_prefill_items) break;
+      a.prefill_items[2 * idx] = seq;
+      a.prefill_items[2 * idx + 1] = static_cast<int32_t>(q);
+    }
+  }
+}
+
+template <bool kFused>
 __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -134,6 +232,7 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
   __shared__ Counts s_wave[kScanWaves];
   __shared__ int32_t s_bucket_wave[kScanWaves][kPackBuckets];  // per-chunk counts, then offsets
   __shared__ int32_t s_bucket_carry[kPackBuckets];
+  __shared__ int32_t s_bases[kFused ? kPackBuckets : 1];
   if (tid < kPackBuckets) s_bucket_carry[tid] = 0;
   if (tid == 0) {
     a.cu_seqlens[0] = 0;
@@ -146,6 +245,9 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
   int64_t tok_carry = 0, ctx_carry = 0;
   int32_t full_carry = 0, merge_carry = 0, tiles_carry = 0;
   SeqInput next = load_input(a, tid);
+  // One chunk when fused: the thread's sequence, kept for the fill below.
+  int4 f_e = {0, 0, 0, -1}, f_in = {0, 0, -1, 0};
+  int64_t f_tok = 0, f_ctx = 0;
   for (int base = 0; base < a.num_seqs; base += kScanThreads) {
     const int seq = base + tid;
     const bool valid = seq < a.num_seqs;
@@ -235,6 +337,13 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
       in.w = 0;
       a.ws_seq[2 * seq] = e;
       a.ws_seq[2 * seq + 1] = in;
+      if (a.step_rows != nullptr) a.step_rows[seq] = row;
+      if constexpr (kFused) {
+        f_e = e;
+        f_in = in;
+        f_tok = tok;
+        f_ctx = ctx;
+      }
     }
     tok_carry += total.tok;
     ctx_carry += total.ctx;
@@ -250,104 +359,38 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
     const int32_t incl = wave_inclusive_sum(mine);
     a.ws_header[1 + kPackBuckets - 1 - lane] = full_carry + incl - mine;
     if (lane == 0) a.ws_header[0] = full_carry;
+    if constexpr (kFused) s_bases[kPackBuckets - 1 - lane] = full_carry + incl - mine;
+  }
+  if constexpr (kFused) {
+    // The fill, one thread per sequence.  The barrier also makes the table
+    // updates above visible to every thread reading a row.
+    __syncthreads();
+    if (tid < a.num_seqs) fill_sequence(a, tid, f_e, f_in, f_tok, f_ctx, s_bases, 0, 1);
   }
 }
 
 __global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(PackArgs a) {
   const int seq = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int4 e = a.ws_seq[2 * seq];
-  const int4 in = a.ws_seq[2 * seq + 1];
-  const int64_t start = in.x;
-  const int64_t count = in.y;
-  const int64_t clen = start + count;
-  const int64_t tok = a.cu_seqlens[seq];
-  const int64_t ctx = a.cu_context_offsets[seq];
-  const int32_t row = in.z;
-  const int32_t* bt = row >= 0 && row < a.num_table_rows
-                          ? a.block_tables + static_cast<int64_t>(row) * a.block_table_stride
-                          : nullptr;
-  const int64_t stride = bt != nullptr ? a.block_table_stride : 0;
-  const int64_t bs = a.block_size;
-
-  // The sequence's row of the step's own block table (-1 past its row).
-  if (a.step_block_tables != nullptr) {
-    int32_t* out = a.step_block_tables + static_cast<int64_t>(seq) * a.step_table_width;
-    for (int j = tid; j < a.step_table_width; j += kFillThreads) out[j] = j < stride ? bt[j] : -1;
-  }
-
-  // New tokens: scatter slots + positions.
-  for (int64_t j = tid; j < count; j += kFillThreads) {
-    const int64_t idx = tok + j;
-    if (idx >= a.max_query_tokens) break;
-    const int64_t p = start + j;
-    const int64_t col = p / bs;
-    int64_t slot = -1;
-    if (col < stride) {
-      const int32_t b = bt[col];
-      if (b >= 0) slot = static_cast<int64_t>(b) * bs + (p - col * bs);
-    }
-    a.scatter_slots[idx] = slot;
-    a.position_ids[idx] = p;
-  }
-
-  // Whole context: gather slots.
-  if (a.gather_slots != nullptr) {
-    for (int64_t c = tid; c < clen; c += kFillThreads) {
-      const int64_t idx = ctx + c;
-      if (idx >= a.max_context_tokens) break;
-      const int64_t col = c / bs;
-      int64_t slot = -1;
-      if (col < stride) {
-        const int32_t b = bt[col];
-        if (b >= 0) slot = static_cast<int64_t>(b) * bs + (c - col * bs);
-      }
-      a.gather_slots[idx] = slot;
-    }
-  }
-
-  // Attention work lists.
-  const int64_t P = a.partition;
-  const int64_t nfull = count == 1 ? clen / P : 0;
-  const int64_t rem_idx =
-      e.w >= 0 ? static_cast<int64_t>(a.ws_header[1 + ((clen % P - 1) * kPackBuckets) / P]) + e.w : -1;
-  if (count == 1 && a.merge_items != nullptr && tid == 0 && e.y < a.max_merge_items &&
-      nfull + (rem_idx >= 0 ? 1 : 0) > 1) {
-    int4 m;
-    m.x = e.x;
-    m.y = static_cast<int32_t>(nfull);
-    m.z = seq;
-    m.w = static_cast<int32_t>(rem_idx);
-    reinterpret_cast<int4*>(a.merge_items)[e.y] = m;
-  }
-  if (count == 1 && a.decode_items != nullptr) {
-    for (int64_t p = tid; p < nfull; p += kFillThreads) {
-      const int64_t idx = e.x + p;
-      if (idx >= a.max_decode_items) break;
-      a.decode_items[2 * idx] = seq;
-      a.decode_items[2 * idx + 1] = static_cast<int32_t>(p);
-    }
-    if (tid == 0 && rem_idx >= 0 && rem_idx < a.max_decode_items) {
-      a.decode_items[2 * rem_idx] = seq;
-      a.decode_items[2 * rem_idx + 1] = static_cast<int32_t>(nfull);
-    }
-  } else if (count > 1 && a.prefill_items != nullptr) {
-    const int64_t ntiles = (count + a.prefill_tile - 1) / a.prefill_tile;
-    for (int64_t q = tid; q < ntiles; q += kFillThreads) {
-      const int64_t idx = e.z + q;
-      if (idx >= a.max_prefill_items) break;
-      a.prefill_items[2 * idx] = seq;
-      a.prefill_items[2 * idx + 1] = static_cast<int32_t>(q);
-    }
-  }
+  fill_sequence(a, seq, a.ws_seq[2 * seq], a.ws_seq[2 * seq + 1], a.cu_seqlens[seq], a.cu_context_offsets[seq],
+                a.ws_header + 1, threadIdx.x, kFillThreads);
 }
 
 size_t pack_workspace_size(int64_t num_seqs) {
   return kPackHeaderBytes + static_cast<size_t>(num_seqs > 0 ? num_seqs : 0) * 2 * sizeof(int4);
 }
 
+bool pack_fusable(const PackArgs& a, int32_t max_new_tokens, int32_t max_context) {
+  return a.num_seqs > 0 && a.num_seqs <= kScanThreads && a.gather_slots == nullptr &&
+         a.step_block_tables == nullptr && max_new_tokens > 0 && max_new_tokens <= kFusedMaxWork &&
+         max_context > 0 && max_context / a.partition <= kFusedMaxWork;
+}
+
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, a);
+  if (a.fused) {
+    hipLaunchKernelGGL(pack_scan_kernel<true>, dim3(1), dim3(kScanThreads), 0, stream, a);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(pack_scan_kernel<false>, dim3(1), dim3(kScanThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.num_seqs == 0) return e;
   hipLaunchKernelGGL(pack_fill_kernel, dim3(static_cast<uint32_t>(a.num_seqs)), dim3(kFillThreads), 0,

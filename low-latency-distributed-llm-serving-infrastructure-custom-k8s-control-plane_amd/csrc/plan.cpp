@@ -2,6 +2,7 @@
 // from the host arrays the scheduler already holds, and chooses the decode
 // split-K partition.  Plain C++: no HIP call, so the host can size and
 // launch a step without reading anything back from the device.
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -88,6 +89,7 @@ int pa_plan_step(const int64_t* starts, const int64_t* counts, const int64_t* al
     plan->num_query_tokens += c;
     plan->num_context_tokens += ctx;
     if (ctx > plan->max_context) plan->max_context = ctx;
+    if (c > plan->max_new_tokens) plan->max_new_tokens = c < INT32_MAX ? static_cast<int32_t>(c) : INT32_MAX;
     const int64_t blocks = ceil_div(ctx, params.block_size);
     if (blocks > plan->max_blocks) plan->max_blocks = static_cast<int32_t>(blocks);
     if (c == 1) {

@@ -167,7 +167,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // under 4 GiB, so a row offset is one 32 x 32 -> 64-bit multiply-add).
   const uint32_t row_bytes = static_cast<uint32_t>(hkv) * ROW_BYTES;
   const uint32_t block_bytes = row_bytes << log2_bs;
-  const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
+  const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
+  const bool row_ok = trow >= 0 && trow < a.num_table_rows;
+  const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
+  const int bt_stride = row_ok ? a.block_table_stride : 1;
   const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * ROW_BYTES;
   const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * ROW_BYTES;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_lds));
@@ -194,13 +197,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
   // Positions that have a block-table column (the rest are never read).
   const int kv_read = static_cast<int>(
-      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(a.block_table_stride) << log2_bs));
+      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
   const int ntiles = (kv_end + kKvTile - 1) / kKvTile;
   const int nstages = (kv_end + kStage - 1) / kStage;
   // Tiles below this index need no mask for any row of the workgroup.
   const int first_masked = min(start + tok0 + 1, kv_end) / kKvTile;
   const float scale = a.scale_log2e;
-  const int last_col = a.block_table_stride - 1;
+  const int last_col = bt_stride - 1;
 
   // ---- staging ---------------------------------------------------------------
   // Block ids: wave 0 copies the table entries a stage needs (at most 64)

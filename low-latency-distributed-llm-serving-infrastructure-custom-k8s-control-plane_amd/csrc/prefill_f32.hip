@@ -87,7 +87,10 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
   const int64_t row_elems = static_cast<int64_t>(hkv) * D;  // cache row of one token
-  const int32_t* bt = a.block_tables + static_cast<int64_t>(seq) * a.block_table_stride;
+  const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
+  const bool row_ok = trow >= 0 && trow < a.num_table_rows;
+  const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
+  const int bt_stride = row_ok ? a.block_table_stride : 1;
   const float* kbase = reinterpret_cast<const float*>(a.key_cache) + kvh * D;
   const float* vbase = reinterpret_cast<const float*>(a.value_cache) + kvh * D;
   const int hq = hkv * a.group;
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
   const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
   // Positions that have a block-table column (the rest are never read).
   const int kv_read = static_cast<int>(
-      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(a.block_table_stride) << log2_bs));
+      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
   const int nstages = (kv_end + kF32Stage - 1) / kF32Stage;
   const float scale = a.scale_log2e;
 

@@ -76,6 +76,9 @@ def prefill_tile_for(num_query_heads: int, num_kv_heads: int) -> int:
 # (a) packing
 
 
+_INT32_MAX = (1 << 31) - 1
+
+
 def _align(n: int, a: int = 256) -> int:
     return (n + a - 1) // a * a
 
@@ -103,25 +106,31 @@ class _HostStaging:
     from (through their device addresses, pa_map_host_memory), so no copy
     launch precedes it.
 
-    A slot is reused only after the launch that last read it has run (an
-    event recorded behind it), so the host never overwrites bytes a pending
-    launch still reads, and never waits in the steady state."""
+    The ring's 16 slots form two halves.  One event is recorded on the stream
+    when a half has been handed out, and a half is reused only after its
+    event has completed, so the host never overwrites bytes a pending launch
+    still reads and, in the steady state, never waits.  Recording one event
+    per 8 steps instead of one per step matters: every event record puts a
+    few microseconds of idle time between two kernels."""
 
-    SLOTS = 8
+    SLOTS = 16
+    HALF = SLOTS // 2
 
     def __init__(self) -> None:
         self._bufs = [None] * self.SLOTS
         self._arrays = [None] * self.SLOTS
         self._device = [0] * self.SLOTS
-        self._events = [None] * self.SLOTS
+        self._events = [None, None]  # per half: recorded after its last slot's use
         self._next = 0
 
     def take(self, nbytes: int):
         """(slot, numpy view, device address) of a free buffer of >= nbytes."""
         slot = self._next
         self._next = (slot + 1) % self.SLOTS
-        if self._events[slot] is not None:
-            self._events[slot].synchronize()
+        if slot % self.HALF == 0:  # entering a half: its previous uses must be done
+            ev = self._events[slot // self.HALF]
+            if ev is not None:
+                ev.synchronize()
         buf = self._bufs[slot]
         if buf is None or buf.numel() < nbytes:
             buf = torch.empty(max(_align(nbytes, 1 << 16), 1 << 16), dtype=torch.uint8, pin_memory=True)
@@ -132,10 +141,13 @@ class _HostStaging:
         return slot, self._arrays[slot], self._device[slot]
 
     def done(self, slot: int, stream) -> None:
-        ev = self._events[slot]
-        if ev is None:
-            ev = self._events[slot] = torch.cuda.Event()
-        ev.record(stream)
+        """The launch reading ``slot`` is enqueued on ``stream``."""
+        if slot % self.HALF == self.HALF - 1:  # a half handed out: mark its end
+            half = slot // self.HALF
+            ev = self._events[half]
+            if ev is None:
+                ev = self._events[half] = torch.cuda.Event()
+            ev.record(stream)
 
 
 _STAGING: dict = {}  # device -> _HostStaging
@@ -167,14 +179,19 @@ class PackedStep:
     Host-side counts come from the host planner (pa_plan_step), so no
     device-to-host synchronisation sizes the grids.
 
-    Arrays: block_tables int32 [B, width] (the step's table), start_positions
-    / new_token_counts int64 [B], cu_seqlens / cu_context_offsets int64
-    [B+1], context_lens int32 [B], scatter_slots / position_ids int64 [T],
-    decode_items int32 [n, 2], merge_items int32 [n, 4], prefill_items int32
-    [n, 2]; gather_slots int64 [C] is built on first use.
+    Arrays: cu_seqlens / cu_context_offsets int64 [B+1], context_lens int32
+    [B], scatter_slots / position_ids int64 [T], decode_items int32 [n, 2],
+    merge_items int32 [n, 4], prefill_items int32 [n, 2]; gather_slots int64
+    [C] is built on first use.  A step packed from a pool of table rows also
+    has rows int32 [B] (each sequence's row): the attention kernels read the
+    pool in place through it.  block_tables int32 [B, width] is the step's
+    table: the caller's own, the pool rows pa_pack copied (``step_table``),
+    or else gathered from the pool when first read (a convenience view, not
+    used by the kernels).  start_positions / new_token_counts are the host
+    arrays of the step.
     """
 
-    def __init__(self, buffer, layout, plan, block_size, prefill_tile, table, table_rows, rows_name,
+    def __init__(self, buffer, layout, plan, block_size, prefill_tile, table, table_rows, pooled,
                  head_shape, inputs):
         self.buffer = buffer
         self._layout = layout
@@ -192,16 +209,20 @@ class PackedStep:
         self.num_decode_seqs = int(plan.num_decode_seqs)
         self.num_prefill_seqs = int(plan.num_prefill_seqs)
         self.max_context = int(plan.max_context)
-        self._source_table = table  # the table pa_pack reads (the step's own, or a pool)
+        self.max_new_tokens = int(plan.max_new_tokens)
+        self._max_blocks = int(plan.max_blocks)
+        self._source_table = table  # the table pa_pack and the kernels read (the step's own, or a pool)
         self._source_rows = table_rows
-        self._rows_name = rows_name  # None when block_tables is the step's own table
+        self._pooled = bool(pooled)
         self._head_shape = head_shape  # (H_q, D) the workspace was sized for, or None
         self._gather = None
         self._extra_ws = None
 
     # -- addresses and views ---------------------------------------------------
     def ptr(self, name: str) -> int:
-        if name == "block_tables" and self._rows_name is None:
+        """Device address of an array; "block_tables" is the table the
+        kernels read (the caller's table or the pool)."""
+        if name == "block_tables":
             return self._source_table.data_ptr()
         return self._base + self._layout.fields[name][0]
 
@@ -218,11 +239,29 @@ class PackedStep:
         layout = self.__dict__.get("_layout")
         if layout is None:
             raise AttributeError(name)
-        if name == "block_tables" and self.__dict__["_rows_name"] is None:
-            return self.__dict__["_source_table"]
         if name in layout.fields:
             return self._view(name)
+        if name == "block_tables":
+            if not self.__dict__["_pooled"]:
+                return self.__dict__["_source_table"]
+            table = self._gathered_table()
+            self.__dict__[name] = table
+            return table
         raise AttributeError(name)
+
+    def _gathered_table(self) -> torch.Tensor:
+        """[B, max_blocks] rows of the pool for the step's sequences (-1 for a
+        row outside the pool and past the pool's width)."""
+        src = self._source_table
+        width = max(self._max_blocks, 1)
+        out = torch.full((self.num_seqs, width), -1, dtype=torch.int32, device=self.buffer.device)
+        if self.num_seqs == 0 or src.numel() == 0:
+            return out
+        rows = self.rows.long()
+        ok = (rows >= 0) & (rows < self._source_rows)
+        n = min(width, int(src.shape[1]))
+        out[ok, :n] = src.index_select(0, rows[ok])[:, :n]
+        return out
 
     @property
     def start_positions(self) -> np.ndarray:
@@ -256,9 +295,8 @@ class PackedStep:
 
     @property
     def table_width(self) -> int:
-        if self._rows_name is None:
-            return int(self._source_table.shape[1])
-        return int(self._layout.fields["block_tables"][2][1])
+        """Row stride of the table the kernels read."""
+        return int(self._source_table.shape[1]) if self._source_table.dim() == 2 else 0
 
     @property
     def gather_slots(self) -> torch.Tensor:
@@ -423,7 +461,7 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
         gather = torch.empty(step.num_context_tokens, dtype=torch.int64, device=device)
     starts, counts, rows = step._inputs
     b = step.num_seqs
-    pooled = rows is not None
+    pooled = step._pooled
     n_upd = 0 if updates is None else int(updates.shape[0])
     staging = slot = None
     dev = o_counts = o_rows = o_upd = 0
@@ -441,15 +479,18 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
         if n_upd:
             host[o_upd:nbytes].view(np.int32)[:] = updates.reshape(-1)
     table = step._source_table
+    step_table = step._layout.fields.get("block_tables")
     dims = _native.PaPackDims(
         num_seqs=b,
         block_size=step.block_size,
-        max_blocks_per_seq=int(table.shape[1]) if table.dim() == 2 else 0,
+        max_blocks_per_seq=step.table_width,
         partition_size=step.partition_size,
         prefill_tile=step.prefill_tile,
         num_table_rows=step._source_rows,
         num_updates=n_upd,
-        step_table_width=step.table_width if pooled else 0,
+        step_table_width=step_table[2][1] if step_table else 0,
+        max_new_tokens=min(step.max_new_tokens, _INT32_MAX),
+        max_context=min(step.max_context, _INT32_MAX),
         max_query_tokens=step.num_query_tokens,
         max_context_tokens=step.num_context_tokens,
         max_decode_items=step.num_decode_items,
@@ -464,7 +505,8 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
         dev or None,
         dev + o_counts if dev else None,
         dims,
-        step.ptr("block_tables") if pooled else None,
+        step._base + step_table[0] if step_table else None,
+        step.ptr("rows") if pooled else None,
         step.ptr("cu_seqlens"),
         step.ptr("cu_context_offsets"),
         step.ptr("context_lens"),
@@ -500,15 +542,18 @@ def pack_step(
     rows=None,
     updates: Optional[np.ndarray] = None,
     allocated_tokens=None,
+    step_table: bool = False,
 ) -> PackedStep:
     """Plan a step on the host, upload its description once, and run the GPU
     packing kernels.
 
     ``block_tables``: int32 [B, max_blocks] device tensor (-1 padded), the
     step's own table; or, with ``rows`` (one row index per sequence), a
-    device-resident pool of table rows from which pa_pack gathers the step's
-    table (``PackedStep.block_tables``), after applying ``updates`` (int32
-    [n, 3] (row, col, block) triples, host array) to it.
+    device-resident pool of table rows that pa_pack first applies
+    ``updates`` (int32 [n, 3] (row, col, block) triples, host array) to, and
+    that the attention kernels then read in place through the step's
+    ``rows``.  ``step_table``: also have pa_pack copy the step's rows of
+    the pool into a table of its own (``PackedStep.block_tables``).
     ``start_positions`` / ``new_token_counts``: the host lists of the step.
     ``allocated_tokens``: per sequence, the tokens it has slots for; a step
     reaching past them is a ValueError (as the reference's slot mapping).
@@ -554,7 +599,9 @@ def pack_step(
     layout = _Layout()
     t, c = int(plan.num_query_tokens), int(plan.num_context_tokens)
     if pooled:
-        layout.add("block_tables", torch.int32, (b, max(int(plan.max_blocks), 1)))
+        layout.add("rows", torch.int32, (b,))
+        if step_table:
+            layout.add("block_tables", torch.int32, (b, max(int(plan.max_blocks), 1)))
     layout.add("cu_seqlens", torch.int64, (b + 1,))
     layout.add("cu_context_offsets", torch.int64, (b + 1,))
     layout.add("context_lens", torch.int32, (b,))
@@ -573,8 +620,8 @@ def pack_step(
     buffer = torch.empty(layout.nbytes, dtype=torch.uint8, device=device)
     rows_arr = None if rows is None else np.ascontiguousarray(np.asarray(rows, dtype=np.int32).reshape(-1))
     table_rows = int(block_tables.shape[0]) if block_tables.numel() else 0
-    step = PackedStep(buffer, layout, plan, block_size, prefill_tile, block_tables, table_rows,
-                      "rows" if pooled else None, head_shape, (starts, counts, rows_arr))
+    step = PackedStep(buffer, layout, plan, block_size, prefill_tile, block_tables, table_rows, pooled,
+                      head_shape, (starts, counts, rows_arr))
     upd = None if not n_upd else np.ascontiguousarray(updates, dtype=np.int32)
     gather = _run_pack(step, with_gather=with_gather, updates=upd, fresh=True)
     if with_gather:
@@ -743,8 +790,10 @@ def _step_dims(query_t: torch.Tensor, key_cache: torch.Tensor, step: PackedStep)
         max_blocks_per_seq=step.table_width,
         partition_size=step.partition_size,
         dtype=dtype_code(key_cache.dtype),
+        num_table_rows=step._source_rows,
         q_token_stride=query_t.stride(0),
         q_head_stride=query_t.stride(1),
+        block_table_rows=step.ptr("rows") if step._pooled else None,
     )
 
 

@@ -92,20 +92,20 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == native.PA_ERR_INVALID_ARGUMENT and b"missing" in lib.pa_last_error_message()
     assert lib.pa_copy_blocks(None, None, None, 0, 1, 1, 1, 16, None) == native.PA_OK
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
-    args = [None] * 5 + [pdims] + [None] * 10 + [None, 0, None]
+    args = [None] * 5 + [pdims] + [None] * 11 + [None, 0, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     pdims.block_size = 16
     pdims.step_table_width = 4
-    fake = [0x1000 * (i + 1) for i in range(16)]
-    args = fake[:5] + [pdims] + fake[5:15] + [None, 0, None]
+    fake = [0x1000 * (i + 1) for i in range(17)]
+    args = fake[:5] + [pdims] + fake[5:16] + [None, 0, None]
     rc = lib.pa_pack(*args)
     assert rc == native.PA_ERR_WORKSPACE and b"workspace of 544 bytes" in lib.pa_last_error_message()
     assert lib.pa_pack_workspace_size(1) == 544 and lib.pa_pack_workspace_size(0) == 512
-    args = fake[:3] + [None, fake[4], pdims] + fake[5:15] + [fake[15], 4096, None]
+    args = fake[:3] + [None, fake[4], pdims] + fake[5:16] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"both NULL" in lib.pa_last_error_message()
     pdims.num_updates = 2
-    args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:15] + [fake[15], 4096, None]
+    args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:16] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"2 updates" in lib.pa_last_error_message()
     for direction in (-1, 2):

@@ -150,6 +150,33 @@ def test_pack_matches_oracle_on_ragged_edges(device, seed):
     _check_pack(step, _pack_expect(starts, counts, lists, bs, step.partition_size, 16))
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_pack_one_launch_matches_oracle(device, seed):
+    """Steps that pa_pack does in one launch (at most 1024 sequences, at most
+    32 new tokens and 32 full partitions per sequence, no gather slots):
+    every output equals the oracle's, and so does a two-launch re-run of the
+    same step that adds the gather slots."""
+    rng = np.random.default_rng(100 + seed)
+    bs = [16, 1, 32, 4][seed]
+    b = [1, 37, 1000, 1024][seed]
+    partition = [None, 100, 512, 64][seed]
+    starts = [int(x) for x in rng.integers(0, 1900, size=b)]
+    counts = [int(rng.choice([0, 1, 1, 1, 1, 2, int(rng.integers(3, 33))])) for _ in range(b)]
+    lists, off = [], 0
+    perm = rng.permutation(1 << 19)  # enough distinct blocks for 1024 contexts of up to 1932 tokens at bs 4
+    for s_, c in zip(starts, counts):
+        n = -(-(s_ + c) // bs)
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    table = torch.from_numpy(op.build_block_tables(lists, [s_ + c for s_, c in zip(starts, counts)])[0]).to(device)
+    step = ops.pack_step(table, starts, counts, bs, prefill_tile=16, partition_size=partition)
+    log(f"one-launch pack B={b} bs={bs} partition={step.partition_size} items={step.num_decode_items}")
+    assert step.max_context // step.partition_size <= 32 and max(counts) <= 32
+    exp = _pack_expect(starts, counts, lists, bs, step.partition_size, 16)
+    _check_pack(step, exp)  # reading gather_slots re-runs the step in two launches
+    _check_pack(step, exp)
+
+
 def test_pack_empty_batch(device):
     table = torch.empty((0, 1), dtype=torch.int32, device=device)
     step = ops.pack_step(table, [], [], 16, with_gather=True)

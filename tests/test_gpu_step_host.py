@@ -47,12 +47,15 @@ def _check(step, exp):
         assert np.array_equal(got.reshape(want.shape), want), name
 
 
-@pytest.mark.parametrize("seed", range(3))
-def test_pack_from_pool_rows_with_updates(device, seed):
+@pytest.mark.parametrize("seed,one_launch", [(0, False), (1, False), (2, False), (3, True), (4, True)])
+def test_pack_from_pool_rows_with_updates(device, seed, one_launch):
     """A pool of rows on the device, queued (row, col, block) updates (two of
     them outside the table, skipped) and a step over a shuffled subset of
-    rows: the device pool ends updated, and the gathered step table, slots
-    and work lists equal the oracle's on the updated rows."""
+    rows: the device pool ends updated, and the step's rows, its table
+    (copied by pa_pack, or gathered from the pool), slots and work lists
+    equal the oracle's on the updated rows.  With ``one_launch`` the step
+    has at most 32 new tokens per sequence and no gather slots or step
+    table: pa_pack does it in one launch, the table updates included."""
     rng = np.random.default_rng(seed)
     bs, rows_n, width = 16, 300, 40
     pool = np.full((rows_n, width), -1, dtype=np.int32)
@@ -73,21 +76,28 @@ def test_pack_from_pool_rows_with_updates(device, seed):
     starts, counts = [], []
     for r in rows:
         cap = int(nblocks[r]) * bs
-        c = int(rng.choice([1, 1, 1, int(rng.integers(2, min(cap, 200) + 1)) if cap > 1 else 1]))
+        most = 32 if one_launch else 200
+        c = int(rng.choice([1, 1, 1, int(rng.integers(2, min(cap, most) + 1)) if cap > 1 else 1]))
         c = min(c, cap)
         s = int(rng.integers(0, cap - c + 1))
         starts.append(s)
         counts.append(c)
     lists = [[int(b) for b in pool[r, : nblocks[r]]] for r in rows]
     step = ops.pack_step(dev_pool, starts, counts, bs, rows=rows, updates=np.asarray(upd, dtype=np.int32),
-                         prefill_tile=32, with_gather=True, num_kv_heads=8, num_query_heads=32)
+                         prefill_tile=32, with_gather=not one_launch, step_table=not one_launch, num_kv_heads=8,
+                         num_query_heads=32)
     torch.cuda.synchronize()
-    log(f"pool pack seed {seed}: B={len(rows)} partition={step.partition_size}")
+    log(f"pool pack seed {seed}: B={len(rows)} partition={step.partition_size} one_launch={one_launch}")
     assert np.array_equal(dev_pool.cpu().numpy(), pool)
+    assert np.array_equal(step.rows.cpu().numpy(), rows)
+    assert step.table_width == width and step.ptr("block_tables") == dev_pool.data_ptr()
     width_step = max(-(-(s + c) // bs) for s, c in zip(starts, counts))
     assert step.block_tables.shape == (len(rows), width_step)
     assert np.array_equal(step.block_tables.cpu().numpy(), pool[rows, :width_step])
-    _check(step, _expect(starts, counts, lists, bs, step.partition_size, 32))
+    exp = _expect(starts, counts, lists, bs, step.partition_size, 32)
+    if one_launch:
+        assert max(counts) <= 32 and step.max_context // step.partition_size <= 32
+    _check(step, exp)  # gather_slots of a one-launch step: built on first use by the two-launch path
 
 
 @pytest.mark.parametrize("b", [1, 1023, 1024, 1025, 4097])
