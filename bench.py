@@ -385,7 +385,8 @@ def host_step_us(store, seqs, w, reps=200):
 
 
 def decode_main(args, w, t, device):
-    """The headline decode line (cfg 4 by default; cfg 3 with --workload)."""
+    """The headline decode line (Llama-3-8B GQA decode by default; another decode
+    workload with --workload)."""
     import torch
 
     ops = pkg("paged_ops")
@@ -479,7 +480,7 @@ def rotated_copies(nbytes_per_copy: int) -> int:
 
 
 def decode_rotated(args, w, device):
-    """A launch-bound decode (cfg 1) timed from a HIP graph over R copies of
+    """A launch-bound decode (fp32 MHA, 8 sequences) timed from a HIP graph over R copies of
     the pool, one per launch, so no launch finds its K/V in the MALL."""
     import torch
 
@@ -514,7 +515,7 @@ def decode_rotated(args, w, device):
 
 
 def kv_write_pack_line(args, w, device):
-    """cfg 2: the packing kernels over the step's block tables plus the K/V
+    """The K/V write + packing step: the packing kernels over the step's block tables plus the K/V
     write of its new tokens, timed from a HIP graph over R rotated copies of
     the new rows and the cache."""
     import numpy as np
@@ -589,7 +590,7 @@ def kv_write_pack_line(args, w, device):
 
 
 def decode_config_line(args, w, t, device):
-    """cfg 3 inside `configs`: the decode step, its partition kernel and the
+    """Llama-7B MHA decode inside `configs`: the decode step, its partition kernel and the
     CPU baseline (the pool, 2.2 GB, is far larger than the MALL)."""
     import torch
 
@@ -623,7 +624,7 @@ def decode_config_line(args, w, t, device):
 
 
 def mixed_line(args, w, t, device):
-    """cfg 5: four 512-token prefill chunks + 128 long-context decodes in one
+    """The mixed step: four 512-token prefill chunks + 128 long-context decodes in one
     flattened step: the attention step (prefill + split-K decode), the whole
     step with packing and the K/V write, the decode kernel's GB/s, and the
     prefill kernel's TFLOP/s against the bf16 MFMA peak."""

@@ -39,8 +39,10 @@
 // publishes them (the compiler would otherwise drain every copy before each
 // LDS read, as it cannot tell the buffers apart).
 // Masking is applied only to tiles that cross the causal diagonal or the end
-// of the context, and the accumulator is rescaled only when some row's
-// maximum grew by more than 2^8 over the reference maximum in use.
+// of the context (or to every tile when some block id of the sequence lies
+// outside the pool: those positions are skipped, as in decode), and the
+// accumulator is rescaled only when some row's maximum grew by more than 2^8
+// over the reference maximum in use.
 //
 // Reference: the block-diagonal causal mask of app/model/paged_attention.py:
 // 92-118 applied by SDPA (paged_attention.py:170-178); query token j of a
@@ -123,7 +125,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   constexpr int kRowsPerDma = kWave / CHUNKS;             // rows one wave load covers
   // The copies are issued by the waves of the first context half (0-3):
   // they reach the barrier earlier, and issuing from all eight waves bunched
-  // the copies behind the barrier (59.6 -> 57.1 us median on cfg 5, one box).
+  // the copies behind the barrier (59.6 -> 57.1 us median on the mixed
+  // prefill + decode step).
   constexpr int kCopyWaves = kPrefillWaves / 2;
   constexpr int kDmaPerWave = kStage / kCopyWaves / kRowsPerDma;  // per tensor
   constexpr int kRegionBytes = kStage * ROW_BYTES;        // K (or V) rows of a stage
@@ -200,10 +203,17 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
   const int ntiles = (kv_end + kKvTile - 1) / kKvTile;
   const int nstages = (kv_end + kStage - 1) / kStage;
-  // Tiles below this index need no mask for any row of the workgroup.
-  const int first_masked = min(start + tok0 + 1, kv_end) / kKvTile;
   const float scale = a.scale_log2e;
   const int last_col = bt_stride - 1;
+  // Positions whose block id lies outside the pool are skipped, as the
+  // decode kernels skip them: one pass over the row's columns tells whether
+  // there are any (then every tile takes the masked path below).
+  int bad_local = 0;
+  for (int c = tid; c < ((kv_read + bs_mask) >> log2_bs); c += kPrefillThreads)
+    bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+  const bool bad_ids = __syncthreads_or(bad_local) != 0;
+  // Tiles below this index need no mask for any row of the workgroup.
+  const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
 
   // ---- staging ---------------------------------------------------------------
   // Block ids: wave 0 copies the table entries a stage needs (at most 64)
@@ -211,19 +221,22 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // copying wave w copies rows [16 w, 16 w + 16) of a stage (lane -> row
   // lane / CHUNKS of its load, chunk position lane % CHUNKS, fetching the
   // chunk that the swizzle puts there), three stages ahead.  Rows past the
-  // readable context re-read its last row (finite; their scores are
-  // masked); an out-of-pool block id reads block 0 (the reference leaves
-  // such ids undefined).  Every copy is issued unconditionally, so each
-  // wave's outstanding count is the same every step.
+  // readable context re-read its last row, and an out-of-pool block id
+  // reads block 0 (finite values; their scores are masked).  Every copy is
+  // issued unconditionally, so each wave's outstanding count is the same
+  // every step.
   auto dma_ids = [&](int stage) {
     const int col = min(((stage * kStage) >> log2_bs) + lane, last_col);
     dma4(lds0 + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes, bt + col);
+  };
+  auto stage_ids = [&](int stage) {
+    return reinterpret_cast<const int*>(s_lds + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes);
   };
   const int dma_row0 = (wave % kCopyWaves) * (kStage / kCopyWaves) + lane / CHUNKS;  // + j * kRowsPerDma
   auto dma_kv = [&](int stage, int buf_off) {
     if (wave >= kCopyWaves) return;
     const int col0 = (stage * kStage) >> log2_bs;
-    const int* ids = reinterpret_cast<const int*>(s_lds + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes);
+    const int* ids = stage_ids(stage);
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
       const int r = dma_row0 + j * kRowsPerDma;  // row inside the stage
@@ -339,10 +352,16 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       f32x16 s = s_in;
       const int kv0 = t * kKvTile;
       if (t >= first_masked) {
+        const int* ids = stage_ids(st);
+        const int col0 = (st * kStage) >> log2_bs;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
-          if (kv > qpos || kv >= kv_end) s[i] = -INFINITY;
+          bool off = kv > qpos || kv >= kv_read;
+          if (bad_ids)
+            off = off || static_cast<uint32_t>(ids[(kv >> log2_bs) - col0]) >=
+                             static_cast<uint32_t>(a.total_blocks);
+          if (off) s[i] = -INFINITY;
         }
       }
       float tmax = s[0];

@@ -61,6 +61,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
   __shared__ __attribute__((aligned(16))) float s_q[kF32Rows * LD];
   __shared__ __attribute__((aligned(16))) float s_kp[KP];
   __shared__ __attribute__((aligned(16))) float s_v[kF32Stage * LD];
+  __shared__ int s_ok[kF32Stage];  // the stage's token has a block in the pool
   float* const s_k = s_kp;
   float* const s_p = s_kp;
 
@@ -137,13 +138,16 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
   for (int st = 0; st < nstages; ++st) {
     __syncthreads();  // the previous stage's K, V and p are consumed
     // 1. K and V rows of the stage -> LDS.  Rows past the readable context
-    // re-read its last row (finite; their scores are masked); an
-    // out-of-pool block id reads block 0.
+    // re-read its last row and an out-of-pool block id reads block 0 (finite
+    // values; their scores are masked: such positions are skipped, as in
+    // decode).
     for (int i = tid; i < kF32Stage * (D / 4); i += kF32Threads) {
       const int r = i / (D / 4), q4 = i - r * (D / 4);
       const int pos = min(st * kF32Stage + r, kv_read - 1);
       int b = bt[pos >> log2_bs];
-      b = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks) ? b : 0;
+      const bool in_pool = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks);
+      if (q4 == 0) s_ok[r] = in_pool && st * kF32Stage + r < kv_read;
+      b = in_pool ? b : 0;
       const int64_t off = ((static_cast<int64_t>(b) << log2_bs) + (pos & bs_mask)) * row_elems + 4 * q4;
       *reinterpret_cast<f32x4*>(s_k + r * LD + 4 * q4) = *reinterpret_cast<const f32x4*>(kbase + off);
       *reinterpret_cast<f32x4*>(s_v + r * LD + 4 * q4) = *reinterpret_cast<const f32x4*>(vbase + off);
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int pos = st * kF32Stage + 8 * j + c;
-        if (pos > qpos[i] || pos >= kv_end) s[i][j] = -INFINITY;
+        if (pos > qpos[i] || pos >= kv_end || !s_ok[8 * j + c]) s[i][j] = -INFINITY;
         tmax = fmaxf(tmax, s[i][j]);
       }
       const float m_new = fmaxf(m[i], max8(tmax));

@@ -552,6 +552,62 @@ def test_prefill_fp32_matches_oracle(device, hq, hkv, d):
     _prefill_case(device, hq, hkv, d, torch.float32)
 
 
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (16, 2, 64, torch.float16),
+                                           (8, 8, 64, torch.float32), (8, 2, 80, torch.bfloat16)])
+def test_attention_skips_out_of_pool_blocks(device, hq, hkv, d, dtype):
+    """Block ids outside [0, total_blocks) (negative or past the pool) in a
+    step's table: the positions they cover are skipped by every kernel --
+    the MFMA prefill (bf16, fp16), the fp32 prefill, the generic kernel (head
+    dim 80) and decode -- and the result is the closed-form attention over
+    the remaining positions (float64)."""
+    starts, counts = [100, 0, 300, 40], [40, 70, 1, 33]
+    bs = 16
+    rng = np.random.Generator(np.random.PCG64(d + hq))
+    ctx = [s_ + c for s_, c in zip(starts, counts)]
+    need = [-(-c // bs) for c in ctx]
+    total = sum(need) + 2
+    perm = rng.permutation(total)
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    w = wl.StepWorkload("bad_block_ids", hq, hkv, d, bs, dtype, 1.0, starts, counts, lists, total)
+    t = wl.make_tensors(w, device, seed=4)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    tile = ops.prefill_tile_for(hq, hkv)
+    step = ops.pack_step(table, starts, counts, bs, prefill_tile=tile, num_kv_heads=hkv, num_query_heads=hq,
+                         head_dim=d, dtype=dtype)
+    bad = {(0, 2): -7, (1, 1): total + 3, (2, 5): -1, (2, 17): total, (3, 0): -2}
+    host_table = w.block_table_array().copy()
+    for (r, c), b in bad.items():
+        host_table[r, c] = b
+    table.copy_(torch.from_numpy(host_table))  # the kernels read the caller's table in place
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    log(f"out-of-pool ids {dtype} {hq}/{hkv}/{d}: prefill items {step.num_prefill_items}")
+
+    kc = t.key_cache[0].float().cpu().numpy()  # [N, bs, H_kv, D]
+    vc = t.value_cache[0].float().cpu().numpy()
+    q_all = t.query[0].float().cpu().numpy()  # [H_q, T, D]
+    got = out.float().cpu().numpy()
+    cu = op.cumulative_offsets(counts)
+    for i in range(len(starts)):
+        pos = np.arange(ctx[i])
+        blocks = host_table[i, pos // bs]
+        valid = (blocks >= 0) & (blocks < total)
+        safe = np.where(valid, blocks, 0)
+        keys = kc[safe, pos % bs].transpose(1, 0, 2)  # [H_kv, ctx, D]
+        vals = vc[safe, pos % bs].transpose(1, 0, 2)
+        mask = (pos[None, :] <= starts[i] + np.arange(counts[i])[:, None]) & valid[None, :]
+        want = oa.attention_f64(q_all[:, cu[i] : cu[i + 1]], keys, vals, mask, w.scaling)
+        rows = got[cu[i] : cu[i + 1]]
+        if dtype == torch.float32:
+            assert np.max(np.abs(rows - want)) <= FP32_TOL, i
+        else:
+            ok, worst = bf16_close(rows, want)
+            assert ok, f"seq {i}: relative error {worst}"
+
+
 def _prefill_case(device, hq, hkv, d, dtype):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]
