@@ -30,12 +30,14 @@ Also on the line:
                  write + packing step timed over rotated pool copies (their
                  data would otherwise sit in the 256 MB MALL), Llama-7B MHA
                  decode, and the mixed prefill + decode step (decode GB/s,
-                 tokens/s, the prefill kernel's TFLOP/s against the bf16 MFMA
-                 peak), each with its CPU baseline on a bounded sample;
+                 tokens/s, the prefill kernel's TFLOP/s against the nominal
+                 bf16 MFMA peak and against the rate the device sustains on
+                 MFMAs alone, pa_calibrate_mfma), each with its CPU baseline
+                 on a bounded sample;
   cpu_baseline   the reference CPU kernel on a bounded sample of the same
                  workload on this host's cores.
 
-python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs]
+python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--calibrate-mfma]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack]
 """
 
@@ -332,6 +334,36 @@ def calibrate_copy(device, nbytes: int = 1 << 30, reps: int = 5) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}), flush=True)
+
+
+def sustained_mfma_tflops(device, iters: int = 4096, reps: int = 9, warmup: int = 20, valu_per_mfma: int = 0) -> float:
+    """The bf16 matrix-core rate the device sustains (pa_calibrate_mfma: two
+    independent 32x32x16 MFMA chains per wave on register operands, two
+    workgroups of 8 waves per CU), median of `reps` launches timed with HIP
+    events after `warmup` untimed ones (the clock settles under the load):
+    the ceiling an MFMA kernel's TFLOP/s is read against beside the nominal
+    peak."""
+    import torch
+
+    native = pkg("_native")
+    lib = native.load_library()
+    wgs = 2 * torch.cuda.get_device_properties(device).multi_processor_count
+    out = torch.empty(wgs * 512, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device)
+    flops = lib.pa_calibrate_mfma_flops(wgs, iters)
+    for _ in range(warmup):
+        native.check(lib.pa_calibrate_mfma(out.data_ptr(), wgs, iters, valu_per_mfma, stream.cuda_stream),
+                     "pa_calibrate_mfma")
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        native.check(lib.pa_calibrate_mfma(out.data_ptr(), wgs, iters, valu_per_mfma, stream.cuda_stream),
+                     "pa_calibrate_mfma")
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    return flops / (median(times) * 1e-3) / 1e12
 
 
 # ---------------------------------------------------------------------------
@@ -657,6 +689,7 @@ def mixed_line(args, w, t, device):
         ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
 
     full_ms = timed_ms(whole, max(5, args.steps // 2), 2, stream)
+    sustained = sustained_mfma_tflops(device)
     kv_bytes = wl.decode_bytes(w)
     pf = wl.prefill_flops(w)
     line = {
@@ -670,7 +703,9 @@ def mixed_line(args, w, t, device):
                    "algorithmic_bytes": kv_bytes},
         "prefill": {"kernel": "prefill_kernel", "gflop": round(pf / 1e9, 2), "kernel_ms": round(prefill_ms, 5),
                     "tflops": round(pf / (prefill_ms * 1e-3) / 1e12, 1),
-                    "mfma_frac": round(pf / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+                    "mfma_frac": round(pf / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "mfma_sustained_tflops": round(sustained, 1),
+                    "frac_of_sustained": round(pf / (prefill_ms * 1e-3) / 1e12 / sustained, 4)},
     }
     if not args.no_cpu_baseline:
         dec = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "decode")
@@ -695,6 +730,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
+    ap.add_argument("--calibrate-mfma", action="store_true",
+                    help="only measure the sustained bf16 MFMA rate (pa_calibrate_mfma)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU sharding "
@@ -709,6 +746,13 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.calibrate_copy:
         calibrate_copy(device)
+        return 0
+    if args.calibrate_mfma:
+        tf = sustained_mfma_tflops(device)
+        mixed = {str(nv): round(sustained_mfma_tflops(device, valu_per_mfma=nv), 1) for nv in (4, 8, 16)}
+        print(json.dumps({"mfma_bf16_sustained_tflops": round(tf, 1), "nominal_tflops": MFMA_BF16_PEAK_TFLOPS,
+                          "frac_of_nominal": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                          "mfma_tflops_with_fp32_fmas_per_mfma": mixed}), flush=True)
         return 0
 
     w = wl.WORKLOADS[args.workload](seed=args.seed)

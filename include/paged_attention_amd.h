@@ -458,6 +458,17 @@ int pa_prefill(const void *query, const void *key_cache,
  * the reference. */
 int pa_map_host_memory(const void *host_ptr, void **device_ptr);
 
+/* Measurement aid, no counterpart in the reference: `workgroups` x 8 waves
+ * each run `iters` x 2 independent bf16 32x32x16 MFMAs on register operands,
+ * with `valu_per_mfma` (0, 4, 8 or 16) independent fp32 FMAs after each, and
+ * write one float per lane to `out` (workgroups x 512 floats, device).
+ * Timing the launch gives the matrix-core rate the device sustains (0) and
+ * how much vector work it overlaps with it; pa_calibrate_mfma_flops gives
+ * the MFMA flops of such a launch. */
+int pa_calibrate_mfma(float *out, int32_t workgroups, int32_t iters, int32_t valu_per_mfma,
+                      void *stream);
+int64_t pa_calibrate_mfma_flops(int32_t workgroups, int32_t iters);
+
 const char *pa_error_string(int code);
 const char *pa_last_error_message(void);
 /* ABI version: bumped whenever a signature or a struct above changes. */

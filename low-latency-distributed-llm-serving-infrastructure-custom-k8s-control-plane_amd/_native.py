@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "pa_decode_no_alloc",
     "pa_prefill",
     "pa_map_host_memory",
+    "pa_calibrate_mfma",
+    "pa_calibrate_mfma_flops",
     "pa_error_string",
     "pa_last_error_message",
     "pa_abi_version",
@@ -159,6 +161,8 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
     "pa_plan_step": (ctypes.c_int, [_vp, _vp, _vp, _i32, PaPlanParams, ctypes.POINTER(PaStepPlan)]),
+    "pa_calibrate_mfma": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp]),
+    "pa_calibrate_mfma_flops": (ctypes.c_int64, [_i32, _i32]),
     "pa_reshape_and_cache": (
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],

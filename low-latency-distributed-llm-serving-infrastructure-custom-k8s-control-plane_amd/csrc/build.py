@@ -25,7 +25,7 @@ LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
 OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "plan.cpp", "pack.hip", "cache_write.hip", "decode.hip", "generic.hip", "prefill.hip",
-           "prefill_f32.hip", "copy_blocks.hip"]
+           "prefill_f32.hip", "copy_blocks.hip", "calibrate.hip"]
 
 HIP_FLAGS = [
     "-O3",

@@ -108,6 +108,12 @@ def test_invalid_arguments_rejected_before_launch():
     args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:16] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"2 updates" in lib.pa_last_error_message()
+    assert lib.pa_calibrate_mfma(None, 1, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_calibrate_mfma(0x1000, 0, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_calibrate_mfma(0x1000, 1, 1, 3, None) == native.PA_ERR_INVALID_ARGUMENT
+    assert b"valu_per_mfma" in lib.pa_last_error_message()
+    assert lib.pa_calibrate_mfma_flops(512, 4096) == 512 * 8 * 4096 * 2 * 32768
+    assert lib.pa_calibrate_mfma_flops(0, 4096) == 0
     for direction in (-1, 2):
         rc = lib.pa_swap_blocks(None, None, None, 1, 1, 1, 1, 16, direction, None)
         assert rc == native.PA_ERR_INVALID_ARGUMENT and b"direction" in lib.pa_last_error_message()
