@@ -106,12 +106,15 @@ class _HostStaging:
     from (through their device addresses, pa_map_host_memory), so no copy
     launch precedes it.
 
-    The ring's 16 slots form two halves.  One event is recorded on the stream
-    when a half has been handed out, and a half is reused only after its
-    event has completed, so the host never overwrites bytes a pending launch
-    still reads and, in the steady state, never waits.  Recording one event
-    per 8 steps instead of one per step matters: every event record puts a
-    few microseconds of idle time between two kernels."""
+    The ring's 16 slots form two halves.  Entering a half, the host records
+    an event on every stream that launched from the other half (all of those
+    launches are enqueued by then), and waits for the events recorded the
+    last time it entered the other half, which follow every launch that
+    read this half.  So the host never overwrites bytes a pending launch
+    still reads, whatever streams the launches went to, and in the steady
+    state it never waits.  Recording events once per 8 steps instead of once
+    per step matters: every event record puts a few microseconds of idle
+    time between two kernels."""
 
     SLOTS = 16
     HALF = SLOTS // 2
@@ -120,17 +123,26 @@ class _HostStaging:
         self._bufs = [None] * self.SLOTS
         self._arrays = [None] * self.SLOTS
         self._device = [0] * self.SLOTS
-        self._events = [None, None]  # per half: recorded after its last slot's use
+        self._streams = [{}, {}]  # per half: the streams its launches went to (by handle)
+        self._events = [[], []]  # per half: events that follow every launch reading it
         self._next = 0
 
     def take(self, nbytes: int):
         """(slot, numpy view, device address) of a free buffer of >= nbytes."""
         slot = self._next
         self._next = (slot + 1) % self.SLOTS
-        if slot % self.HALF == 0:  # entering a half: its previous uses must be done
-            ev = self._events[slot // self.HALF]
-            if ev is not None:
+        if slot % self.HALF == 0:  # entering a half
+            half, other = slot // self.HALF, 1 - slot // self.HALF
+            marks = []
+            for stream in self._streams[other].values():
+                ev = torch.cuda.Event()
+                ev.record(stream)
+                marks.append(ev)
+            self._events[other] = marks
+            self._streams[other] = {}
+            for ev in self._events[half]:
                 ev.synchronize()
+            self._events[half] = []
         buf = self._bufs[slot]
         if buf is None or buf.numel() < nbytes:
             buf = torch.empty(max(_align(nbytes, 1 << 16), 1 << 16), dtype=torch.uint8, pin_memory=True)
@@ -142,12 +154,7 @@ class _HostStaging:
 
     def done(self, slot: int, stream) -> None:
         """The launch reading ``slot`` is enqueued on ``stream``."""
-        if slot % self.HALF == self.HALF - 1:  # a half handed out: mark its end
-            half = slot // self.HALF
-            ev = self._events[half]
-            if ev is None:
-                ev = self._events[half] = torch.cuda.Event()
-            ev.record(stream)
+        self._streams[slot // self.HALF].setdefault(stream.cuda_stream, stream)
 
 
 _STAGING: dict = {}  # device -> _HostStaging

@@ -100,6 +100,31 @@ def test_pack_from_pool_rows_with_updates(device, seed, one_launch):
     _check(step, exp)  # gather_slots of a one-launch step: built on first use by the two-launch path
 
 
+def test_host_staging_ring_across_streams(device):
+    """Steps packed alternately on two streams, many more than the staging
+    ring's 16 slots, each from its own host arrays: every step's outputs are
+    those of its own inputs (no slot is overwritten while a launch on either
+    stream may still read it)."""
+    rng = np.random.default_rng(11)
+    bs, b = 16, 64
+    table = torch.from_numpy(rng.integers(0, 1 << 16, size=(b, 64)).astype(np.int32)).to(device)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+    steps = []
+    for i in range(40):
+        starts = [int(x) for x in rng.integers(0, 1000, size=b)]
+        counts = [int(x) for x in rng.choice([1, 1, 1, 2, 5], size=b)]
+        with torch.cuda.stream(streams[i % 2]):
+            steps.append((ops.pack_step(table, starts, counts, bs, prefill_tile=16, partition_size=256),
+                          starts, counts))
+    torch.cuda.synchronize()
+    for step, starts, counts in steps:
+        ctx = [s_ + c for s_, c in zip(starts, counts)]
+        assert np.array_equal(step.cu_seqlens.cpu().numpy(), op.cumulative_offsets(counts))
+        assert np.array_equal(step.cu_context_offsets.cpu().numpy(), op.cumulative_offsets(ctx))
+        assert np.array_equal(step.position_ids.cpu().numpy(), op.position_ids(starts, counts)[0])
+
+
 @pytest.mark.parametrize("b", [1, 1023, 1024, 1025, 4097])
 def test_pack_large_batches(device, b):
     """Batches across the scan's 1024-sequence chunks: bit-exact outputs, and
