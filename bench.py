@@ -19,7 +19,8 @@ Also on the line:
   full_step_ms   a whole step through the product path, host included: the
                  step context built on an HBM store (checks, plan, the
                  inputs handed over in pinned memory, the packing launch),
-                 the K/V write of the step's tokens, and the attention;
+                 and the attention given the step's new K/V rows (written
+                 inside the decode launches for a decode step);
                  full_vs_decode_step times it in alternation with the decode
                  step alone (the gap is what the step's plumbing costs);
   host_step_us   the host time of building that step context (median), for
@@ -453,9 +454,11 @@ def decode_main(args, w, t, device):
     sout = torch.empty_like(out)
 
     def full_step():
+        # as the layer hook runs it: the step context, then the attention
+        # given the layer's new rows (written inside the decode launches)
         ctx = pa.PagedStepContext(store, seqs, w.start_positions, w.new_token_counts)
-        store.scatter_layer_kv(0, new_k, new_v, ctx.scatter_slots)
-        ops.attention(t.query, store.key_cache, store.value_cache, 0, ctx.packed, w.scaling, out=sout)
+        ops.attention(t.query, store.key_cache, store.value_cache, 0, ctx.packed, w.scaling, out=sout,
+                      new_key=new_k, new_value=new_v)
 
     full_ms = timed_ms(full_step, args.steps, args.warmup, stream)
     dec_alt, full_alt = paired_ms(decode_step, full_step, args.steps, stream)
@@ -685,8 +688,8 @@ def mixed_line(args, w, t, device):
         s = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, prefill_tile=tile,
                           num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
                           dtype=w.dtype)
-        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, s.scatter_slots, 0)
-        ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out)
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, s, w.scaling, out=out, new_key=t.new_keys,
+                      new_value=t.new_values)
 
     full_ms = timed_ms(whole, max(5, args.steps // 2), 2, stream)
     sustained = sustained_mfma_tflops(device)

@@ -403,6 +403,42 @@ int pa_decode_phases(int32_t phases, const void *query, const void *key_cache,
                      int64_t num_merge_items, float scaling, void *output,
                      void *workspace, size_t workspace_bytes, void *stream);
 
+/* The step's new K and V rows ([T, H_kv, head_dim], any token / head element
+ * strides, unit stride along head_dim), as pa_reshape_and_cache takes them. */
+typedef struct {
+    const void *key;
+    const void *value;
+    int64_t key_token_stride;
+    int64_t key_head_stride;
+    int64_t value_token_stride;
+    int64_t value_head_stride;
+} PaNewRows;
+
+/*
+ * Replaces, for a step whose every sequence has one new token (or none):
+ * scatter_layer_kv (app/memory/manager.py:150-168, called at
+ * app/model/paged_attention.py:152-154) followed by the decode attention
+ * (attention_backends.py:88-117) -- pa_reshape_and_cache + pa_decode in the
+ * decode launches.  The workgroups that attend a sequence's last partition
+ * first write its new K and V rows into the cache at the slot its block
+ * table gives position context_len - 1 (bit-exact, as pa_reshape_and_cache
+ * writes them; an out-of-pool block id writes nothing), then attend; no
+ * other workgroup reads that position.  Rows of sequences with more than
+ * one new token are NOT written: use pa_reshape_and_cache for a step with
+ * prefill tokens.  Arguments as pa_decode, with writable caches.
+ * PA_ERR_UNSUPPORTED (nothing launched) for a shape or alignment the fused
+ * path does not take (16-byte aligned rows and strides, the tuned decode's
+ * shapes): the caller then writes with pa_reshape_and_cache and calls
+ * pa_decode.
+ */
+int pa_decode_append(const void *query, void *key_cache, void *value_cache,
+                     int32_t layer_idx, PaStepDims dims, PaNewRows new_rows,
+                     const int32_t *block_tables, const int32_t *context_lens,
+                     const int64_t *cu_seqlens, const int32_t *decode_items,
+                     int64_t num_decode_items, const int32_t *merge_items,
+                     int64_t num_merge_items, float scaling, void *output,
+                     void *workspace, size_t workspace_bytes, void *stream);
+
 /* Bytes of the file-scope device array behind pa_decode_no_alloc (64 MiB:
  * the split-K partials of about 4000 decode work items of 32 query heads of
  * 128; pa_decode_workspace_size gives the need of a step). */

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode",
     "pa_decode_phases",
     "pa_decode_no_alloc",
+    "pa_decode_append",
     "pa_prefill",
     "pa_map_host_memory",
     "pa_calibrate_mfma",
@@ -93,6 +94,17 @@ class PaStepDims(ctypes.Structure):
         ("q_token_stride", ctypes.c_int64),
         ("q_head_stride", ctypes.c_int64),
         ("block_table_rows", ctypes.c_void_p),
+    ]
+
+
+class PaNewRows(ctypes.Structure):
+    _fields_ = [
+        ("key", ctypes.c_void_p),
+        ("value", ctypes.c_void_p),
+        ("key_token_stride", ctypes.c_int64),
+        ("key_head_stride", ctypes.c_int64),
+        ("value_token_stride", ctypes.c_int64),
+        ("value_head_stride", ctypes.c_int64),
     ]
 
 
@@ -184,6 +196,11 @@ _SIGNATURES = {
     "pa_decode_no_alloc": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp],
+    ),
+    "pa_decode_append": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, PaStepDims, PaNewRows, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _f32, _vp, _vp, _sz,
+         _vp],
     ),
     "pa_prefill": (
         ctypes.c_int,

@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 9; }
+int pa_abi_version(void) { return 10; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -477,7 +477,7 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
                   const int64_t* cu_seqlens, const int32_t* decode_items,
                   int64_t num_decode_items, const int32_t* merge_items, int64_t num_merge_items,
                   float scaling, void* output, void* workspace, size_t workspace_bytes,
-                  void* stream) {
+                  void* stream, const PaNewRows* new_rows = nullptr) {
   if (phases <= 0 || (phases & ~(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE)) != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "%s: phases must be a non-empty mask of "
                 "PA_DECODE_PHASE_PARTITIONS and PA_DECODE_PHASE_MERGE, got %d", who, phases);
@@ -509,6 +509,16 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
                                      dims.partition_size) &&
       aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&
       (dims.q_token_stride * eb) % 16 == 0 && (dims.q_head_stride * eb) % 16 == 0;
+  if (new_rows != nullptr) {
+    // The fused write moves 16-byte pieces of whole heads.
+    const bool fused = fast && aligned16(new_rows->key) && aligned16(new_rows->value) &&
+                       (dims.head_dim * eb) % 16 == 0 && (new_rows->key_token_stride * eb) % 16 == 0 &&
+                       (new_rows->key_head_stride * eb) % 16 == 0 &&
+                       (new_rows->value_token_stride * eb) % 16 == 0 &&
+                       (new_rows->value_head_stride * eb) % 16 == 0;
+    if (!fused)
+      return fail(PA_ERR_UNSUPPORTED, "%s: this shape or alignment takes pa_reshape_and_cache + pa_decode", who);
+  }
   if (fast) {
     const size_t need = pa_decode_workspace_size(dims, num_decode_items);
     if (use_scratch) {
@@ -553,6 +563,15 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
     a.pair = pair ? 1 : 0;
     a.group = pair ? 2 * group : group;
     a.sub_groups = pair ? 1 : pa::decode_sub_groups(group);
+    a.head_dim = dims.head_dim;
+    if (new_rows != nullptr) {
+      a.new_key = new_rows->key;
+      a.new_value = new_rows->value;
+      a.new_key_token_stride = new_rows->key_token_stride;
+      a.new_key_head_stride = new_rows->key_head_stride;
+      a.new_value_token_stride = new_rows->value_token_stride;
+      a.new_value_head_stride = new_rows->value_head_stride;
+    }
     return from_hip(
         pa::launch_decode(a, dims.dtype, dims.head_dim, group, num_decode_items, phases, s), who);
   }
@@ -602,6 +621,20 @@ int pa_decode_phases(int32_t phases, const void* query, const void* key_cache,
                        block_tables, context_lens, cu_seqlens, decode_items, num_decode_items,
                        merge_items, num_merge_items, scaling, output, workspace, workspace_bytes,
                        stream);
+}
+
+int pa_decode_append(const void* query, void* key_cache, void* value_cache, int32_t layer_idx,
+                     PaStepDims dims, PaNewRows new_rows, const int32_t* block_tables,
+                     const int32_t* context_lens, const int64_t* cu_seqlens,
+                     const int32_t* decode_items, int64_t num_decode_items,
+                     const int32_t* merge_items, int64_t num_merge_items, float scaling,
+                     void* output, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = require("pa_decode_append", {{new_rows.key, "new_rows.key"}, {new_rows.value, "new_rows.value"}});
+  if (rc != PA_OK) return rc;
+  return decode_phases("pa_decode_append", false, PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE, query,
+                       key_cache, value_cache, layer_idx, dims, block_tables, context_lens, cu_seqlens,
+                       decode_items, num_decode_items, merge_items, num_merge_items, scaling, output,
+                       workspace, workspace_bytes, stream, &new_rows);
 }
 
 int pa_decode_no_alloc(const void* query, const void* key_cache, const void* value_cache,

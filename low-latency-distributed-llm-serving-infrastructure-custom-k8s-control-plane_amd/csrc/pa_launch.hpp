@@ -41,6 +41,17 @@ struct DecodeArgs {
   // exceeds the largest kernel group; each then re-reads the unit's K/V).
   int32_t group;
   int32_t sub_groups;
+  // pa_decode_append: the step's new K/V rows ([T, H_kv, head_dim], element
+  // strides), written into the cache slot of position context_len - 1 by the
+  // workgroups of each sequence's last partition before they read it; null
+  // for the other entry points.
+  const void* new_key;
+  const void* new_value;
+  int64_t new_key_token_stride;
+  int64_t new_key_head_stride;
+  int64_t new_value_token_stride;
+  int64_t new_value_head_stride;
+  int32_t head_dim;  // real head dim (the pair's unit row holds two heads)
 };
 
 // Generic one-wave-per-(query token, head) attention: any head_dim <= 256,

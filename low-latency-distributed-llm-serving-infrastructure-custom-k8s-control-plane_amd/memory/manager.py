@@ -240,6 +240,16 @@ class PagedKVCacheManager:
         for layer_idx in range(self.num_layers):
             self.scatter_layer_kv(layer_idx, keys[:, layer_idx], values[:, layer_idx], slot_mapping)
 
+    def checked_layer_kv(self, layer_idx: int, keys: torch.Tensor, values: torch.Tensor,
+                         num_tokens: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """One layer's new K/V ([T, H, D]) checked as scatter_layer_kv checks
+        them, on the cache's device and in its dtype: what the GPU backend
+        writes itself."""
+        self._validate_layer_idx(layer_idx)
+        self._validate_token_tensors(keys, values, (num_tokens, self.num_heads, self.head_dim))
+        dev = self.key_cache.device
+        return keys.to(dev, self.dtype), values.to(dev, self.dtype)
+
     def scatter_layer_kv(self, layer_idx: int, keys: torch.Tensor, values: torch.Tensor,
                          slot_mapping: torch.Tensor) -> None:
         """One layer's new K/V ([T, H, D], any token / head strides) into the

@@ -213,7 +213,7 @@ def paged_attention_forward(
     store = context.store
     layer_idx = module.layer_idx
     # [1, H_kv, T, D] projections -> [T, H_kv, D] views (no copy)
-    store.scatter_layer_kv(layer_idx, key[0].transpose(0, 1), value[0].transpose(0, 1), context.scatter_slots)
+    new_key, new_value = key[0].transpose(0, 1), value[0].transpose(0, 1)
     scale = module.scaling if scaling is None else scaling
     backend = _BACKEND if _BACKEND is not None else _default_backend(store)
     if store.on_gpu:
@@ -225,7 +225,12 @@ def paged_attention_forward(
                 "(dense SDPA would gather every context and build a T x C mask on the device)")
         if query.shape[2] == 0:
             return query.new_empty((1, 0, query.shape[1], query.shape[3])), None
-        return backend.attend(query, store, layer_idx, context, scale, dropout), None
+        # The backend writes the new rows (inside the decode launches for a
+        # step of single-token sequences) before it attends.
+        new_key, new_value = store.checked_layer_kv(layer_idx, new_key, new_value, context.num_query_tokens)
+        return backend.attend(query, store, layer_idx, context, scale, dropout, new_key=new_key,
+                              new_value=new_value), None
+    store.scatter_layer_kv(layer_idx, new_key, new_value, context.scatter_slots)
     if backend is not None:
         if not backend.supports(context, query.shape[2]):
             backend = _get_fallback_backend()

@@ -956,6 +956,51 @@ def prefill(
     return out
 
 
+def _new_rows(new_key: torch.Tensor, new_value: torch.Tensor, key_cache: torch.Tensor,
+              step: PackedStep) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The step's new K/V rows checked against the cache: [T, H_kv, D] of the
+    cache dtype on its device, unit stride along D (copied otherwise)."""
+    _require_device(new_key, new_value, key_cache)
+    shape = (step.num_query_tokens, int(key_cache.shape[3]), int(key_cache.shape[4]))
+    if tuple(new_key.shape) != shape or tuple(new_value.shape) != shape:
+        raise ValueError(f"new_key / new_value must have shape {shape}, got {tuple(new_key.shape)} "
+                         f"and {tuple(new_value.shape)}")
+    if new_key.dtype != key_cache.dtype or new_value.dtype != key_cache.dtype:
+        raise ValueError("new_key / new_value dtype must match the cache dtype")
+    if new_key.stride(2) != 1:
+        new_key = new_key.contiguous()
+    if new_value.stride(2) != 1:
+        new_value = new_value.contiguous()
+    return new_key, new_value
+
+
+def _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v) -> int:
+    """pa_decode_append; returns its status (PA_ERR_UNSUPPORTED: not fused)."""
+    ws_ptr, ws_bytes = step.workspace_ptr(int(q.shape[1]), int(q.shape[2]))
+    rows = _native.PaNewRows(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1))
+    lib = _native.load_library()
+    return lib.pa_decode_append(
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        rows,
+        step.ptr("block_tables"),
+        step.ptr("context_lens"),
+        step.ptr("cu_seqlens"),
+        step.ptr("decode_items"),
+        step.num_decode_items,
+        step.ptr("merge_items") if step.num_merge_items else None,
+        step.num_merge_items,
+        float(scaling),
+        out.data_ptr(),
+        ws_ptr,
+        ws_bytes,
+        _stream(q.device),
+    )
+
+
 def attention(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -964,10 +1009,32 @@ def attention(
     step: PackedStep,
     scaling: float,
     out: Optional[torch.Tensor] = None,
+    new_key: Optional[torch.Tensor] = None,
+    new_value: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D]."""
+    """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D].
+
+    With ``new_key`` / ``new_value`` ([T, H_kv, D], the step's new rows) the
+    rows are first written into the caches at the step's scatter slots, as
+    :func:`reshape_and_cache` does: for a step of single-token sequences
+    inside the decode launches themselves (pa_decode_append), otherwise (or
+    for a shape the fused write does not take) by the cache-write kernel.
+    """
     q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
+    if (new_key is None) != (new_value is None):
+        raise ValueError("new_key and new_value are given together")
+    if new_key is not None:
+        k, v = _new_rows(new_key, new_value, key_cache, step)
+        if step.num_prefill_seqs == 0 and step.num_decode_items > 0 and not step.__dict__.get("_no_append"):
+            status = _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v)
+            if status == _native.PA_OK:
+                return out
+            if status != _native.PA_ERR_UNSUPPORTED:
+                _native.check(status, "pa_decode_append")
+            step.__dict__["_no_append"] = True
+        if step.num_query_tokens > 0:
+            reshape_and_cache(k, v, key_cache, value_cache, step.scatter_slots, layer_idx)
     if step.num_prefill_items > 0:
         _launch_prefill(q, key_cache, value_cache, layer_idx, step, scaling, out, dims)
     if step.num_decode_items > 0:

@@ -608,6 +608,69 @@ def test_attention_skips_out_of_pool_blocks(device, hq, hkv, d, dtype):
             assert ok, f"seq {i}: relative error {worst}"
 
 
+def _bits(t):
+    return t.view({torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}[t.dtype])
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (64, 8, 128, torch.bfloat16),
+                                           (32, 2, 128, torch.bfloat16), (8, 8, 64, torch.float32),
+                                           (16, 4, 80, torch.bfloat16), (16, 4, 256, torch.float16),
+                                           (12, 4, 96, torch.float32), (16, 8, 64, torch.float16)])
+def test_decode_append_equals_write_then_decode(device, hq, hkv, d, dtype):
+    """A decode step given its new K/V rows (the rows written inside the decode
+    launches, pa_decode_append) leaves the same cache bytes and returns the
+    same output bits as pa_reshape_and_cache followed by pa_decode -- paired
+    heads, groups of 8, sub-groups, heads of 80, 96 and 256, fp32 and fp16,
+    strided rows (the model's head-major view), and one sequence whose last
+    block id lies outside the pool (written by neither)."""
+    rng = np.random.Generator(np.random.PCG64(hq * 7 + d))
+    ctx = [int(c) for c in np.clip(np.round(rng.lognormal(np.log(600.0), 1.0, size=24)), 1, 5000)]
+    ctx[0], ctx[1] = 1, 4096  # a one-token context and a full multi-partition one
+    need = [-(-c // 16) for c in ctx]
+    total = sum(need) + 4
+    perm = rng.permutation(total)
+    lists, off = [], 0
+    for n_ in need:
+        lists.append([int(x) for x in perm[off : off + n_]])
+        off += n_
+    w = wl.StepWorkload("decode_append", hq, hkv, d, 16, dtype, 1.0, [c - 1 for c in ctx], [1] * len(ctx),
+                        lists, total)
+    t = wl.make_tensors(w, device, seed=3)
+    table_np = w.block_table_array()
+    table_np[5, need[5] - 1] = total + 3  # the last block of sequence 5 is outside the pool
+    table = torch.from_numpy(table_np).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, 16, partition_size=512,
+                         num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+    # the model hands over its head-major projections: token stride D, head stride T * D
+    nk = t.new_keys.transpose(0, 1).contiguous().transpose(0, 1)
+    nv = t.new_values.transpose(0, 1).contiguous().transpose(0, 1)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv)
+    torch.cuda.synchronize()
+    log(f"decode append {dtype} {hq}/{hkv}/{d}: items {step.num_decode_items}, merges {step.num_merge_items}")
+    assert not step.__dict__.get("_no_append"), "the fused write was not taken"
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
+def test_attention_with_new_rows_on_a_mixed_step(device):
+    """A step with prefill tokens given its new rows writes them with the
+    cache-write kernel first (the fused write covers single-token sequences
+    only): the same cache bytes and output bits as writing them beforehand."""
+    w = wl.WORKLOADS["mixed_step"](seed=2)
+    t = wl.make_tensors(w, device, seed=2)
+    step = pack_workload(w, device)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
 def _prefill_case(device, hq, hkv, d, dtype):
     starts = [0, 0, 37, 512, 100]
     counts = [1, 200, 64, 300, 7]
