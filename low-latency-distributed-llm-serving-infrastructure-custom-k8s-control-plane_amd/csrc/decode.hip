@@ -324,32 +324,34 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const T* vbase = reinterpret_cast<const T*>(a.value_cache) + kvh * DM;
 
   // pa_decode_append: the workgroups of the partition holding the new token
-  // (position ctx - 1) first write its K and V rows of this unit (one KV
-  // head, or the pair's two) into the cache, as pa_reshape_and_cache would;
-  // sibling sub-groups write the same bytes.  The barrier below orders the
-  // writes before this workgroup's own reads of that position; no other
-  // workgroup of the launch reads it.
-  if (a.new_key != nullptr && n > 0 && p0 + n == ctx) {
+  // (position ctx - 1) write its K and V rows of this unit (one KV head, or
+  // the pair's two) into the cache, as pa_reshape_and_cache would; sibling
+  // sub-groups write the same bytes.  A thread per 16-byte piece loads it
+  // here, so the load overlaps the staging below, and stores it before the
+  // barrier that ends the staging, which orders the stores before this
+  // workgroup's own reads of that position; no other workgroup of the
+  // launch reads it.
+  constexpr int kPieceElems = 16 / static_cast<int>(sizeof(T));
+  constexpr int kAppendPieces = DM / kPieceElems;  // 16-byte pieces of the unit's row
+  static_assert(2 * kAppendPieces <= kDecodeThreads, "one piece of K or V per thread");
+  const bool append = a.new_key != nullptr && n > 0 && p0 + n == ctx;
+  T* append_dst = nullptr;
+  uint4 append_piece = make_uint4(0, 0, 0, 0);
+  if (append && tid < 2 * kAppendPieces) {
     const int col = (ctx - 1) >> log2_bs;
     const int b = row_ok && col < a.block_table_stride ? a.block_tables[trow * a.block_table_stride + col] : -1;
     if (b >= 0 && b < a.total_blocks) {
-      constexpr int kPieceElems = 16 / static_cast<int>(sizeof(T));
-      constexpr int kPieces = DM / kPieceElems;  // 16-byte pieces of the unit's row
+      const bool is_v = tid >= kAppendPieces;
+      const int g = kvh * DM + (is_v ? tid - kAppendPieces : tid) * kPieceElems;  // element in the token's row
+      const int h = g / a.head_dim;
+      const T* src = reinterpret_cast<const T*>(is_v ? a.new_value : a.new_key) +
+                     qtok * (is_v ? a.new_value_token_stride : a.new_key_token_stride) +
+                     static_cast<int64_t>(h) * (is_v ? a.new_value_head_stride : a.new_key_head_stride) +
+                     (g - h * a.head_dim);
       const int64_t slot = (static_cast<int64_t>(b) << log2_bs) + ((ctx - 1) & bs_mask);
-      for (int i = tid; i < 2 * kPieces; i += kDecodeThreads) {
-        const bool is_v = i >= kPieces;
-        const int e = (is_v ? i - kPieces : i) * kPieceElems;  // element in the unit's row
-        const int g = kvh * DM + e;                            // element in the token's row
-        const int h = g / a.head_dim;
-        const T* src = reinterpret_cast<const T*>(is_v ? a.new_value : a.new_key) +
-                       qtok * (is_v ? a.new_value_token_stride : a.new_key_token_stride) +
-                       static_cast<int64_t>(h) * (is_v ? a.new_value_head_stride : a.new_key_head_stride) +
-                       (g - h * a.head_dim);
-        T* dst = const_cast<T*>(reinterpret_cast<const T*>(is_v ? a.value_cache : a.key_cache)) +
-                 slot * row_stride + g;
-        st16(dst, ld16(src));
-      }
-      __threadfence_block();
+      append_dst = const_cast<T*>(reinterpret_cast<const T*>(is_v ? a.value_cache : a.key_cache)) +
+                   slot * row_stride + g;
+      append_piece = ld16(src);
     }
   }
 
@@ -400,6 +402,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       s_q[i] = (!MASKD || c < KPM) ? ld16(qrow + c * CE) : make_uint4(0, 0, 0, 0);
     }
   }
+  if (append_dst != nullptr) st16(append_dst, append_piece);
+  if (append) __threadfence_block();
   __syncthreads();
 
   const float scale = a.scale_log2e;
