@@ -41,7 +41,7 @@ def test_struct_layouts(tmp_path):
     program built against the header prints every offset and size."""
     native = pkg("_native")
     structs = {name: getattr(native, name) for name in
-               ("PagedAttentionDims", "PaStepDims", "PaPackDims", "PaPlanParams", "PaStepPlan")}
+               ("PagedAttentionDims", "PaStepDims", "PaPackDims", "PaPlanParams", "PaStepPlan", "PaNewRows")}
     lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "paged_attention_amd.h"', "int main(void) {"]
     for name, st in structs.items():
         lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
@@ -108,6 +108,10 @@ def test_invalid_arguments_rejected_before_launch():
     args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:16] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"2 updates" in lib.pa_last_error_message()
+    rows = native.PaNewRows(None, 0x1000, 128, 1024, 128, 1024)
+    rc = lib.pa_decode_append(*([None] * 3), 0, native.PaStepDims(), rows, *([None] * 4), 1, None, 0, 1.0,
+                              None, None, 0, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT and b"new_rows.key" in lib.pa_last_error_message()
     assert lib.pa_calibrate_mfma(None, 1, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
     assert lib.pa_calibrate_mfma(0x1000, 0, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
     assert lib.pa_calibrate_mfma(0x1000, 1, 1, 3, None) == native.PA_ERR_INVALID_ARGUMENT
