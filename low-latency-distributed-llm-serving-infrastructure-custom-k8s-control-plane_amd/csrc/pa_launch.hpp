@@ -88,8 +88,8 @@ struct GenericArgs {
   float scale_log2e;
 };
 
-// Packing of one step (pack.hip): two launches, a one-workgroup scan and a
-// per-sequence fill, sharing a small workspace.
+// Packing of one step (pack.hip): a one-workgroup scan and a per-sequence
+// fill sharing a small workspace, or the scan alone for a small decode step.
 constexpr int kPackBuckets = 64;          // length buckets of the partial partitions
 constexpr size_t kPackHeaderBytes = 512;  // workspace header: full count + bucket bases
 

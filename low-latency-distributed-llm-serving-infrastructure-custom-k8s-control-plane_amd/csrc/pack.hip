@@ -1,5 +1,5 @@
 // Ragged-batch packing on the GPU, in two launches that are linear in the
-// batch:
+// batch (one for a small decode step, below):
 //
 //   pack_scan_kernel   one workgroup of 1024 threads.  Applies the queued
 //                      block-table updates, then walks the sequences in

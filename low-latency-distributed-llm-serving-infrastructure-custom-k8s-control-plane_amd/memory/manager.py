@@ -170,7 +170,9 @@ class PagedKVCacheManager:
 
     def pack_step(self, sequences: Sequence, start_tokens, token_counts, *, num_query_heads: Optional[int] = None,
                   with_gather: bool = False, partition_size: Optional[int] = None) -> paged_ops.PackedStep:
-        """Check, plan and pack one step on the GPU (one upload, two launches)."""
+        """Check, plan and pack one step on the GPU: the step's host arrays
+        handed over in pinned memory, the queued block-table updates applied,
+        one launch for a decode batch (two for a larger or prefill step)."""
         rows, starts, counts = self.step_rows(sequences, start_tokens, token_counts)
         return self.pack_rows(rows, starts, counts, num_query_heads=num_query_heads, with_gather=with_gather,
                               partition_size=partition_size)

@@ -7,11 +7,13 @@ ALL_ATTENTION_FUNCTIONS, ``register_paged_attention`` and
 ``run_paged_forward``.  The step runs flat: all sequences of a step are one
 ``[1, T]`` batch.
 
-On a GPU store the context is packed once per step (``self.packed``: the
-step's block table gathered from the device-resident row pool, cu_seqlens,
-slots, positions and the attention work lists, from one upload and the
-packing kernels), and every layer then runs pa_reshape_and_cache + the HIP
-attention kernels on the device without host syncs.  A GPU store always
+On a GPU store the context is packed once per step (``self.packed``: each
+sequence's row of the device-resident block-table pool, cu_seqlens, slots,
+positions and the attention work lists, from the step's host arrays handed
+over in pinned memory and the packing kernels), and every layer then writes
+its new K/V rows and runs the HIP attention kernels on the device without
+host syncs (for a decode step the rows are written inside the decode
+launches).  A GPU store always
 takes the HIP path: with no backend installed the hook installs it, and the
 reference's dense SDPA path is refused there (it would gather the whole
 context and build a T x C mask on the device).

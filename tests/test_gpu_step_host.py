@@ -147,9 +147,10 @@ def test_pack_large_batches(device, b):
 
 
 def test_pack_time_is_linear_in_the_batch(device):
-    """Pack time (two launches, replayed from a HIP graph of 20 re-runs) per
-    sequence stays flat from 1024 to 4096 decode sequences (the kernels are
-    linear in B), and a re-run gives the first run's outputs."""
+    """Pack time (replayed from a HIP graph of 20 re-runs: one launch at 256
+    and 1024 decode sequences, two at 4096) per sequence does not grow from
+    1024 to 4096 sequences (the kernels are linear in B), and a re-run gives
+    the first run's outputs."""
     per_seq = {}
     for b in (256, 1024, 4096):
         rng = np.random.default_rng(b)
@@ -176,12 +177,15 @@ def test_pack_time_is_linear_in_the_batch(device):
     assert per_seq[4096] <= 1.5 * per_seq[1024]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_manager_steps_track_growth_and_reuse(device, dtype):
+@pytest.mark.parametrize("dtype,with_gather", [(torch.bfloat16, True), (torch.float32, True),
+                                              (torch.bfloat16, False)])
+def test_manager_steps_track_growth_and_reuse(device, dtype, with_gather):
     """A GPU store over several steps: prompts, decodes that open new blocks,
     frees and new sequences reusing freed rows, and a pool that grows its
-    rows and columns.  Every step's gathered block table, slots and work
-    lists equal the oracle's on the sequences' block lists."""
+    rows and columns.  Every step's block table (gathered from the pool),
+    slots and work lists equal the oracle's on the sequences' block lists.
+    Without gather slots at pack time the decode-only steps are packed in
+    one launch, queued table updates included."""
     m = manager_mod.PagedKVCacheManager(total_blocks=4000, block_size=16, num_heads=8, head_dim=128, dtype=dtype,
                                         num_layers=1, device=device)
     m.num_query_heads = 32
@@ -209,7 +213,7 @@ def test_manager_steps_track_growth_and_reuse(device, dtype):
                 starts.append(seq.block_table.get_tokens_count() - 1)
                 counts.append(1)
             seqs.append(seq)
-        step = m.pack_step(seqs, starts, counts, with_gather=True)
+        step = m.pack_step(seqs, starts, counts, with_gather=with_gather)
         lists = [s.block_table.get_physical_blocks() for s in seqs]
         ctx = [s + c for s, c in zip(starts, counts)]
         width = max(-(-c // 16) for c in ctx)
