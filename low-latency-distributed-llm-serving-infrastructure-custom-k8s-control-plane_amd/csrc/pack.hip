@@ -220,8 +220,13 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
 
+  // The first chunk's inputs are loaded before the updates are applied (both
+  // may come over PCIe from pinned host memory: the two round trips overlap;
+  // the compiler would not move these loads above the updates' stores).
+  SeqInput next = load_input(a, tid);
   // Queued block-table updates land before anything reads the table (the
-  // fill kernel runs after this launch on the same stream).
+  // fill kernel runs after this launch on the same stream; the fused fill
+  // after a barrier).
   for (int u = tid; u < a.num_updates; u += kScanThreads) {
     const int32_t row = a.updates[3 * u];
     const int32_t col = a.updates[3 * u + 1];
@@ -244,7 +249,6 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
   const int log2_p = (P & (P - 1)) == 0 ? __builtin_ctz(P) : -1;
   int64_t tok_carry = 0, ctx_carry = 0;
   int32_t full_carry = 0, merge_carry = 0, tiles_carry = 0;
-  SeqInput next = load_input(a, tid);
   // One chunk when fused: the thread's sequence, kept for the fill below.
   int4 f_e = {0, 0, 0, -1}, f_in = {0, 0, -1, 0};
   int64_t f_tok = 0, f_ctx = 0;
