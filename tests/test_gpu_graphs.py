@@ -22,7 +22,11 @@ ops = pkg("paged_ops")
 wl = pkg("workloads")
 
 
-def test_decode_layers_replay_bit_exact(device):
+@pytest.mark.parametrize("in_launch_write", [False, True])
+def test_decode_layers_replay_bit_exact(device, in_launch_write):
+    """``in_launch_write``: the layers hand their new rows to the attention
+    (written inside the decode launches, pa_decode_append) instead of
+    writing them with the cache-write kernel first."""
     layers, b, hq, hkv, d, bs = 4, 48, 32, 8, 128, 16
     rng = np.random.Generator(np.random.PCG64(5))
     steps = 3
@@ -64,8 +68,12 @@ def test_decode_layers_replay_bit_exact(device):
 
     def run_layers(outs):
         for l in range(layers):
-            ops.reshape_and_cache(new_k[l], new_v[l], key_cache, value_cache, step.scatter_slots, l)
-            ops.decode(q[l], key_cache, value_cache, l, step, scale, out=outs[l])
+            if in_launch_write:
+                ops.attention(q[l], key_cache, value_cache, l, step, scale, out=outs[l], new_key=new_k[l],
+                              new_value=new_v[l])
+            else:
+                ops.reshape_and_cache(new_k[l], new_v[l], key_cache, value_cache, step.scatter_slots, l)
+                ops.decode(q[l], key_cache, value_cache, l, step, scale, out=outs[l])
 
     run_layers(out)  # warm-up: sizes the workspace outside the capture
     torch.cuda.synchronize()
@@ -89,5 +97,6 @@ def test_decode_layers_replay_bit_exact(device):
         torch.cuda.synchronize()
         for l in range(layers):
             assert torch.equal(replayed[l].view(torch.int16), eager[l].view(torch.int16)), (k, l)
+        assert not in_launch_write or not step.__dict__.get("_no_append")
         # the step geometry the graph was captured for still holds
         assert ops.work_counts(starts, [1] * b, 1024, step.prefill_tile)[2:4] == counts
