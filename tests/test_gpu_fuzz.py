@@ -5,11 +5,14 @@ seed 32 on also 9, 10, 12 or 16, which run as sub-groups; D 64 or 128,
 256 from seed 80 on, 80 or 96 from seed 96 on), a dtype (bf16 or fp32; fp16
 from seed 64 on, bf16 or fp16 from seed 80 on), a block size (1-64), a ragged
 batch of decodes (contexts 1-700) and prefill chunks (2-90 tokens at starts
-0-400) and a split-K partition (automatic or 32-512 tokens).  The step is
-packed, its new K/V rows are written into a random non-contiguous pool,
-decode and prefill run, and every output row is compared with the oracle run
-on the cache the GPU read (fp32 to 1e-4 absolute, bf16 and fp16 to the
-relative bound of the parity tests).  This covers the combinations the
+0-400) and a split-K partition (automatic or 32-512 tokens); every fourth
+seed (seed % 4 == 1) is a decode-only batch.  The step is packed, its new
+K/V rows are written into a random non-contiguous pool -- by the cache-write
+kernel for even seeds, handed to the attention for odd ones (written inside
+the decode launches for a decode-only batch) -- decode and prefill run, and
+every output row is compared with the oracle run on the cache the GPU read
+(fp32 to 1e-4 absolute, bf16 and fp16 to the relative bound of the parity
+tests).  This covers the combinations the
 fixed-shape tests do not name: paired and unpaired heads of 64 and 128,
 groups that do not divide 128, groups above 8, tiny blocks with short
 partitions, and prefill chunks beside split-K decodes.
@@ -41,8 +44,9 @@ def random_case(seed):
         dtype = torch.bfloat16 if seed % 2 else torch.float16
     bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
     starts, counts = [], []
+    decode_only = seed % 4 == 1
     for _ in range(int(rng.integers(1, 11))):
-        if rng.random() < 0.6:
+        if decode_only or rng.random() < 0.6:
             c = int(rng.integers(1, 700))
             starts.append(c - 1)
             counts.append(1)
@@ -72,7 +76,11 @@ def test_random_steps_match_oracle(device, seed):
     step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
                          partition_size=partition, num_kv_heads=w.num_kv_heads,
                          num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
-    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
-    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    if seed % 2:
+        out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, new_key=t.new_keys,
+                            new_value=t.new_values)
+    else:
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+        out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
     check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=w.dtype == torch.float32)
