@@ -9,15 +9,14 @@
 // the end (this halves the longest chain of a causal tile).
 //
 // Both products are computed transposed so that a lane owns one query row:
-//   S^T[kv][row] = sum_d K[kv][d] Q[row][d]       (A = K from LDS, B = Q regs)
-//   O^T[d][row] += sum_kv V^T[d][kv] P^T[kv][row]  (A = V^T, B = P^T regs)
+//   S^T[kv][row] = sum_d K[kv][d] Q[row][d]       (A = K regs, B = Q regs)
+//   O^T[d][row] += sum_kv V^T[d][kv] P^T[kv][row]  (A = V^T regs, B = P^T regs)
 // with v_mfma_f32_32x32x16_bf16 (or _f16 for fp16 caches).  In the 32x32
-// accumulator lane l holds
-// column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4), i = 0..15, so the
-// softmax max/sum of a query row needs only its own 16 values plus the
-// partner lane l ^ 32, and the probabilities a lane holds are the B operand
-// of the PV product with the context index of k-slot j being
-// 8*(j/4) + 4*(l/32) + (j%4) inside each 16-token step.
+// accumulator lane l holds column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4),
+// i = 0..15, so the softmax max/sum of a query row needs only its own 16
+// values plus the partner lane l ^ 32, and the probabilities a lane holds
+// are the B operand of the PV product with the context index of k-slot j
+// being 8*(j/4) + 4*(l/32) + (j%4) inside each 16-token step.
 //
 // K and V go from HBM straight into LDS with the gfx950 direct loads
 // (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i), into
@@ -29,24 +28,41 @@
 // addresses V[kv0 + (i/4)][d0 + 4*(i%4)] and receives V[kv0 + j][d0 + i],
 // j = 0..3: four context tokens of its own output column.
 //
-// Pipeline (one barrier per 64-token stage): four LDS stage buffers hold
-// stage t (its V is read), stage t+1 (its K is read: the scores of the next
-// tile are computed while this tile's exponentials run), stage t+2 (landed)
-// and stage t+3 (being copied).  The block ids of a stage are copied into an
-// LDS ring two stages before its rows.  The copies are issued from inline
-// assembly, every step the same number per wave, and each wave waits for
-// its own copies with an exact s_waitcnt vmcnt before the barrier that
-// publishes them (the compiler would otherwise drain every copy before each
-// LDS read, as it cannot tell the buffers apart).
-// Masking is applied only to tiles that cross the causal diagonal or the end
-// of the context (or to every tile when some block id of the sequence lies
-// outside the pool: those positions are skipped, as in decode), and the
-// accumulator is rescaled only when some row's maximum grew by more than 2^8
-// over the reference maximum in use.
+// Copies.  Waves 0-3 copy 16 rows each of every stage.  One copy covers 4
+// rows (8 for 64-dim heads) of one cache block, so its source is a scalar
+// base (block id from a scalar load of the table, row offset) plus a fixed
+// per-lane offset: no vector address arithmetic and no wait on the block
+// ids, which arrive one step ahead of their use.  (Blocks smaller than one
+// copy take the per-lane form of the address.)  The copies are issued from
+// inline assembly and each copying wave waits for its own copies with an
+// exact s_waitcnt vmcnt before the barrier that publishes them: the compiler
+// would otherwise drain every copy before each LDS read, as it cannot tell
+// the buffers apart.
+//
+// Pipeline (one barrier per stage).  K and V have separate LDS rings: the K
+// of stage st+2 is read into registers during step st and consumed by the
+// QK MFMAs of step st+1, so every step starts its MFMAs right after the
+// barrier; the V of stage st is read during step st.  A step is two phases,
+// each interleaved at the instruction level (sched_group_barrier):
+//   A: QK MFMAs of stage st+1  |  softmax of stage st (exp2, pack, row sum)
+//                              |  V^T reads of stage st
+//   B: PV MFMAs of stage st    |  row maxima of stage st+1  |  K reads of st+2
+// so each wave alternates matrix and vector work instead of running long
+// runs of one kind in lock-step with the other wave of its SIMD.
+// The row sum is accumulated from the rounded probabilities the PV product
+// uses (v_dot2 against ones), per lane half, and the halves are added once
+// at the end.  Masking is applied only to tiles that cross the causal
+// diagonal or the end of the context (or to every tile when some block id of
+// the sequence lies outside the pool: those positions are skipped, as in
+// decode), in a separate loop after the unmasked one, and the accumulator is
+// rescaled only when some row's maximum grew by more than 2^8 over the
+// reference maximum in use.
 //
 // Reference: the block-diagonal causal mask of app/model/paged_attention.py:
 // 92-118 applied by SDPA (paged_attention.py:170-178); query token j of a
 // sequence at position start + j attends context positions [0, start + j].
+#include <type_traits>
+
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
 
@@ -56,16 +72,25 @@ typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4v __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(4))) int32_t const_i32;
 
 constexpr int kPrefillThreads = 512;  // 4 row groups x 2 context halves
 constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kKvTile = 32;        // context tokens per wave per stage
 constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
 constexpr float kLazyRescale = 8.f;  // log2 headroom before the row maximum moves
-constexpr int kStageBufs = 4;       // LDS stage buffers in flight
 constexpr int kPrefillWaves = kPrefillThreads / 64;
-constexpr int kIdRing = 8;          // block-id slots (one per stage in flight)
-constexpr int kIdSlotBytes = 256;   // up to 64 table entries per stage
+constexpr int kCopyWaves = 4;  // waves 0-3 copy, one per SIMD
+constexpr int kCopyRows = kStage / kCopyWaves;  // rows of a stage each copying wave copies
+constexpr int kKBufs = 4;  // K ring: read in step st-2, consumed in st-1, refilled in st
+constexpr int kVBufs = 4;  // V ring: landed in st-1, read in step st, refilled in st+2
+constexpr int kIdSlots = 8;      // block-id ring slots
+constexpr int kIdSlotBytes = 256;  // 64 table entries: every column of a stage
+constexpr int kIdAhead = 8;      // stages between an id slot's copy and the stage's K copy + 4
+// sched_group_barrier classes
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
@@ -85,24 +110,42 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-// Direct global -> LDS loads.  Each lane's 16 (or 4) bytes land at
-// lds_base + 16 * lane (4 * lane); lds_base must be wave-uniform.  They are
+// Direct global -> LDS loads.  Each lane's 16 bytes land at lds_base + 16 *
+// lane; lds_base must be wave-uniform.  dma16 takes a per-lane address,
+// dma16_s a wave-uniform base plus a per-lane 32-bit offset.  They are
 // issued from inline assembly so that the compiler, which cannot tell the
 // stage buffers apart, does not drain them before every LDS read; the
 // kernel waits for them itself (s_waitcnt vmcnt) before the barrier that
-// publishes a stage.
+// publishes a stage, and every LDS access is ordered against them by that
+// barrier (an asm statement with a memory clobber).
 __device__ __forceinline__ void dma16(uint32_t lds_base, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
                : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(uint32_t lds_base, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_base), "v"(src)
+// A wave-uniform pointer in scalar registers (the scalar-base copies take
+// their base from an SGPR pair).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ void dma4_s(uint32_t lds_base, uint32_t voff, const void* sbase) {
+  sbase = uniform_ptr(sbase);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_s(uint32_t lds_base, uint32_t voff, const void* sbase) {
+  sbase = uniform_ptr(sbase);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff),
+               "s"(sbase)
                : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Swizzle of the 16-byte chunks of an unpadded LDS row: chunk c of row r sits
 // at position c ^ chunk_swizzle(r).  It keeps the 16-byte K reads (16 rows,
@@ -114,7 +157,7 @@ __device__ __forceinline__ int chunk_swizzle(int r) {
   else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, bool LANE_IDS>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
   static_assert(Elem<T>::kBytes == 2, "16-bit caches (bf16 or fp16)");
   constexpr int MTOK = kPrefillRows / G;  // query tokens per workgroup
@@ -122,22 +165,20 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   constexpr int DB = D / 32;              // 32-wide d blocks of the output
   constexpr int CHUNKS = D / 8;           // 16-byte pieces per row
   constexpr int ROW_BYTES = D * 2;
-  constexpr int kRowsPerDma = kWave / CHUNKS;             // rows one wave load covers
-  // The copies are issued by the waves of the first context half (0-3):
-  // they reach the barrier earlier, and issuing from all eight waves bunched
-  // the copies behind the barrier (59.6 -> 57.1 us median on the mixed
-  // prefill + decode step).
-  constexpr int kCopyWaves = kPrefillWaves / 2;
-  constexpr int kDmaPerWave = kStage / kCopyWaves / kRowsPerDma;  // per tensor
-  constexpr int kRegionBytes = kStage * ROW_BYTES;        // K (or V) rows of a stage
-  constexpr int kStageBytes = 2 * kRegionBytes;
-  constexpr int kIdsOff = kStageBufs * kStageBytes;       // block-id ring
+  constexpr int kRowsPerDma = kWave / CHUNKS;          // rows one wave copy covers
+  constexpr int kDmaPerWave = kCopyRows / kRowsPerDma;  // copies per tensor per stage
+  constexpr int kRegion = kStage * ROW_BYTES;         // K (or V) rows of a stage
+  constexpr int kVBase = kKBufs * kRegion;
+  constexpr int kIdBase = (kKBufs + kVBufs) * kRegion;
+  constexpr int kLdsBytes = kIdBase + kIdSlots * kIdSlotBytes;
+  constexpr int kVReads = 2 * DB * 2;                 // V^T transpose reads per tile
+  constexpr int kPerQk = 16 / KS;                     // probabilities per QK k-step
   static_assert(kDmaPerWave >= 1, "stage / wave mismatch");
-  static_assert(kStageBufs * kStageBytes >= 4 * (16 * DB + 2) * kWave * 4, "merge scratch must fit");
+  static_assert(kLdsBytes >= 4 * (16 * DB + 2) * kWave * 4, "merge scratch must fit");
+  static_assert(kVReads % KS == 0, "V^T reads spread over the QK k-steps");
 
-  // Four stage buffers (K rows, then V rows, swizzled) and the block-id ring;
-  // the stage buffers are reused for the final merge.
-  __shared__ __attribute__((aligned(16))) char s_lds[kIdsOff + kIdRing * kIdSlotBytes];
+  // K ring, then V ring (rows swizzled); reused for the final merge.
+  __shared__ __attribute__((aligned(16))) char s_lds[kLdsBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -198,92 +239,134 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   }
 
   const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
-  // Positions that have a block-table column (the rest are never read).
+  // Positions that have a block-table column (the rest are never read); at
+  // least one, as the host passes tables of one column or more.
   const int kv_read = static_cast<int>(
       min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
-  const int ntiles = (kv_end + kKvTile - 1) / kKvTile;
+  const int kv_last = kv_read - 1;
   const int nstages = (kv_end + kStage - 1) / kStage;
   const float scale = a.scale_log2e;
   const int last_col = bt_stride - 1;
   // Positions whose block id lies outside the pool are skipped, as the
   // decode kernels skip them: one pass over the row's columns tells whether
-  // there are any (then every tile takes the masked path below).
-  int bad_local = 0;
-  for (int c = tid; c < ((kv_read + bs_mask) >> log2_bs); c += kPrefillThreads)
-    bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
-  const bool bad_ids = __syncthreads_or(bad_local) != 0;
-  // Tiles below this index need no mask for any row of the workgroup.
-  const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
+  // there are any (then every tile takes the masked path below).  Its first
+  // load is issued here and checked after the first copies have landed, so
+  // the two memory round trips overlap.
+  const int ncols = (kv_read + bs_mask) >> log2_bs;
+  int scan0 = tid < ncols ? bt[tid] : 0;
+  bool bad_ids = false;  // set once the scan is complete (before any tile is masked)
 
-  // ---- staging ---------------------------------------------------------------
-  // Block ids: wave 0 copies the table entries a stage needs (at most 64)
-  // into slot (stage & 7) of an LDS ring, five stages ahead of use.  K/V:
-  // copying wave w copies rows [16 w, 16 w + 16) of a stage (lane -> row
-  // lane / CHUNKS of its load, chunk position lane % CHUNKS, fetching the
-  // chunk that the swizzle puts there), three stages ahead.  Rows past the
-  // readable context re-read its last row, and an out-of-pool block id
-  // reads block 0 (finite values; their scores are masked).  Every copy is
+  // ---- copies ----------------------------------------------------------------
+  // Wave cw < 4 copies rows [16 cw, 16 cw + 16) of a stage, kRowsPerDma rows
+  // per copy: lane -> row delta = lane / CHUNKS of the copy, chunk position
+  // lane % CHUNKS (fetching the chunk that the swizzle puts there).  Rows
+  // past the readable context re-read its last row, and an out-of-pool block
+  // id reads block 0 (finite values; their scores are masked).  Every copy is
   // issued unconditionally, so each wave's outstanding count is the same
-  // every step.
-  auto dma_ids = [&](int stage) {
-    const int col = min(((stage * kStage) >> log2_bs) + lane, last_col);
-    dma4(lds0 + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes, bt + col);
-  };
-  auto stage_ids = [&](int stage) {
-    return reinterpret_cast<const int*>(s_lds + kIdsOff + (stage & (kIdRing - 1)) * kIdSlotBytes);
-  };
-  const int dma_row0 = (wave % kCopyWaves) * (kStage / kCopyWaves) + lane / CHUNKS;  // + j * kRowsPerDma
-  auto dma_kv = [&](int stage, int buf_off) {
-    if (wave >= kCopyWaves) return;
-    const int col0 = (stage * kStage) >> log2_bs;
-    const int* ids = stage_ids(stage);
+  // every step.  (Copying from every wave instead raised each SIMD's scalar
+  // work per step by a third and the step time with it.)
+  const int cw = wave & (kCopyWaves - 1);
+  const int delta = lane / CHUNKS;
+  uint32_t chunk_off[kDmaPerWave];
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) {
-      const int r = dma_row0 + j * kRowsPerDma;  // row inside the stage
-      const int pos = min(stage * kStage + r, kv_read - 1);
-      // (clamped: past the last stage pos may precede the stage's first column)
-      const int b = ids[min(max((pos >> log2_bs) - col0, 0), kIdSlotBytes / 4 - 1)];
-      const uint32_t bb = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks)
-                              ? static_cast<uint32_t>(b) : 0u;
-      const int chunk = (lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(r);
-      const uint64_t off = static_cast<uint64_t>(bb) * block_bytes +
-                           (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk * 16);
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          lds0 + buf_off + (r - lane / CHUNKS) * ROW_BYTES);
-      dma16(dst, kbase + off);
-      dma16(dst + kRegionBytes, vbase + off);
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int r = cw * kCopyRows + j * kRowsPerDma + delta;
+    chunk_off[j] = static_cast<uint32_t>(((lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(r)) * 16);
+  }
+  // Per-lane offsets of a wave's copies when its 16 rows share one block.
+  uint32_t row_off[kDmaPerWave];
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j)
+    row_off[j] = __umul24(static_cast<uint32_t>(j * kRowsPerDma + delta), row_bytes) + chunk_off[j];
+  const bool one_block = (1 << log2_bs) >= kCopyRows;
+  auto valid_block = [&](int b) {
+    return static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks) ? static_cast<uint32_t>(b) : 0u;
+  };
+  // Block ids of the first stages come from scalar loads of the table
+  // (constant address space: the table does not change during the launch).
+  const_i32* btc = (const_i32*)(bt);
+  // Block-id ring: slot x % kIdSlots holds the table entries of columns
+  // [col0(x), col0(x) + 64) (clamped to the row): every column a stage's
+  // positions use.  Wave 0 copies a stage's slot kIdAhead stages ahead, and
+  // a copying wave reads the id of its next copies one step ahead, so no
+  // copy waits on a table read and the loop issues no scalar loads (their
+  // out-of-order returns would force every LDS wait to drain).
+  auto col0 = [&](int x) { return min((x * kStage) >> log2_bs, last_col); };
+  auto dma_ids = [&](int x) {
+    const int c0 = col0(x);
+    dma4_s(lds0 + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes,
+           static_cast<uint32_t>(min(lane, last_col - c0)) * 4u, bt + c0);
+  };
+  // Ring entry of position p of stage x (p inside the readable context and
+  // the stage; other positions read some valid entry, which is not used).
+  auto ring_id = [&](int x, int p) {
+    const int idx = min(max((p >> log2_bs) - col0(x), 0), kWave - 1);
+    return *reinterpret_cast<const int*>(s_lds + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes + idx * 4);
+  };
+  // The ring entry of a copying wave's first row when its 16 rows share one
+  // block and the stage lies inside the readable context (blocks of 16 or
+  // more start on a stage boundary, or contain the whole stage).
+  const int fast_idx4 = kIdBase + ((cw * kCopyRows) >> log2_bs) * 4;
+  auto ring_fast = [&](int x) {
+    return *reinterpret_cast<const int*>(s_lds + fast_idx4 + (x & (kIdSlots - 1)) * kIdSlotBytes);
+  };
+  const int id_last = btc[min(kv_last >> log2_bs, last_col)];  // block of the last readable row
+  // Copies of this wave's rows of tensor stage x into LDS region `region`,
+  // one per kRowsPerDma rows, with get_id(j, p): the block id of position p
+  // (readable) of copy j.
+  auto copy_each = [&](int x, uint32_t region, const char* base, auto get_id) {
+    const int p0 = x * kStage + cw * kCopyRows;
+    const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
+    if constexpr (!LANE_IDS) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int p = p0 + j * kRowsPerDma;
+        const int pc = min(p, kv_last);
+        const uint32_t bb = valid_block(p <= kv_last ? get_id(j, p) : id_last);
+        const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
+                                  static_cast<uint32_t>(pc & bs_mask) * row_bytes);
+        // Rows of the copy past the readable context re-read its last row
+        // (same block: a copy never spans blocks here).
+        const uint32_t voff =
+            __umul24(min(static_cast<uint32_t>(delta), static_cast<uint32_t>(kv_last - pc)), row_bytes) +
+            chunk_off[j];
+        dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+      }
+    } else {
+      // Blocks smaller than one copy: each lane's row has its own block.
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int pos = min(p0 + j * kRowsPerDma + delta, kv_last);
+        const int b = pos >= x * kStage ? ring_id(x, pos) : id_last;
+        dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
+              base + (static_cast<uint64_t>(valid_block(b)) * block_bytes +
+                      (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk_off[j])));
+      }
     }
   };
-  // Outstanding copies a copying wave leaves behind the stage it must see
-  // landed: its K/V copies of one stage plus, for wave 0, one id copy.
-  auto wait_stage = [&]() {
-    if (wave == 0) wait_vmcnt<2 * kDmaPerWave + 1>();
-    else if (wave < kCopyWaves) wait_vmcnt<2 * kDmaPerWave>();
+  // A loop step's copies: one scalar base for the wave's 16 rows when they
+  // share a block and are readable (id_fast: their block id, read from the
+  // ring a step ahead), else one copy at a time with ids from the ring.
+  auto copy_step = [&](int x, uint32_t region, const char* base, int id_fast) {
+    const int p0 = x * kStage + cw * kCopyRows;
+    if (!LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last) {
+      const uint32_t bb = valid_block(__builtin_amdgcn_readfirstlane(id_fast));
+      const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
+                                static_cast<uint32_t>(p0 & bs_mask) * row_bytes);
+      const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
+    } else {
+      copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
+    }
+  };
+  auto copy_prologue = [&](int x, uint32_t region, const char* base) {
+    copy_each(x, region, base, [&](int, int p) { return btc[p >> log2_bs]; });
   };
 
-  // Prologue: ids of stages 0-4, then K/V of stages 0-2 (the loop's step st
-  // copies K/V of stage st+3 and ids of stage st+5).
-  if (wave == 0) {
-#pragma unroll
-    for (int s = 0; s < 5; ++s) dma_ids(s);
-    wait_vmcnt<0>();
-  }
-  __syncthreads();
-  dma_kv(0, 0);
-  dma_kv(1, kStageBytes);
-  dma_kv(2, 2 * kStageBytes);
-  if (wave < kCopyWaves) wait_vmcnt<2 * kDmaPerWave>();  // stages 0 and 1 landed
-  __syncthreads();
-
-  f32x16 acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  float m = kScoreFloor, l = 0.f;
-
-  // Per-lane byte offsets of the MFMA operands inside a stage buffer (this
-  // wave's half of the stage; chunk positions follow the swizzle).
+  // ---- LDS operands --------------------------------------------------------------
+  // Offsets inside slot 0 of the K ring and of the V ring; a slot adds a
+  // multiple of kRegion (an immediate offset when the slot is static).
   const int k_row = kh * kKvTile + (lane & 31);
   int k_off[KS];
 #pragma unroll
@@ -297,145 +380,241 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const int col = 16 * ((lane >> 4) & 1) + 4 * (li & 3) + 32 * db;  // element
-      v_off[hi][db] = kRegionBytes + r * ROW_BYTES +
-                      (((col >> 3) ^ chunk_swizzle<CHUNKS>(r)) * 16) + (col & 7) * 2;
+      v_off[hi][db] = kVBase + r * ROW_BYTES + (((col >> 3) ^ chunk_swizzle<CHUNKS>(r)) * 16) + (col & 7) * 2;
     }
   }
-  auto read_k = [&](int buf_off, uint4* ka) {
+  auto read_k = [&](int slot, uint4* ka) {
+    const char* buf = s_lds + slot * kRegion;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(s_lds + buf_off + k_off[ks]);
+    for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(buf + k_off[ks]);
   };
-  auto read_vt = [&](int buf_off, uint4 (*va)[DB]) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const char* base = s_lds + buf_off + ks * 16 * ROW_BYTES;
-        const uint2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + v_off[0][db]));
-        const uint2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + v_off[1][db]));
-        va[ks][db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      }
+  // Transpose read r of V^T (r = (k-step, d block, 8-row half)).
+  auto read_vt = [&](int slot, int r, uint4 (*va)[DB]) {
+    const int kk = r / (2 * DB), db = (r / 2) % DB, hi = r % 2;
+    const uint2 w = lds_read_tr16(
+        reinterpret_cast<const uint16_t*>(s_lds + slot * kRegion + kk * 16 * ROW_BYTES + v_off[hi][db]));
+    if (hi == 0) { va[kk][db].x = w.x; va[kk][db].y = w.y; }
+    else { va[kk][db].z = w.x; va[kk][db].w = w.y; }
   };
 
-  // The scores of stage st+1 are computed while stage st's are turned into
-  // probabilities: the QK MFMAs of the next tile are interleaved with the
-  // exponentials of this one, so the matrix pipe and the VALU overlap inside
-  // a wave.  Stage buffers rotate through byte offsets kept in scalars:
-  // stage st (V read), st+1 (K read), st+2 (landed), st+3 (being copied).
-  // (computed unconditionally -- unused when the wave has no tile -- so the
-  // query loads are complete on every path into the loop and the compiler
-  // adds no memory-counter wait inside it)
-  f32x16 s_cur;
+  // Scores of tile t (positions [32 t, 32 t + 32)) masked for this lane's row:
+  // past its causal limit, past the readable context, or (bad_ids) in a
+  // block outside the pool.
+  const int kv_lim = min(qpos, kv_last);  // last position this row attends
+  auto mask_tile = [&](int t, f32x16& s) {
+    // (positions relative to the tile, so each test is one compare)
+    const int lim = kv_lim - (t * kKvTile + 4 * half);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s_cur[i] = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      if (8 * (i >> 2) + (i & 3) > lim) s[i] = -INFINITY;
+    }
+    if (bad_ids) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+          s[i] = -INFINITY;
+      }
+    }
+  };
+  auto tile_max = [&](const f32x16& s) {
+    float m01 = fmaxf(fmaxf(s[0], s[1]), s[2]);
+    float m23 = fmaxf(fmaxf(s[3], s[4]), s[5]);
+    float m45 = fmaxf(fmaxf(s[6], s[7]), s[8]);
+    float m67 = fmaxf(fmaxf(s[9], s[10]), s[11]);
+    float m89 = fmaxf(fmaxf(s[12], s[13]), s[14]);
+    return max_halves(fmaxf(fmaxf(fmaxf(m01, m23), fmaxf(m45, m67)), fmaxf(m89, s[15])));
+  };
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
+  float m = kScoreFloor, l = 0.f;  // l: this lane's half of the row sum
+  // Lazy rescale: the reference maximum m of a row moves only when a tile's
+  // maximum exceeds it by more than kLazyRescale (log2 units), so
+  // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
+  // same softmax.
+  auto rescale = [&](float tmax) {
+    const bool grow = (tmax - m) * scale > kLazyRescale;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? tmax : m;
+      const float alpha = fast_exp2((m - m_new) * scale);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+      m = m_new;
+    }
+  };
+
+  // ---- prologue --------------------------------------------------------------
+  // K of stages 0-2, V of stage 0 and the id ring of stages 0-7 landed, then
+  // K 3 / V 1 in flight.
   {
-    uint4 ka[KS];
+    if (wave == 0) {
+#pragma unroll
+      for (int x = 0; x < kIdAhead; ++x) dma_ids(x);
+    }
+    if constexpr (LANE_IDS) {
+      // (these copies read their ids from the ring)
+      wait_vmcnt<0>();
+      __syncthreads();
+    }
+    if (wave < kCopyWaves) {
+#pragma unroll
+      for (int x = 0; x < 3; ++x) copy_prologue(x, x * kRegion, kbase);
+      copy_prologue(0, kVBase, vbase);
+    }
+    wait_vmcnt<0>();
+  }
+  asm volatile("" : "+v"(scan0));  // the scan's first load is checked after the copies
+  int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+  for (int c = tid + kPrefillThreads; c < ncols; c += kPrefillThreads)
+    bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+  // (also publishes the first stages and the id ring)
+  bad_ids = __syncthreads_or(bad_local) != 0;
+  // Tiles below this index need no mask for any row of the workgroup.
+  const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
+  if (wave < kCopyWaves) {
+    copy_prologue(3, 3 * kRegion, kbase);
+    copy_prologue(1, kVBase + kRegion, vbase);
+  }
+  // Ids of step 0's copies (K of stage 4, V of stage 2), from the ring.
+  int idk = 0, idv = 0;
+  auto prefetch_ids = [&](int st) {
+    if (wave < kCopyWaves) {
+      idk = ring_fast(st + 4);
+      idv = ring_fast(st + 2);
+    }
+  };
+  prefetch_ids(0);
+  f32x16 s0, s1;
+  uint4 ka[KS];
+  {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s0[i] = 0.f;
     read_k(0, ka);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s_cur = mfma32<T>(ka[ks], qreg[ks], s_cur);
+    for (int ks = 0; ks < KS; ++ks) s0 = mfma32<T>(ka[ks], qreg[ks], s0);
+    read_k(1, ka);
+    mask_tile(kh, s0);
+    rescale(tile_max(s0));
   }
-  int off_cur = 0, off_next = kStageBytes, off_land = 2 * kStageBytes, off_copy = 3 * kStageBytes;
+  // Every wave has read K of stage 0 before step 0 refills its buffer.
+  stage_barrier();
 
-  auto step = [&](int st, const f32x16& s_in) {
-    dma_kv(st + 3, off_copy);
-    if (wave == 0) dma_ids(st + 5);
-    const int t = 2 * st + kh;  // this wave's 32-token tile
-    f32x16 s_next = s_in;
-    if (t < ntiles) {
-      // LDS operands: V^T of this stage, K of the next one (read even when
-      // there is no next tile: the stale scores are never used).
-      uint4 va[2][DB], ka[KS];
-      read_vt(off_cur, va);
-      read_k(off_next, ka);
+  // 1.0 in both halves of a packed pair (bf16 0x3F80, fp16 0x3C00).
+  constexpr uint32_t kOnes = Elem<T>::kDtype == PA_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u;
 
-      // ---- online softmax of s_in (unscaled scores; exp2 folds the scale)
-      f32x16 s = s_in;
-      const int kv0 = t * kKvTile;
-      if (t >= first_masked) {
-        const int* ids = stage_ids(st);
-        const int col0 = (st * kStage) >> log2_bs;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kv = kv0 + 8 * (i >> 2) + 4 * half + (i & 3);
-          bool off = kv > qpos || kv >= kv_read;
-          if (bad_ids)
-            off = off || static_cast<uint32_t>(ids[(kv >> log2_bs) - col0]) >=
-                             static_cast<uint32_t>(a.total_blocks);
-          if (off) s[i] = -INFINITY;
-        }
-      }
-      float tmax = s[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-      tmax = max_halves(tmax);
-      // Lazy rescale: the reference maximum m of a row moves only when the
-      // tile's maximum exceeds it by more than kLazyRescale (log2 units), so
-      // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
-      // same softmax.
-      const bool grow = (tmax - m) * scale > kLazyRescale;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = grow ? tmax : m;
-        const float alpha = fast_exp2((m - m_new) * scale);
-        l *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-        m = m_new;
-      }
-      const float msc = m * scale;
+  // One step: see the header comment.  s_cur holds the scores of this
+  // wave's tile of stage st, s_nxt receives those of stage st + 1.  The K
+  // and V rings have four slots each; stage x lives in slot x % 4 (SLOT, a
+  // compile-time constant in both loops below).
+  auto step = [&](int st, f32x16& s_cur, f32x16& s_nxt, auto masked, auto slot_c) {
+    constexpr bool MASKED = decltype(masked)::value;
+    constexpr int SLOT = decltype(slot_c)::value;
+    const int slot = SLOT >= 0 ? SLOT : (st & (kKBufs - 1));
+    if (wave < kCopyWaves) copy_step(st + 4, slot * kRegion, kbase, idk);
+    const int idv_cur = idv;  // (the prefetch below replaces idv)
 
-      // ---- interleaved: S_next = K_next Q^T | P = exp2(S - m) | O^T += V^T P^T
+    // ---- A: S_next = K_next Q^T | P = exp2(S - m) | V^T reads
+    const float msc = m * scale;
+    f32x16 sn;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_next[i] = 0.f;
-      float rsum = 0.f;
-      uint4 pb[2];
+    for (int i = 0; i < 16; ++i) sn[i] = 0.f;
+    uint4 va[2][DB];
+    uint4 pb[2];
+    float rsum0 = 0.f, rsum1 = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s_next = mfma32<T>(ka[ks], qreg[ks], s_next);
-        // two (D = 128) or four (D = 64) probabilities per QK step
+    for (int ks = 0; ks < KS; ++ks) {
+      sn = mfma32<T>(ka[ks], qreg[ks], sn);
 #pragma unroll
-        for (int j = ks * 16 / KS; j < (ks + 1) * 16 / KS; ++j) {
-          s[j] = fast_exp2(fmaf(s[j], scale, -msc));
-          rsum += s[j];
-        }
-        if ((ks + 1) * 16 / KS % 8 == 0) {
-          const int c = (ks + 1) * 16 / KS / 8 - 1;
-          pb[c].x = pack_half2<T>(s[8 * c + 0], s[8 * c + 1]);
-          pb[c].y = pack_half2<T>(s[8 * c + 2], s[8 * c + 3]);
-          pb[c].z = pack_half2<T>(s[8 * c + 4], s[8 * c + 5]);
-          pb[c].w = pack_half2<T>(s[8 * c + 6], s[8 * c + 7]);
-        }
+      for (int j = ks * kPerQk; j < (ks + 1) * kPerQk; ++j) s_cur[j] = fast_exp2(fmaf(s_cur[j], scale, -msc));
+#pragma unroll
+      for (int r = ks * (kVReads / KS); r < (ks + 1) * (kVReads / KS); ++r) read_vt(slot, r, va);
+      if (((ks + 1) * kPerQk) % 8 == 0) {
+        const int c = (ks + 1) * kPerQk / 8 - 1;
+        pb[c].x = pack_half2<T>(s_cur[8 * c + 0], s_cur[8 * c + 1]);
+        pb[c].y = pack_half2<T>(s_cur[8 * c + 2], s_cur[8 * c + 3]);
+        pb[c].z = pack_half2<T>(s_cur[8 * c + 4], s_cur[8 * c + 5]);
+        pb[c].w = pack_half2<T>(s_cur[8 * c + 6], s_cur[8 * c + 7]);
+        rsum0 = dot2_half<T>(pb[c].x, kOnes, rsum0);
+        rsum1 = dot2_half<T>(pb[c].y, kOnes, rsum1);
+        rsum0 = dot2_half<T>(pb[c].z, kOnes, rsum0);
+        rsum1 = dot2_half<T>(pb[c].w, kOnes, rsum1);
       }
+    }
+    // ---- B: O^T += V^T P^T | row maxima of S_next | K reads of stage st+2
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] = mfma32<T>(va[ks][db], pb[ks], acc[db]);
-      rsum = sum_halves(rsum);
-      l += rsum;
-    }  // t < ntiles
-    const int o = off_cur;
-    off_cur = off_next;
-    off_next = off_land;
-    off_land = off_copy;
-    off_copy = o;
-    // Stage st+2 (read as K next step) and the ids of stage st+4 must have
-    // landed before the barrier publishes them.
-    wait_stage();
-    __syncthreads();
-    return s_next;
+      for (int db = 0; db < DB; ++db) acc[db] = mfma32<T>(va[kk][db], pb[kk], acc[db]);
+    read_k((slot + 2) & (kKBufs - 1), ka);
+    prefetch_ids(st + 1);
+    if constexpr (MASKED) mask_tile(2 * (st + 1) + kh, sn);
+    const float tmax = tile_max(sn);
+    l += rsum0 + rsum1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kVReads / KS, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 6 * 8 / KS, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * DB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (KS + 2) / (2 * DB), 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+    }
+    rescale(tmax);
+    s_nxt = sn;
+    // The V copies and the id slot go out after the math, so that a copying
+    // wave issues its copies in two short runs rather than one long one.
+    if (wave < kCopyWaves) copy_step(st + 2, kVBase + ((slot + 2) & (kKBufs - 1)) * kRegion, vbase, idv_cur);
+    if (wave == 0) dma_ids(st + kIdAhead);
+    // K of stage st+3, V of stage st+1 and (wave 0) the id slot of stage
+    // st+7, copied last step, must have landed before the barrier
+    // publishes them.
+    if (wave == 0) wait_vmcnt<2 * kDmaPerWave + 1>();
+    else if (wave < kCopyWaves) wait_vmcnt<2 * kDmaPerWave>();
+    stage_barrier();
   };
 
-  // Two steps per trip (the compiler then keeps the scores in place).  A
-  // trailing step past the last stage computes nothing and only copies
-  // clamped rows into a free buffer.
-  for (int st = 0; st < nstages; st += 2) {
-    const f32x16 s_mid = step(st, s_cur);
-    s_cur = step(st + 1, s_mid);
+  // Every step runs a body with its ring slot (st % 4) and score registers
+  // (st % 2) fixed at compile time: four unmasked steps per trip while both
+  // tiles of stage st+1 lie below first_masked, then masked steps, four per
+  // trip with an exit test after each (no step past the last stage).
+  using U = std::false_type;
+  using M = std::true_type;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  const int n_main = min(max(first_masked / 2 - 1, 0), nstages);
+  int st = 0;
+  for (; st + 3 < n_main; st += 4) {
+    step(st, s0, s1, U{}, S0{});
+    step(st + 1, s1, s0, U{}, S1{});
+    step(st + 2, s0, s1, U{}, S2{});
+    step(st + 3, s1, s0, U{}, S3{});
+  }
+  while (st < nstages) {
+    step(st, s0, s1, M{}, S0{});
+    if (++st == nstages) break;
+    step(st, s1, s0, M{}, S1{});
+    if (++st == nstages) break;
+    step(st, s0, s1, M{}, S2{});
+    if (++st == nstages) break;
+    step(st, s1, s0, M{}, S3{});
+    ++st;
   }
   // Let every copy land before the buffers are reused for the merge.
   wait_vmcnt<0>();
   __syncthreads();
+  l += __shfl_xor(l, 32, kWave);
 
   // ---- merge the two context halves of every row group ---------------------
   float* scratch = reinterpret_cast<float*>(s_lds) + rg * (16 * DB + 2) * kWave;
@@ -494,19 +673,29 @@ int prefill_tile_for(int group) {
   return group > 0 ? kPrefillRows / (group / decode_sub_groups(group)) : kPrefillRows;
 }
 
+template <typename T, int D, int G>
+static void launch_prefill_g(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+  // One copy covers 64 / (D / 8) rows; blocks smaller than that take the
+  // per-lane copy addresses.
+  if ((1 << a.log2_block_size) >= kWave / (D / 8))
+    hipLaunchKernelGGL((prefill_kernel<T, D, G, false>), grid, dim3(kPrefillThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<T, D, G, true>), grid, dim3(kPrefillThreads), 0, s, a);
+}
+
 template <typename T, int D>
 static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items,
                                    hipStream_t s) {
   const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
   switch (group / a.sub_groups) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<T, D, 1>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<T, D, 2>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((prefill_kernel<T, D, 3>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<T, D, 4>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((prefill_kernel<T, D, 5>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((prefill_kernel<T, D, 6>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((prefill_kernel<T, D, 7>), grid, dim3(kPrefillThreads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((prefill_kernel<T, D, 8>), grid, dim3(kPrefillThreads), 0, s, a); break;
+    case 1: launch_prefill_g<T, D, 1>(a, grid, s); break;
+    case 2: launch_prefill_g<T, D, 2>(a, grid, s); break;
+    case 3: launch_prefill_g<T, D, 3>(a, grid, s); break;
+    case 4: launch_prefill_g<T, D, 4>(a, grid, s); break;
+    case 5: launch_prefill_g<T, D, 5>(a, grid, s); break;
+    case 6: launch_prefill_g<T, D, 6>(a, grid, s); break;
+    case 7: launch_prefill_g<T, D, 7>(a, grid, s); break;
+    case 8: launch_prefill_g<T, D, 8>(a, grid, s); break;
     default: return hipErrorNotSupported;
   }
   return hipGetLastError();
