@@ -398,23 +398,26 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   };
 
   // Scores of tile t (positions [32 t, 32 t + 32)) masked for this lane's row:
-  // past its causal limit, past the readable context, or (bad_ids) in a
-  // block outside the pool.
+  // past its causal limit or past the readable context (positions relative
+  // to the tile, so each test is one compare) ...
   const int kv_lim = min(qpos, kv_last);  // last position this row attends
   auto mask_tile = [&](int t, f32x16& s) {
-    // (positions relative to the tile, so each test is one compare)
     const int lim = kv_lim - (t * kKvTile + 4 * half);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (8 * (i >> 2) + (i & 3) > lim) s[i] = -INFINITY;
     }
-    if (bad_ids) {
+  };
+  // ... and (bad_ids only) in a block outside the pool.  This one is applied
+  // at the start of the step that turns the tile into probabilities, outside
+  // the interleaved phases; the tile's maximum may then include such a
+  // position's (finite) score, which only moves the reference maximum.
+  auto mask_bad = [&](int t, f32x16& s) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
-          s[i] = -INFINITY;
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
+      if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+        s[i] = -INFINITY;
     }
   };
   auto tile_max = [&](const f32x16& s) {
@@ -519,6 +522,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     const int slot = SLOT >= 0 ? SLOT : (st & (kKBufs - 1));
     if (wave < kCopyWaves) copy_step(st + 4, slot * kRegion, kbase, idk);
     const int idv_cur = idv;  // (the prefetch below replaces idv)
+    if (bad_ids) mask_bad(2 * st + kh, s_cur);
 
     // ---- A: S_next = K_next Q^T | P = exp2(S - m) | V^T reads
     const float msc = m * scale;
