@@ -420,13 +420,20 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         s[i] = -INFINITY;
     }
   };
+  // Row maximum of a tile: v_max3 written out, because fmaxf makes the
+  // compiler quiet each MFMA result first (a v_max x, x per input in IEEE
+  // mode), which doubled the instructions; the scores are never NaN.
+  auto max3 = [](float x, float y, float z) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+    return r;
+  };
   auto tile_max = [&](const f32x16& s) {
-    float m01 = fmaxf(fmaxf(s[0], s[1]), s[2]);
-    float m23 = fmaxf(fmaxf(s[3], s[4]), s[5]);
-    float m45 = fmaxf(fmaxf(s[6], s[7]), s[8]);
-    float m67 = fmaxf(fmaxf(s[9], s[10]), s[11]);
-    float m89 = fmaxf(fmaxf(s[12], s[13]), s[14]);
-    return max_halves(fmaxf(fmaxf(fmaxf(m01, m23), fmaxf(m45, m67)), fmaxf(m89, s[15])));
+    const float a0 = max3(s[0], s[1], s[2]), a1 = max3(s[3], s[4], s[5]), a2 = max3(s[6], s[7], s[8]);
+    const float a3 = max3(s[9], s[10], s[11]), a4 = max3(s[12], s[13], s[14]);
+    const float b0 = max3(a0, a1, a2), b1 = max3(a3, a4, s[15]);
+    const float t = max3(b0, b1, b1);
+    return max_halves(t);
   };
 
   f32x16 acc[DB];
