@@ -157,10 +157,15 @@ __device__ __forceinline__ int chunk_swizzle(int r) {
   else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-template <typename T, int D, int G, bool LANE_IDS>
+// D: the head dim of the LDS rows and MFMA tiles; DM: the head dim in
+// memory (80 and 96 run on rows of 128 whose pieces past DM are zero: the
+// copies skip them, the query's are zero and the output's are not stored).
+template <typename T, int D, int DM, bool LANE_IDS>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
   static_assert(Elem<T>::kBytes == 2, "16-bit caches (bf16 or fp16)");
-  constexpr int MTOK = kPrefillRows / G;  // query tokens per workgroup
+  static_assert(DM <= D && DM % 16 == 0, "memory head dim: a multiple of 16 up to D");
+  constexpr bool MASKD = DM < D;
+  constexpr int MEM_ROW = DM * 2;         // bytes of a head's row in memory
   constexpr int KS = D / 16;              // MFMA k-steps of QK^T
   constexpr int DB = D / 32;              // 32-wide d blocks of the output
   constexpr int CHUNKS = D / 8;           // 16-byte pieces per row
@@ -180,6 +185,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // K ring, then V ring (rows swizzled); reused for the final merge.
   __shared__ __attribute__((aligned(16))) char s_lds[kLdsBytes];
 
+  const int G = a.group / a.sub_groups;  // query heads of this workgroup
+  const int MTOK = kPrefillRows / G;     // query tokens per workgroup
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // Wave-uniform (scalar): branches on it are whole-wave branches, and the
@@ -209,14 +216,14 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int bs_mask = (1 << log2_bs) - 1;
   // Byte strides of a cache row and a cache block (the host keeps a block
   // under 4 GiB, so a row offset is one 32 x 32 -> 64-bit multiply-add).
-  const uint32_t row_bytes = static_cast<uint32_t>(hkv) * ROW_BYTES;
+  const uint32_t row_bytes = static_cast<uint32_t>(hkv) * MEM_ROW;
   const uint32_t block_bytes = row_bytes << log2_bs;
   const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
   const bool row_ok = trow >= 0 && trow < a.num_table_rows;
   const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
   const int bt_stride = row_ok ? a.block_table_stride : 1;
-  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * ROW_BYTES;
-  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * ROW_BYTES;
+  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * MEM_ROW;
+  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * MEM_ROW;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_lds));
 
   // This lane's query row.
@@ -235,7 +242,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
                            (first + tok0 + tok) * a.q_token_stride + h * a.q_head_stride;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qreg[ks] = row_live ? ld16(qrow + ks * 16 + half * 8) : make_uint4(0, 0, 0, 0);
+      qreg[ks] = row_live && (2 * ks + half) * 8 < DM ? ld16(qrow + ks * 16 + half * 8) : make_uint4(0, 0, 0, 0);
   }
 
   const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
@@ -268,10 +275,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int cw = wave & (kCopyWaves - 1);
   const int delta = lane / CHUNKS;
   uint32_t chunk_off[kDmaPerWave];
+  bool chunk_in[kDmaPerWave];  // the fetched piece lies inside the head in memory
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = cw * kCopyRows + j * kRowsPerDma + delta;
-    chunk_off[j] = static_cast<uint32_t>(((lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(r)) * 16);
+    const int c = (lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(r);
+    chunk_off[j] = static_cast<uint32_t>(c * 16);
+    chunk_in[j] = c * 8 < DM;
   }
   // Per-lane offsets of a wave's copies when its 16 rows share one block.
   uint32_t row_off[kDmaPerWave];
@@ -330,7 +340,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         const uint32_t voff =
             __umul24(min(static_cast<uint32_t>(delta), static_cast<uint32_t>(kv_last - pc)), row_bytes) +
             chunk_off[j];
-        dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+        if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
       }
     } else {
       // Blocks smaller than one copy: each lane's row has its own block.
@@ -338,9 +348,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       for (int j = 0; j < kDmaPerWave; ++j) {
         const int pos = min(p0 + j * kRowsPerDma + delta, kv_last);
         const int b = pos >= x * kStage ? ring_id(x, pos) : id_last;
-        dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
-              base + (static_cast<uint64_t>(valid_block(b)) * block_bytes +
-                      (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk_off[j])));
+        if (!MASKD || chunk_in[j])
+          dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
+                base + (static_cast<uint64_t>(valid_block(b)) * block_bytes +
+                        (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk_off[j])));
       }
     }
   };
@@ -355,7 +366,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
                                 static_cast<uint32_t>(p0 & bs_mask) * row_bytes);
       const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
 #pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
+      for (int j = 0; j < kDmaPerWave; ++j)
+        if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
     } else {
       copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
     }
@@ -463,6 +475,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // ---- prologue --------------------------------------------------------------
   // K of stages 0-2, V of stage 0 and the id ring of stages 0-7 landed, then
   // K 3 / V 1 in flight.
+  if constexpr (MASKD) {
+    // Row pieces past the head are never copied: zero them once, before any
+    // copy lands.
+    for (int i = tid; i < (kKBufs + kVBufs) * kRegion / 16; i += kPrefillThreads)
+      st16(s_lds + 16 * i, make_uint4(0, 0, 0, 0));
+    __syncthreads();
+  }
   {
     if (wave == 0) {
 #pragma unroll
@@ -656,12 +675,13 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   if (!row_live) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = reinterpret_cast<uint16_t*>(a.output) +
-                   ((first + tok0 + tok) * (hkv * a.group) + h) * static_cast<int64_t>(D);
+                   ((first + tok0 + tok) * (hkv * a.group) + h) * static_cast<int64_t>(DM);
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = db * 32 + 8 * q4 + 4 * half;
+      if (MASKD && d >= DM) continue;
       uint2 w;
       w.x = pack_half2<T>(acc[db][4 * q4 + 0] * inv, acc[db][4 * q4 + 1] * inv);
       w.y = pack_half2<T>(acc[db][4 * q4 + 2] * inv, acc[db][4 * q4 + 3] * inv);
@@ -670,9 +690,11 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 }
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
-  // bf16 / fp16: the MFMA kernel below; fp32: prefill_f32_kernel (VALU).
+  // bf16 / fp16: the MFMA kernel below (heads of 80 and 96 on rows of 128);
+  // fp32: prefill_f32_kernel (VALU), heads of 64 and 128.
   if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16 && dtype != PA_DTYPE_F32) return false;
-  if (head_dim != 64 && head_dim != 128) return false;
+  const bool mfma_dim = head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128;
+  if (dtype == PA_DTYPE_F32 ? head_dim != 64 && head_dim != 128 : !mfma_dim) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   return true;
@@ -684,31 +706,17 @@ int prefill_tile_for(int group) {
   return group > 0 ? kPrefillRows / (group / decode_sub_groups(group)) : kPrefillRows;
 }
 
-template <typename T, int D, int G>
-static void launch_prefill_g(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+template <typename T, int D, int DM>
+static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items, hipStream_t s) {
+  const int g = group / a.sub_groups;
+  if (g < 1 || g > 8) return hipErrorNotSupported;
+  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
   // One copy covers 64 / (D / 8) rows; blocks smaller than that take the
   // per-lane copy addresses.
   if ((1 << a.log2_block_size) >= kWave / (D / 8))
-    hipLaunchKernelGGL((prefill_kernel<T, D, G, false>), grid, dim3(kPrefillThreads), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D, DM, false>), grid, dim3(kPrefillThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((prefill_kernel<T, D, G, true>), grid, dim3(kPrefillThreads), 0, s, a);
-}
-
-template <typename T, int D>
-static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items,
-                                   hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
-  switch (group / a.sub_groups) {
-    case 1: launch_prefill_g<T, D, 1>(a, grid, s); break;
-    case 2: launch_prefill_g<T, D, 2>(a, grid, s); break;
-    case 3: launch_prefill_g<T, D, 3>(a, grid, s); break;
-    case 4: launch_prefill_g<T, D, 4>(a, grid, s); break;
-    case 5: launch_prefill_g<T, D, 5>(a, grid, s); break;
-    case 6: launch_prefill_g<T, D, 6>(a, grid, s); break;
-    case 7: launch_prefill_g<T, D, 7>(a, grid, s); break;
-    case 8: launch_prefill_g<T, D, 8>(a, grid, s); break;
-    default: return hipErrorNotSupported;
-  }
+    hipLaunchKernelGGL((prefill_kernel<T, D, DM, true>), grid, dim3(kPrefillThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -717,11 +725,15 @@ hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int gro
   if (num_items <= 0) return hipSuccess;
   if (dtype == PA_DTYPE_F32) return launch_prefill_f32(a, head_dim, group, num_items, stream);
   if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return launch_prefill_d<bf16_t, 128>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_prefill_d<bf16_t, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_prefill_d<bf16_t, 128, 128>(a, group, num_items, stream);
+    if (head_dim == 96) return launch_prefill_d<bf16_t, 128, 96>(a, group, num_items, stream);
+    if (head_dim == 80) return launch_prefill_d<bf16_t, 128, 80>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_d<bf16_t, 64, 64>(a, group, num_items, stream);
   } else if (dtype == PA_DTYPE_F16) {
-    if (head_dim == 128) return launch_prefill_d<f16_t, 128>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_prefill_d<f16_t, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_prefill_d<f16_t, 128, 128>(a, group, num_items, stream);
+    if (head_dim == 96) return launch_prefill_d<f16_t, 128, 96>(a, group, num_items, stream);
+    if (head_dim == 80) return launch_prefill_d<f16_t, 128, 80>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_d<f16_t, 64, 64>(a, group, num_items, stream);
   }
   return hipErrorNotSupported;
 }

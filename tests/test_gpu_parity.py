@@ -534,12 +534,14 @@ def test_device_strategy_copy_blocks(device):
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 2, 64), (8, 1, 64),
                                      (9, 3, 64), (12, 4, 128), (10, 2, 128), (12, 2, 64), (28, 4, 128),
                                      # groups above 8: sub-groups of 8 and of 6 query heads
-                                     (32, 2, 128), (24, 2, 64)])
+                                     (32, 2, 128), (24, 2, 64),
+                                     # heads of 96 (Phi-3-mini) and 80 (Phi-2) on rows of 128
+                                     (8, 8, 96), (24, 4, 96), (12, 2, 80), (32, 32, 80)])
 def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
     _prefill_case(device, hq, hkv, d, torch.bfloat16)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64), (32, 2, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64), (32, 2, 128), (8, 8, 80), (16, 4, 96)])
 def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
     """fp16 caches run the same MFMA kernel with the f16 MFMA (the reference's
     LLM_DTYPE=fp16, app/memory/strategies.py:14-33)."""
