@@ -25,7 +25,7 @@ LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
 OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "plan.cpp", "pack.hip", "cache_write.hip", "decode.hip", "generic.hip", "prefill.hip",
-           "prefill_f32.hip", "copy_blocks.hip", "calibrate.hip"]
+           "prefill256.hip", "prefill_f32.hip", "copy_blocks.hip", "calibrate.hip"]
 
 HIP_FLAGS = [
     "-O3",
@@ -42,8 +42,10 @@ HIP_FLAGS = [
 ]
 
 
-# Per-source additions: the MFMA kernels keep their accumulators in
-# architectural VGPRs (no AGPR copies around the softmax rescale).
+# Per-source additions: the MFMA prefill for heads of 64-128 keeps its
+# accumulators in architectural VGPRs (no AGPR copies around the softmax
+# rescale); the one for heads of 256 (one wave per SIMD) leaves them to the
+# AGPRs.
 EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 

@@ -220,6 +220,7 @@ int prefill_tile_for(int group);
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream);
 // fp32 caches: the VALU kernel of prefill_f32.hip (same items and tile).
+hipError_t launch_prefill256(const PrefillArgs& a, int dtype, int group, int64_t num_items, hipStream_t stream);
 hipError_t launch_prefill_f32(const PrefillArgs& a, int head_dim, int group, int64_t num_items,
                               hipStream_t stream);
 

@@ -65,20 +65,14 @@
 
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
+#include "prefill_common.hpp"
 
 namespace pa {
-
-typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short i16x4v __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(4))) int32_t const_i32;
 
 constexpr int kPrefillThreads = 512;  // 4 row groups x 2 context halves
 constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kKvTile = 32;        // context tokens per wave per stage
 constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
-constexpr float kLazyRescale = 8.f;  // log2 headroom before the row maximum moves
 constexpr int kPrefillWaves = kPrefillThreads / 64;
 constexpr int kCopyWaves = 4;  // waves 0-3 copy, one per SIMD
 constexpr int kCopyRows = kStage / kCopyWaves;  // rows of a stage each copying wave copies
@@ -87,75 +81,6 @@ constexpr int kVBufs = 4;  // V ring: landed in st-1, read in step st, refilled 
 constexpr int kIdSlots = 8;      // block-id ring slots
 constexpr int kIdSlotBytes = 256;  // 64 table entries: every column of a stage
 constexpr int kIdAhead = 8;      // stages between an id slot's copy and the stage's K copy + 4
-// sched_group_barrier classes
-constexpr int kSchedValu = 0x002;
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
-
-template <typename T>
-__device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
-  if constexpr (Elem<T>::kDtype == PA_DTYPE_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
-                                                   __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a),
-                                                  __builtin_bit_cast(f16x8v, b), c, 0, 0, 0);
-  }
-}
-
-// ds_read_b64_tr_b16 at an LDS address (see the header comment).
-__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) i16x4v lds_i16x4;
-  const i16x4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  return __builtin_bit_cast(uint2, r);
-}
-
-// Direct global -> LDS loads.  Each lane's 16 bytes land at lds_base + 16 *
-// lane; lds_base must be wave-uniform.  dma16 takes a per-lane address,
-// dma16_s a wave-uniform base plus a per-lane 32-bit offset.  They are
-// issued from inline assembly so that the compiler, which cannot tell the
-// stage buffers apart, does not drain them before every LDS read; the
-// kernel waits for them itself (s_waitcnt vmcnt) before the barrier that
-// publishes a stage, and every LDS access is ordered against them by that
-// barrier (an asm statement with a memory clobber).
-__device__ __forceinline__ void dma16(uint32_t lds_base, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
-               : "memory", "m0");
-}
-// A wave-uniform pointer in scalar registers (the scalar-base copies take
-// their base from an SGPR pair).
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-__device__ __forceinline__ void dma4_s(uint32_t lds_base, uint32_t voff, const void* sbase) {
-  sbase = uniform_ptr(sbase);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_s(uint32_t lds_base, uint32_t voff, const void* sbase) {
-  sbase = uniform_ptr(sbase);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff),
-               "s"(sbase)
-               : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// Swizzle of the 16-byte chunks of an unpadded LDS row: chunk c of row r sits
-// at position c ^ chunk_swizzle(r).  It keeps the 16-byte K reads (16 rows,
-// one chunk) and the transpose reads of V (4 rows x 4 chunks per 32 lanes)
-// free of bank conflicts.
-template <int CHUNKS>
-__device__ __forceinline__ int chunk_swizzle(int r) {
-  if constexpr (CHUNKS == 16) return 4 * (r & 3) + ((r >> 2) & 3);
-  else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
-}
 
 // D: the head dim of the LDS rows and MFMA tiles; DM: the head dim in
 // memory (80 and 96 run on rows of 128 whose pieces past DM are zero: the
@@ -690,10 +615,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 }
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
-  // bf16 / fp16: the MFMA kernel below (heads of 80 and 96 on rows of 128);
-  // fp32: prefill_f32_kernel (VALU), heads of 64 and 128.
+  // bf16 / fp16: the MFMA kernel below (heads of 80 and 96 on rows of 128)
+  // and prefill256_kernel for heads of 256; fp32: prefill_f32_kernel (VALU),
+  // heads of 64 and 128.
   if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16 && dtype != PA_DTYPE_F32) return false;
-  const bool mfma_dim = head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128;
+  const bool mfma_dim =
+      head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128 || head_dim == 256;
   if (dtype == PA_DTYPE_F32 ? head_dim != 64 && head_dim != 128 : !mfma_dim) return false;
   if (group < 1 || group > kMaxDecodeQueryGroup) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
@@ -724,6 +651,7 @@ hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int gro
                           int64_t num_items, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   if (dtype == PA_DTYPE_F32) return launch_prefill_f32(a, head_dim, group, num_items, stream);
+  if (head_dim == 256) return launch_prefill256(a, dtype, group, num_items, stream);
   if (dtype == PA_DTYPE_BF16) {
     if (head_dim == 128) return launch_prefill_d<bf16_t, 128, 128>(a, group, num_items, stream);
     if (head_dim == 96) return launch_prefill_d<bf16_t, 128, 96>(a, group, num_items, stream);

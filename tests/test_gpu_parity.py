@@ -536,12 +536,15 @@ def test_device_strategy_copy_blocks(device):
                                      # groups above 8: sub-groups of 8 and of 6 query heads
                                      (32, 2, 128), (24, 2, 64),
                                      # heads of 96 (Phi-3-mini) and 80 (Phi-2) on rows of 128
-                                     (8, 8, 96), (24, 4, 96), (12, 2, 80), (32, 32, 80)])
+                                     (8, 8, 96), (24, 4, 96), (12, 2, 80), (32, 32, 80),
+                                     # heads of 256 (Gemma): the one-wave-per-SIMD kernel
+                                     (16, 16, 256), (16, 8, 256), (8, 1, 256), (24, 2, 256)])
 def test_prefill_bf16_matches_oracle(device, hq, hkv, d):
     _prefill_case(device, hq, hkv, d, torch.bfloat16)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64), (32, 2, 128), (8, 8, 80), (16, 4, 96)])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64), (32, 2, 128), (8, 8, 80), (16, 4, 96),
+                                     (16, 4, 256)])
 def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
     """fp16 caches run the same MFMA kernel with the f16 MFMA (the reference's
     LLM_DTYPE=fp16, app/memory/strategies.py:14-33)."""
@@ -555,7 +558,8 @@ def test_prefill_fp32_matches_oracle(device, hq, hkv, d):
 
 
 @pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (16, 2, 64, torch.float16),
-                                           (8, 8, 64, torch.float32), (8, 2, 80, torch.bfloat16)])
+                                           (8, 8, 64, torch.float32), (8, 2, 80, torch.bfloat16),
+                                           (16, 4, 256, torch.bfloat16)])
 def test_attention_skips_out_of_pool_blocks(device, hq, hkv, d, dtype):
     """Block ids outside [0, total_blocks) (negative or past the pool) in a
     step's table: the positions they cover are skipped by every kernel --
