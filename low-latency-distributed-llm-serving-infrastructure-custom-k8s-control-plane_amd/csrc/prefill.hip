@@ -30,10 +30,11 @@
 //
 // Copies.  Waves 0-3 copy 16 rows each of every stage.  One copy covers 4
 // rows (8 for 64-dim heads) of one cache block, so its source is a scalar
-// base (block id from a scalar load of the table, row offset) plus a fixed
-// per-lane offset: no vector address arithmetic and no wait on the block
-// ids, which arrive one step ahead of their use.  (Blocks smaller than one
-// copy take the per-lane form of the address.)  The copies are issued from
+// base (block id, row offset) plus a fixed per-lane offset: no vector
+// address arithmetic.  The block ids come from an LDS ring of table entries
+// that wave 0 fills eight stages ahead, read one step ahead of their use.
+// (Blocks smaller than one copy take the per-lane form of the address.)
+// The copies are issued from
 // inline assembly and each copying wave waits for its own copies with an
 // exact s_waitcnt vmcnt before the barrier that publishes them: the compiler
 // would otherwise drain every copy before each LDS read, as it cannot tell
