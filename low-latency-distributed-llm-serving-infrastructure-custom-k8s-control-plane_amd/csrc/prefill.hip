@@ -269,18 +269,24 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
       }
     } else {
-      // Blocks smaller than one copy: each lane's row has its own block.
+      // Blocks smaller than a copying wave's rows: each lane's row has its own
+      // block, read from the ring for every copy of the tensor first (one
+      // wait for all of them, not one per copy).
+      int pos[kDmaPerWave], b[kDmaPerWave];
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) {
-        const int pos = min(p0 + j * kRowsPerDma + delta, kv_last);
-        const int b = pos >= x * kStage ? ring_id(x, pos) : id_last;
+        pos[j] = min(p0 + j * kRowsPerDma + delta, kv_last);
+        b[j] = pos[j] >= x * kStage ? ring_id(x, pos[j]) : id_last;
+      }
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j)
         if (!MASKD || chunk_in[j])
           dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
-                base + (static_cast<uint64_t>(valid_block(b)) * block_bytes +
-                        (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk_off[j])));
-      }
+                base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
+                        (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j])));
     }
   };
+
   // A loop step's copies: one scalar base for the wave's 16 rows when they
   // share a block and are readable (id_fast: their block id, read from the
   // ring a step ahead), else one copy at a time with ids from the ring.
@@ -639,9 +645,11 @@ static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_
   const int g = group / a.sub_groups;
   if (g < 1 || g > 8) return hipErrorNotSupported;
   const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
-  // One copy covers 64 / (D / 8) rows; blocks smaller than that take the
-  // per-lane copy addresses.
-  if ((1 << a.log2_block_size) >= kWave / (D / 8))
+  // A copying wave's 16 rows of a stage share one block from blocks of 16
+  // up; smaller blocks take the per-lane copy addresses (ids read per lane
+  // from the ring), which beat one scalar base per copy with its id read
+  // just before it.
+  if ((1 << a.log2_block_size) >= kCopyRows)
     hipLaunchKernelGGL((prefill_kernel<T, D, DM, false>), grid, dim3(kPrefillThreads), 0, s, a);
   else
     hipLaunchKernelGGL((prefill_kernel<T, D, DM, true>), grid, dim3(kPrefillThreads), 0, s, a);

@@ -170,16 +170,23 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
         dma16_s(dst0 + j * kRowsPerDma * kRowBytes, voff, src);
       }
     } else {
+      // Blocks smaller than a copying wave's rows: each lane's row has its own
+      // block, read from the ring for every copy of the tensor first (one
+      // wait for all of them, not one per copy).
+      int pos[kDmaPerWave], b[kDmaPerWave];
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) {
-        const int pos = min(p0 + j * kRowsPerDma + delta, kv_last);
-        const int b = pos >= x * kTile ? ring_id(x, pos) : id_last;
-        dma16(dst0 + j * kRowsPerDma * kRowBytes,
-              base + (static_cast<uint64_t>(valid_block(b)) * block_bytes +
-                      (static_cast<uint32_t>(pos & bs_mask) * row_bytes + chunk_off[j])));
+        pos[j] = min(p0 + j * kRowsPerDma + delta, kv_last);
+        b[j] = pos[j] >= x * kTile ? ring_id(x, pos[j]) : id_last;
       }
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j)
+        dma16(dst0 + j * kRowsPerDma * kRowBytes,
+              base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
+                      (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j])));
     }
   };
+
   auto copy_step = [&](int x, uint32_t region, const char* base, int id_fast) {
     const int p0 = x * kTile + cw * kCopyRows;
     if (!LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last) {
