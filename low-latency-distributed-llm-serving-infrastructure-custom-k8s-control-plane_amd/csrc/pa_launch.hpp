@@ -181,6 +181,9 @@ struct PrefillArgs {
   // sub_groups heads and walks the context itself).
   int32_t group;
   int32_t sub_groups;
+  // Work units of the launch (items x KV heads x sub-groups): the MFMA
+  // prefill runs fewer workgroups than units, each looping over its share.
+  int64_t num_units;
 };
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,

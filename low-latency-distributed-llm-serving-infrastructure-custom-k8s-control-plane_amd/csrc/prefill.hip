@@ -1,12 +1,17 @@
 // Causal chunked prefill over the paged cache with gfx950 MFMA tiles.
 //
-// One workgroup (8 waves) per (sequence, query tile, KV head).  The tile
-// holds 128 query rows = (128 / G) query tokens x the G query heads that
-// share the KV head.  The context is walked in stages of 64 tokens; wave w
-// owns rows [32 (w%4), 32 (w%4) + 32) and the 32-token half w/4 of every
-// stage, with flash-style online softmax in fp32, so the two waves of a row
-// group split the context and merge their partial results through LDS at
-// the end (this halves the longest chain of a causal tile).
+// A unit of work is (sequence, query tile, KV head).  The tile holds 128
+// query rows = (128 / G) query tokens x the G query heads that share the KV
+// head.  The launch runs one workgroup (8 waves) per CU, and each walks its
+// share of the units in turn (longest first, snake order), so a unit's
+// start costs no workgroup launch.  The context is walked in stages of 64
+// tokens; wave w owns rows [32 (w%4), 32 (w%4) + 32) and the 32-token half
+// w/4 of every stage, with flash-style online softmax in fp32, so the two
+// waves of a row group split the context and merge their partial results
+// through LDS at the end (this halves the longest chain of a causal tile).
+// The query tile comes into LDS and the finished rows leave through it, in
+// whole rows: a lane's own row in registers would take one 16-byte piece of
+// 32 different rows per load or store.
 //
 // Both products are computed transposed so that a lane owns one query row:
 //   S^T[kv][row] = sum_d K[kv][d] Q[row][d]       (A = K regs, B = Q regs)
@@ -62,6 +67,8 @@
 // Reference: the block-diagonal causal mask of app/model/paged_attention.py:
 // 92-118 applied by SDPA (paged_attention.py:170-178); query token j of a
 // sequence at position start + j attends context positions [0, start + j].
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "pa_common.hpp"
@@ -105,14 +112,20 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   constexpr int kVReads = 2 * DB * 2;                 // V^T transpose reads per tile
   constexpr int kPerQk = 16 / KS;                     // probabilities per QK k-step
   static_assert(kDmaPerWave >= 1, "stage / wave mismatch");
-  static_assert(kLdsBytes >= 4 * (16 * DB + 2) * kWave * 4, "merge scratch must fit");
+  constexpr int kQBase = kVBase + 2 * kRegion;       // query tile: V slots 2-3 during the prologue
+  constexpr int kQRowsPerWave = kPrefillRows / kPrefillWaves;
+  constexpr int kQDmaPerWave = kQRowsPerWave / kRowsPerDma;
+  static_assert(kQRowsPerWave % kRowsPerDma == 0 && kPrefillRows * ROW_BYTES <= 2 * kRegion, "query tile");
+  constexpr int kMergeChunks = 4 * DB + 1;  // 16-byte pieces of a lane's acc + (m, l)
+  constexpr int kOutBase = 4 * kMergeChunks * kWave * 16;  // finished rows, after the merge regions
+  static_assert(kOutBase + kPrefillRows * ROW_BYTES <= kIdBase, "merge scratch and finished rows must fit");
   static_assert(kVReads % KS == 0, "V^T reads spread over the QK k-steps");
 
-  // K ring, then V ring (rows swizzled); reused for the final merge.
+  // K ring, then V ring (rows swizzled); reused for each unit's final merge.
   __shared__ __attribute__((aligned(16))) char s_lds[kLdsBytes];
 
-  const int G = a.group / a.sub_groups;  // query heads of this workgroup
-  const int MTOK = kPrefillRows / G;     // query tokens per workgroup
+  const int G = a.group / a.sub_groups;  // query heads of a unit
+  const int MTOK = kPrefillRows / G;     // query tokens per unit
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // Wave-uniform (scalar): branches on it are whole-wave branches, and the
@@ -121,83 +134,28 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   const int rg = wave & 3;   // row group
   const int kh = wave >> 2;  // context half of every stage
   const int hkv = a.num_kv_heads;
-  // Highest item first: the last query tiles of a sequence see the most context.
-  const int64_t blk_id = static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x;
-  // -> (item, KV head, sub-group of G of the head's a.group query heads).
-  const int units = hkv * a.sub_groups;
-  const int64_t item = blk_id / units;
-  const int unit = static_cast<int>(blk_id - item * units);
-  const int kvh = unit / a.sub_groups;
-  const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
-  const int seq = a.items[2 * item];
-  const int qt = a.items[2 * item + 1];
-  const int64_t first = a.cu_seqlens[seq];
-  const int count = static_cast<int>(a.cu_seqlens[seq + 1] - first);
-  const int ctx = a.context_lens[seq];
-  const int start = ctx - count;
-  const int tok0 = qt * MTOK;
-  const int ntok = min(MTOK, count - tok0);
-  if (ntok <= 0) return;
+  const int units = hkv * a.sub_groups;  // units per item
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
   // Byte strides of a cache row and a cache block (the host keeps a block
   // under 4 GiB, so a row offset is one 32 x 32 -> 64-bit multiply-add).
   const uint32_t row_bytes = static_cast<uint32_t>(hkv) * MEM_ROW;
   const uint32_t block_bytes = row_bytes << log2_bs;
-  const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
-  const bool row_ok = trow >= 0 && trow < a.num_table_rows;
-  const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
-  const int bt_stride = row_ok ? a.block_table_stride : 1;
-  const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * MEM_ROW;
-  const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * MEM_ROW;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_lds));
+  const float scale = a.scale_log2e;
 
-  // This lane's query row.
+  // This lane's query row of a unit's tile.
   const int row = rg * 32 + (lane & 31);
   const int half = lane >> 5;
   const int g = row / MTOK;
   const int tok = row - g * MTOK;
-  // Rows past G * MTOK (when G does not divide 128) belong to no head.
-  const bool row_live = tok < ntok && g < G;
-  const int qpos = start + tok0 + tok;  // causal limit (inclusive)
-  const int h = h0 + g;
 
-  uint4 qreg[KS];
-  {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.query) +
-                           (first + tok0 + tok) * a.q_token_stride + h * a.q_head_stride;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qreg[ks] = row_live && (2 * ks + half) * 8 < DM ? ld16(qrow + ks * 16 + half * 8) : make_uint4(0, 0, 0, 0);
-  }
-
-  const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
-  // Positions that have a block-table column (the rest are never read); at
-  // least one, as the host passes tables of one column or more.
-  const int kv_read = static_cast<int>(
-      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
-  const int kv_last = kv_read - 1;
-  const int nstages = (kv_end + kStage - 1) / kStage;
-  const float scale = a.scale_log2e;
-  const int last_col = bt_stride - 1;
-  // Positions whose block id lies outside the pool are skipped, as the
-  // decode kernels skip them: one pass over the row's columns tells whether
-  // there are any (then every tile takes the masked path below).  Its first
-  // load is issued here and checked after the first copies have landed, so
-  // the two memory round trips overlap.
-  const int ncols = (kv_read + bs_mask) >> log2_bs;
-  int scan0 = tid < ncols ? bt[tid] : 0;
-  bool bad_ids = false;  // set once the scan is complete (before any tile is masked)
-
-  // ---- copies ----------------------------------------------------------------
+  // ---- copy geometry ------------------------------------------------------------
   // Wave cw < 4 copies rows [16 cw, 16 cw + 16) of a stage, kRowsPerDma rows
   // per copy: lane -> row delta = lane / CHUNKS of the copy, chunk position
-  // lane % CHUNKS (fetching the chunk that the swizzle puts there).  Rows
-  // past the readable context re-read its last row, and an out-of-pool block
-  // id reads block 0 (finite values; their scores are masked).  Every copy is
-  // issued unconditionally, so each wave's outstanding count is the same
-  // every step.  (Copying from every wave instead raised each SIMD's scalar
-  // work per step by a third and the step time with it.)
+  // lane % CHUNKS (fetching the chunk that the swizzle puts there).  (Copying
+  // from every wave instead raised each SIMD's scalar work per step by a
+  // third and the step time with it.)
   const int cw = wave & (kCopyWaves - 1);
   const int delta = lane / CHUNKS;
   uint32_t chunk_off[kDmaPerWave];
@@ -218,94 +176,12 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   auto valid_block = [&](int b) {
     return static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks) ? static_cast<uint32_t>(b) : 0u;
   };
-  // Block ids of the first stages come from scalar loads of the table
-  // (constant address space: the table does not change during the launch).
-  const_i32* btc = (const_i32*)(bt);
-  // Block-id ring: slot x % kIdSlots holds the table entries of columns
-  // [col0(x), col0(x) + 64) (clamped to the row): every column a stage's
-  // positions use.  Wave 0 copies a stage's slot kIdAhead stages ahead, and
-  // a copying wave reads the id of its next copies one step ahead, so no
-  // copy waits on a table read and the loop issues no scalar loads (their
-  // out-of-order returns would force every LDS wait to drain).
-  auto col0 = [&](int x) { return min((x * kStage) >> log2_bs, last_col); };
-  auto dma_ids = [&](int x) {
-    const int c0 = col0(x);
-    dma4_s(lds0 + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes,
-           static_cast<uint32_t>(min(lane, last_col - c0)) * 4u, bt + c0);
-  };
-  // Ring entry of position p of stage x (p inside the readable context and
-  // the stage; other positions read some valid entry, which is not used).
-  auto ring_id = [&](int x, int p) {
-    const int idx = min(max((p >> log2_bs) - col0(x), 0), kWave - 1);
-    return *reinterpret_cast<const int*>(s_lds + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes + idx * 4);
-  };
   // The ring entry of a copying wave's first row when its 16 rows share one
-  // block and the stage lies inside the readable context (blocks of 16 or
-  // more start on a stage boundary, or contain the whole stage).
+  // block (blocks of 16 or more start on a stage boundary, or contain the
+  // whole stage).
   const int fast_idx4 = kIdBase + ((cw * kCopyRows) >> log2_bs) * 4;
   auto ring_fast = [&](int x) {
     return *reinterpret_cast<const int*>(s_lds + fast_idx4 + (x & (kIdSlots - 1)) * kIdSlotBytes);
-  };
-  const int id_last = btc[min(kv_last >> log2_bs, last_col)];  // block of the last readable row
-  // Copies of this wave's rows of tensor stage x into LDS region `region`,
-  // one per kRowsPerDma rows, with get_id(j, p): the block id of position p
-  // (readable) of copy j.
-  auto copy_each = [&](int x, uint32_t region, const char* base, auto get_id) {
-    const int p0 = x * kStage + cw * kCopyRows;
-    const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
-    if constexpr (!LANE_IDS) {
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        const int p = p0 + j * kRowsPerDma;
-        const int pc = min(p, kv_last);
-        const uint32_t bb = valid_block(p <= kv_last ? get_id(j, p) : id_last);
-        const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
-                                  static_cast<uint32_t>(pc & bs_mask) * row_bytes);
-        // Rows of the copy past the readable context re-read its last row
-        // (same block: a copy never spans blocks here).
-        const uint32_t voff =
-            __umul24(min(static_cast<uint32_t>(delta), static_cast<uint32_t>(kv_last - pc)), row_bytes) +
-            chunk_off[j];
-        if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
-      }
-    } else {
-      // Blocks smaller than a copying wave's rows: each lane's row has its own
-      // block, read from the ring for every copy of the tensor first (one
-      // wait for all of them, not one per copy).
-      int pos[kDmaPerWave], b[kDmaPerWave];
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        pos[j] = min(p0 + j * kRowsPerDma + delta, kv_last);
-        b[j] = pos[j] >= x * kStage ? ring_id(x, pos[j]) : id_last;
-      }
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j)
-        if (!MASKD || chunk_in[j])
-          dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
-                base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
-                        (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j])));
-    }
-  };
-
-  // A loop step's copies: one scalar base for the wave's 16 rows when they
-  // share a block and are readable (id_fast: their block id, read from the
-  // ring a step ahead), else one copy at a time with ids from the ring.
-  auto copy_step = [&](int x, uint32_t region, const char* base, int id_fast) {
-    const int p0 = x * kStage + cw * kCopyRows;
-    if (!LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last) {
-      const uint32_t bb = valid_block(__builtin_amdgcn_readfirstlane(id_fast));
-      const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
-                                static_cast<uint32_t>(p0 & bs_mask) * row_bytes);
-      const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j)
-        if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
-    } else {
-      copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
-    }
-  };
-  auto copy_prologue = [&](int x, uint32_t region, const char* base) {
-    copy_each(x, region, base, [&](int, int p) { return btc[p >> log2_bs]; });
   };
 
   // ---- LDS operands --------------------------------------------------------------
@@ -316,6 +192,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     k_off[ks] = k_row * ROW_BYTES + (((half + 2 * ks) ^ chunk_swizzle<CHUNKS>(k_row)) * 16);
+  // This lane's query row in the staged tile: rows rg * 32 + (lane & 31) and
+  // k_row share their low bits, hence their swizzle, so the offsets are
+  // k_off plus a wave-uniform row shift.
+  const int q_shift = kQBase + (rg - kh) * 32 * ROW_BYTES;
   const int li = lane & 15;
   int v_off[2][DB];  // [8-row half][d block]; +16 rows per k-step is added below
 #pragma unroll
@@ -340,30 +220,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     if (hi == 0) { va[kk][db].x = w.x; va[kk][db].y = w.y; }
     else { va[kk][db].z = w.x; va[kk][db].w = w.y; }
   };
-
-  // Scores of tile t (positions [32 t, 32 t + 32)) masked for this lane's row:
-  // past its causal limit or past the readable context (positions relative
-  // to the tile, so each test is one compare) ...
-  const int kv_lim = min(qpos, kv_last);  // last position this row attends
-  auto mask_tile = [&](int t, f32x16& s) {
-    const int lim = kv_lim - (t * kKvTile + 4 * half);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (8 * (i >> 2) + (i & 3) > lim) s[i] = -INFINITY;
-    }
-  };
-  // ... and (bad_ids only) in a block outside the pool.  This one is applied
-  // at the start of the step that turns the tile into probabilities, outside
-  // the interleaved phases; the tile's maximum may then include such a
-  // position's (finite) score, which only moves the reference maximum.
-  auto mask_bad = [&](int t, f32x16& s) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
-      if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
-        s[i] = -INFINITY;
-    }
-  };
   // Row maximum of a tile: v_max3 written out, because fmaxf makes the
   // compiler quiet each MFMA result first (a v_max x, x per input in IEEE
   // mode), which doubled the instructions; the scores are never NaN.
@@ -379,246 +235,533 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     const float t = max3(b0, b1, b1);
     return max_halves(t);
   };
-
-  f32x16 acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  float m = kScoreFloor, l = 0.f;  // l: this lane's half of the row sum
-  // Lazy rescale: the reference maximum m of a row moves only when a tile's
-  // maximum exceeds it by more than kLazyRescale (log2 units), so
-  // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
-  // same softmax.
-  auto rescale = [&](float tmax) {
-    const bool grow = (tmax - m) * scale > kLazyRescale;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float m_new = grow ? tmax : m;
-      const float alpha = fast_exp2((m - m_new) * scale);
-      l *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-      m = m_new;
-    }
-  };
-
-  // ---- prologue --------------------------------------------------------------
-  // K of stages 0-2, V of stage 0 and the id ring of stages 0-7 landed, then
-  // K 3 / V 1 in flight.
-  if constexpr (MASKD) {
-    // Row pieces past the head are never copied: zero them once, before any
-    // copy lands.
-    for (int i = tid; i < (kKBufs + kVBufs) * kRegion / 16; i += kPrefillThreads)
-      st16(s_lds + 16 * i, make_uint4(0, 0, 0, 0));
-    __syncthreads();
-  }
-  {
-    if (wave == 0) {
-#pragma unroll
-      for (int x = 0; x < kIdAhead; ++x) dma_ids(x);
-    }
-    if constexpr (LANE_IDS) {
-      // (these copies read their ids from the ring)
-      wait_vmcnt<0>();
-      __syncthreads();
-    }
-    if (wave < kCopyWaves) {
-#pragma unroll
-      for (int x = 0; x < 3; ++x) copy_prologue(x, x * kRegion, kbase);
-      copy_prologue(0, kVBase, vbase);
-    }
-    wait_vmcnt<0>();
-  }
-  asm volatile("" : "+v"(scan0));  // the scan's first load is checked after the copies
-  int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
-  for (int c = tid + kPrefillThreads; c < ncols; c += kPrefillThreads)
-    bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
-  // (also publishes the first stages and the id ring)
-  bad_ids = __syncthreads_or(bad_local) != 0;
-  // Tiles below this index need no mask for any row of the workgroup.
-  const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
-  if (wave < kCopyWaves) {
-    copy_prologue(3, 3 * kRegion, kbase);
-    copy_prologue(1, kVBase + kRegion, vbase);
-  }
-  // Ids of step 0's copies (K of stage 4, V of stage 2), from the ring.
-  int idk = 0, idv = 0;
-  auto prefetch_ids = [&](int st) {
-    if (wave < kCopyWaves) {
-      idk = ring_fast(st + 4);
-      idv = ring_fast(st + 2);
-    }
-  };
-  prefetch_ids(0);
-  f32x16 s0, s1;
-  uint4 ka[KS];
-  {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s0[i] = 0.f;
-    read_k(0, ka);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s0 = mfma32<T>(ka[ks], qreg[ks], s0);
-    read_k(1, ka);
-    mask_tile(kh, s0);
-    rescale(tile_max(s0));
-  }
-  // Every wave has read K of stage 0 before step 0 refills its buffer.
-  stage_barrier();
-
   // 1.0 in both halves of a packed pair (bf16 0x3F80, fp16 0x3C00).
   constexpr uint32_t kOnes = Elem<T>::kDtype == PA_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u;
 
-  // One step: see the header comment.  s_cur holds the scores of this
-  // wave's tile of stage st, s_nxt receives those of stage st + 1.  The K
-  // and V rings have four slots each; stage x lives in slot x % 4 (SLOT, a
-  // compile-time constant in both loops below).
-  auto step = [&](int st, f32x16& s_cur, f32x16& s_nxt, auto masked, auto slot_c) {
-    constexpr bool MASKED = decltype(masked)::value;
-    constexpr int SLOT = decltype(slot_c)::value;
-    const int slot = SLOT >= 0 ? SLOT : (st & (kKBufs - 1));
-    if (wave < kCopyWaves) copy_step(st + 4, slot * kRegion, kbase, idk);
-    const int idv_cur = idv;  // (the prefetch below replaces idv)
-    if (bad_ids) mask_bad(2 * st + kh, s_cur);
+  // ---- the workgroup's units ---------------------------------------------------
+  // A unit is (item, KV head, sub-group); block id b = item * units + unit.
+  // The launch runs W workgroups (one per CU) over U units: workgroup w takes
+  // the units of rank w, 2W-1-w, 2W+w, 4W-1-w, ... in the order of block ids
+  // from the highest down (the last query tiles of a sequence see the most
+  // context), a snake that evens out each workgroup's total context.  Every
+  // unit starts with a memory round trip for its table entries and one for
+  // its first copies; the item and sequence records of the next unit are
+  // loaded while the current one runs (one lane-indexed load into one
+  // register), so they add none.
+  const int U = static_cast<int>(a.num_units);
+  const int W = static_cast<int>(gridDim.x);
+  const int wg = static_cast<int>(blockIdx.x);
+  auto rank_of = [&](int r) { return (r & 1) ? (r + 1) * W - 1 - wg : r * W + wg; };
+  auto item_of = [&](int rk) { return (U - 1 - rk) / units; };
+  int rank = rank_of(0);
+  if (rank >= U) return;
+  // The first unit's records, then the item of the second.
+  int seq = a.items[2 * item_of(rank)];
+  int qt = a.items[2 * item_of(rank) + 1];
+  int first = static_cast<int>(a.cu_seqlens[seq]);  // token indices stay below 2^31
+  int count = static_cast<int>(a.cu_seqlens[seq + 1]) - first;
+  int ctx = a.context_lens[seq];
+  int trow = a.rows != nullptr ? a.rows[seq] : seq;
+  int rank_n = rank_of(1);
+  int seq_n = 0, qt_n = 0;
+  if (rank_n < U) {
+    seq_n = a.items[2 * item_of(rank_n)];
+    qt_n = a.items[2 * item_of(rank_n) + 1];
+  }
 
-    // ---- A: S_next = K_next Q^T | P = exp2(S - m) | V^T reads
-    const float msc = m * scale;
-    f32x16 sn;
+  for (int r = 1;; ++r) {
+    // Lane k of `pre` loads field k of the next unit's records: 0-1 the
+    // (seq, query tile) of the unit after it, 2-3 the low words of
+    // cu_seqlens[seq_n], cu_seqlens[seq_n + 1], 4 context_lens[seq_n], 5 the
+    // table row of seq_n.  Read back when the next unit starts.
+    const bool more = rank_n < U;
+    const int rank_nn = rank_of(r + 1);
+    int pre = 0;
+    if (more) {
+      const int it_nn = rank_nn < U ? item_of(rank_nn) : 0;
+      const int32_t* p = a.items + 2 * it_nn + (lane & 1);
+      if (lane == 2 || lane == 3) p = reinterpret_cast<const int32_t*>(a.cu_seqlens + seq_n + (lane - 2));
+      if (lane == 4 || (lane == 5 && a.rows == nullptr)) p = a.context_lens + seq_n;
+      if (lane == 5 && a.rows != nullptr) p = a.rows + seq_n;
+      pre = *p;
+    }
+
+    const int unit = (U - 1 - rank) - item_of(rank) * units;
+    const int kvh = unit / a.sub_groups;
+    const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
+    const int start = ctx - count;
+    const int tok0 = qt * MTOK;
+    const int ntok = min(MTOK, count - tok0);
+
+    if (ntok > 0) {
+      const bool row_ok = trow >= 0 && trow < a.num_table_rows;
+      const int32_t* bt = row_ok ? a.block_tables + static_cast<int64_t>(trow) * a.block_table_stride : kNoBlockRow;
+      const int bt_stride = row_ok ? a.block_table_stride : 1;
+      const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * MEM_ROW;
+      const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * MEM_ROW;
+
+      // Rows past G * MTOK (when G does not divide 128) belong to no head.
+      const bool row_live = tok < ntok && g < G;
+      const int qpos = start + tok0 + tok;  // causal limit (inclusive)
+      const int h = h0 + g;
+
+      uint4 qreg[KS];  // this lane's query row, read from the staged tile below
+
+      const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
+      // Positions that have a block-table column (the rest are never read); at
+      // least one, as the host passes tables of one column or more.
+      const int kv_read = static_cast<int>(
+          min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
+      const int kv_last = kv_read - 1;
+      const int nstages = (kv_end + kStage - 1) / kStage;  // >= 1
+      const int last_col = bt_stride - 1;
+      // Positions whose block id lies outside the pool are skipped, as the
+      // decode kernels skip them: one pass over the row's columns tells whether
+      // there are any (then every tile takes the masked path below).  Its first
+      // load is issued here and checked after the first copies have landed, so
+      // the two memory round trips overlap.
+      const int ncols = (kv_read + bs_mask) >> log2_bs;
+      int scan0 = tid < ncols ? bt[tid] : 0;
+      bool bad_ids = false;  // set once the scan is complete (before any tile is masked)
+
+      // ---- copies ------------------------------------------------------------
+      // Rows past the readable context re-read its last row, and an
+      // out-of-pool block id reads block 0 (finite values; their scores are
+      // masked).  No stage past the last is copied: a step's copies, and the
+      // count of them its wait allows in flight, depend on how many stages
+      // remain.
+      // Block ids of the first stages come from scalar loads of the table
+      // (constant address space: the table does not change during the launch).
+      const_i32* btc = (const_i32*)(bt);
+      // Block-id ring: slot x % kIdSlots holds the table entries of columns
+      // [col0(x), col0(x) + 64) (clamped to the row): every column a stage's
+      // positions use.  Wave 0 copies a stage's slot kIdAhead stages ahead, and
+      // a copying wave reads the id of its next copies one step ahead, so no
+      // copy waits on a table read and the loop issues no scalar loads (their
+      // out-of-order returns would force every LDS wait to drain).
+      auto col0 = [&](int x) { return min((x * kStage) >> log2_bs, last_col); };
+      auto dma_ids = [&](int x) {
+        const int c0 = col0(x);
+        dma4_s(lds0 + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes,
+               static_cast<uint32_t>(min(lane, last_col - c0)) * 4u, bt + c0);
+      };
+      // Ring entry of position p of stage x (p inside the readable context and
+      // the stage; other positions read some valid entry, which is not used).
+      auto ring_id = [&](int x, int p) {
+        const int idx = min(max((p >> log2_bs) - col0(x), 0), kWave - 1);
+        return *reinterpret_cast<const int*>(s_lds + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes + idx * 4);
+      };
+      const int id_last = btc[min(kv_last >> log2_bs, last_col)];  // block of the last readable row
+      // Copies of this wave's rows of tensor stage x into LDS region `region`,
+      // one per kRowsPerDma rows, with get_id(j, p): the block id of position p
+      // (readable) of copy j.
+      auto copy_each = [&](int x, uint32_t region, const char* base, auto get_id) {
+        const int p0 = x * kStage + cw * kCopyRows;
+        const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
+        if constexpr (!LANE_IDS) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sn[i] = 0.f;
-    uint4 va[2][DB];
-    uint4 pb[2];
-    float rsum0 = 0.f, rsum1 = 0.f;
+          for (int j = 0; j < kDmaPerWave; ++j) {
+            const int p = p0 + j * kRowsPerDma;
+            const int pc = min(p, kv_last);
+            const uint32_t bb = valid_block(p <= kv_last ? get_id(j, p) : id_last);
+            const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
+                                      static_cast<uint32_t>(pc & bs_mask) * row_bytes);
+            // Rows of the copy past the readable context re-read its last row
+            // (same block: a copy never spans blocks here).
+            const uint32_t voff =
+                __umul24(min(static_cast<uint32_t>(delta), static_cast<uint32_t>(kv_last - pc)), row_bytes) +
+                chunk_off[j];
+            if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+          }
+        } else {
+          // Blocks smaller than a copying wave's rows: each lane's row has its own
+          // block, read from the ring for every copy of the tensor first (one
+          // wait for all of them, not one per copy).
+          int pos[kDmaPerWave], b[kDmaPerWave];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      sn = mfma32<T>(ka[ks], qreg[ks], sn);
+          for (int j = 0; j < kDmaPerWave; ++j) {
+            pos[j] = min(p0 + j * kRowsPerDma + delta, kv_last);
+            b[j] = pos[j] >= x * kStage ? ring_id(x, pos[j]) : id_last;
+          }
 #pragma unroll
-      for (int j = ks * kPerQk; j < (ks + 1) * kPerQk; ++j) s_cur[j] = fast_exp2(fmaf(s_cur[j], scale, -msc));
+          for (int j = 0; j < kDmaPerWave; ++j)
+            if (!MASKD || chunk_in[j])
+              dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
+                    base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
+                            (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j])));
+        }
+      };
+
+      // A loop step's copies: one scalar base for the wave's 16 rows when they
+      // share a block and are readable (id_fast: their block id, read from the
+      // ring a step ahead), else one copy at a time with ids from the ring.
+      auto copy_step = [&](int x, uint32_t region, const char* base, int id_fast) {
+        const int p0 = x * kStage + cw * kCopyRows;
+        if (!LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last) {
+          const uint32_t bb = valid_block(__builtin_amdgcn_readfirstlane(id_fast));
+          const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
+                                    static_cast<uint32_t>(p0 & bs_mask) * row_bytes);
+          const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
 #pragma unroll
-      for (int r = ks * (kVReads / KS); r < (ks + 1) * (kVReads / KS); ++r) read_vt(slot, r, va);
-      if (((ks + 1) * kPerQk) % 8 == 0) {
-        const int c = (ks + 1) * kPerQk / 8 - 1;
-        pb[c].x = pack_half2<T>(s_cur[8 * c + 0], s_cur[8 * c + 1]);
-        pb[c].y = pack_half2<T>(s_cur[8 * c + 2], s_cur[8 * c + 3]);
-        pb[c].z = pack_half2<T>(s_cur[8 * c + 4], s_cur[8 * c + 5]);
-        pb[c].w = pack_half2<T>(s_cur[8 * c + 6], s_cur[8 * c + 7]);
-        rsum0 = dot2_half<T>(pb[c].x, kOnes, rsum0);
-        rsum1 = dot2_half<T>(pb[c].y, kOnes, rsum1);
-        rsum0 = dot2_half<T>(pb[c].z, kOnes, rsum0);
-        rsum1 = dot2_half<T>(pb[c].w, kOnes, rsum1);
+          for (int j = 0; j < kDmaPerWave; ++j)
+            if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
+        } else {
+          copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
+        }
+      };
+      // The first stages' copies, with `id` the block of the wave's rows in
+      // stage x (blocks of 16 or more: one block per copying wave and stage;
+      // smaller blocks read their ids from the ring).
+      auto copy_first = [&](int x, uint32_t region, const char* base, int id) {
+        copy_each(x, region, base, [&](int, int) { return id; });
+      };
+
+      // Scores of tile t (positions [32 t, 32 t + 32)) masked for this lane's row:
+      // past its causal limit or past the readable context (positions relative
+      // to the tile, so each test is one compare) ...
+      const int kv_lim = min(qpos, kv_last);  // last position this row attends
+      auto mask_tile = [&](int t, f32x16& s) {
+        const int lim = kv_lim - (t * kKvTile + 4 * half);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (8 * (i >> 2) + (i & 3) > lim) s[i] = -INFINITY;
+        }
+      };
+      // ... and (bad_ids only) in a block outside the pool.  This one is applied
+      // at the start of the step that turns the tile into probabilities, outside
+      // the interleaved phases; the tile's maximum may then include such a
+      // position's (finite) score, which only moves the reference maximum.
+      auto mask_bad = [&](int t, f32x16& s) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
+          if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+            s[i] = -INFINITY;
+        }
+      };
+
+      f32x16 acc[DB];
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
+      float m = kScoreFloor, l = 0.f;  // l: this lane's half of the row sum
+      // Lazy rescale: the reference maximum m of a row moves only when a tile's
+      // maximum exceeds it by more than kLazyRescale (log2 units), so
+      // p <= 2^kLazyRescale; l and acc use the same m, and the result is the
+      // same softmax.
+      auto rescale = [&](float tmax) {
+        const bool grow = (tmax - m) * scale > kLazyRescale;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = grow ? tmax : m;
+          const float alpha = fast_exp2((m - m_new) * scale);
+          l *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+          m = m_new;
+        }
+      };
+
+      // ---- prologue ----------------------------------------------------------
+      // The id ring of stages 0-7, K of stages 0-3 and V of stages 0-1 (those
+      // that exist) go out together and land before the first barrier.
+      if constexpr (MASKD) {
+        // Row pieces past the head are never copied: zero them before any
+        // copy lands (the previous unit's merge wrote over the rings).
+        for (int i = tid; i < (kKBufs + kVBufs) * kRegion / 16; i += kPrefillThreads)
+          st16(s_lds + 16 * i, make_uint4(0, 0, 0, 0));
+        __syncthreads();
       }
-    }
-    // ---- B: O^T += V^T P^T | row maxima of S_next | K reads of stage st+2
+      {
+        // The query tile goes into V slots 2-3 (free until step 0 copies V of
+        // stage 2) in whole rows, swizzled like the K rows: wave w copies rows
+        // [w kQRowsPerWave, (w + 1) kQRowsPerWave), kRowsPerDma per copy.
+        // Rows that belong to no head fetch the tile's first row (their
+        // results are never stored).
+        // (The row arithmetic is kept inside the unit loop: hoisted out of
+        // it, its per-copy values would be held in registers for the whole
+        // launch and spilled.)
+        int qr = wave * kQRowsPerWave + delta;
+        asm volatile("" : "+v"(qr));
+        int qg = qr / MTOK;
+        int qtok = qr - qg * MTOK;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+        for (int j = 0; j < kQDmaPerWave; ++j) {
+          const bool live = qtok < ntok && qg < G;
+          const int c = (lane % CHUNKS) ^ chunk_swizzle<CHUNKS>(qr);
+          const uint16_t* src = reinterpret_cast<const uint16_t*>(a.query) +
+                                static_cast<int64_t>(first + tok0 + (live ? qtok : 0)) * a.q_token_stride +
+                                static_cast<int64_t>(h0 + (live ? qg : 0)) * a.q_head_stride + c * 8;
+          if (!MASKD || c * 8 < DM)
+            dma16(lds0 + kQBase + (wave * kQRowsPerWave + j * kRowsPerDma) * ROW_BYTES, src);
+          // next copy's row: kRowsPerDma further (less than a head's tokens)
+          qr += kRowsPerDma;
+          qtok += kRowsPerDma;
+          if (qtok >= MTOK) { qtok -= MTOK; ++qg; }
+        }
+        if (wave == 0) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] = mfma32<T>(va[kk][db], pb[kk], acc[db]);
-    read_k((slot + 2) & (kKBufs - 1), ka);
-    prefetch_ids(st + 1);
-    if constexpr (MASKED) mask_tile(2 * (st + 1) + kh, sn);
-    const float tmax = tile_max(sn);
-    l += rsum0 + rsum1;
+          for (int x = 0; x < kIdAhead; ++x)
+            if (x < nstages) dma_ids(x);
+        }
+        if constexpr (LANE_IDS) {
+          // (these copies read their ids from the ring)
+          wait_vmcnt<0>();
+          __syncthreads();
+        }
+        if (wave < kCopyWaves) {
+          // The block of this wave's rows in each of stages 0-3, all loaded
+          // before the first copy (one round trip, not one per copy).
+          int pid[4];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kVReads / KS, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 6 * 8 / KS, 0);
-    }
+          for (int x = 0; x < 4; ++x) pid[x] = btc[min(x * kStage + cw * kCopyRows, kv_last) >> log2_bs];
+          copy_first(0, 0, kbase, pid[0]);
+          copy_first(0, kVBase, vbase, pid[0]);
+          if (nstages > 1) copy_first(1, kRegion, kbase, pid[1]);
+          if (nstages > 2) copy_first(2, 2 * kRegion, kbase, pid[2]);
+          if (nstages > 3) copy_first(3, 3 * kRegion, kbase, pid[3]);
+          if (nstages > 1) copy_first(1, kVBase + kRegion, vbase, pid[1]);
+        }
+        wait_vmcnt<0>();
+      }
+      asm volatile("" : "+v"(scan0));  // the scan's first load is checked after the copies
+      int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+      for (int c = tid + kPrefillThreads; c < ncols; c += kPrefillThreads)
+        bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+      // (also publishes the first stages and the id ring)
+      bad_ids = __syncthreads_or(bad_local) != 0;
+      // Tiles below this index need no mask for any row of the workgroup.
+      const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
+      // Ids of step 0's copies (K of stage 4, V of stage 2), from the ring.
+      int idk = 0, idv = 0;
+      auto prefetch_ids = [&](int st) {
+        if (wave < kCopyWaves) {
+          idk = ring_fast(st + 4);
+          idv = ring_fast(st + 2);
+        }
+      };
+      prefetch_ids(0);
+      f32x16 s0, s1;
+      uint4 ka[KS];
+      {
 #pragma unroll
-    for (int i = 0; i < 2 * DB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (KS + 2) / (2 * DB), 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
-    }
-    rescale(tmax);
-    s_nxt = sn;
-    // The V copies and the id slot go out after the math, so that a copying
-    // wave issues its copies in two short runs rather than one long one.
-    if (wave < kCopyWaves) copy_step(st + 2, kVBase + ((slot + 2) & (kKBufs - 1)) * kRegion, vbase, idv_cur);
-    if (wave == 0) dma_ids(st + kIdAhead);
-    // K of stage st+3, V of stage st+1 and (wave 0) the id slot of stage
-    // st+7, copied last step, must have landed before the barrier
-    // publishes them.
-    if (wave == 0) wait_vmcnt<2 * kDmaPerWave + 1>();
-    else if (wave < kCopyWaves) wait_vmcnt<2 * kDmaPerWave>();
-    stage_barrier();
-  };
+        for (int i = 0; i < 16; ++i) s0[i] = 0.f;
+        read_k(0, ka);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(s_lds + q_shift + k_off[ks]);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s0 = mfma32<T>(ka[ks], qreg[ks], s0);
+        read_k(1, ka);
+        mask_tile(kh, s0);
+        rescale(tile_max(s0));
+      }
+      // Every wave has read K of stage 0 before step 0 refills its buffer.
+      stage_barrier();
 
-  // Every step runs a body with its ring slot (st % 4) and score registers
-  // (st % 2) fixed at compile time: four unmasked steps per trip while both
-  // tiles of stage st+1 lie below first_masked, then masked steps, four per
-  // trip with an exit test after each (no step past the last stage).
-  using U = std::false_type;
-  using M = std::true_type;
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  using S3 = std::integral_constant<int, 3>;
-  const int n_main = min(max(first_masked / 2 - 1, 0), nstages);
-  int st = 0;
-  for (; st + 3 < n_main; st += 4) {
-    step(st, s0, s1, U{}, S0{});
-    step(st + 1, s1, s0, U{}, S1{});
-    step(st + 2, s0, s1, U{}, S2{});
-    step(st + 3, s1, s0, U{}, S3{});
-  }
-  while (st < nstages) {
-    step(st, s0, s1, M{}, S0{});
-    if (++st == nstages) break;
-    step(st, s1, s0, M{}, S1{});
-    if (++st == nstages) break;
-    step(st, s0, s1, M{}, S2{});
-    if (++st == nstages) break;
-    step(st, s1, s0, M{}, S3{});
-    ++st;
-  }
-  // Let every copy land before the buffers are reused for the merge.
-  wait_vmcnt<0>();
-  __syncthreads();
-  l += __shfl_xor(l, 32, kWave);
+      // One step: see the header comment.  s_cur holds the scores of this
+      // wave's tile of stage st, s_nxt receives those of stage st + 1.  The K
+      // and V rings have four slots each; stage x lives in slot x % 4 (SLOT, a
+      // compile-time constant in both loops below).
+      auto step = [&](int st, f32x16& s_cur, f32x16& s_nxt, auto masked, auto slot_c) {
+        constexpr bool MASKED = decltype(masked)::value;
+        constexpr int SLOT = decltype(slot_c)::value;
+        const int slot = SLOT >= 0 ? SLOT : (st & (kKBufs - 1));
+        // Copies of this step: K of stage st+4, V of stage st+2 and (wave 0)
+        // the id slot of stage st+8, each only if that stage exists.
+        const bool cpk = st + 4 < nstages, cpv = st + 2 < nstages, cpi = st + kIdAhead < nstages;
+        if (wave < kCopyWaves && cpk) copy_step(st + 4, slot * kRegion, kbase, idk);
+        const int idv_cur = idv;  // (the prefetch below replaces idv)
+        if (bad_ids) mask_bad(2 * st + kh, s_cur);
 
-  // ---- merge the two context halves of every row group ---------------------
-  float* scratch = reinterpret_cast<float*>(s_lds) + rg * (16 * DB + 2) * kWave;
-  if (kh == 1) {
+        // ---- A: S_next = K_next Q^T | P = exp2(S - m) | V^T reads
+        const float msc = m * scale;
+        f32x16 sn;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+        for (int i = 0; i < 16; ++i) sn[i] = 0.f;
+        uint4 va[2][DB];
+        uint4 pb[2];
+        float rsum0 = 0.f, rsum1 = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) scratch[(db * 16 + i) * kWave + lane] = acc[db][i];
-    scratch[(16 * DB) * kWave + lane] = m;
-    scratch[(16 * DB + 1) * kWave + lane] = l;
-  }
-  __syncthreads();
-  if (kh == 1) return;
-  {
-    const float m2 = scratch[(16 * DB) * kWave + lane];
-    const float l2 = scratch[(16 * DB + 1) * kWave + lane];
-    const float mm = fmaxf(m, m2);
-    const float a1 = fast_exp2((m - mm) * scale);
-    const float a2 = fast_exp2((m2 - mm) * scale);
-    l = l * a1 + l2 * a2;
+        for (int ks = 0; ks < KS; ++ks) {
+          sn = mfma32<T>(ka[ks], qreg[ks], sn);
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+          for (int j = ks * kPerQk; j < (ks + 1) * kPerQk; ++j) s_cur[j] = fast_exp2(fmaf(s_cur[j], scale, -msc));
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        acc[db][i] = acc[db][i] * a1 + scratch[(db * 16 + i) * kWave + lane] * a2;
-  }
+          for (int r = ks * (kVReads / KS); r < (ks + 1) * (kVReads / KS); ++r) read_vt(slot, r, va);
+          if (((ks + 1) * kPerQk) % 8 == 0) {
+            const int c = (ks + 1) * kPerQk / 8 - 1;
+            pb[c].x = pack_half2<T>(s_cur[8 * c + 0], s_cur[8 * c + 1]);
+            pb[c].y = pack_half2<T>(s_cur[8 * c + 2], s_cur[8 * c + 3]);
+            pb[c].z = pack_half2<T>(s_cur[8 * c + 4], s_cur[8 * c + 5]);
+            pb[c].w = pack_half2<T>(s_cur[8 * c + 6], s_cur[8 * c + 7]);
+            rsum0 = dot2_half<T>(pb[c].x, kOnes, rsum0);
+            rsum1 = dot2_half<T>(pb[c].y, kOnes, rsum1);
+            rsum0 = dot2_half<T>(pb[c].z, kOnes, rsum0);
+            rsum1 = dot2_half<T>(pb[c].w, kOnes, rsum1);
+          }
+        }
+        // ---- B: O^T += V^T P^T | row maxima of S_next | K reads of stage st+2
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[db] = mfma32<T>(va[kk][db], pb[kk], acc[db]);
+        read_k((slot + 2) & (kKBufs - 1), ka);
+        prefetch_ids(st + 1);
+        if constexpr (MASKED) mask_tile(2 * (st + 1) + kh, sn);
+        const float tmax = tile_max(sn);
+        l += rsum0 + rsum1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kVReads / KS, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, 6 * 8 / KS, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * DB; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (KS + 2) / (2 * DB), 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+        }
+        rescale(tmax);
+        s_nxt = sn;
+        // The V copies and the id slot go out after the math, so that a copying
+        // wave issues its copies in two short runs rather than one long one.
+        if (wave < kCopyWaves && cpv)
+          copy_step(st + 2, kVBase + ((slot + 2) & (kKBufs - 1)) * kRegion, vbase, idv_cur);
+        if (wave == 0 && cpi) dma_ids(st + kIdAhead);
+        // K of stage st+3, V of stage st+1 and (wave 0) the id slot of stage
+        // st+7, copied last step, must have landed before the barrier
+        // publishes them; this step's copies may stay in flight (copies
+        // complete in issue order, so their count is the wait).
+        if (wave < kCopyWaves) {
+          const int n = (cpk ? kDmaPerWave : 0) + (cpv ? kDmaPerWave : 0) + (wave == 0 && cpi ? 1 : 0);
+          wait_vmcnt_at_most<2 * kDmaPerWave + 1>(n);
+        }
+        stage_barrier();
+      };
 
-  if (!row_live) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* orow = reinterpret_cast<uint16_t*>(a.output) +
-                   ((first + tok0 + tok) * (hkv * a.group) + h) * static_cast<int64_t>(DM);
+      // Every step runs a body with its ring slot (st % 4) and score registers
+      // (st % 2) fixed at compile time: four unmasked steps per trip while both
+      // tiles of stage st+1 lie below first_masked, then masked steps, four per
+      // trip with an exit test after each (no step past the last stage).
+      using U0 = std::false_type;
+      using M1 = std::true_type;
+      using S0 = std::integral_constant<int, 0>;
+      using S1 = std::integral_constant<int, 1>;
+      using S2 = std::integral_constant<int, 2>;
+      using S3 = std::integral_constant<int, 3>;
+      const int n_main = min(max(first_masked / 2 - 1, 0), nstages);
+      int st = 0;
+      for (; st + 3 < n_main; st += 4) {
+        step(st, s0, s1, U0{}, S0{});
+        step(st + 1, s1, s0, U0{}, S1{});
+        step(st + 2, s0, s1, U0{}, S2{});
+        step(st + 3, s1, s0, U0{}, S3{});
+      }
+      while (st < nstages) {
+        step(st, s0, s1, M1{}, S0{});
+        if (++st == nstages) break;
+        step(st, s1, s0, M1{}, S1{});
+        if (++st == nstages) break;
+        step(st, s0, s1, M1{}, S2{});
+        if (++st == nstages) break;
+        step(st, s1, s0, M1{}, S3{});
+        ++st;
+      }
+      // (the last step waited for every copy; no stage past the last is copied)
+      l += __shfl_xor(l, 32, kWave);
+
+      // ---- merge the two context halves of every row group -----------------
+      // (after the last step's barrier no wave reads the rings any more)
+      // Wave (rg, 1) hands its accumulator and (m, l) to wave (rg, 0) in
+      // 16-byte pieces (piece c of lane i at (c * 64 + i) * 16 of the row
+      // group's region), which reads them back a d block (four pieces) at a
+      // time.
+      {
+        char* region = s_lds + rg * kMergeChunks * kWave * 16 + lane * 16;
+        if (kh == 1) {
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+          for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = db * 32 + 8 * q4 + 4 * half;
-      if (MASKD && d >= DM) continue;
-      uint2 w;
-      w.x = pack_half2<T>(acc[db][4 * q4 + 0] * inv, acc[db][4 * q4 + 1] * inv);
-      w.y = pack_half2<T>(acc[db][4 * q4 + 2] * inv, acc[db][4 * q4 + 3] * inv);
-      *reinterpret_cast<uint2*>(orow + d) = w;
+            for (int q = 0; q < 4; ++q)
+              st16(region + (db * 4 + q) * kWave * 16,
+                   make_uint4(__float_as_uint(acc[db][4 * q + 0]), __float_as_uint(acc[db][4 * q + 1]),
+                              __float_as_uint(acc[db][4 * q + 2]), __float_as_uint(acc[db][4 * q + 3])));
+          st16(region + (4 * DB) * kWave * 16, make_uint4(__float_as_uint(m), __float_as_uint(l), 0u, 0u));
+        }
+        __syncthreads();
+        if (kh == 0) {
+          const uint4 ml = ld16(region + (4 * DB) * kWave * 16);
+          const float m2 = __uint_as_float(ml.x);
+          const float l2 = __uint_as_float(ml.y);
+          const float mm = fmaxf(m, m2);
+          const float a1 = fast_exp2((m - mm) * scale);
+          const float a2 = fast_exp2((m2 - mm) * scale);
+          const float lt = l * a1 + l2 * a2;
+          const float inv = lt > 0.f ? 1.f / lt : 0.f;
+          // The finished rows go through LDS (swizzled like the K rows) so that
+          // each store writes whole rows: lane i stores 16 bytes of row
+          // k kRowsPerStore + i / CHUNKS of the row group.
+          char* stage_rows = s_lds + kOutBase + rg * 32 * ROW_BYTES;
+          int r_lane = lane;  // (kept inside the unit loop, as the copies' rows above)
+          asm volatile("" : "+v"(r_lane));
+          const int r32w = r_lane & 31;
+          const int sw_w = chunk_swizzle<CHUNKS>(r32w);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            uint4 pv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pv[q] = ld16(region + (db * 4 + q) * kWave * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              uint2 w;
+              w.x = pack_half2<T>((acc[db][4 * q + 0] * a1 + __uint_as_float(pv[q].x) * a2) * inv,
+                                  (acc[db][4 * q + 1] * a1 + __uint_as_float(pv[q].y) * a2) * inv);
+              w.y = pack_half2<T>((acc[db][4 * q + 2] * a1 + __uint_as_float(pv[q].z) * a2) * inv,
+                                  (acc[db][4 * q + 3] * a1 + __uint_as_float(pv[q].w) * a2) * inv);
+              *reinterpret_cast<uint2*>(stage_rows + r32w * ROW_BYTES + (((db * 4 + q) ^ sw_w) * 16) + half * 8) = w;
+            }
+          }
+          constexpr int kRowsPerStore = kWave / CHUNKS;
+          const int c = r_lane % CHUNKS;
+          int r32 = r_lane / CHUNKS;  // row of the row group this lane stores
+          int og = (rg * 32 + r32) / MTOK;
+          int otok = rg * 32 + r32 - og * MTOK;
+#pragma unroll
+          for (int k = 0; k < 32 / kRowsPerStore; ++k) {
+            const uint4 v =
+                *reinterpret_cast<const uint4*>(stage_rows + r32 * ROW_BYTES + ((c ^ chunk_swizzle<CHUNKS>(r32)) * 16));
+            if (otok < ntok && og < G && (!MASKD || c * 8 < DM)) {
+              uint16_t* dst = reinterpret_cast<uint16_t*>(a.output) +
+                              (static_cast<int64_t>(first + tok0 + otok) * (hkv * a.group) + h0 + og) *
+                                  static_cast<int64_t>(DM) +
+                              c * 8;
+              st16(dst, v);
+            }
+            r32 += kRowsPerStore;
+            otok += kRowsPerStore;
+            if (otok >= MTOK) { otok -= MTOK; ++og; }
+          }
+        }
+      }
+      // The next unit's copies overwrite the merge scratch.
+      if (more) __syncthreads();
     }
+
+    if (!more) break;
+    rank = rank_n;
+    rank_n = rank_nn;
+    seq = seq_n;
+    qt = qt_n;
+    first = __builtin_amdgcn_readlane(pre, 2);
+    count = __builtin_amdgcn_readlane(pre, 3) - first;
+    ctx = __builtin_amdgcn_readlane(pre, 4);
+    trow = a.rows != nullptr ? __builtin_amdgcn_readlane(pre, 5) : seq;
+    seq_n = __builtin_amdgcn_readlane(pre, 0);
+    qt_n = __builtin_amdgcn_readlane(pre, 1);
+  }
 }
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
@@ -640,11 +783,33 @@ int prefill_tile_for(int group) {
   return group > 0 ? kPrefillRows / (group / decode_sub_groups(group)) : kPrefillRows;
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+static int device_compute_units() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <typename T, int D, int DM>
-static hipError_t launch_prefill_d(const PrefillArgs& a, int group, int64_t num_items, hipStream_t s) {
-  const int g = group / a.sub_groups;
+static hipError_t launch_prefill_d(const PrefillArgs& args, int group, int64_t num_items, hipStream_t s) {
+  const int g = group / args.sub_groups;
   if (g < 1 || g > 8) return hipErrorNotSupported;
-  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
+  PrefillArgs a = args;
+  a.num_units = num_items * a.num_kv_heads * a.sub_groups;
+  // Unit ranks are 32-bit and a workgroup's ranks reach about twice the count.
+  if (a.num_units > (int64_t{1} << 30)) return hipErrorInvalidValue;
+  // One workgroup per CU (the rings hold one per CU), each looping over its
+  // share of the units; fewer units than CUs run one each.
+  const int cus = device_compute_units();
+  const int64_t wgs = cus > 0 ? std::min<int64_t>(a.num_units, cus) : a.num_units;
+  const dim3 grid(static_cast<uint32_t>(wgs));
   // A copying wave's 16 rows of a stage share one block from blocks of 16
   // up; smaller blocks take the per-lane copy addresses (ids read per lane
   // from the ring), which beat one scalar base per copy with its id read

@@ -74,6 +74,17 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Wait until at most n (wave-uniform, 0 <= n <= MAX) vector memory
+// operations are outstanding: one s_waitcnt with the count as its immediate.
+template <int MAX>
+__device__ __forceinline__ void wait_vmcnt_at_most(int n) {
+  if constexpr (MAX <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= MAX) wait_vmcnt<MAX>();
+    else wait_vmcnt_at_most<MAX - 1>(n);
+  }
+}
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Swizzle of the 16-byte chunks of an unpadded LDS row: chunk c of row r sits
