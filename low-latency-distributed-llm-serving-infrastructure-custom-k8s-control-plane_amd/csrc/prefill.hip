@@ -465,8 +465,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       };
 
       // ---- prologue ----------------------------------------------------------
-      // The id ring of stages 0-7, K of stages 0-3 and V of stages 0-1 (those
-      // that exist) go out together and land before the first barrier.
+      // The query tile, the id ring of stages 0-7 and K of stage 0 land
+      // before the first barrier; K of stages 1-2 and V of stage 0 land while
+      // the first QK runs, before the second; K of stage 3 and V of stage 1
+      // before the end of step 0 (only stages that exist are copied).
       if constexpr (MASKD) {
         // Row pieces past the head are never copied: zero them before any
         // copy lands (the previous unit's merge wrote over the rings).
@@ -518,22 +520,39 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 #pragma unroll
           for (int x = 0; x < 4; ++x) pid[x] = btc[min(x * kStage + cw * kCopyRows, kv_last) >> log2_bs];
           copy_first(0, 0, kbase, pid[0]);
-          copy_first(0, kVBase, vbase, pid[0]);
           if (nstages > 1) copy_first(1, kRegion, kbase, pid[1]);
           if (nstages > 2) copy_first(2, 2 * kRegion, kbase, pid[2]);
-          if (nstages > 3) copy_first(3, 3 * kRegion, kbase, pid[3]);
-          if (nstages > 1) copy_first(1, kVBase + kRegion, vbase, pid[1]);
+          copy_first(0, kVBase, vbase, pid[0]);
+          // everything but K 1-2 and V 0 (issued last)
+          wait_vmcnt_at_most<3 * kDmaPerWave>(kDmaPerWave * (1 + (nstages > 1 ? 1 : 0) + (nstages > 2 ? 1 : 0)));
+        } else {
+          wait_vmcnt<0>();
         }
-        wait_vmcnt<0>();
       }
-      asm volatile("" : "+v"(scan0));  // the scan's first load is checked after the copies
+      __syncthreads();  // the query tile, K of stage 0 and the id ring
+      f32x16 s0, s1;
+      uint4 ka[KS];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s0[i] = 0.f;
+      read_k(0, ka);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(s_lds + q_shift + k_off[ks]);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s0 = mfma32<T>(ka[ks], qreg[ks], s0);
+      asm volatile("" : "+v"(scan0));  // the scan's first load is checked after all copies landed
       int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
       for (int c = tid + kPrefillThreads; c < ncols; c += kPrefillThreads)
         bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
-      // (also publishes the first stages and the id ring)
+      wait_vmcnt<0>();
+      // (also publishes K of stages 1-2 and V of stage 0, and tells that every
+      // wave has read K of stage 0 before step 0 refills its slot)
       bad_ids = __syncthreads_or(bad_local) != 0;
       // Tiles below this index need no mask for any row of the workgroup.
       const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
+      if (wave < kCopyWaves) {
+        if (nstages > 3) copy_step(3, 3 * kRegion, kbase, ring_fast(3));
+        if (nstages > 1) copy_step(1, kVBase + kRegion, vbase, ring_fast(1));
+      }
       // Ids of step 0's copies (K of stage 4, V of stage 2), from the ring.
       int idk = 0, idv = 0;
       auto prefetch_ids = [&](int st) {
@@ -543,22 +562,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         }
       };
       prefetch_ids(0);
-      f32x16 s0, s1;
-      uint4 ka[KS];
-      {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s0[i] = 0.f;
-        read_k(0, ka);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(s_lds + q_shift + k_off[ks]);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s0 = mfma32<T>(ka[ks], qreg[ks], s0);
-        read_k(1, ka);
-        mask_tile(kh, s0);
-        rescale(tile_max(s0));
-      }
-      // Every wave has read K of stage 0 before step 0 refills its buffer.
-      stage_barrier();
+      read_k(1, ka);
+      mask_tile(kh, s0);
+      rescale(tile_max(s0));
 
       // One step: see the header comment.  s_cur holds the scores of this
       // wave's tile of stage st, s_nxt receives those of stage st + 1.  The K
