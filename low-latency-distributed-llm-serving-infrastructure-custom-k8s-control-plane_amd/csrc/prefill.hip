@@ -735,10 +735,17 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
           int r32 = r_lane / CHUNKS;  // row of the row group this lane stores
           int og = (rg * 32 + r32) / MTOK;
           int otok = rg * 32 + r32 - og * MTOK;
+          // All of the lane's pieces are read before the first store (one LDS
+          // round trip, not one per store).
+          uint4 piece[32 / kRowsPerStore];
 #pragma unroll
           for (int k = 0; k < 32 / kRowsPerStore; ++k) {
-            const uint4 v =
-                *reinterpret_cast<const uint4*>(stage_rows + r32 * ROW_BYTES + ((c ^ chunk_swizzle<CHUNKS>(r32)) * 16));
+            const int rk = r32 + k * kRowsPerStore;
+            piece[k] = *reinterpret_cast<const uint4*>(stage_rows + rk * ROW_BYTES + ((c ^ chunk_swizzle<CHUNKS>(rk)) * 16));
+          }
+#pragma unroll
+          for (int k = 0; k < 32 / kRowsPerStore; ++k) {
+            const uint4 v = piece[k];
             if (otok < ntok && og < G && (!MASKD || c * 8 < DM)) {
               uint16_t* dst = reinterpret_cast<uint16_t*>(a.output) +
                               (static_cast<int64_t>(first + tok0 + otok) * (hkv * a.group) + h0 + og) *
@@ -746,7 +753,6 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
                               c * 8;
               st16(dst, v);
             }
-            r32 += kRowsPerStore;
             otok += kRowsPerStore;
             if (otok >= MTOK) { otok -= MTOK; ++og; }
           }
