@@ -551,6 +551,32 @@ def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
     _prefill_case(device, hq, hkv, d, torch.float16)
 
 
+@pytest.mark.parametrize("hq,hkv,d,dtype,bs", [(32, 8, 128, torch.bfloat16, 16), (16, 2, 64, torch.float16, 16),
+                                              (32, 8, 128, torch.bfloat16, 4), (24, 4, 96, torch.bfloat16, 32)])
+def test_prefill_many_units_matches_oracle(device, hq, hkv, d, dtype, bs):
+    """Several times more (query tile, KV head) units than CUs, of ragged
+    lengths and starts, with decodes mixed in: each prefill workgroup walks
+    several units in turn (the rounds of its longest/shortest order), and
+    every sequence's rows are checked against the oracle."""
+    rng = np.random.Generator(np.random.PCG64(1000 + hq + d + bs))
+    counts = [int(c) for c in rng.integers(1, 256, size=40)]
+    counts[::7] = [1] * len(counts[::7])  # decodes between the chunks
+    starts = [int(s) for s in rng.integers(0, 900, size=40)]
+    ctx = [s + c for s, c in zip(starts, counts)]
+    lists, total = wl._block_tables(rng, ctx, bs, pool=sum(-(-c // bs) for c in ctx) + 5)
+    w = wl.StepWorkload("prefill_many_units", hq, hkv, d, bs, dtype, 1.0, starts, counts, lists, total)
+    t = wl.make_tensors(w, device, seed=11)
+    step = pack_workload(w, device)
+    units = step.num_prefill_items * hkv * max(1, (hq // hkv) // 8)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    log(f"prefill many units {dtype} hq={hq} hkv={hkv} d={d} bs={bs} items={step.num_prefill_items} "
+        f"units~{units} cus={cus}")
+    assert units > 2 * cus
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 64), (32, 2, 128), (9, 3, 64)])
 def test_prefill_fp32_matches_oracle(device, hq, hkv, d):
     """fp32 caches prefill on the VALU kernel (fp32 throughout), to 1e-4."""
