@@ -78,7 +78,7 @@
 namespace pa {
 
 constexpr int kPrefillThreads = 512;  // 4 row groups x 2 context halves
-constexpr int kPrefillRows = 128;  // query rows per workgroup
+constexpr int kPrefillRows = 128;  // query rows per unit
 constexpr int kKvTile = 32;        // context tokens per wave per stage
 constexpr int kStage = 2 * kKvTile;  // context tokens per LDS stage
 constexpr int kPrefillWaves = kPrefillThreads / 64;
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       // (also publishes K of stages 1-2 and V of stage 0, and tells that every
       // wave has read K of stage 0 before step 0 refills its slot)
       bad_ids = __syncthreads_or(bad_local) != 0;
-      // Tiles below this index need no mask for any row of the workgroup.
+      // Tiles below this index need no mask for any row of the unit.
       const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
       if (wave < kCopyWaves) {
         if (nstages > 3) copy_step(3, 3 * kRegion, kbase, ring_fast(3));

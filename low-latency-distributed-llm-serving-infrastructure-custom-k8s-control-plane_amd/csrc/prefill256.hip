@@ -200,8 +200,17 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
       copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
     }
   };
+  // Block ids of this wave's copies in stages 0-3, all loaded before the
+  // first copy: one memory round trip, where loads issued copy by copy were
+  // waited for one at a time.
+  int first_ids[4][kDmaPerWave];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j)
+      first_ids[x][j] = btc[min(x * kTile + cw * kCopyRows + j * kRowsPerDma, kv_last) >> log2_bs];
   auto copy_prologue = [&](int x, uint32_t region, const char* base) {
-    copy_each(x, region, base, [&](int, int p) { return btc[p >> log2_bs]; });
+    copy_each(x, region, base, [&](int j, int) { return first_ids[x][j]; });
   };
 
   // ---- LDS operands ------------------------------------------------------------
