@@ -552,7 +552,9 @@ def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
 
 
 @pytest.mark.parametrize("hq,hkv,d,dtype,bs", [(32, 8, 128, torch.bfloat16, 16), (16, 2, 64, torch.float16, 16),
-                                              (32, 8, 128, torch.bfloat16, 4), (24, 4, 96, torch.bfloat16, 32)])
+                                              (32, 8, 128, torch.bfloat16, 4), (24, 4, 96, torch.bfloat16, 32),
+                                              # a group of 16: two sub-group units per item and KV head
+                                              (32, 2, 128, torch.bfloat16, 16)])
 def test_prefill_many_units_matches_oracle(device, hq, hkv, d, dtype, bs):
     """Several times more (query tile, KV head) units than CUs, of ragged
     lengths and starts, with decodes mixed in: each prefill workgroup walks
