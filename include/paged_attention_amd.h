@@ -477,7 +477,8 @@ int pa_decode_no_alloc(const void *query, const void *key_cache,
  * query token j of sequence i (flat index cu_seqlens[i] + j, position
  * context_lens[i] - count_i + j) attends positions [0, that position].
  * K/V are read from the paged cache, so the new tokens must already have
- * been written with pa_reshape_and_cache.
+ * been written with pa_reshape_and_cache.  A launch takes at most 2^30
+ * (item, KV head, query-head sub-group) units (PA_ERR_LAUNCH beyond).
  */
 int pa_prefill(const void *query, const void *key_cache,
                const void *value_cache, int32_t layer_idx, PaStepDims dims,
