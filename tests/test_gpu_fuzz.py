@@ -84,3 +84,45 @@ def test_random_steps_match_oracle(device, seed):
         out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
     check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=w.dtype == torch.float32)
+
+
+def random_wide_case(seed):
+    """A wide step: 40 sequences of ragged decodes and prefill chunks (2-200
+    tokens at starts 0-600) over 4 or 8 KV heads, so that the prefill has
+    from about 200 to 1600 (query tile, KV head) units and its workgroups
+    (one per CU) walk one to several of them."""
+    rng = np.random.Generator(np.random.PCG64(5000 + seed))
+    hkv = int(rng.choice([4, 8]))
+    group = int(rng.choice([2, 4] if hkv == 8 else [2, 4, 8]))
+    d = int(rng.choice([64, 128]))
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    bs = int(rng.choice([2, 4, 8, 16, 32]))
+    starts, counts = [], []
+    for _ in range(40):
+        if rng.random() < 0.3:
+            c = int(rng.integers(1, 900))
+            starts.append(c - 1)
+            counts.append(1)
+        else:
+            starts.append(int(rng.integers(0, 600)))
+            counts.append(int(rng.integers(2, 200)))
+    ctx = [s + c for s, c in zip(starts, counts)]
+    lists, pool = wl._block_tables(rng, ctx, bs, pool=sum(-(-c // bs) for c in ctx) + 7)
+    w = wl.StepWorkload(f"wide{seed}", hkv * group, hkv, d, bs, dtype, 1.0, starts, counts, lists, pool)
+    return w
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_wide_steps_match_oracle(device, seed):
+    w = random_wide_case(seed)
+    t = wl.make_tensors(w, device, seed=100 + seed)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                         dtype=w.dtype)
+    log(f"wide seed={seed}: H_q={w.num_query_heads} H_kv={w.num_kv_heads} D={w.head_dim} {w.dtype} "
+        f"bs={w.block_size} prefill units={step.num_prefill_items * w.num_kv_heads}")
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
