@@ -90,7 +90,10 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
   const int64_t row_elems = static_cast<int64_t>(hkv) * D;  // cache row of one token
   const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
   const bool row_ok = trow >= 0 && trow < a.num_table_rows;
-  const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
+  // A sequence without a table row reads as one block of id -1.  The pointer
+  // stays a global one (a select with a constant array would make every
+  // table read a flat load, which the LDS waits then also wait for).
+  const int32_t* bt = a.block_tables + (row_ok ? trow * a.block_table_stride : 0);
   const int bt_stride = row_ok ? a.block_table_stride : 1;
   const float* kbase = reinterpret_cast<const float*>(a.key_cache) + kvh * D;
   const float* vbase = reinterpret_cast<const float*>(a.value_cache) + kvh * D;
@@ -135,22 +138,59 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a)
     for (int e = 0; e < DS; ++e) acc[i][e] = 0.f;
   }
 
-  for (int st = 0; st < nstages; ++st) {
-    __syncthreads();  // the previous stage's K, V and p are consumed
-    // 1. K and V rows of the stage -> LDS.  Rows past the readable context
-    // re-read its last row and an out-of-pool block id reads block 0 (finite
-    // values; their scores are masked: such positions are skipped, as in
-    // decode).
-    for (int i = tid; i < kF32Stage * (D / 4); i += kF32Threads) {
+  // K and V rows of a stage: each thread's NPT 16-byte pieces of both are
+  // loaded into registers a stage ahead (during the previous stage's
+  // arithmetic) and stored into LDS when the stage starts.  Rows past the
+  // readable context re-read its last row and an out-of-pool block id reads
+  // block 0 (finite values; their scores are masked: such positions are
+  // skipped, as in decode).
+  constexpr int NPT = kF32Stage * (D / 4) / kF32Threads;
+  static_assert(NPT * kF32Threads == kF32Stage * (D / 4), "whole pieces per thread");
+  // The block ids of a stage's rows are loaded one stage earlier still, so
+  // that no copy waits on its table read.
+  f32x4 pk[NPT], pv[NPT];
+  bool pok[NPT];
+  int bid[NPT];
+  auto load_ids = [&](int st) {
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int r = (tid + j * kF32Threads) / (D / 4);
+      bid[j] = row_ok ? bt[min(st * kF32Stage + r, kv_read - 1) >> log2_bs] : -1;
+    }
+  };
+  auto load_stage = [&](int st) {
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int i = tid + j * kF32Threads;
       const int r = i / (D / 4), q4 = i - r * (D / 4);
       const int pos = min(st * kF32Stage + r, kv_read - 1);
-      int b = bt[pos >> log2_bs];
+      int b = bid[j];
       const bool in_pool = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks);
-      if (q4 == 0) s_ok[r] = in_pool && st * kF32Stage + r < kv_read;
+      pok[j] = in_pool && st * kF32Stage + r < kv_read;
       b = in_pool ? b : 0;
       const int64_t off = ((static_cast<int64_t>(b) << log2_bs) + (pos & bs_mask)) * row_elems + 4 * q4;
-      *reinterpret_cast<f32x4*>(s_k + r * LD + 4 * q4) = *reinterpret_cast<const f32x4*>(kbase + off);
-      *reinterpret_cast<f32x4*>(s_v + r * LD + 4 * q4) = *reinterpret_cast<const f32x4*>(vbase + off);
+      pk[j] = *reinterpret_cast<const f32x4*>(kbase + off);
+      pv[j] = *reinterpret_cast<const f32x4*>(vbase + off);
+    }
+  };
+  load_ids(0);
+  load_stage(0);
+  if (nstages > 1) load_ids(1);
+
+  for (int st = 0; st < nstages; ++st) {
+    __syncthreads();  // the previous stage's K, V and p are consumed
+    // 1. K and V rows of the stage -> LDS; then the next stage's loads.
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int i = tid + j * kF32Threads;
+      const int r = i / (D / 4), q4 = i - r * (D / 4);
+      if (q4 == 0) s_ok[r] = pok[j];
+      *reinterpret_cast<f32x4*>(s_k + r * LD + 4 * q4) = pk[j];
+      *reinterpret_cast<f32x4*>(s_v + r * LD + 4 * q4) = pv[j];
+    }
+    if (st + 1 < nstages) {
+      load_stage(st + 1);
+      if (st + 2 < nstages) load_ids(st + 2);
     }
     __syncthreads();
 
