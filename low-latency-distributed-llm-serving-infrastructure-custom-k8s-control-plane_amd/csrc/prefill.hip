@@ -296,6 +296,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
     if (ntok > 0) {
       const bool row_ok = trow >= 0 && trow < a.num_table_rows;
       const int32_t* bt = row_ok ? a.block_tables + static_cast<int64_t>(trow) * a.block_table_stride : kNoBlockRow;
+      global_i32* btg = (global_i32*)(bt);
       const int bt_stride = row_ok ? a.block_table_stride : 1;
       const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * MEM_ROW;
       const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * MEM_ROW;
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       // load is issued here and checked after the first copies have landed, so
       // the two memory round trips overlap.
       const int ncols = (kv_read + bs_mask) >> log2_bs;
-      int scan0 = tid < ncols ? bt[tid] : 0;
+      int scan0 = tid < ncols ? btg[tid] : 0;
       bool bad_ids = false;  // set once the scan is complete (before any tile is masked)
 
       // ---- copies ------------------------------------------------------------
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kv = t * kKvTile + 8 * (i >> 2) + 4 * half + (i & 3);
-          if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+          if (kv <= kv_lim && static_cast<uint32_t>(btg[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
             s[i] = -INFINITY;
         }
       };
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       asm volatile("" : "+v"(scan0));  // the scan's first load is checked after all copies landed
       int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
       for (int c = tid + kPrefillThreads; c < ncols; c += kPrefillThreads)
-        bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+        bad_local |= static_cast<uint32_t>(btg[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
       wait_vmcnt<0>();
       // (also publishes K of stages 1-2 and V of stage 0, and tells that every
       // wave has read K of stage 0 before step 0 refills its slot)

@@ -87,6 +87,7 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
   const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
   const bool row_ok = trow >= 0 && trow < a.num_table_rows;
   const int32_t* bt = row_ok ? a.block_tables + trow * a.block_table_stride : kNoBlockRow;
+  global_i32* btg = (global_i32*)(bt);
   const int bt_stride = row_ok ? a.block_table_stride : 1;
   const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * kRowBytes;
   const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * kRowBytes;
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
   const float scale = a.scale_log2e;
   const int last_col = bt_stride - 1;
   const int ncols = (kv_read + bs_mask) >> log2_bs;
-  int scan0 = tid < ncols ? bt[tid] : 0;
+  int scan0 = tid < ncols ? btg[tid] : 0;
   bool bad_ids = false;
 
   // ---- copies (wave cw copies rows [8 cw, 8 cw + 8) of a stage) ----------------
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int kv = t * kTile + 8 * (i >> 2) + 4 * half + (i & 3);
-      if (kv <= kv_lim && static_cast<uint32_t>(bt[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+      if (kv <= kv_lim && static_cast<uint32_t>(btg[kv >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
         s[i] = -INFINITY;
     }
   };
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void prefill256_kernel(PrefillArgs a) {
   asm volatile("" : "+v"(scan0));
   int bad_local = static_cast<uint32_t>(scan0) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
   for (int c = tid + kThreads; c < ncols; c += kThreads)
-    bad_local |= static_cast<uint32_t>(bt[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
+    bad_local |= static_cast<uint32_t>(btg[c]) >= static_cast<uint32_t>(a.total_blocks) ? 1 : 0;
   bad_ids = __syncthreads_or(bad_local) != 0;
   const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kTile;
   copy_prologue(3, 3 * kRegion, kbase);

@@ -13,6 +13,10 @@ typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4v __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(4))) int32_t const_i32;
+// A global-address view of a block-table row: the row pointer may also point
+// at a __device__ constant (no table row), which makes plain reads through it
+// flat loads, and an LDS wait (lgkmcnt) would then wait for them as well.
+typedef const __attribute__((address_space(1))) int32_t global_i32;
 
 // sched_group_barrier classes
 constexpr int kSchedValu = 0x002;
