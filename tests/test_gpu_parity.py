@@ -642,6 +642,48 @@ def test_attention_skips_out_of_pool_blocks(device, hq, hkv, d, dtype):
             assert ok, f"seq {i}: relative error {worst}"
 
 
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (8, 8, 64, torch.float32),
+                                           (16, 4, 256, torch.float16), (16, 4, 80, torch.bfloat16),
+                                           (32, 8, 128, torch.float32)])
+def test_attention_rows_outside_the_pool(device, hq, hkv, d, dtype):
+    """A step packed from a pool of table rows in which two sequences (one
+    prefill chunk, one decode) name a row outside the pool (past its end, and
+    -1): such a row reads as all -1, so those sequences attend no position
+    and their outputs are exactly zero, while every other sequence, read from
+    its shuffled pool row, equals the oracle -- the MFMA prefill (heads of
+    128 and of 80 on rows of 128), the heads-of-256 prefill, the fp32
+    prefill and decode."""
+    starts, counts = [100, 0, 300, 40, 700, 9], [40, 70, 1, 33, 1, 150]
+    outside = {1: 1000, 4: -1}  # sequence -> row outside the pool
+    bs = 16
+    rng = np.random.Generator(np.random.PCG64(hq + d))
+    lists, total = wl._block_tables(rng, [s_ + c for s_, c in zip(starts, counts)], bs, pool=120)
+    w = wl.StepWorkload("rows_outside", hq, hkv, d, bs, dtype, 1.0, starts, counts, lists, total)
+    t = wl.make_tensors(w, device, seed=5)
+    table = w.block_table_array()
+    b = len(starts)
+    pool_rows = b + 3
+    place = rng.permutation(pool_rows)[:b]
+    pool = np.full((pool_rows, table.shape[1]), -1, dtype=np.int32)
+    pool[place] = table
+    rows = place.astype(np.int32)
+    for i, r in outside.items():
+        rows[i] = r
+    tile = ops.prefill_tile_for(hq, hkv)
+    step = ops.pack_step(torch.from_numpy(pool).to(device), starts, counts, bs, rows=rows, prefill_tile=tile,
+                         num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+    out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    torch.cuda.synchronize()
+    log(f"rows outside the pool {dtype} {hq}/{hkv}/{d}: prefill items {step.num_prefill_items}, "
+        f"decode items {step.num_decode_items}")
+    cu = op.cumulative_offsets(counts)
+    for i in outside:
+        got = out[cu[i] : cu[i + 1]]
+        assert torch.count_nonzero(got).item() == 0, f"seq {i}"
+    inside = [i for i in range(b) if i not in outside]
+    check_rows(w, out, oracle_rows(w, t, inside), fp32=dtype == torch.float32)
+
+
 def _bits(t):
     return t.view({torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}[t.dtype])
 
