@@ -154,7 +154,9 @@ size_t pa_pack_workspace_size(int32_t num_seqs);
  * updates (int32 [num_updates, 3], may be NULL when num_updates is 0):
  * (row, col, block id) entries written into block_tables before anything
  * reads it (entries outside the table are skipped) -- how a host appends
- * the blocks it allocated since the last step.
+ * the blocks it allocated since the last step.  The entries are stored in
+ * no fixed order: each (row, col) may appear at most once (a host that
+ * queued several values for one entry passes only the last).
  * start_positions / new_token_counts: int64 [B].
  * rows, updates, start_positions and new_token_counts are read once, by
  * the first launch, and may sit in pinned host memory (the device address

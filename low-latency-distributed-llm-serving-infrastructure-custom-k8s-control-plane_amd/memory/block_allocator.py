@@ -238,11 +238,24 @@ class BlockTablePool:
 
     def take_updates(self):
         """(rebuild, updates): whether the device copy must be rebuilt from
-        ``host``, else the int32 [n, 3] triples to apply; clears the queue."""
+        ``host``, else the int32 [n, 3] triples to apply; clears the queue.
+
+        The queue can hold one (row, col) several times: a row released and
+        taken again before the next step queues its -1 resets and then the
+        new blocks.  pa_pack stores the triples in no fixed order, so only
+        the last value queued per (row, col) is returned, and it equals
+        ``host[row, col]``."""
         with self._lock:
             rebuild, self._rebuild = self._rebuild, False
             updates = np.asarray(self._pending, dtype=np.int32).reshape(-1, 3)
             self._pending.clear()
+            if updates.shape[0] > 1:
+                keys = updates[:, 0].astype(np.int64) * self.width + updates[:, 1]
+                # first occurrence in the reversed queue = last one queued
+                _, last = np.unique(keys[::-1], return_index=True)
+                keep = np.sort(updates.shape[0] - 1 - last)
+                if keep.shape[0] != updates.shape[0]:
+                    updates = np.ascontiguousarray(updates[keep])
             return rebuild, updates
 
     def mark_rebuild(self) -> None:

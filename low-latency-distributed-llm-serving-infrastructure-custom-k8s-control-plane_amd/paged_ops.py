@@ -224,6 +224,7 @@ class PackedStep:
         self._head_shape = head_shape  # (H_q, D) the workspace was sized for, or None
         self._gather = None
         self._extra_ws = None
+        self._generation = 0  # the pool's pack count when this step was packed
 
     # -- addresses and views ---------------------------------------------------
     def ptr(self, name: str) -> int:
@@ -307,8 +308,15 @@ class PackedStep:
 
     @property
     def gather_slots(self) -> torch.Tensor:
-        """int64 [C] slots of every context token (built on first use)."""
+        """int64 [C] slots of every context token (built on first use, by a
+        re-run of the packing kernel over the table as it is now).  On a pool
+        of rows it must be first read before the next step is packed on the
+        same pool: a later step's updates (a row freed and reused) would
+        change what the re-run reads, so a stale step raises instead."""
         if self._gather is None:
+            if self._pooled and _pack_generation(self._source_table) != self._generation:
+                raise RuntimeError("gather_slots of an earlier step: a later step was packed on the same "
+                                   "block-table pool since; read gather_slots before packing the next step")
             self._gather = _run_pack(self, with_gather=True)
         return self._gather
 
@@ -454,6 +462,11 @@ def choose_partition(
     return int(p.partition_size)
 
 
+def _pack_generation(table: torch.Tensor) -> int:
+    """Fresh packs so far on a block-table pool (a tensor attribute)."""
+    return getattr(table, "_pa_pack_generation", 0)
+
+
 def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.ndarray] = None,
               fresh: bool = False) -> Optional[torch.Tensor]:
     """Launch pa_pack for ``step``: all outputs are rewritten, plus the gather
@@ -530,6 +543,9 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
     if staging is not None:
         staging.done(slot, torch.cuda.current_stream(device))
     _native.check(status, "pa_pack")
+    if fresh and pooled:
+        table._pa_pack_generation = _pack_generation(table) + 1
+        step._generation = table._pa_pack_generation
     return gather
 
 

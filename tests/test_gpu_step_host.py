@@ -177,31 +177,45 @@ def test_pack_time_is_linear_in_the_batch(device):
     assert per_seq[4096] <= 1.5 * per_seq[1024]
 
 
-@pytest.mark.parametrize("dtype,with_gather", [(torch.bfloat16, True), (torch.float32, True),
-                                              (torch.bfloat16, False)])
-def test_manager_steps_track_growth_and_reuse(device, dtype, with_gather):
+@pytest.mark.parametrize("dtype,with_gather,free_first", [(torch.bfloat16, True, False),
+                                                         (torch.float32, True, False),
+                                                         (torch.bfloat16, False, False),
+                                                         (torch.bfloat16, False, True),
+                                                         (torch.float32, True, True)])
+def test_manager_steps_track_growth_and_reuse(device, dtype, with_gather, free_first):
     """A GPU store over several steps: prompts, decodes that open new blocks,
     frees and new sequences reusing freed rows, and a pool that grows its
     rows and columns.  Every step's block table (gathered from the pool),
     slots and work lists equal the oracle's on the sequences' block lists.
     Without gather slots at pack time the decode-only steps are packed in
-    one launch, queued table updates included."""
+    one launch, queued table updates included.  With ``free_first`` the
+    sequences that finish are freed before the same step admits new ones,
+    so the new ones take the freed rows at once: the queue then holds a -1
+    reset and a new block for one (row, col), and only the new block may
+    reach the device pool."""
     m = manager_mod.PagedKVCacheManager(total_blocks=4000, block_size=16, num_heads=8, head_dim=128, dtype=dtype,
                                         num_layers=1, device=device)
     m.num_query_heads = 32
     rng = np.random.default_rng(1)
     live, next_id = [], 1
+
+    def finish_some():
+        for k in sorted(rng.choice(len(live), size=8, replace=False), reverse=True):
+            m.free_sequence(live[k][0])
+            del live[k]
+
     for step_no in range(12):
-        if step_no % 3 == 0:  # new requests (more than the pool's first 64 rows, over time)
+        if free_first and step_no % 4 == 3:
+            finish_some()
+        if step_no % 3 == 0 or (free_first and step_no % 4 == 3):
+            # new requests (more than the pool's first 64 rows, over time)
             for _ in range(30):
                 seq = request_mod.Request(next_id, list(range(int(rng.integers(1, 200)))))
                 next_id += 1
                 m.allocate_prefix_blocks(seq)
                 live.append((seq, True))
-        if step_no % 4 == 3:  # some finish
-            for k in sorted(rng.choice(len(live), size=8, replace=False), reverse=True):
-                m.free_sequence(live[k][0])
-                del live[k]
+        if not free_first and step_no % 4 == 3:  # some finish
+            finish_some()
         seqs, starts, counts = [], [], []
         for i, (seq, fresh) in enumerate(live):
             if fresh:
@@ -223,6 +237,35 @@ def test_manager_steps_track_growth_and_reuse(device, dtype, with_gather):
         assert np.array_equal(step.block_tables.cpu().numpy(), want_table), step_no
         _check(step, _expect(starts, counts, lists, 16, step.partition_size, step.prefill_tile))
     assert m.tables.num_rows > 64 or m.tables.width > 64
+
+
+def test_gather_slots_of_a_stale_step_raise(device):
+    """Gather slots built on first read re-run the packing kernel over the
+    pool as it is then: read before the next step on the same pool they
+    equal the oracle's; after a later step freed a row and gave it to a new
+    sequence, reading them raises instead of returning the new row's slots."""
+    m = manager_mod.PagedKVCacheManager(total_blocks=256, block_size=16, num_heads=2, head_dim=64,
+                                        dtype=torch.bfloat16, num_layers=1, device=device)
+    m.num_query_heads = 4
+    a = request_mod.Request(1, list(range(40)))
+    b = request_mod.Request(2, list(range(70)))
+    for seq in (a, b):
+        m.allocate_prefix_blocks(seq)
+    first = m.pack_step([a, b], [0, 0], [40, 70], with_gather=False)
+    lists = [s.block_table.get_physical_blocks() for s in (a, b)]
+    want = op.build_slot_mapping(lists, [40, 70], 16, [0, 0], [40, 70])
+    assert np.array_equal(first.gather_slots.cpu().numpy(), want)
+    second = m.pack_step([a, b], [0, 0], [40, 70], with_gather=False)
+    m.free_sequence(a)
+    c = request_mod.Request(3, list(range(25)))
+    m.allocate_prefix_blocks(c)  # takes a's row
+    third = m.pack_step([b, c], [0, 0], [70, 25], with_gather=False)
+    with pytest.raises(RuntimeError, match="earlier step"):
+        second.gather_slots
+    assert torch.equal(first.gather_slots.cpu(), torch.from_numpy(want))  # built before: kept
+    lists = [s.block_table.get_physical_blocks() for s in (b, c)]
+    want = op.build_slot_mapping(lists, [70, 25], 16, [0, 0], [70, 25])
+    assert np.array_equal(third.gather_slots.cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

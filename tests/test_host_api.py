@@ -9,6 +9,7 @@ the reference's own fallback interface; the HIP path is covered by the GPU
 parity tests.
 """
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -380,6 +381,61 @@ def test_pool_rows_track_block_lists_and_queue_updates():
     assert not rebuild and sorted(upd.tolist()) == [[row, col, -1] for col in range(4)]
     assert (pool.host[row] == -1).all() and pool.tokens[row] == 0
     assert alloc.get_num_free_blocks() == 64 - 1  # b's block only
+
+
+def test_pool_updates_unique_after_release_and_reuse():
+    """A row freed and taken again before the next step queues its -1 resets
+    and then its new blocks for the same (row, col).  The packing kernel
+    stores the triples in no fixed order, so the queue handed over must hold
+    each (row, col) once, with the last value: applied in any order, it
+    turns the previous device copy into the host rows."""
+    rng = np.random.default_rng(3)
+    alloc = alloc_mod.PageAllocator(256, 4, 8, total_cpu_blocks=16)
+    pool = alloc_mod.BlockTablePool(rows=8, width=8)
+    live = [alloc_mod.SequenceBlockTable(alloc, pool) for _ in range(5)]
+    for t in live:
+        t.append_tokens(int(rng.integers(1, 20)))
+    assert pool.take_updates()[0]  # first upload: the whole table
+    device = pool.host.copy()
+    for step in range(40):
+        # free some sequences, then admit new ones: LIFO rows are reused at once
+        for _ in range(int(rng.integers(0, 3))):
+            if live:
+                live.pop(int(rng.integers(0, len(live)))).release()
+        for _ in range(int(rng.integers(0, 3))):
+            t = alloc_mod.SequenceBlockTable(alloc, pool)
+            t.append_tokens(int(rng.integers(1, 12)))
+            live.append(t)
+        if live and step % 5 == 2:  # a swap-style detach: row released and re-acquired
+            t = live[int(rng.integers(0, len(live)))]
+            blocks = t.take_blocks()
+            t.put_blocks(blocks)
+        for t in live:
+            t.append_tokens(int(rng.integers(0, 6)))
+        rebuild, upd = pool.take_updates()
+        if rebuild:
+            device = pool.host.copy()
+            continue
+        keys = upd[:, 0].astype(np.int64) * pool.width + upd[:, 1]
+        assert np.unique(keys).shape[0] == keys.shape[0], f"duplicate (row, col) at step {step}"
+        for order in (upd, upd[::-1], upd[rng.permutation(upd.shape[0])]):
+            got = device.copy()
+            got[order[:, 0], order[:, 1]] = order[:, 2]
+            assert (got == pool.host).all(), f"step {step}"
+        device[upd[:, 0], upd[:, 1]] = upd[:, 2]
+    # a release followed by a reuse of the same row within one step
+    t = live[0]
+    row = t.row
+    t.release()
+    u = alloc_mod.SequenceBlockTable(alloc, pool)
+    assert u.row == row
+    u.append_tokens(5)
+    rebuild, upd = pool.take_updates()
+    assert not rebuild
+    entries = {(r, c): b for r, c, b in upd.tolist()}
+    assert len(entries) == upd.shape[0]
+    for col, block in enumerate(u.get_physical_blocks()):
+        assert entries[(row, col)] == block
 
 
 def test_swap_bookkeeping_matches_reference_messages():

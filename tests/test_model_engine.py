@@ -271,14 +271,22 @@ def _generate(model, prompt, n, device):
     return out[0, len(prompt):].tolist()
 
 
-def run_engine(model, device, prompts, late_prompt, max_tokens, total_blocks=256):
+def run_engine(model, device, prompts, late_prompt, max_tokens, total_blocks=256, block_size=BLOCK_SIZE,
+               scheduler=None, total_cpu_blocks=32):
     """Serve ``prompts`` (and ``late_prompt``, added after the second step so
-    that a prefill shares a step with decodes) through LLMEngine.step()."""
+    that a prefill shares a step with decodes) through LLMEngine.step().
+    ``max_tokens`` is one limit for all or one per prompt (late prompt last);
+    ``scheduler`` builds the scheduler from the store (default: first come,
+    first served).  Returns (requests, steps, store, scheduler)."""
     from fcfs import FcfsScheduler
 
     store = manager_mod.PagedKVCacheManager.from_model_config(
-        model.config, total_blocks=total_blocks, block_size=BLOCK_SIZE, dtype=model.dtype, device=device)
-    engine = engine_mod.LLMEngine(store, FcfsScheduler(store), model=model)
+        model.config, total_blocks=total_blocks, block_size=block_size, dtype=model.dtype, device=device,
+        total_cpu_blocks=total_cpu_blocks)
+    sched = (scheduler or FcfsScheduler)(store)
+    engine = engine_mod.LLMEngine(store, sched, model=model)
+    limits = list(max_tokens) if isinstance(max_tokens, (list, tuple)) else \
+        [max_tokens] * (len(prompts) + (late_prompt is not None))
     calls = {"n": 0}
     forward = model.forward
 
@@ -289,26 +297,32 @@ def run_engine(model, device, prompts, late_prompt, max_tokens, total_blocks=256
     model.forward = counted
     try:
         eos = model.config.eos_token_id  # generate() stops there too
-        reqs = [engine.add_request(p, max_tokens=max_tokens, eos_token_id=eos) for p in prompts]
-        steps = mixed = 0
+        reqs = [engine.add_request(p, max_tokens=n, eos_token_id=eos) for p, n in zip(prompts, limits)]
+        steps = mixed = idle = 0
         late = None
         while engine.has_unfinished_requests():
             if steps == 2 and late_prompt is not None:
-                late = engine.add_request(late_prompt, max_tokens=max_tokens, eos_token_id=eos)
+                late = engine.add_request(late_prompt, max_tokens=limits[-1], eos_token_id=eos)
             before = calls["n"]
             result = engine.step()
             steps += 1
+            if calls["n"] == before:  # nothing was runnable (a request is swapped out)
+                idle += 1
+                assert idle < 8, "the scheduler stalled"
+                continue
             assert calls["n"] == before + 1, "one forward per step"
             if late is not None and late in result["running"] and len(late.output_token_ids) == 1:
                 mixed += 1
     finally:
         model.forward = forward
-    assert engine.forward_passes == steps
+    assert engine.forward_passes == steps - idle
     if late_prompt is not None:
         assert mixed == 1, "the late prompt was prefilled in a step with decodes"
         reqs.append(late)
     assert store.get_allocator().get_num_free_blocks() == total_blocks
-    return reqs, steps
+    assert store.get_allocator().get_num_free_cpu_blocks() == total_cpu_blocks
+    assert all(r.block_table is None for r in reqs)
+    return reqs, steps, store, sched
 
 
 def test_cpu_engine_greedy_matches_generate(monkeypatch):
@@ -316,33 +330,97 @@ def test_cpu_engine_greedy_matches_generate(monkeypatch):
     model = tiny_llama(torch.float32, "cpu")
     prompts = [[5, 9, 2, 7, 1], [3, 3, 8], list(range(40, 75))]
     late = [11, 12, 13, 14]
-    reqs, steps = run_engine(model, "cpu", prompts, late, max_tokens=6)
+    reqs, steps, _, _ = run_engine(model, "cpu", prompts, late, max_tokens=6)
     # the first prompts finish at step 6; the late one, prefilled at step 3, at step 8
     assert steps == 8
     for req, prompt in zip(reqs, prompts + [late]):
         assert req.output_token_ids == _generate(model, prompt, 6, "cpu"), req.seq_id
 
 
-@pytest.mark.gpu
-def test_gpu_engine_greedy_matches_generate(monkeypatch):
-    """The product engine on an HBM store with no backend installed beforehand:
-    it installs the HIP backend itself, never runs dense SDPA, makes one
-    forward per step, and its greedy tokens equal the model's own generate()
-    (fp32 model: HIP decode and fp32 prefill kernels)."""
-    monkeypatch.setattr(paged_attention, "_BACKEND", None)
-
+def _no_dense(monkeypatch):
     def no_dense(*args, **kwargs):
         raise AssertionError("dense SDPA ran on a GPU store")
 
     monkeypatch.setattr(backends, "dense_sdpa", no_dense)
     monkeypatch.setattr(backends.TorchSdpBackend, "attend", no_dense)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("block_size", [1, 4, 16, 32, 64])
+def test_gpu_engine_greedy_matches_generate(monkeypatch, block_size):
+    """The product engine on an HBM store with no backend installed beforehand:
+    it installs the HIP backend itself, never runs dense SDPA, makes one
+    forward per step, and its greedy tokens equal the model's own generate()
+    (fp32 model: HIP decode and fp32 prefill kernels), at the block sizes of
+    the reference's end-to-end sweep (tests/correctness/
+    test_correctness_spec.py:70-142); the pool holds 4096 tokens at each."""
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    _no_dense(monkeypatch)
     model = tiny_llama(torch.float32, "cuda")
     prompts = [list(range(3, 40)), [7, 1, 4], list(range(100, 300)), [11] * 70]
     late = list(range(50, 95))
-    reqs, _ = run_engine(model, "cuda", prompts, late, max_tokens=12)
+    reqs, *_ = run_engine(model, "cuda", prompts, late, max_tokens=12, total_blocks=4096 // block_size,
+                          block_size=block_size)
     assert isinstance(paged_attention._BACKEND, backends.NativePagedBackend)
     for req, prompt in zip(reqs, prompts + [late]):
         assert req.output_token_ids == _generate(model, prompt, 12, "cuda"), req.seq_id
+
+
+# Preempt and resume (tests/correctness/test_correctness_spec.py:236-259):
+# greedy output must not change when the scheduler preempts.  Six requests
+# with staggered limits, so requests finish at different steps and waiting
+# ones are admitted into the rows they free.
+PREEMPT_PROMPTS = [list(range(3, 40)), [7, 1, 4], list(range(100, 160)), [11] * 70, list(range(200, 221)),
+                   [5, 9, 2, 7, 1, 8, 8]]
+PREEMPT_LIMITS = [14, 9, 12, 6, 11, 16]
+
+
+def _preempting(plan, **kw):
+    from fcfs import PreemptingScheduler
+
+    return lambda store: PreemptingScheduler(store, plan=plan, **kw)
+
+
+def _check_preempted_run(model, device, reqs, sched):
+    for req, prompt, n in zip(reqs, PREEMPT_PROMPTS, PREEMPT_LIMITS):
+        assert req.output_token_ids == _generate(model, prompt, n, device), req.seq_id
+
+
+def test_cpu_engine_preempt_recompute_matches_generate(monkeypatch):
+    """Recompute preemption on a CPU store: forced at chosen steps (the
+    request is re-admitted in the same step), and by running out of blocks
+    in a pool too small for every request at once."""
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    model = tiny_llama(torch.float32, "cpu")
+    plan = {3: [(1, "recompute")], 5: [(3, "recompute"), (2, "recompute")], 9: [(1, "recompute")]}
+    reqs, _, _, sched = run_engine(model, "cpu", PREEMPT_PROMPTS, None, PREEMPT_LIMITS, total_blocks=14,
+                                   block_size=8, scheduler=_preempting(plan))
+    assert sched.preempted["recompute"] >= 3 and sched.preempted["oom"] >= 1, sched.preempted
+    _check_preempted_run(model, "cpu", reqs, sched)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("block_size,total_blocks", [(16, 16), (16, 12), (4, 46)])
+def test_gpu_engine_preempt_and_resume_matches_generate(monkeypatch, block_size, total_blocks):
+    """The product engine on an HBM store with requests preempted mid-run,
+    both ways: by recompute (blocks freed, re-prefilled from prompt and
+    outputs through the HIP prefill) and by swap (blocks copied to the
+    pinned host pool, the device blocks reused by others, copied back into
+    fresh blocks two steps later, decoding on).  The pool is too small for
+    every request at once, so requests also get preempted when blocks run
+    out and wait for others to finish.  Every request's greedy tokens equal
+    generate(); device and host blocks all return to the free lists."""
+    monkeypatch.setattr(paged_attention, "_BACKEND", None)
+    _no_dense(monkeypatch)
+    model = tiny_llama(torch.float32, "cuda")
+    plan = {2: [(1, "swap")], 3: [(3, "recompute")], 6: [(2, "swap"), (5, "recompute")], 8: [(1, "recompute")],
+            10: [(6, "swap")]}
+    reqs, _, store, sched = run_engine(model, "cuda", PREEMPT_PROMPTS, None, PREEMPT_LIMITS,
+                                       total_blocks=total_blocks, block_size=block_size,
+                                       scheduler=_preempting(plan), total_cpu_blocks=64)
+    assert sched.preempted["swap"] >= 2 and sched.preempted["recompute"] >= 2, sched.preempted
+    assert sched.preempted["oom"] >= 1, sched.preempted
+    _check_preempted_run(model, "cuda", reqs, sched)
 
 
 @pytest.mark.gpu
@@ -354,7 +432,23 @@ def test_gpu_engine_bf16_long_context(monkeypatch):
     model = tiny_llama(torch.bfloat16, "cuda", head_dim=128)
     torch.manual_seed(7)
     prompt = torch.randint(0, 512, (2500,)).tolist()
-    reqs, _ = run_engine(model, "cuda", [prompt, prompt[:300]], None, max_tokens=4, total_blocks=512)
+    reqs, *_ = run_engine(model, "cuda", [prompt, prompt[:300]], None, max_tokens=4, total_blocks=512)
+    reference = Reference(model, "cuda", None)
+    decisive_total = 0
     for req, p in zip(reqs, [prompt, prompt[:300]]):
         assert 1 <= len(req.output_token_ids) <= 4
         assert req.output_token_ids[0] == _generate(model, p, 1, "cuda")[0]
+        # every generated token, teacher-forced on the engine's own outputs:
+        # where the fp32 copy's top-2 margin is decisive against the model's
+        # own bf16 error on that row, the engine's token is its argmax
+        ids = p + req.output_token_ids
+        exact, own = reference(ids)
+        rows = slice(len(p) - 1, len(ids) - 1)
+        want, err = exact[rows], own[rows]
+        bound = 1.5 * err.max(dim=-1).values + 0.02
+        top2 = torch.topk(want, 2, dim=-1).values
+        decisive = (top2[:, 0] - top2[:, 1]) > 4 * bound
+        got = torch.tensor(req.output_token_ids, device=want.device)
+        assert torch.equal(got[decisive], want.argmax(-1)[decisive]), req.seq_id
+        decisive_total += int(decisive.sum())
+    assert decisive_total >= 1
