@@ -426,17 +426,19 @@ def test_gpu_engine_preempt_and_resume_matches_generate(monkeypatch, block_size,
 @pytest.mark.gpu
 def test_gpu_engine_bf16_long_context(monkeypatch):
     """bf16 GQA heads of 128 with a 2500-token prompt (split-K decode): the
-    engine's first token equals generate()'s, and every step is one forward."""
+    engine's first token equals generate()'s, every step is one forward, and
+    every later token whose top-2 margin is decisive (about one in ten on
+    this random model) is the fp32 model's argmax on the engine's own prefix."""
     monkeypatch.setattr(paged_attention, "_BACKEND", None)
     monkeypatch.setattr(backends, "dense_sdpa", lambda *a, **k: (_ for _ in ()).throw(AssertionError("dense")))
     model = tiny_llama(torch.bfloat16, "cuda", head_dim=128)
     torch.manual_seed(7)
     prompt = torch.randint(0, 512, (2500,)).tolist()
-    reqs, *_ = run_engine(model, "cuda", [prompt, prompt[:300]], None, max_tokens=4, total_blocks=512)
-    reference = Reference(model, "cuda", None)
+    reference = Reference(model, "cuda", None)  # its fp32 copy is taken before the engine hooks the model
+    reqs, *_ = run_engine(model, "cuda", [prompt, prompt[:300]], None, max_tokens=24, total_blocks=512)
     decisive_total = 0
     for req, p in zip(reqs, [prompt, prompt[:300]]):
-        assert 1 <= len(req.output_token_ids) <= 4
+        assert 1 <= len(req.output_token_ids) <= 24
         assert req.output_token_ids[0] == _generate(model, p, 1, "cuda")[0]
         # every generated token, teacher-forced on the engine's own outputs:
         # where the fp32 copy's top-2 margin is decisive against the model's
