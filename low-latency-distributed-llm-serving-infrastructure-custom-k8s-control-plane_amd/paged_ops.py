@@ -301,6 +301,14 @@ class PackedStep:
         self._gather = None
         _run_pack(self, fresh=True)
 
+    def rerun(self) -> None:
+        """Rerun the packing kernels on the inputs the last pack or repack of
+        this step left in its workspace: no host memory is read and nothing
+        is allocated, so a serving loop can capture it in a HIP graph ahead
+        of the layers and change the step with :meth:`repack` between
+        replays."""
+        _run_pack(self)
+
     @property
     def table_width(self) -> int:
         """Row stride of the table the kernels read."""

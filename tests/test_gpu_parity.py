@@ -773,20 +773,23 @@ def _prefill_case(device, hq, hkv, d, dtype):
 
 def test_mixed_step_end_to_end(device):
     """4 x 512-token prefill chunks + 128 long-context decodes: pack, write the
-    step's K/V, attend -- all on the GPU -- then check the K and V cache bytes
-    and the output rows of all 132 sequences against the oracle."""
+    step's K/V, attend -- all on the GPU -- then check the whole K and V
+    pools (the oracle's scatter applied to copies taken before the step:
+    the written slots hold the new rows, every other byte is untouched) and
+    the output rows of all 132 sequences against the oracle."""
     w = wl.mixed_step(seed=5)
     t = wl.make_tensors(w, device, seed=5)
+    before = [c.view(torch.int16).cpu().numpy().view(np.uint16) for c in (t.key_cache, t.value_cache)]
     step = pack_workload(w, device)
     ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
-    slots = torch.from_numpy(op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size,
-                                                   w.start_positions, w.new_token_counts)).to(device)
-    got_k = t.key_cache[0].view(-1, w.num_kv_heads, w.head_dim)[slots]
-    got_v = t.value_cache[0].view(-1, w.num_kv_heads, w.head_dim)[slots]
-    assert torch.equal(got_k.view(torch.int16), t.new_keys.view(torch.int16))
-    assert torch.equal(got_v.view(torch.int16), t.new_values.view(torch.int16))
+    slots = op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size, w.start_positions,
+                                  w.new_token_counts)
+    for want, new, cache in zip(before, (t.new_keys, t.new_values), (t.key_cache, t.value_cache)):
+        op.scatter_layer_kv(want, 0, new.view(torch.int16).cpu().numpy().view(np.uint16), slots)
+        assert np.array_equal(cache.view(torch.int16).cpu().numpy().view(np.uint16), want)
+    del before
     log(f"mixed step: checking rows of all {w.num_seqs} sequences")
     rows = oracle_rows(w, t, range(w.num_seqs))
     assert len(rows) == w.num_seqs and sum(c > 1 for c in w.new_token_counts) == 4
