@@ -186,6 +186,10 @@ size_t pa_pack_workspace_size(int32_t num_seqs);
  *   16-byte aligned),
  *   prefill_items int32 pairs (seq, query tile) for every sequence with more
  *   than one new token (may be NULL).
+ * clear / clear_bytes (may be NULL / 0): a 16-byte aligned region of whole
+ * 16-byte words the first launch sets to zero -- the merge records of the
+ * step's decode workspace (pa_decode_merge_state_size), so the step needs
+ * no separate memset.
  * Writes past a capacity in PaPackDims are dropped, never performed.
  * A block-table entry that is negative or past its row yields slot -1.
  * workspace: pa_pack_workspace_size(B) bytes, 16-byte aligned; calls that
@@ -201,8 +205,9 @@ int pa_pack(int32_t *block_tables, const int32_t *rows, const int32_t *updates,
             int64_t *cu_context_offsets, int32_t *context_lens,
             int64_t *scatter_slots, int64_t *position_ids,
             int64_t *gather_slots, int32_t *decode_items,
-            int32_t *merge_items, int32_t *prefill_items, void *workspace,
-            size_t workspace_bytes, void *stream);
+            int32_t *merge_items, int32_t *prefill_items, void *clear,
+            size_t clear_bytes, void *workspace, size_t workspace_bytes,
+            void *stream);
 
 /* ---- host-side step planning ------------------------------------------- */
 
@@ -324,9 +329,19 @@ int pa_swap_blocks(void *device_cache, void *host_cache,
 
 /* ---- (c) paged-attention decode (split-K) ------------------------------ */
 
-/* Bytes of workspace pa_decode needs for `num_decode_items` work items (the
- * split-K partials).  Calls that share a workspace must not overlap in time. */
+/* Bytes of workspace pa_decode needs for `num_decode_items` work items: the
+ * split-K partials, then the merge records (pa_decode_merge_state_size
+ * bytes at the end of the workspace).  Calls that share a workspace must
+ * not overlap in time. */
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items);
+
+/* Bytes of merge records at the end of a pa_decode workspace of this size
+ * (8 per sequence and decode workgroup of an item; 0 when the workspace is
+ * 0).  They must be zero when a workspace is first used -- pa_pack clears
+ * them when passed as its `clear` region -- and every pa_decode call leaves
+ * them zero.  The rest of the workspace needs no initial value.  (No
+ * counterpart in the reference.) */
+size_t pa_decode_merge_state_size(PaStepDims dims, int64_t num_decode_items);
 
 /* Partition workgroups pa_decode launches per decode work item:
  *  - num_kv_heads / 2 when two adjacent KV heads run as one workgroup
@@ -364,9 +379,14 @@ int32_t pa_decode_workgroups_per_cu(int32_t dtype, int32_t head_dim,
  * (app/model/attention_backends.py:88-117) and the paged_attention kernel
  * it calls, over block tables instead of a dense mask.
  * Runs every (sequence, partition) item of `decode_items` (from pa_pack) for
- * every KV head, then a merge kernel over `merge_items` (from pa_pack)
- * combines the split-K partials of the multi-partition sequences;
- * merge_items may be NULL only when num_merge_items is 0.  The single query token
+ * every KV head in one launch; the split-K partials of a multi-partition
+ * sequence are combined in the same launch by whichever of its partition
+ * workgroups finishes last (counted in the workspace's merge records), or,
+ * for a step of 65535 or more items, by a second launch.
+ * decode_items must list each partition of a sequence once, its full
+ * partitions as consecutive items (as pa_pack writes them).  merge_items
+ * (from pa_pack) serve the separate merge phase; they may be NULL only when
+ * num_merge_items is 0.  The single query token
  * of decode sequence i is flat token cu_seqlens[i]; it attends positions
  * [0, context_lens[i]).  query: [T, H_q, D] through PaStepDims strides;
  * output: [T, H_q, D] contiguous, dtype of the caches; rows of tokens that
@@ -388,14 +408,17 @@ int pa_decode(const void *query, const void *key_cache,
 enum { PA_DECODE_PHASE_PARTITIONS = 1, PA_DECODE_PHASE_MERGE = 2 };
 
 /*
- * pa_decode split in its two launches (same arguments and rules).  The
- * partition phase writes the final rows of single-partition sequences and
- * the split-K partials of the others into `workspace`; the merge phase then
- * combines those partials (a no-op when every sequence fits one partition
- * or the step runs on the generic kernel).  pa_decode(...) equals
+ * pa_decode's two phases (same arguments and rules).  The partition phase
+ * writes the final rows of single-partition sequences and the split-K
+ * partials of the others into `workspace`, and merges those partials in the
+ * same launch; the merge phase alone runs the merge kernel over merge_items,
+ * which combines the partials the last partition phase left (a no-op when
+ * every sequence fits one partition or the step runs on the generic
+ * kernel).  Both merges run the same arithmetic: pa_decode(...) equals
  * pa_decode_phases(PA_DECODE_PHASE_PARTITIONS | PA_DECODE_PHASE_MERGE, ...),
- * and a partition call followed by a merge call on one stream gives the same
- * bits.  No reference counterpart: the reference's decode is one CPU call.
+ * which launches the partition kernel only, and a partition call followed
+ * by a merge call on one stream gives the same bits.  No reference
+ * counterpart: the reference's decode is one CPU call.
  */
 int pa_decode_phases(int32_t phases, const void *query, const void *key_cache,
                      const void *value_cache, int32_t layer_idx, PaStepDims dims,
@@ -443,8 +466,11 @@ int pa_decode_append(const void *query, void *key_cache, void *value_cache,
 
 /* Bytes of the file-scope device array behind pa_decode_no_alloc (64 MiB:
  * the split-K partials of about 4000 decode work items of 32 query heads of
- * 128; pa_decode_workspace_size gives the need of a step). */
+ * 128 -- pa_decode_workspace_size less pa_decode_merge_state_size gives the
+ * need of a step -- in the first 63 MiB, and the merge records in the last
+ * PA_DECODE_SCRATCH_STATE_BYTES). */
 #define PA_DECODE_SCRATCH_BYTES ((size_t)64 << 20)
+#define PA_DECODE_SCRATCH_STATE_BYTES ((size_t)1 << 20)
 
 /*
  * No counterpart in the reference: pa_decode for callers that cannot
@@ -455,12 +481,17 @@ int pa_decode_append(const void *query, void *key_cache, void *value_cache,
  * library runs on holds from its first use until the process ends.  The
  * first call on a device (with that device current) looks up the array's
  * address with hipGetSymbolAddress; no call allocates or frees anything.
- * A step whose partials exceed the array (pa_decode_workspace_size) is
- * rejected with PA_ERR_WORKSPACE and nothing is launched.  The array keeps
- * the last call's contents and nothing in it needs to start at zero: the
- * partition phase writes every partial the merge reads.  Every call on one
- * device shares that device's array, so calls that overlap in time on one
- * device (two streams, two threads) race; serialise them on one stream.
+ * A step whose partials exceed the first PA_DECODE_SCRATCH_BYTES -
+ * PA_DECODE_SCRATCH_STATE_BYTES bytes of the array is rejected with
+ * PA_ERR_WORKSPACE and nothing is launched.  The array keeps the last call's
+ * contents.  Its partials need no initial value (the partition phase writes
+ * every partial a merge reads); its merge records sit at a fixed place, the
+ * last PA_DECODE_SCRATCH_STATE_BYTES, which hold zeros from the load of the
+ * code object on and which every call leaves zero.  A step with more
+ * records than that region holds merges in a second launch instead.  Every
+ * call on one device shares that device's array, so calls that overlap in
+ * time on one device (two streams, two threads) race; serialise them on
+ * one stream.
  */
 int pa_decode_no_alloc(const void *query, const void *key_cache,
                        const void *value_cache, int32_t layer_idx,

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -31,6 +31,7 @@ PA_DECODE_MAX_PARTITION = 4096
 PA_DECODE_PHASE_PARTITIONS = 1
 PA_DECODE_PHASE_MERGE = 2
 PA_DECODE_SCRATCH_BYTES = 64 << 20
+PA_DECODE_SCRATCH_STATE_BYTES = 1 << 20
 PA_SWAP_OUT = 0
 PA_SWAP_IN = 1
 
@@ -45,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "pa_copy_blocks",
     "pa_swap_blocks",
     "pa_decode_workspace_size",
+    "pa_decode_merge_state_size",
     "pa_decode_workgroups_per_item",
     "pa_decode_workgroups_per_cu",
     "pa_prefill_tile",
@@ -170,7 +172,8 @@ _SIGNATURES = {
     "pa_pack_workspace_size": (_sz, [_i32]),
     "pa_pack": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+        [_vp, _vp, _vp, _vp, _vp, PaPackDims, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp, _sz, _vp, _sz, _vp],
     ),
     "pa_plan_step": (ctypes.c_int, [_vp, _vp, _vp, _i32, PaPlanParams, ctypes.POINTER(PaStepPlan)]),
     "pa_calibrate_mfma": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp]),
@@ -182,6 +185,7 @@ _SIGNATURES = {
     "pa_copy_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _vp]),
     "pa_swap_blocks": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _vp]),
     "pa_decode_workspace_size": (_sz, [PaStepDims, _i64]),
+    "pa_decode_merge_state_size": (_sz, [PaStepDims, _i64]),
     "pa_decode_workgroups_per_item": (_i32, [_i32, _i32, _i32, _i32]),
     "pa_decode_workgroups_per_cu": (_i32, [_i32, _i32, _i32, _i32]),
     "pa_prefill_tile": (_i32, [_i32, _i32]),

@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 10; }
+int pa_abi_version(void) { return 11; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -227,8 +227,13 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
             int32_t* step_block_tables, int32_t* step_rows, int64_t* cu_seqlens, int64_t* cu_context_offsets,
             int32_t* context_lens, int64_t* scatter_slots, int64_t* position_ids,
             int64_t* gather_slots, int32_t* decode_items, int32_t* merge_items,
-            int32_t* prefill_items, void* workspace, size_t workspace_bytes, void* stream) {
+            int32_t* prefill_items, void* clear, size_t clear_bytes, void* workspace,
+            size_t workspace_bytes, void* stream) {
   if (dims.num_seqs < 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: negative num_seqs");
+  if (clear_bytes > 0 && (clear == nullptr || !aligned16(clear) || clear_bytes % 16 != 0))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_pack: clear must be a 16-byte aligned region of whole 16-byte words (%zu bytes given)",
+                clear_bytes);
   if (dims.block_size <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_pack: block_size must be positive");
   if (dims.max_blocks_per_seq < 0 || dims.num_table_rows < 0 || dims.num_updates < 0 ||
       dims.step_table_width < 0)
@@ -294,6 +299,8 @@ int pa_pack(int32_t* block_tables, const int32_t* rows, const int32_t* updates,
   a.max_decode_items = decode_items ? dims.max_decode_items : 0;
   a.max_merge_items = merge_items ? dims.max_merge_items : 0;
   a.max_prefill_items = prefill_items ? dims.max_prefill_items : 0;
+  a.clear = static_cast<uint4*>(clear);
+  a.clear_words = static_cast<int64_t>(clear_bytes / 16);
   a.fused = pa::pack_fusable(a, dims.max_new_tokens, dims.max_context) ? 1 : 0;
   return from_hip(pa::launch_pack(a, static_cast<hipStream_t>(stream)), "pa_pack");
 }
@@ -396,24 +403,39 @@ bool decode_pairs(const PaStepDims& d) {
   const int group = d.num_kv_heads > 0 ? d.num_query_heads / d.num_kv_heads : 0;
   return pa::decode_pairs_heads(d.dtype, d.head_dim, d.num_kv_heads, group);
 }
+// Bytes of merge records of a step: 8 per (sequence, decode unit,
+// sub-group), rounded up to 256 bytes.
+size_t merge_state_bytes(const PaStepDims& d) {
+  if (d.num_seqs <= 0 || d.num_kv_heads <= 0 || d.num_query_heads < d.num_kv_heads) return 0;
+  const int group = d.num_query_heads / d.num_kv_heads;
+  const bool pair = decode_pairs(d);
+  const int64_t units = (pair ? d.num_kv_heads / 2 : d.num_kv_heads) *
+                        static_cast<int64_t>(pair ? 1 : pa::decode_sub_groups(group));
+  return (static_cast<size_t>(d.num_seqs) * units * 8 + 255) & ~size_t(255);
+}
 struct DecodeWorkspaceLayout {
-  size_t acc, ml, total;
+  size_t acc, ml, state, total;
 };
-// part_acc [items, H_q, D] fp32 | part_ml [items, H_q, 2] fp32, each
-// rounded up to 256 bytes.
+// part_acc [items, H_q, D] fp32 | part_ml [items, H_q, 2] fp32 | merge
+// records (merge_state_bytes), each rounded up to 256 bytes.
 DecodeWorkspaceLayout decode_workspace_layout(const PaStepDims& dims, int64_t items) {
-  DecodeWorkspaceLayout w{0, 0, 0};
+  DecodeWorkspaceLayout w{0, 0, 0, 0};
   if (items <= 0 || dims.num_query_heads <= 0 || dims.head_dim <= 0) return w;
   const size_t rows = static_cast<size_t>(items) * dims.num_query_heads;
   w.acc = (rows * dims.head_dim * sizeof(float) + 255) & ~size_t(255);
   w.ml = (rows * 2 * sizeof(float) + 255) & ~size_t(255);
-  w.total = w.acc + w.ml;
+  w.state = merge_state_bytes(dims);
+  w.total = w.acc + w.ml + w.state;
   return w;
 }
 }  // namespace
 
 size_t pa_decode_workspace_size(PaStepDims dims, int64_t num_decode_items) {
   return decode_workspace_layout(dims, num_decode_items).total;
+}
+
+size_t pa_decode_merge_state_size(PaStepDims dims, int64_t num_decode_items) {
+  return decode_workspace_layout(dims, num_decode_items).state;
 }
 
 int32_t pa_decode_workgroups_per_item(int32_t dtype, int32_t head_dim, int32_t num_kv_heads,
@@ -520,22 +542,34 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
       return fail(PA_ERR_UNSUPPORTED, "%s: this shape or alignment takes pa_reshape_and_cache + pa_decode", who);
   }
   if (fast) {
-    const size_t need = pa_decode_workspace_size(dims, num_decode_items);
+    const DecodeWorkspaceLayout wl = decode_workspace_layout(dims, num_decode_items);
+    int32_t* merge_state = nullptr;
     if (use_scratch) {
-      if (need > PA_DECODE_SCRATCH_BYTES)
+      // Partials from the start of the array; merge records in its fixed
+      // last PA_DECODE_SCRATCH_STATE_BYTES (zero from the load of the code
+      // object on, and left zero by every launch), so what a call of another
+      // shape left in the partials never reads as a record.
+      const size_t partials = wl.acc + wl.ml;
+      if (partials > PA_DECODE_SCRATCH_BYTES - PA_DECODE_SCRATCH_STATE_BYTES)
         return fail(PA_ERR_WORKSPACE,
                     "%s: %lld decode items need %zu bytes of split-K partials, more than the %zu "
                     "bytes of scratch; use pa_decode with a workspace",
-                    who, static_cast<long long>(num_decode_items), need,
-                    static_cast<size_t>(PA_DECODE_SCRATCH_BYTES));
+                    who, static_cast<long long>(num_decode_items), partials,
+                    static_cast<size_t>(PA_DECODE_SCRATCH_BYTES - PA_DECODE_SCRATCH_STATE_BYTES));
       rc = scratch_address(&workspace, who);
       if (rc != PA_OK) return rc;
       workspace_bytes = PA_DECODE_SCRATCH_BYTES;
+      // More records than the region holds: the merge kernel combines the
+      // partials instead.
+      if (wl.state <= PA_DECODE_SCRATCH_STATE_BYTES)
+        merge_state = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + PA_DECODE_SCRATCH_BYTES -
+                                                 PA_DECODE_SCRATCH_STATE_BYTES);
+    } else {
+      if (workspace == nullptr || workspace_bytes < wl.total)
+        return fail(PA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, wl.total,
+                    workspace_bytes);
+      if (wl.state > 0) merge_state = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + wl.acc + wl.ml);
     }
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(PA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need,
-                  workspace_bytes);
-    const DecodeWorkspaceLayout wl = decode_workspace_layout(dims, num_decode_items);
     pa::DecodeArgs a{};
     a.query = query;
     a.q_token_stride = dims.q_token_stride;
@@ -564,6 +598,9 @@ int decode_phases(const char* who, bool use_scratch, int32_t phases, const void*
     a.group = pair ? 2 * group : group;
     a.sub_groups = pair ? 1 : pa::decode_sub_groups(group);
     a.head_dim = dims.head_dim;
+    // A record's fields hold counts and items below 65535.
+    a.merge_state = num_decode_items < 65535 ? merge_state : nullptr;
+    a.num_seqs = dims.num_seqs;
     if (new_rows != nullptr) {
       a.new_key = new_rows->key;
       a.new_value = new_rows->value;

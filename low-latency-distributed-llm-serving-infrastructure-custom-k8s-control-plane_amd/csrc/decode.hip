@@ -213,6 +213,72 @@ __device__ __forceinline__ float across_groups_max(float x) {
   return max_halves(x);
 }
 
+// One output element of a multi-partition sequence from its split-K
+// partials: partitions 0 .. nfull-1 are items first .. first + nfull - 1,
+// partition nfull (when nparts > nfull) is item rem.  ml / acc address the
+// element's (max, sum) pair and accumulator in item 0; ml_stride / stride
+// step one item.  kMergeBatch partitions per round trip, with a running
+// maximum (the stored maxima are already in the exp2 domain); slots past the
+// last partition read the first one again and get no weight.  Both merge
+// paths (the merge kernel and the in-launch merge of the partition kernel)
+// run this, so they give the same bits.
+constexpr int kMergeBatch = 8;
+
+// Partials read by the in-launch merge are written by workgroups on other
+// XCDs in the same launch: they are stored and loaded as device-scope
+// relaxed atomics, which write through and read past the XCD's L2, so no
+// L2 write-back or invalidate is needed (see the partition kernel's tail).
+__device__ __forceinline__ void store_device(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_device(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, bool DEVICE_LOADS = false>
+__device__ __forceinline__ void merge_partials(const float* ml, const float* acc, int64_t ml_stride, int64_t stride,
+                                               int64_t first, int nfull, int64_t rem, int nparts, T* out) {
+  auto item_of = [&](int p) -> int64_t { return p < nfull ? first + p : rem; };
+  float mx = kScoreFloor, sum = 0.f, o = 0.f;
+  for (int p = 0; p < nparts; p += kMergeBatch) {
+    float mp[kMergeBatch], lp[kMergeBatch], xp[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int64_t it = item_of(p + u < nparts ? p + u : 0);
+      if constexpr (DEVICE_LOADS) {
+        mp[u] = load_device(ml + it * ml_stride);
+        lp[u] = load_device(ml + it * ml_stride + 1);
+        xp[u] = load_device(acc + it * stride);
+      } else {
+        mp[u] = ml[it * ml_stride];
+        lp[u] = ml[it * ml_stride + 1];
+        xp[u] = acc[it * stride];
+      }
+    }
+    float mn = mx;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (u > 0 && p + u >= nparts) {
+        mp[u] = kScoreFloor;
+        lp[u] = 0.f;
+        xp[u] = 0.f;
+      }
+      mn = fmaxf(mn, mp[u]);
+    }
+    const float r = fast_exp2(mx - mn);
+    sum *= r;
+    o *= r;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float w = fast_exp2(mp[u] - mn);
+      sum = fmaf(lp[u], w, sum);
+      o = fmaf(xp[u], w, o);
+    }
+    mx = mn;
+  }
+  store_scalar<T>(out, sum > 0.f ? o / sum : 0.f);
+}
+
 // PAIR: two adjacent real KV heads of D/2 run as one head of D with the G
 // query heads of both (the first G/2 belong to the first real head); every
 // query head reads only its own real head's half of the rows.  QK layout:
@@ -903,11 +969,68 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     if (nparts <= 1) {
       store_scalar<T>(out + i, l > 0.f ? o / l : 0.f);
     } else {
-      pacc[i] = o;
+      store_device(pacc + i, o);
       if (i % ODM == 0) {
         float* pml = a.part_ml + (item * hq + h0 + g) * 2;
-        pml[0] = mx;
-        pml[1] = l;
+        store_device(pml, mx);
+        store_device(pml + 1, l);
+      }
+    }
+  }
+
+  // ---- in-launch split-K merge ---------------------------------------------
+  // The last of a sequence's partition workgroups (for this unit and
+  // sub-group) to finish merges the sequence's partials; no workgroup waits
+  // for another.  The workgroups run on different XCDs, whose L2s are
+  // separate: the partials above are device-scope stores (written through
+  // past the L2), and every wave waits for its stores to complete before
+  // the barrier.  Then one thread adds the workgroup's arrival to the
+  // sequence's 64-bit record with one device-scope atomic: bits 0-15 count
+  // arrivals, bits 16-39 hold 1 + the item of the partial last partition
+  // (added by that workgroup) and bits 40-63 1 + the item of partition 0,
+  // the first of the sequence's full partitions, which pa_pack lists as
+  // consecutive items (added by that workgroup; the host passes records
+  // only for fewer than 65535 items, so every field fits).  The workgroup
+  // whose addition brings the count to nparts has every field in the value
+  // the atomic returns; it resets the record for the next launch (the
+  // records start at zero and every launch leaves them at zero) and merges
+  // as the merge kernel does, with device-scope loads that read past its
+  // L2.  An agent-scope release or acquire fence here instead writes back or
+  // invalidates a whole L2 per workgroup, and made the decode slower than a
+  // second launch.
+  if (nparts > 1 && n > 0 && a.merge_state != nullptr && seq >= 0 && seq < a.num_seqs) {
+    __shared__ int64_t s_merge[3];
+    const int nfull = ctx / a.partition;
+    const bool has_rem = nfull * a.partition < ctx;
+    uint64_t* rec = reinterpret_cast<uint64_t*>(a.merge_state) +
+                    ((static_cast<int64_t>(seq) * hkv + kvh) * a.sub_groups + sg);
+    uint64_t add = 1;
+    if (part == 0) add += static_cast<uint64_t>(item + 1) << 40;
+    if (part == nfull) add += static_cast<uint64_t>(item + 1) << 16;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint64_t now = __hip_atomic_fetch_add(rec, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+      const bool last = static_cast<int>(now & 0xffff) == nparts;
+      if (last) {
+        __hip_atomic_store(rec, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_merge[1] = static_cast<int64_t>(now >> 40) - 1;
+        s_merge[2] = static_cast<int64_t>((now >> 16) & 0xffffff) - 1;
+      }
+      s_merge[0] = last;
+    }
+    __syncthreads();
+    if (s_merge[0]) {
+      const int64_t first = s_merge[1];
+      const int64_t rem = has_rem ? s_merge[2] : -1;
+      const bool ok = first >= 0 && first + nfull <= a.num_items && (!has_rem || (rem >= 0 && rem < a.num_items));
+      if (ok) {
+        for (int i = tid; i < G * ODM; i += kDecodeThreads) {
+          const int g = i / ODM;
+          merge_partials<T, true>(a.part_ml + 2 * (h0 + g), a.part_acc + static_cast<int64_t>(h0) * ODM + i,
+                            2 * static_cast<int64_t>(hq), static_cast<int64_t>(hq) * ODM, first, nfull, rem, nparts,
+                            out + i);
+        }
       }
     }
   }
@@ -919,14 +1042,11 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
 // written by pa_pack, is (first full-partition item, number of full
 // partitions, sequence, item of the partial last partition or -1): the full
 // partitions of a sequence are contiguous items, its partial one sits among
-// the short work at the end.  Every thread owns one output and merges the
-// partitions in one pass with a running maximum (the stored maxima are
-// already in the exp2 domain): no LDS and no barrier, so the only dependent
-// global round trips are the entry and then the partials.  (With several
-// outputs per thread their round trips queued one behind the other: eight
-// heads of 128 at partition 2048 took 19 us.)
-constexpr int kMergeBatch = 8;  // partitions whose partials one round trip loads
-
+// the short work at the end.  Every thread owns one output (merge_partials):
+// no LDS and no barrier, so the only dependent global round trips are the
+// entry and then the partials.  (With several outputs per thread their
+// round trips queued one behind the other: eight heads of 128 at partition
+// 2048 took 19 us.)
 template <typename T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs a, int G, int D) {
   const int hkv = a.num_kv_heads;
@@ -938,53 +1058,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const bool has_rem = e.w >= 0 && e.w < a.num_items;
   const int nparts = nfull + (has_rem ? 1 : 0);
   if (nfull < 0 || nparts <= 1) return;
-  auto item_of = [&](int p) -> int64_t { return p < nfull ? first + p : static_cast<int64_t>(e.w); };
   const int hq = hkv * G;
-  const int64_t stride = static_cast<int64_t>(hq) * D;  // acc elements per item
-  const int64_t ml_stride = 2 * static_cast<int64_t>(hq);
   T* out = reinterpret_cast<T*>(a.output) + (a.cu_seqlens[e.z] * hq + kvh * G) * D;
-  {
-    const int i = static_cast<int>(blockIdx.y) * kDecodeThreads + static_cast<int>(threadIdx.x);
-    if (i >= G * D) return;
-    const int h = kvh * G + i / D;
-    const float* ml = a.part_ml + 2 * h;
-    const float* acc = a.part_acc + static_cast<int64_t>(kvh) * G * D + i;
-    float mx = kScoreFloor, sum = 0.f, o = 0.f;
-    // kMergeBatch partitions per round trip; slots past the last one read
-    // the first partition again and are given no weight.
-    for (int p = 0; p < nparts; p += kMergeBatch) {
-      float mp[kMergeBatch], lp[kMergeBatch], xp[kMergeBatch];
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        const int64_t it = item_of(p + u < nparts ? p + u : 0);
-        mp[u] = ml[it * ml_stride];
-        lp[u] = ml[it * ml_stride + 1];
-        xp[u] = acc[it * stride];
-      }
-      float mn = mx;
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        if (u > 0 && p + u >= nparts) {
-          mp[u] = kScoreFloor;
-          lp[u] = 0.f;
-          xp[u] = 0.f;
-        }
-        mn = fmaxf(mn, mp[u]);
-      }
-      const float r = fast_exp2(mx - mn);
-      sum *= r;
-      o *= r;
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        const float w = fast_exp2(mp[u] - mn);
-        sum = fmaf(lp[u], w, sum);
-        o = fmaf(xp[u], w, o);
-      }
-      mx = mn;
-    }
-    const float r = sum > 0.f ? o / sum : 0.f;
-    store_scalar<T>(out + i, r);
-  }
+  const int i = static_cast<int>(blockIdx.y) * kDecodeThreads + static_cast<int>(threadIdx.x);
+  if (i >= G * D) return;
+  const int h = kvh * G + i / D;
+  merge_partials<T>(a.part_ml + 2 * h, a.part_acc + static_cast<int64_t>(kvh) * G * D + i, 2 * static_cast<int64_t>(hq),
+                    static_cast<int64_t>(hq) * D, first, nfull, has_rem ? e.w : -1, nparts, out + i);
 }
 
 // ---- host-side dispatch ------------------------------------------------
@@ -1007,6 +1087,8 @@ struct LaunchOp {
       if (err != hipSuccess) return err;
     }
     if (!(phases & PA_DECODE_PHASE_MERGE) || merge_grid <= 0) return hipSuccess;
+    // The partition launch merged in place (merge records given).
+    if ((phases & PA_DECODE_PHASE_PARTITIONS) && a.merge_state != nullptr) return hipSuccess;
     // Partials are in the real layout: rows of D/2 when paired; all a.group
     // query heads of a KV head (or pair) merge in one workgroup row.
     constexpr int kOutD = PAIR ? D / 2 : DM;

@@ -52,6 +52,13 @@ struct DecodeArgs {
   int64_t new_value_token_stride;
   int64_t new_value_head_stride;
   int32_t head_dim;  // real head dim (the pair's unit row holds two heads)
+  // Merge records of the in-launch split-K merge, 8 bytes per (sequence,
+  // unit, sub-group): arrivals, first full-partition item, partial item.
+  // Zero before the launch and left zero by it; null (always for 65535 or
+  // more items): the partition phase stores partials only and the merge
+  // kernel combines them.
+  int32_t* merge_state;
+  int32_t num_seqs;  // sequences the records cover
 };
 
 // Generic one-wave-per-(query token, head) attention: any head_dim <= 256,
@@ -127,6 +134,8 @@ struct PackArgs {
   int64_t max_decode_items;
   int64_t max_merge_items;
   int64_t max_prefill_items;
+  uint4* clear;                   // 16-byte words zeroed by the scan kernel (the decode merge records)
+  int64_t clear_words;
 };
 
 struct CacheWriteArgs {

@@ -233,6 +233,9 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(PackArgs a) {
     if (row >= 0 && row < a.num_table_rows && col >= 0 && col < a.block_table_stride)
       a.block_tables[static_cast<int64_t>(row) * a.block_table_stride + col] = a.updates[3 * u + 2];
   }
+  // The region the step's later launches need zeroed (the decode's merge
+  // records); nothing in this launch reads it.
+  for (int64_t w = tid; w < a.clear_words; w += kScanThreads) a.clear[w] = make_uint4(0, 0, 0, 0);
 
   __shared__ Counts s_wave[kScanWaves];
   __shared__ int32_t s_bucket_wave[kScanWaves][kPackBuckets];  // per-chunk counts, then offsets

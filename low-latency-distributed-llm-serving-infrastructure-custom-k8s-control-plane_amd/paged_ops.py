@@ -225,6 +225,7 @@ class PackedStep:
         self._gather = None
         self._extra_ws = None
         self._generation = 0  # the pool's pack count when this step was packed
+        self._merge_state_bytes = 0  # merge records at the end of the decode workspace
 
     # -- addresses and views ---------------------------------------------------
     def ptr(self, name: str) -> int:
@@ -328,26 +329,32 @@ class PackedStep:
             self._gather = _run_pack(self, with_gather=True)
         return self._gather
 
-    def workspace(self, num_query_heads: int, head_dim: int, device: torch.device) -> torch.Tensor:
-        """Decode workspace (split-K partials), reused across the layers of the
-        step; calls that share it must not overlap in time."""
-        need = decode_workspace_bytes(self.num_decode_items, num_query_heads, head_dim)
-        if self._head_shape == (int(num_query_heads), int(head_dim)):
-            return self._view("decode_workspace") if "decode_workspace" not in self.__dict__ \
-                else self.__dict__["decode_workspace"]
-        ws = self._extra_ws
-        if ws is None or ws.numel() < need or ws.device != device:
-            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
-            self._extra_ws = ws
-        return ws
-
-    def workspace_ptr(self, num_query_heads: int, head_dim: int) -> Tuple[int, int]:
-        """(address, bytes) of the decode workspace for these head counts."""
-        if self._head_shape == (int(num_query_heads), int(head_dim)):
+    def workspace_ptr(self, dims: _native.PaStepDims) -> Tuple[int, int]:
+        """(address, bytes) of the decode workspace of a launch with these
+        dims, reused across the layers of the step (calls that share it must
+        not overlap in time): the step's own region when it was sized for
+        these head counts and holds what pa_decode needs, else a zeroed one
+        kept for the step (the merge records at its end must start at zero;
+        every launch leaves them zero)."""
+        lib = _native.load_library()
+        need = int(lib.pa_decode_workspace_size(dims, self.num_decode_items))
+        if self._head_shape == (int(dims.num_query_heads), int(dims.head_dim)):
             off, _, shape = self._layout.fields["decode_workspace"]
-            return self._base + off, shape[0]
-        ws = self.workspace(num_query_heads, head_dim, self.buffer.device)
+            if shape[0] >= need:
+                return self._base + off, shape[0]
+        ws = self._extra_ws
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=self.buffer.device)
+            self._extra_ws = ws
         return ws.data_ptr(), ws.numel()
+
+    def _merge_state_region(self) -> Tuple[Optional[int], int]:
+        """(address, bytes) of the merge records of the step's own decode
+        workspace, which pa_pack clears, or (None, 0)."""
+        if self._merge_state_bytes <= 0:
+            return None, 0
+        off, _, shape = self._layout.fields["decode_workspace"]
+        return self._base + off + shape[0] - self._merge_state_bytes, self._merge_state_bytes
 
 
 def _plan(starts: np.ndarray, counts: np.ndarray, block_size: int, prefill_tile: int, partition_size: int,
@@ -526,6 +533,7 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
         max_prefill_items=step.num_prefill_items,
     )
     ws_off, _, ws_shape = step._layout.fields["pack_workspace"]
+    clear, clear_bytes = step._merge_state_region()
     status = lib.pa_pack(
         table.data_ptr() if table.numel() else None,
         dev + o_rows if pooled and dev else None,
@@ -544,6 +552,8 @@ def _run_pack(step: PackedStep, with_gather: bool = False, updates: Optional[np.
         step.ptr("decode_items"),
         step.ptr("merge_items"),
         step.ptr("prefill_items"),
+        clear,
+        clear_bytes,
         step._base + ws_off,
         ws_shape[0],
         _stream(device),
@@ -644,15 +654,22 @@ def pack_step(
     lib = _native.load_library()
     layout.add("pack_workspace", torch.uint8, (int(lib.pa_pack_workspace_size(b)),))
     head_shape = None
+    ws_bytes = state_bytes = 0
     if head_dim is not None:
         head_shape = (hq, int(head_dim))
-        layout.add("decode_workspace", torch.uint8,
-                   (max(decode_workspace_bytes(int(plan.num_decode_items), hq, int(head_dim)), 1),))
+        # An unknown cache dtype is sized as fp32, whose unpaired KV heads
+        # need the most merge records.
+        ws_dims = _native.PaStepDims(num_seqs=b, num_query_heads=hq, num_kv_heads=int(num_kv_heads),
+                                     head_dim=int(head_dim), dtype=dtype_code(dtype or torch.float32))
+        ws_bytes = int(lib.pa_decode_workspace_size(ws_dims, int(plan.num_decode_items)))
+        state_bytes = int(lib.pa_decode_merge_state_size(ws_dims, int(plan.num_decode_items)))
+        layout.add("decode_workspace", torch.uint8, (max(ws_bytes, 1),))
     buffer = torch.empty(layout.nbytes, dtype=torch.uint8, device=device)
     rows_arr = None if rows is None else np.ascontiguousarray(np.asarray(rows, dtype=np.int32).reshape(-1))
     table_rows = int(block_tables.shape[0]) if block_tables.numel() else 0
     step = PackedStep(buffer, layout, plan, block_size, prefill_tile, block_tables, table_rows, pooled,
                       head_shape, (starts, counts, rows_arr))
+    step._merge_state_bytes = state_bytes  # cleared by every pa_pack of the step
     upd = None if not n_upd else np.ascontiguousarray(updates, dtype=np.int32)
     gather = _run_pack(step, with_gather=with_gather, updates=upd, fresh=True)
     if with_gather:
@@ -796,8 +813,9 @@ def swap_blocks(device_cache: torch.Tensor, host_cache: torch.Tensor, block_mapp
 
 
 def decode_workspace_bytes(num_decode_items: int, num_query_heads: int, head_dim: int) -> int:
-    """Bytes pa_decode needs for its split-K partials: fp32 acc[items, H_q, D]
-    and (max, sum)[items, H_q], each rounded up to 256 bytes."""
+    """Bytes of pa_decode's split-K partials: fp32 acc[items, H_q, D] and
+    (max, sum)[items, H_q], each rounded up to 256 bytes (the workspace adds
+    the merge records, pa_decode_merge_state_size, after them)."""
     if num_decode_items <= 0:
         return 0
     rows = num_decode_items * num_query_heads
@@ -896,7 +914,7 @@ def _checked(query, key_cache, value_cache, step: PackedStep):
 
 
 def _launch_decode(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, phases) -> None:
-    ws_ptr, ws_bytes = step.workspace_ptr(int(q.shape[1]), int(q.shape[2]))
+    ws_ptr, ws_bytes = step.workspace_ptr(dims)
     lib = _native.load_library()
     status = lib.pa_decode_phases(
         int(phases),
@@ -1000,7 +1018,7 @@ def _new_rows(new_key: torch.Tensor, new_value: torch.Tensor, key_cache: torch.T
 
 def _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v) -> int:
     """pa_decode_append; returns its status (PA_ERR_UNSUPPORTED: not fused)."""
-    ws_ptr, ws_bytes = step.workspace_ptr(int(q.shape[1]), int(q.shape[2]))
+    ws_ptr, ws_bytes = step.workspace_ptr(dims)
     rows = _native.PaNewRows(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1))
     lib = _native.load_library()
     return lib.pa_decode_append(

@@ -92,20 +92,24 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == native.PA_ERR_INVALID_ARGUMENT and b"missing" in lib.pa_last_error_message()
     assert lib.pa_copy_blocks(None, None, None, 0, 1, 1, 1, 16, None) == native.PA_OK
     pdims = native.PaPackDims(num_seqs=1, block_size=0, max_blocks_per_seq=1, partition_size=512, prefill_tile=32)
-    args = [None] * 5 + [pdims] + [None] * 11 + [None, 0, None]
+    args = [None] * 5 + [pdims] + [None] * 11 + [None, 0] + [None, 0, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     pdims.block_size = 16
     pdims.step_table_width = 4
     fake = [0x1000 * (i + 1) for i in range(17)]
-    args = fake[:5] + [pdims] + fake[5:16] + [None, 0, None]
+    for clear, nbytes in ((None, 16), (fake[0] + 8, 16), (fake[0], 24)):  # a clear region of whole aligned words
+        args = fake[:5] + [pdims] + fake[5:16] + [clear, nbytes] + [fake[16], 4096, None]
+        assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
+        assert b"clear must be" in lib.pa_last_error_message()
+    args = fake[:5] + [pdims] + fake[5:16] + [None, 0] + [None, 0, None]
     rc = lib.pa_pack(*args)
     assert rc == native.PA_ERR_WORKSPACE and b"workspace of 544 bytes" in lib.pa_last_error_message()
     assert lib.pa_pack_workspace_size(1) == 544 and lib.pa_pack_workspace_size(0) == 512
-    args = fake[:3] + [None, fake[4], pdims] + fake[5:16] + [fake[16], 4096, None]
+    args = fake[:3] + [None, fake[4], pdims] + fake[5:16] + [None, 0] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"both NULL" in lib.pa_last_error_message()
     pdims.num_updates = 2
-    args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:16] + [fake[16], 4096, None]
+    args = [fake[0], fake[1], None] + fake[3:5] + [pdims] + fake[5:16] + [None, 0] + [fake[16], 4096, None]
     assert lib.pa_pack(*args) == native.PA_ERR_INVALID_ARGUMENT
     assert b"2 updates" in lib.pa_last_error_message()
     rows = native.PaNewRows(None, 0x1000, 128, 1024, 128, 1024)
@@ -177,6 +181,29 @@ def test_workspace_size():
     # paired heads keep the real partial layout
     dims = native.PaStepDims(num_query_heads=16, num_kv_heads=4, head_dim=64, dtype=native.PA_DTYPE_BF16)
     assert lib.pa_decode_workspace_size(dims, 77) == ops.decode_workspace_bytes(77, 16, 64)
+    assert lib.pa_decode_merge_state_size(dims, 77) == 0  # no sequences: no merge records
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,units", [
+    (32, 8, 128, "PA_DTYPE_BF16", 4),    # paired KV heads: one record per pair
+    (32, 8, 128, "PA_DTYPE_F32", 8),     # one per KV head
+    (64, 2, 128, "PA_DTYPE_BF16", 2 * 4),  # a group of 32 runs as 4 sub-groups of 8 per KV head
+    (8, 8, 64, "PA_DTYPE_F32", 8),
+])
+def test_merge_state_size(hq, hkv, d, dtype, units):
+    """8 bytes of merge records per (sequence, decode workgroup of an item),
+    rounded up to 256, after the partials; none without decode items."""
+    native = pkg("_native")
+    lib = native.load_library()
+    ops = pkg("paged_ops")
+    for b in (1, 37, 256):
+        dims = native.PaStepDims(num_seqs=b, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
+                                 dtype=getattr(native, dtype))
+        assert lib.pa_decode_workgroups_per_item(dims.dtype, d, hkv, hq) == units
+        state = -(-8 * b * units // 256) * 256
+        assert lib.pa_decode_merge_state_size(dims, 50) == state
+        assert lib.pa_decode_workspace_size(dims, 50) == ops.decode_workspace_bytes(50, hq, d) + state
+        assert lib.pa_decode_workspace_size(dims, 0) == lib.pa_decode_merge_state_size(dims, 0) == 0
 
 
 def test_workgroups_per_item():

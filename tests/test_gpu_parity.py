@@ -441,7 +441,11 @@ def test_pack_step_partition_uses_the_kernel_queries(device):
 
 
 def test_decode_phases_equal_one_call(device):
-    """Partition phase then merge phase (two launches) gives pa_decode's bits."""
+    """The partition phase alone gives pa_decode's bits (its last workgroup
+    per sequence merges in the launch); the merge phase alone, over the
+    partials the partition phase left, rewrites the multi-partition rows
+    with the same bits (the merge kernel runs the same arithmetic) and
+    touches no other row."""
     w = wl.llama3_8b_gqa_decode(seed=2)
     t = wl.make_tensors(w, device, seed=2)
     step = pack_workload(w, device, partition=512)
@@ -449,8 +453,37 @@ def test_decode_phases_equal_one_call(device):
     whole = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     split = torch.zeros_like(whole)
     ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=split, phases=1)
-    ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=split, phases=2)
+    torch.cuda.synchronize()
     assert torch.equal(whole.view(torch.int16), split.view(torch.int16))
+    split.fill_(float("nan"))
+    ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=split, phases=2)
+    torch.cuda.synchronize()
+    merged = torch.tensor([c > 512 for c in w.context_lens], device=device)
+    assert int(merged.sum()) == step.num_merge_items
+    assert torch.equal(whole[merged].view(torch.int16), split[merged].view(torch.int16))
+    assert torch.isnan(split[~merged]).all()
+
+
+def test_decode_with_many_items_merges_in_a_second_launch(device):
+    """A step of 76800 decode items (600 sequences of 4096 tokens, partitions
+    of 32): too many for the merge records' fields, so the partials are
+    merged by a second launch.  Sampled sequences match the oracle, and the
+    same step with partitions of 64 (38400 items, merged inside the
+    partition launch) agrees within the fp32 tolerance."""
+    rng = np.random.Generator(np.random.PCG64(9))
+    b, ctx, bs = 600, 4096, 16
+    perm = rng.permutation(b * ctx // bs)
+    lists = [[int(x) for x in perm[i * ctx // bs : (i + 1) * ctx // bs]] for i in range(b)]
+    w = wl.StepWorkload("many_items", 1, 1, 64, bs, torch.float32, 1.0, [ctx - 1] * b, [1] * b, lists,
+                        b * ctx // bs)
+    t = wl.make_tensors(w, device, seed=9)
+    step = pack_workload(w, device, partition=32)
+    assert step.num_decode_items == b * ctx // 32 >= 65535 and step.num_merge_items == b
+    out = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    other = ops.decode(t.query, t.key_cache, t.value_cache, 0, pack_workload(w, device, partition=64), w.scaling)
+    torch.cuda.synchronize()
+    check_rows(w, out, oracle_rows(w, t, range(0, b, 15)), fp32=True)
+    assert (out - other).abs().max().item() <= FP32_TOL
 
 
 def test_decode_properties_full_size(device):

@@ -66,13 +66,56 @@ def test_no_alloc_decode_equals_pa_decode(device, hq, hkv, d, dtype):
         need = ops.decode_workspace_bytes(step.num_decode_items, hq, d)
         log(f"no_alloc {dtype} {hq}/{hkv}/{d}: B={num_seqs} items={step.num_decode_items} "
             f"merges={step.num_merge_items} partition={step.partition_size} partials={need} B")
-        assert 0 < need <= native.PA_DECODE_SCRATCH_BYTES and step.num_merge_items > 0
+        assert 0 < need <= native.PA_DECODE_SCRATCH_BYTES - native.PA_DECODE_SCRATCH_STATE_BYTES
+        assert step.num_merge_items > 0
         want = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
         got = torch.full_like(want, float("nan"))
         rc = _no_alloc(lib, t, w, step, got)
         native.check(rc, "pa_decode_no_alloc")
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), (seed, num_seqs)
+
+
+def test_no_alloc_with_more_merge_records_than_its_region(device):
+    """10000 sequences of 16 KV heads need 160000 merge records of 8 bytes,
+    more than the array's fixed 1 MiB region holds, while their partials
+    still fit: the merge runs as a second launch.  Every tenth sequence spans
+    two partitions.  The output equals pa_decode's (whose workspace holds
+    every record: merged in the partition launch) bit for bit, and so does
+    that of a smaller step afterwards, which merges in place."""
+    lib = native.load_library()
+    hq = hkv = 16
+    d, dtype, part = 64, torch.float32, 64
+    for seed, num_seqs in ((3, 10000), (4, 300)):
+        rng = np.random.Generator(np.random.PCG64(seed))
+        ctx = [int(rng.integers(part + 1, 2 * part + 1)) if i % 10 == 0 else int(rng.integers(1, part + 1))
+               for i in range(num_seqs)]
+        need = [-(-c // 16) for c in ctx]
+        perm = rng.permutation(sum(need))
+        lists, off = [], 0
+        for n in need:
+            lists.append([int(x) for x in perm[off : off + n]])
+            off += n
+        w = wl.StepWorkload("no_alloc", hq, hkv, d, 16, dtype, 1.0, [c - 1 for c in ctx], [1] * num_seqs,
+                            lists, sum(need))
+        t = wl.make_tensors(w, device, seed=seed)
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        step = ops.pack_step(table, w.start_positions, w.new_token_counts, 16, partition_size=part,
+                             num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+        q = t.query[0].transpose(0, 1)
+        dims = ops._step_dims(q, t.key_cache, step)
+        records = lib.pa_decode_merge_state_size(dims, step.num_decode_items)
+        partials = ops.decode_workspace_bytes(step.num_decode_items, hq, d)
+        log(f"no_alloc records: B={num_seqs} items={step.num_decode_items} records={records} B partials={partials} B")
+        assert step.num_merge_items == -(-num_seqs // 10)
+        assert partials <= native.PA_DECODE_SCRATCH_BYTES - native.PA_DECODE_SCRATCH_STATE_BYTES
+        assert (records > native.PA_DECODE_SCRATCH_STATE_BYTES) == (num_seqs == 10000)
+        want = ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+        got = torch.full_like(want, float("nan"))
+        native.check(_no_alloc(lib, t, w, step, got), "pa_decode_no_alloc")
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), num_seqs
+        del t
 
 
 def test_no_alloc_refuses_steps_beyond_the_scratch(device):
