@@ -4,8 +4,9 @@ Headline workload: Llama-3-8B-shaped GQA decode, bf16 -- 256 sequences, 32
 query / 8 KV heads, head_dim 128, block size 16, contexts
 clip(round(lognormal(ln 1024, 1.0)), 32, 8192), random non-contiguous block
 tables, N(0,1) synthetic values.  A "step" is one decode pass of one layer
-over the batch (the HIP split-K partition kernel + its merge kernel), with
-the batch already packed and resident in HBM.
+over the batch (the HIP split-K partition kernel, which merges the split-K
+partials in the same launch), with the batch already packed and resident in
+HBM.
 
 value    = algorithmic KV-read GB/s = decode bytes / mean step time, where
            decode bytes = sum_i ctx_i * 2 * H_kv * D * 2 (K+V read once per
@@ -34,11 +35,13 @@ Also on the line:
                  tokens/s, the prefill kernel's TFLOP/s against the nominal
                  bf16 MFMA peak and against the rate the device sustains on
                  MFMAs alone, pa_calibrate_mfma), each with its CPU baseline
-                 on a bounded sample;
+                 on a bounded sample, each measured by this script in a
+                 process of its own (its pool the first large allocation of
+                 the process, as a server allocates its KV pool at start-up);
   cpu_baseline   the reference CPU kernel on a bounded sample of the same
                  workload on this host's cores.
 
-python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--calibrate-mfma]
+python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack]
 """
 
@@ -100,6 +103,22 @@ def _kv_of(w, t, i):
     v = t.value_cache[:, blocks].float().cpu().numpy()
     slots = np.arange(len(w.block_lists[i]) * w.block_size, dtype=np.int64)[: w.context_lens[i]]
     return k, v, slots
+
+
+# CPU baselines that take seconds run after every GPU measurement of the
+# process, so that no GPU timing follows seconds of an idle GPU.
+_DEFERRED = []
+
+
+def defer_cpu(fn, into: dict, key: str) -> None:
+    """Run ``fn`` after the GPU measurements; its result goes to into[key]."""
+    _DEFERRED.append((fn, into, key))
+
+
+def run_deferred() -> None:
+    while _DEFERRED:
+        fn, into, key = _DEFERRED.pop(0)
+        into[key] = fn()
 
 
 def cpu_baseline_per_sequence(w, t, budget_s: float, which: str = "decode"):
@@ -441,7 +460,7 @@ def decode_main(args, w, t, device):
     # a few warm-up steps alone do not.  The step is then timed after its W
     # warm-ups.
     kernel_ms = events_ms(
-        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: None,
         lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
         args.steps, max(args.warmup, 500), stream)
     ms = timed_ms(decode_step, args.steps, args.warmup, stream)
@@ -640,7 +659,7 @@ def decode_config_line(args, w, t, device):
     out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
     stream = torch.cuda.current_stream(device)
     kernel_ms = events_ms(
-        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: None,
         lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
         args.steps, 100, stream)
     ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
@@ -654,10 +673,11 @@ def decode_config_line(args, w, t, device):
         "roofline": {"bound": "hbm", "kernel": "decode_partition_kernel",
                      "achieved": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kv_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(w.name),
                      "kernel_ms": round(kernel_ms, 5), "algorithmic_bytes": kv_bytes},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2)
+        defer_cpu(lambda: cpu_baseline_per_sequence(w, t, args.cpu_budget / 2), line, "cpu_baseline")
     return line
 
 
@@ -679,10 +699,12 @@ def mixed_line(args, w, t, device):
     stream = torch.cuda.current_stream(device)
     ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                   args.steps, args.warmup, stream)
+    # 120 untimed launches (about 0.16 s) first: on a GPU that was idle the
+    # first 20 launches averaged 4 % slower than the rest.
     decode_kernel_ms = events_ms(
-        lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=2),
+        lambda: None,
         lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
-        args.steps, 20, stream)
+        args.steps, 120, stream)
     prefill_ms = events_ms(lambda: None,
                            lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                            args.steps, 20, stream)
@@ -706,20 +728,43 @@ def mixed_line(args, w, t, device):
         "decode": {"kernel": "decode_partition_kernel", "kernel_ms": round(decode_kernel_ms, 5),
                    "gbs": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9, 2),
                    "hbm_frac": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                   "algorithmic_bytes": kv_bytes},
+                   "traffic": measured_traffic(w.name), "algorithmic_bytes": kv_bytes},
         "prefill": {"kernel": "prefill_kernel", "gflop": round(pf / 1e9, 2), "kernel_ms": round(prefill_ms, 5),
                     "tflops": round(pf / (prefill_ms * 1e-3) / 1e12, 1),
                     "mfma_frac": round(pf / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "traffic": measured_traffic("mixed_step_prefill"),
                     "mfma_sustained_tflops": round(sustained, 1),
                     "frac_of_sustained": round(pf / (prefill_ms * 1e-3) / 1e12 / sustained, 4)},
     }
     if not args.no_cpu_baseline:
-        dec = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "decode")
-        pre = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "prefill")
-        line["cpu_baseline"] = {"decode": dec, "prefill": pre, "value": dec["value"], "unit": "GB/s",
-                                "cores": dec["cores"], "kind": dec["kind"],
-                                "sample": "decode: " + dec["sample"] + " | prefill: " + pre["sample"]}
+        def both():
+            dec = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "decode")
+            pre = cpu_baseline_per_sequence(w, t, args.cpu_budget / 2, "prefill")
+            return {"decode": dec, "prefill": pre, "value": dec["value"], "unit": "GB/s", "cores": dec["cores"],
+                    "kind": dec["kind"], "sample": "decode: " + dec["sample"] + " | prefill: " + pre["sample"]}
+
+        defer_cpu(both, line, "cpu_baseline")
     return line
+
+
+def config_in_child(args, workload: str) -> dict:
+    """One `configs` line, measured by this script in a process of its own.
+
+    Each workload's pool is then the first large allocation of its process,
+    as a server allocates its KV pool at start-up.  Measured on one box: the
+    mixed step's 8.9 GB pool allocated a second time in one process (freed
+    and allocated again, or after other workloads' tensors) made its decode
+    kernel 1.376-1.379 ms against 1.322 ms for the first allocation; the
+    random 32 KB block reads over the whole pool depend on how it is mapped."""
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--workload", workload, "--steps", str(args.steps),
+           "--warmup", str(args.warmup), "--seed", str(args.seed), "--cpu-budget", str(args.cpu_budget),
+           "--no-configs", "--config-line"]
+    if args.no_cpu_baseline:
+        cmd.append("--no-cpu-baseline")
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900)
+    if proc.returncode != 0:
+        raise RuntimeError(f"bench.py --workload {workload} exited with {proc.returncode}")
+    return json.loads([ln for ln in proc.stdout.splitlines() if ln.startswith("{")][-1])
 
 
 def main() -> int:
@@ -733,6 +778,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="only the headline line, without `configs`")
+    ap.add_argument("--config-line", action="store_true",
+                    help="print the workload's `configs` line (how the headline run measures each config)")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
@@ -770,34 +817,35 @@ def main() -> int:
         return 0
     t = wl.make_tensors(w, device, seed=args.seed)
     if args.workload == "mixed_step":
-        print(json.dumps(mixed_line(args, w, t, device)), flush=True)
+        line = mixed_line(args, w, t, device)
+        if args.config_line:
+            del t
+            torch.cuda.empty_cache()
+            store, seqs = build_store(w, device)
+            line["host_step_us"] = host_step_us(store, seqs, w)
+            del store, seqs
+        run_deferred()
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "llama7b_mha_decode" and args.config_line:
+        line = decode_config_line(args, w, t, device)
+        run_deferred()
+        print(json.dumps(line), flush=True)
         return 0
 
     result = decode_main(args, w, t, device)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_per_sequence(w, t, args.cpu_budget)
+        defer_cpu(lambda t=t: cpu_baseline_per_sequence(w, t, args.cpu_budget), result, "cpu_baseline")
     del t
     if not args.no_configs and args.workload == "llama3_8b_gqa_decode":
-        configs = {}
-        w1 = wl.fp32_mha_decode(seed=args.seed)
-        configs["fp32_mha_decode"] = decode_rotated(args, w1, device)
-        w2 = wl.kv_write_pack(seed=args.seed)
-        configs["kv_write_pack"] = kv_write_pack_line(args, w2, device)
-        torch.cuda.empty_cache()
-        w3 = wl.llama7b_mha_decode(seed=args.seed)
-        t3 = wl.make_tensors(w3, device, seed=args.seed)
-        configs["llama7b_mha_decode"] = decode_config_line(args, w3, t3, device)
-        del t3
-        torch.cuda.empty_cache()
-        w5 = wl.mixed_step(seed=args.seed)
-        t5 = wl.make_tensors(w5, device, seed=args.seed)
-        configs["mixed_step"] = mixed_line(args, w5, t5, device)
-        del t5
-        torch.cuda.empty_cache()
-        store, seqs = build_store(w5, device)
-        result["host_step_us"][w5.name] = host_step_us(store, seqs, w5)
-        del store, seqs
+        # The headline's own CPU baseline first (the children then run with
+        # this process idle), then every config in a process of its own.
+        run_deferred()
+        configs = {name: config_in_child(args, name)
+                   for name in ("fp32_mha_decode", "kv_write_pack", "llama7b_mha_decode", "mixed_step")}
+        result["host_step_us"]["mixed_step"] = configs["mixed_step"].pop("host_step_us")
         result["configs"] = configs
+    run_deferred()
     print(json.dumps(result), flush=True)
     return 0
 
