@@ -228,11 +228,14 @@ hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t st
 hipError_t launch_copy_blocks(const CopyBlocksArgs& a, bool vec16, hipStream_t stream);
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size);
+// Compute units of the current device (cached per device; 0 if unknown): the
+// width of the persistent prefill launches.
+int device_compute_units();
 int prefill_tile_for(int group);
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream);
-// fp32 caches: the VALU kernel of prefill_f32.hip (same items and tile).
 hipError_t launch_prefill256(const PrefillArgs& a, int dtype, int group, int64_t num_items, hipStream_t stream);
+// fp32 caches: the fp32 MFMA kernel of prefill_f32.hip (same units and rows).
 hipError_t launch_prefill_f32(const PrefillArgs& a, int head_dim, int group, int64_t num_items,
                               hipStream_t stream);
 

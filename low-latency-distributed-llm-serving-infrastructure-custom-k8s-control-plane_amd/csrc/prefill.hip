@@ -779,8 +779,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size) {
   // bf16 / fp16: the MFMA kernel below (heads of 80 and 96 on rows of 128)
-  // and prefill256_kernel for heads of 256; fp32: prefill_f32_kernel (VALU),
-  // heads of 64 and 128.
+  // and prefill256_kernel for heads of 256; fp32: prefill_f32_mfma_kernel
+  // (v_mfma_f32_32x32x2_f32), heads of 64 and 128.
   if (dtype != PA_DTYPE_BF16 && dtype != PA_DTYPE_F16 && dtype != PA_DTYPE_F32) return false;
   const bool mfma_dim =
       head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128 || head_dim == 256;
@@ -797,7 +797,7 @@ int prefill_tile_for(int group) {
 }
 
 // Compute units of the current device (cached per device; 0 if unknown).
-static int device_compute_units() {
+int device_compute_units() {
   constexpr int kMaxDevices = 64;
   static std::atomic<int> cached[kMaxDevices];
   int dev = 0;

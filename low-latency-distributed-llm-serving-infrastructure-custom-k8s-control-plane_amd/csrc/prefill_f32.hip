@@ -1,323 +1,364 @@
-// Causal chunked prefill over an fp32 paged cache (VALU, fp32 throughout).
-//
-// The MFMA prefill takes 16-bit caches; this kernel serves fp32 ones with
-// the same work items: one workgroup (4 waves) per (sequence, query tile,
-// KV head, sub-group), 128 query rows = tile tokens x G query heads (row
-// r = g * MTOK + tok, as in the MFMA kernel).  The context is walked in
-// stages of 64 tokens:
-//
-//   1. the stage's K and V rows go from HBM into LDS (each thread moves
-//      16-byte pieces; the block id of a row comes from the block table);
-//   2. scores: thread t owns rows t/8 + 32 i (i < 4) and the stage's tokens
-//      8 j + t%8 (j < 8), and forms its 4 x 8 dot products from 16-byte LDS
-//      reads of q and K (rows padded by 16 bytes: the eight consecutive rows
-//      a wave reads at once fall in different banks);
-//   3. online softmax in base 2 per row (the 8 threads sharing the rows
-//      combine their maxima and sums with DPP), p -> LDS;
-//   4. P x V: the same thread owns the same 4 rows and the head-dimension
-//      elements 32 e + 4 (t%8) .. +3, so the per-row statistics (max, sum,
-//      rescale) never leave the thread and each V read of 8 lanes is one
-//      128-byte run.
+// Causal chunked prefill over an fp32 paged cache, on the matrix cores.
 //
 // Masking follows the reference's block-diagonal causal mask
 // (app/model/paged_attention.py:92-118 applied by SDPA,
 // paged_attention.py:170-178): query token j of a sequence at position
-// start + j attends context positions [0, start + j].
+// start + j attends context positions [0, start + j].  Context positions in
+// a block outside the pool, and every position of a sequence whose table
+// row is outside the table, take no weight.
+//
+#include <algorithm>
+
 #include "pa_common.hpp"
 #include "pa_launch.hpp"
+#include "prefill_common.hpp"
 
 namespace pa {
 
-constexpr int kF32Threads = 256;
-constexpr int kF32Rows = 128;  // query rows per workgroup (as the MFMA kernel)
-constexpr int kF32Stage = 64;  // context tokens per stage
+// Units and rows are those of the 16-bit kernel: a unit is (sequence, query
+// tile, KV head, sub-group) and its 128 query rows are tile tokens x G query
+// heads (row r = g * MTOK + tok).  The products run on
+// v_mfma_f32_32x32x2_f32 (four fp32 products per lane per MFMA; fp32
+// accumulation).  One workgroup of 8 waves per CU walks its share of the
+// units (snake order over the units from the highest item down, as the
+// 16-bit kernel).  Wave w owns query rows [32 (w%4), +32) and
+// the 32-token half w/4 of every 64-token stage; the two waves of a row
+// group merge (max, sum, acc) through LDS at the end.
+//
+//   S^T[t][row] = sum_d K[t][d] Q[row][d]:  A = K (lane l: token l%32, the
+//     head-dim pair 4j + 2(l/32), +1 of an 8-byte LDS read, one per MFMA of
+//     a pair), B = Q (the lane's own row, the same pairs, in 64 registers);
+//   O^T[d][row] += sum_t V^T[d][t] P^T[t][row]:  the context of MFMA j is
+//     taken in the order of the score layout, tokens 8(j/4) + 4(l/32) +
+//     j%4, so that B is the lane's own probability s[j] (no repacking) and
+//     A is V[that token][32 db + l%32], one 4-byte LDS read.
+//
+// Both sums run over every element of the head and of the tile, in another
+// order than the 16-bit kernel (fp32 rounding, within the 1e-4 parity
+// tolerance).  K and V go from HBM straight into LDS (global_load_lds_
+// dwordx4) into unpadded rows with XOR-swizzled 16-byte chunks, two stages
+// in flight (128 KB for heads of 128), one barrier per stage.  Per 32x32
+// tile a wave runs 2 D / 2 MFMAs (64 + 64 for heads of 128) against about 80
+// vector instructions of softmax, so the matrix cores set the pace.
+constexpr int kFmThreads = 512;  // 4 row groups x 2 context halves
+constexpr int kFmRows = 128;     // query rows per unit
+constexpr int kFmTile = 32;      // context tokens per wave per stage
+constexpr int kFmStage = 2 * kFmTile;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f32x4 lds4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-
-// Sum / max over the 8 consecutive lanes of a row block.
-__device__ __forceinline__ float sum8(float x) {
-  x += dpp<kDppQuadXor1>(x);
-  x += dpp<kDppQuadXor2>(x);
-  return x + dpp<kDppRowHalfMirror>(x);
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ float max8(float x) {
-  x = fmaxf(x, dpp<kDppQuadXor1>(x));
-  x = fmaxf(x, dpp<kDppQuadXor2>(x));
-  return fmaxf(x, dpp<kDppRowHalfMirror>(x));
-}
 
-template <int D, int G>
-__global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillArgs a) {
-  constexpr int MTOK = kF32Rows / G;  // query tokens per workgroup
-  constexpr int LD = D + 4;           // padded LDS row (floats)
-  constexpr int DS = D / 8;           // head-dimension slice of a thread in P x V
-  static_assert(DS % 4 == 0, "slices of whole 16-byte pieces");
+template <int D>
+__global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArgs a) {
+  constexpr int ROWB = D * 4;                  // bytes of a K or V row
+  constexpr int CH = D / 4;                    // 16-byte chunks of a row
+  constexpr int DB = D / 32;                   // 32-wide d blocks of the output
+  constexpr int RPC = kWave / CH;              // rows one copy covers
+  constexpr int kWaves = kFmThreads / kWave;
+  constexpr int kCopies = kFmStage / RPC / kWaves;  // copies per wave per tensor and stage
+  constexpr int TBYTES = kFmStage * ROWB;     // one tensor's rows of a stage
+  constexpr int kBufBytes = 2 * TBYTES;        // K, then V
+  constexpr int kMerge = DB * 16 + 4;          // floats a lane hands over (acc, m, l, padding)
+  static_assert(kCopies >= 1 && kCopies * RPC * kWaves == kFmStage, "stage / copy geometry");
+  static_assert(4 * kWave * kMerge * 4 <= 2 * kBufBytes, "the merge fits the stage buffers");
 
-  // K rows of a stage, then (once the scores are formed) its probabilities
-  // p[token][row] in the same space: 132 KB in all for D = 128.
-  constexpr int KP = kF32Stage * LD > kF32Stage * kF32Rows ? kF32Stage * LD : kF32Stage * kF32Rows;
-  __shared__ __attribute__((aligned(16))) float s_q[kF32Rows * LD];
-  __shared__ __attribute__((aligned(16))) float s_kp[KP];
-  __shared__ __attribute__((aligned(16))) float s_v[kF32Stage * LD];
-  __shared__ int s_ok[kF32Stage];  // the stage's token has a block in the pool
-  float* const s_k = s_kp;
-  float* const s_p = s_kp;
+  __shared__ __attribute__((aligned(16))) char s_lds[2 * kBufBytes];
 
+  const int G = a.group / a.sub_groups;
+  const int MTOK = kFmRows / G;
   const int tid = threadIdx.x;
-  const int rb = tid >> 3;  // rows rb + 32 i, i < 4
-  const int c = tid & 7;    // tokens 8 j + c (scores), elements 32 e + 4 c .. (P x V)
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rg = wave & 3;
+  const int kh = wave >> 2;
+  const int t = lane & 31;
+  const int h = lane >> 5;
+  const int row = rg * 32 + t;  // this lane's query row of a unit
+  const int g = row / MTOK;
+  const int tok = row - g * MTOK;
   const int hkv = a.num_kv_heads;
-  // Highest item first: the last query tiles of a sequence see the most context.
-  const int64_t blk_id = static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x;
   const int units = hkv * a.sub_groups;
-  const int64_t item = blk_id / units;
-  const int unit = static_cast<int>(blk_id - item * units);
-  const int kvh = unit / a.sub_groups;
-  const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
-  const int seq = a.items[2 * item];
-  const int qt = a.items[2 * item + 1];
-  const int64_t first = a.cu_seqlens[seq];
-  const int count = static_cast<int>(a.cu_seqlens[seq + 1] - first);
-  const int ctx = a.context_lens[seq];
-  const int start = ctx - count;
-  const int tok0 = qt * MTOK;
-  const int ntok = min(MTOK, count - tok0);
-  if (ntok <= 0) return;
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
-  const int64_t row_elems = static_cast<int64_t>(hkv) * D;  // cache row of one token
-  const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
-  const bool row_ok = trow >= 0 && trow < a.num_table_rows;
-  // A sequence without a table row reads as one block of id -1.  The pointer
-  // stays a global one (a select with a constant array would make every
-  // table read a flat load, which the LDS waits then also wait for).
-  const int32_t* bt = a.block_tables + (row_ok ? trow * a.block_table_stride : 0);
-  const int bt_stride = row_ok ? a.block_table_stride : 1;
-  const float* kbase = reinterpret_cast<const float*>(a.key_cache) + kvh * D;
-  const float* vbase = reinterpret_cast<const float*>(a.value_cache) + kvh * D;
-  const int hq = hkv * a.group;
-
-  // Query rows -> LDS (rows past the tile or past G heads stay zero).
-  for (int i = tid; i < kF32Rows * (D / 4); i += kF32Threads) {
-    const int r = i / (D / 4), q4 = i - r * (D / 4);
-    const int g = r / MTOK, tok = r - g * MTOK;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (tok < ntok && g < G) {
-      const float* qrow = reinterpret_cast<const float*>(a.query) +
-                          (first + tok0 + tok) * a.q_token_stride + static_cast<int64_t>(h0 + g) * a.q_head_stride;
-      v = *reinterpret_cast<const f32x4*>(qrow + 4 * q4);
-    }
-    *reinterpret_cast<f32x4*>(s_q + r * LD + 4 * q4) = v;
-  }
-
-  // This thread's rows: causal limits and liveness.
-  int qpos[4];
-  bool live[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = rb + 32 * i;
-    const int g = r / MTOK, tok = r - g * MTOK;
-    live[i] = tok < ntok && g < G;
-    qpos[i] = start + tok0 + tok;
-  }
-  const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
-  // Positions that have a block-table column (the rest are never read).
-  const int kv_read = static_cast<int>(
-      min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
-  const int nstages = (kv_end + kF32Stage - 1) / kF32Stage;
+  const int64_t row_bytes = static_cast<int64_t>(hkv) * ROWB;  // a cache row of one token
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_lds));
   const float scale = a.scale_log2e;
+  const int hq = hkv * a.group;
+  // Copies: wave w fills rows [8 w, 8 w + 8) of K and of V of a stage, RPC
+  // rows per copy; lane i lands at chunk position i % CH of row i / CH and
+  // fetches the chunk the swizzle puts there.
+  const int crow = lane / CH;
+  const int cpos = lane % CH;
 
-  float m[4], l[4], acc[4][DS];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = kScoreFloor;
-    l[i] = 0.f;
-#pragma unroll
-    for (int e = 0; e < DS; ++e) acc[i][e] = 0.f;
-  }
+  const int U = static_cast<int>(a.num_units);
+  const int W = static_cast<int>(gridDim.x);
+  const int wg = static_cast<int>(blockIdx.x);
+  for (int r = 0;; ++r) {
+    const int rank = (r & 1) ? (r + 1) * W - 1 - wg : r * W + wg;
+    if (rank >= U) break;
+    const int item = (U - 1 - rank) / units;
+    const int unit = (U - 1 - rank) - item * units;
+    const int kvh = unit / a.sub_groups;
+    const int h0 = kvh * a.group + (unit - kvh * a.sub_groups) * G;  // first query head
+    const int seq = a.items[2 * item];
+    const int qt = a.items[2 * item + 1];
+    const int64_t first = a.cu_seqlens[seq];
+    const int count = static_cast<int>(a.cu_seqlens[seq + 1] - first);
+    const int ctx = a.context_lens[seq];
+    const int start = ctx - count;
+    const int tok0 = qt * MTOK;
+    const int ntok = min(MTOK, count - tok0);
+    if (ntok <= 0) continue;  // (the whole workgroup)
+    const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
+    const bool row_ok = trow >= 0 && trow < a.num_table_rows;
+    const int32_t* bt = a.block_tables + (row_ok ? trow * a.block_table_stride : 0);
+    const int bt_stride = row_ok ? a.block_table_stride : 1;
+    const char* kbase = reinterpret_cast<const char*>(a.key_cache) + static_cast<int64_t>(kvh) * ROWB;
+    const char* vbase = reinterpret_cast<const char*>(a.value_cache) + static_cast<int64_t>(kvh) * ROWB;
+    const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
+    // Positions that have a block-table column (the rest are never read).
+    const int kv_read = static_cast<int>(
+        min(static_cast<int64_t>(kv_end), static_cast<int64_t>(bt_stride) << log2_bs));
+    const int kv_last = kv_read - 1;
+    const int nstages = (kv_end + kFmStage - 1) / kFmStage;
+    const bool live = tok < ntok && g < G;
+    const int qpos = start + tok0 + tok;  // causal limit (inclusive)
+    const int lim = min(qpos, kv_last);
 
-  // K and V rows of a stage: each thread's NPT 16-byte pieces of both are
-  // loaded into registers a stage ahead (during the previous stage's
-  // arithmetic) and stored into LDS when the stage starts.  Rows past the
-  // readable context re-read its last row and an out-of-pool block id reads
-  // block 0 (finite values; their scores are masked: such positions are
-  // skipped, as in decode).
-  constexpr int NPT = kF32Stage * (D / 4) / kF32Threads;
-  static_assert(NPT * kF32Threads == kF32Stage * (D / 4), "whole pieces per thread");
-  // The block ids of a stage's rows are loaded one stage earlier still, so
-  // that no copy waits on its table read.
-  f32x4 pk[NPT], pv[NPT];
-  bool pok[NPT];
-  int bid[NPT];
-  auto load_ids = [&](int st) {
+    // Block ids of the rows this lane copies in stage x; -1 without a row.
+    int ids[kCopies];
+    auto load_ids = [&](int x) {
 #pragma unroll
-    for (int j = 0; j < NPT; ++j) {
-      const int r = (tid + j * kF32Threads) / (D / 4);
-      bid[j] = row_ok ? bt[min(st * kF32Stage + r, kv_read - 1) >> log2_bs] : -1;
-    }
-  };
-  auto load_stage = [&](int st) {
+      for (int c = 0; c < kCopies; ++c) {
+        const int p = min(x * kFmStage + kWaves * 0 + 8 * wave + c * RPC + crow, kv_last);
+        ids[c] = row_ok ? bt[p >> log2_bs] : -1;
+      }
+    };
+    // Copies of stage x into buffer b.  Rows past the readable context
+    // re-read its last row and an out-of-pool block reads block 0 (finite
+    // values; their scores are masked).
+    auto issue = [&](int x, int b) {
 #pragma unroll
-    for (int j = 0; j < NPT; ++j) {
-      const int i = tid + j * kF32Threads;
-      const int r = i / (D / 4), q4 = i - r * (D / 4);
-      const int pos = min(st * kF32Stage + r, kv_read - 1);
-      int b = bid[j];
-      const bool in_pool = static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks);
-      pok[j] = in_pool && st * kF32Stage + r < kv_read;
-      b = in_pool ? b : 0;
-      const int64_t off = ((static_cast<int64_t>(b) << log2_bs) + (pos & bs_mask)) * row_elems + 4 * q4;
-      pk[j] = *reinterpret_cast<const f32x4*>(kbase + off);
-      pv[j] = *reinterpret_cast<const f32x4*>(vbase + off);
-    }
-  };
-  load_ids(0);
-  load_stage(0);
-  if (nstages > 1) load_ids(1);
+      for (int c = 0; c < kCopies; ++c) {
+        const int R = 8 * wave + c * RPC + crow;
+        const int p = x * kFmStage + R;
+        const int blk = static_cast<uint32_t>(ids[c]) < static_cast<uint32_t>(a.total_blocks) ? ids[c] : 0;
+        const int pc = min(p, kv_last);
+        const int64_t off = ((static_cast<int64_t>(blk) << log2_bs) + (pc & bs_mask)) * row_bytes +
+                            ((cpos ^ chunk_swizzle<CH>(R)) * 16);
+        const uint32_t dst = lds0 + b * kBufBytes + (8 * wave + c * RPC) * ROWB;
+        dma16(dst, kbase + off);
+        dma16(dst + TBYTES, vbase + off);
+      }
+    };
 
-  for (int st = 0; st < nstages; ++st) {
-    __syncthreads();  // the previous stage's K, V and p are consumed
-    // 1. K and V rows of the stage -> LDS; then the next stage's loads.
+    // ---- prologue: stage 0's copies, the query row, the table scan --------
+    load_ids(0);
+    issue(0, 0);
+    if (nstages > 1) load_ids(1);
+    float2 q[CH];  // the lane's row at head-dim pairs 4 j + 2 h, +1
+    {
+      const float* qrow = reinterpret_cast<const float*>(a.query) +
+                          (first + tok0 + (live ? tok : 0)) * a.q_token_stride +
+                          static_cast<int64_t>(h0 + (live ? g : 0)) * a.q_head_stride + 2 * h;
 #pragma unroll
-    for (int j = 0; j < NPT; ++j) {
-      const int i = tid + j * kF32Threads;
-      const int r = i / (D / 4), q4 = i - r * (D / 4);
-      if (q4 == 0) s_ok[r] = pok[j];
-      *reinterpret_cast<f32x4*>(s_k + r * LD + 4 * q4) = pk[j];
-      *reinterpret_cast<f32x4*>(s_v + r * LD + 4 * q4) = pv[j];
+      for (int j = 0; j < CH; ++j)
+        q[j] = live ? *reinterpret_cast<const float2*>(qrow + 4 * j) : make_float2(0.f, 0.f);
     }
-    if (st + 1 < nstages) {
-      load_stage(st + 1);
-      if (st + 2 < nstages) load_ids(st + 2);
+    // Positions whose block id lies outside the pool are skipped (as in
+    // decode): every wave passes over the row's columns (cached reads) and
+    // ballots whether there are any; such units take the masked path in
+    // every tile.
+    bool bad_ids;
+    {
+      const int ncols = (kv_read + bs_mask) >> log2_bs;
+      bool bad = !row_ok;
+      for (int col = lane; col < ncols && row_ok; col += kWave)
+        bad |= static_cast<uint32_t>(bt[col]) >= static_cast<uint32_t>(a.total_blocks);
+      bad_ids = __builtin_amdgcn_ballot_w64(bad) != 0;
     }
-    __syncthreads();
+    wait_vmcnt<0>();
+    __syncthreads();  // stage 0 has landed
 
-    // 2. scores of rows rb + 32 i x tokens 8 j + c of the stage.
-    float s[4][8];
+    f32x16 acc[DB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s[i][j] = 0.f;
-    for (int d = 0; d < D; d += 4) {
-      f32x4 q[4], k[8];
+      for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
+    float m = kScoreFloor, l = 0.f;  // l: this lane's half of the row sum
+    // The tile of a wave's stage: tokens kh * 32 + [0, 32) of the stage.
+    const int k_row = kh * kFmTile + t;
+    const int k_off = k_row * ROWB + 8 * h;
+    const int k_swz = chunk_swizzle<CH>(k_row);
+
+    for (int st = 0; st < nstages; ++st) {
+      const int b = st & 1;
+      if (st + 1 < nstages) {
+        issue(st + 1, b ^ 1);
+        if (st + 2 < nstages) load_ids(st + 2);
+      }
+      const int p0 = st * kFmStage + kh * kFmTile;  // the tile's first position
+      if (p0 <= kv_last) {  // (wave-uniform: a tile past the context adds nothing)
+        const char* kb = s_lds + b * kBufBytes + k_off;
+        f32x16 s;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) q[i] = lds4(s_q + (rb + 32 * i) * LD + d);
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        // K reads one group of kKGroup pairs ahead of their MFMAs (the
+        // scheduling barriers keep the compiler from hoisting every read,
+        // which needs more registers than a wave has).
+        constexpr int kKGroup = 2;
+        float2 kc[kKGroup], kn[kKGroup];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) k[j] = lds4(s_k + (8 * j + c) * LD + d);
+        for (int u = 0; u < kKGroup; ++u) kc[u] = *reinterpret_cast<const float2*>(kb + ((u ^ k_swz) * 16));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int jj = 0; jj < CH / kKGroup; ++jj) {
+          if (jj + 1 < CH / kKGroup) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          s[i][j] = fmaf(q[i].x, k[j].x, s[i][j]);
-          s[i][j] = fmaf(q[i].y, k[j].y, s[i][j]);
-          s[i][j] = fmaf(q[i].z, k[j].z, s[i][j]);
-          s[i][j] = fmaf(q[i].w, k[j].w, s[i][j]);
+            for (int u = 0; u < kKGroup; ++u)
+              kn[u] = *reinterpret_cast<const float2*>(kb + ((((jj + 1) * kKGroup + u) ^ k_swz) * 16));
+          }
+#pragma unroll
+          for (int u = 0; u < kKGroup; ++u) {
+            s = mfma_f32(kc[u].x, q[jj * kKGroup + u].x, s);
+            s = mfma_f32(kc[u].y, q[jj * kKGroup + u].y, s);
+          }
+#pragma unroll
+          for (int u = 0; u < kKGroup; ++u) kc[u] = kn[u];
+          __builtin_amdgcn_sched_barrier(0);
         }
-    }
-
-    __syncthreads();  // every thread's scores are formed: K's space takes p
-
-    // 3. online softmax per row (8 threads per row block), p -> LDS.
+        // Masks: past the row's causal limit or the readable context, or in
+        // a block outside the pool (the table entry is checked in every
+        // tile that takes masks: the diagonal and end tiles, and every tile
+        // of a unit with such blocks).  The table test stays unconditional
+        // here: gated as `p > lim || (bad_ids && ...)`, this ROCm's hipcc
+        // emitted the -INF write on the `p > lim` path only, and positions in
+        // out-of-pool blocks kept their scores.
+        if (bad_ids || p0 + kFmTile - 1 > min(start + tok0, kv_last)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float tmax = -INFINITY;
+          for (int i = 0; i < 16; ++i) {
+            const int tt = 8 * (i >> 2) + 4 * h + (i & 3);
+            const int p = p0 + tt;
+            if (p > lim || !row_ok || static_cast<uint32_t>(bt[p >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
+              s[i] = -INFINITY;
+          }
+        }
+        float tmax = s[0];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int pos = st * kF32Stage + 8 * j + c;
-        if (pos > qpos[i] || pos >= kv_end || !s_ok[8 * j + c]) s[i][j] = -INFINITY;
-        tmax = fmaxf(tmax, s[i][j]);
+        for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+        tmax = max_halves(tmax);
+        // Lazy rescale: the reference maximum moves only when a tile's
+        // maximum exceeds it by more than kLazyRescale (log2 units).
+        const bool grow = (tmax - m) * scale > kLazyRescale;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = grow ? tmax : m;
+          const float alpha = fast_exp2((m - m_new) * scale);
+          l *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+          m = m_new;
+        }
+        const float msc = m * scale;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s[i] = fast_exp2(fmaf(s[i], scale, -msc));
+          l += s[i];
+        }
+        const char* vb = s_lds + b * kBufBytes + TBYTES;
+        // V^T operand of MFMA j: V[token of score j][32 db + t], read one j ahead.
+        auto read_v = [&](int j, float (&v)[DB]) {
+          const int R = kh * kFmTile + 8 * (j >> 2) + 4 * h + (j & 3);
+          const int sv = chunk_swizzle<CH>(R);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const int d = db * 32 + t;
+            v[db] = *reinterpret_cast<const float*>(vb + R * ROWB + (((d >> 2) ^ sv) * 16) + (d & 3) * 4);
+          }
+        };
+        float vc[DB], vn[DB];
+        read_v(0, vc);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          if (j + 1 < 16) read_v(j + 1, vn);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[db] = mfma_f32(vc[db], s[j], acc[db]);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) vc[db] = vn[db];
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-      const float m_new = fmaxf(m[i], max8(tmax));
-      const float alpha = fast_exp2((m[i] - m_new) * scale);
-      const float msc = m_new * scale;
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        s[i][j] = fast_exp2(fmaf(s[i][j], scale, -msc));
-        psum += s[i][j];
-      }
-      l[i] = l[i] * alpha + sum8(psum);
-#pragma unroll
-      for (int e = 0; e < DS; ++e) acc[i][e] *= alpha;
-      m[i] = m_new;
+      // The next stage's copies have landed and every wave is done with
+      // this stage's buffer (the copies after next refill it).
+      wait_vmcnt<0>();
+      __syncthreads();
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // p[token][rb][i]: a thread's four rows are one 16-byte piece.
-      const f32x4 p = {s[0][j], s[1][j], s[2][j], s[3][j]};
-      *reinterpret_cast<f32x4*>(s_p + (8 * j + c) * kF32Rows + 4 * rb) = p;
-    }
-    __syncthreads();
+    l += __shfl_xor(l, 32, kWave);
 
-    // 4. P x V for rows rb + 32 i and elements 32 e + 4 c ..
-    for (int j = 0; j < kF32Stage; ++j) {
-      const f32x4 p = lds4(s_p + j * kF32Rows + 4 * rb);
+    // ---- merge the two context halves of every row group -------------------
+    {
+      float* region = reinterpret_cast<float*>(s_lds) + (rg * kWave + lane) * kMerge;
+      if (kh == 1) {
 #pragma unroll
-      for (int e4 = 0; e4 < DS / 4; ++e4) {
-        const f32x4 v = lds4(s_v + j * LD + 32 * e4 + 4 * c);
-        acc[0][4 * e4 + 0] = fmaf(p.x, v.x, acc[0][4 * e4 + 0]);
-        acc[0][4 * e4 + 1] = fmaf(p.x, v.y, acc[0][4 * e4 + 1]);
-        acc[0][4 * e4 + 2] = fmaf(p.x, v.z, acc[0][4 * e4 + 2]);
-        acc[0][4 * e4 + 3] = fmaf(p.x, v.w, acc[0][4 * e4 + 3]);
-        acc[1][4 * e4 + 0] = fmaf(p.y, v.x, acc[1][4 * e4 + 0]);
-        acc[1][4 * e4 + 1] = fmaf(p.y, v.y, acc[1][4 * e4 + 1]);
-        acc[1][4 * e4 + 2] = fmaf(p.y, v.z, acc[1][4 * e4 + 2]);
-        acc[1][4 * e4 + 3] = fmaf(p.y, v.w, acc[1][4 * e4 + 3]);
-        acc[2][4 * e4 + 0] = fmaf(p.z, v.x, acc[2][4 * e4 + 0]);
-        acc[2][4 * e4 + 1] = fmaf(p.z, v.y, acc[2][4 * e4 + 1]);
-        acc[2][4 * e4 + 2] = fmaf(p.z, v.z, acc[2][4 * e4 + 2]);
-        acc[2][4 * e4 + 3] = fmaf(p.z, v.w, acc[2][4 * e4 + 3]);
-        acc[3][4 * e4 + 0] = fmaf(p.w, v.x, acc[3][4 * e4 + 0]);
-        acc[3][4 * e4 + 1] = fmaf(p.w, v.y, acc[3][4 * e4 + 1]);
-        acc[3][4 * e4 + 2] = fmaf(p.w, v.z, acc[3][4 * e4 + 2]);
-        acc[3][4 * e4 + 3] = fmaf(p.w, v.w, acc[3][4 * e4 + 3]);
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<float4*>(region + db * 16 + 4 * q4) =
+                make_float4(acc[db][4 * q4], acc[db][4 * q4 + 1], acc[db][4 * q4 + 2], acc[db][4 * q4 + 3]);
+        *reinterpret_cast<float4*>(region + DB * 16) = make_float4(m, l, 0.f, 0.f);
       }
-    }
-  }
-
-  // Normalised rows out ([T, H_q, D]).
+      __syncthreads();
+      if (kh == 0) {
+        const float4 ml = *reinterpret_cast<const float4*>(region + DB * 16);
+        const float mm = fmaxf(m, ml.x);
+        const float a1 = fast_exp2((m - mm) * scale);
+        const float a2 = fast_exp2((ml.x - mm) * scale);
+        const float lt = l * a1 + ml.y * a2;
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        float* orow = reinterpret_cast<float*>(a.output) +
+                      ((first + tok0 + tok) * hq + h0 + g) * static_cast<int64_t>(D) + 4 * h;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (!live[i]) continue;
-    const int r = rb + 32 * i;
-    const int g = r / MTOK, tok = r - g * MTOK;
-    const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
-    float* orow = reinterpret_cast<float*>(a.output) +
-                  ((first + tok0 + tok) * hq + h0 + g) * static_cast<int64_t>(D) + 4 * c;
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int e4 = 0; e4 < DS / 4; ++e4) {
-      const f32x4 o = {acc[i][4 * e4] * inv, acc[i][4 * e4 + 1] * inv, acc[i][4 * e4 + 2] * inv,
-                       acc[i][4 * e4 + 3] * inv};
-      *reinterpret_cast<f32x4*>(orow + 32 * e4) = o;
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 o2 = *reinterpret_cast<const float4*>(region + db * 16 + 4 * q4);
+            const float4 o = make_float4((acc[db][4 * q4] * a1 + o2.x * a2) * inv,
+                                         (acc[db][4 * q4 + 1] * a1 + o2.y * a2) * inv,
+                                         (acc[db][4 * q4 + 2] * a1 + o2.z * a2) * inv,
+                                         (acc[db][4 * q4 + 3] * a1 + o2.w * a2) * inv);
+            // elements 32 db + 8 q4 + 4 h .. + 3 of the row
+            if (live) *reinterpret_cast<float4*>(orow + db * 32 + 8 * q4) = o;
+          }
+      }
+      // The next unit's copies overwrite the merge scratch.
+      __syncthreads();
     }
   }
 }
 
 template <int D>
-static hipError_t launch_prefill_f32_d(const PrefillArgs& a, int group, int64_t num_items,
-                                       hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(num_items * a.num_kv_heads * a.sub_groups));
-  switch (group / a.sub_groups) {
-    case 1: hipLaunchKernelGGL((prefill_f32_kernel<D, 1>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((prefill_f32_kernel<D, 2>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((prefill_f32_kernel<D, 3>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((prefill_f32_kernel<D, 4>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((prefill_f32_kernel<D, 5>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((prefill_f32_kernel<D, 6>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((prefill_f32_kernel<D, 7>), grid, dim3(kF32Threads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((prefill_f32_kernel<D, 8>), grid, dim3(kF32Threads), 0, s, a); break;
-    default: return hipErrorNotSupported;
-  }
+static hipError_t launch_prefill_f32_mfma(const PrefillArgs& args, int group, int64_t num_items,
+                                          hipStream_t s) {
+  const int g = group / args.sub_groups;
+  if (g < 1 || g > 8) return hipErrorNotSupported;
+  PrefillArgs a = args;
+  a.num_units = num_items * a.num_kv_heads * a.sub_groups;
+  // Unit ranks are 32-bit and a workgroup's ranks reach about twice the count.
+  if (a.num_units > (int64_t{1} << 30)) return hipErrorInvalidValue;
+  // One workgroup per CU (the stage buffers hold one per CU), each looping
+  // over its share of the units; fewer units than CUs run one each.
+  const int cus = device_compute_units();
+  const int64_t wgs = cus > 0 ? std::min<int64_t>(a.num_units, cus) : a.num_units;
+  hipLaunchKernelGGL((prefill_f32_mfma_kernel<D>), dim3(static_cast<uint32_t>(wgs)), dim3(kFmThreads), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_prefill_f32(const PrefillArgs& a, int head_dim, int group, int64_t num_items,
                               hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
-  if (head_dim == 128) return launch_prefill_f32_d<128>(a, group, num_items, stream);
-  if (head_dim == 64) return launch_prefill_f32_d<64>(a, group, num_items, stream);
+  if (head_dim == 128) return launch_prefill_f32_mfma<128>(a, group, num_items, stream);
+  if (head_dim == 64) return launch_prefill_f32_mfma<64>(a, group, num_items, stream);
   return hipErrorNotSupported;
 }
 

@@ -587,7 +587,10 @@ def test_prefill_fp16_matches_oracle(device, hq, hkv, d):
 @pytest.mark.parametrize("hq,hkv,d,dtype,bs", [(32, 8, 128, torch.bfloat16, 16), (16, 2, 64, torch.float16, 16),
                                               (32, 8, 128, torch.bfloat16, 4), (24, 4, 96, torch.bfloat16, 32),
                                               # a group of 16: two sub-group units per item and KV head
-                                              (32, 2, 128, torch.bfloat16, 16)])
+                                              (32, 2, 128, torch.bfloat16, 16),
+                                              # fp32 on the matrix cores, blocks of 16, 1 and 4
+                                              (32, 8, 128, torch.float32, 16), (16, 4, 128, torch.float32, 1),
+                                              (16, 2, 64, torch.float32, 4)])
 def test_prefill_many_units_matches_oracle(device, hq, hkv, d, dtype, bs):
     """Several times more (query tile, KV head) units than CUs, of ragged
     lengths and starts, with decodes mixed in: each prefill workgroup walks
@@ -609,12 +612,13 @@ def test_prefill_many_units_matches_oracle(device, hq, hkv, d, dtype, bs):
     assert units > 2 * cus
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
-    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=dtype == torch.float32)
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 64), (32, 2, 128), (9, 3, 64)])
 def test_prefill_fp32_matches_oracle(device, hq, hkv, d):
-    """fp32 caches prefill on the VALU kernel (fp32 throughout), to 1e-4."""
+    """fp32 caches prefill on the fp32 MFMA kernel (fp32 products and
+    accumulation throughout), to 1e-4."""
     _prefill_case(device, hq, hkv, d, torch.float32)
 
 
