@@ -41,8 +41,13 @@ Also on the line:
   cpu_baseline   the reference CPU kernel on a bounded sample of the same
                  workload on this host's cores.
 
+--workload prefill_shapes prints one line of the prefill kernel alone on
+prefill-only steps of four 512-token chunks (32/8 heads, D=128, bf16 and
+fp32), each against its dtype's dense MFMA peak (--shape NAME: one of them).
+
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
-                [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack]
+                [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
+                            prefill_shapes]
 """
 
 from __future__ import annotations
@@ -62,6 +67,7 @@ PACKAGE = "low-latency-distributed-llm-serving-infrastructure-custom-k8s-control
 METRIC = "paged-attn decode KV-read GB/s (% HBM peak) + decode tokens/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 MALL_BYTES = 256 << 20
 
 
@@ -747,6 +753,42 @@ def mixed_line(args, w, t, device):
     return line
 
 
+def prefill_shapes_line(args, device):
+    """The prefill kernel alone on each prefill-only step of PREFILL_SHAPES:
+    HIP-event time per launch, TFLOP/s (4 H_q D (n s + n(n+1)/2) per chunk)
+    and the fraction of the dtype's dense MFMA peak."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    stream = torch.cuda.current_stream(device)
+    shapes = {}
+    for name, (starts, counts, dtype) in wl.PREFILL_SHAPES.items():
+        if args.shape is not None and name != args.shape:
+            continue
+        w = wl.prefill_chunks(name, starts, counts, dtype, seed=args.seed)
+        t = wl.make_tensors(w, device, seed=args.seed)
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                             prefill_tile=ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads),
+                             num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
+                             head_dim=w.head_dim, dtype=w.dtype)
+        out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+        ms = events_ms(lambda: None,
+                       lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                       args.steps, 20, stream)
+        pf = wl.prefill_flops(w)
+        peak = MFMA_F32_PEAK_TFLOPS if dtype == torch.float32 else MFMA_BF16_PEAK_TFLOPS
+        tf = pf / (ms * 1e-3) / 1e12
+        shapes[name] = {"starts": list(starts), "counts": list(counts), "dtype": str(dtype).replace("torch.", ""),
+                        "gflop": round(pf / 1e9, 2), "kernel_ms": round(ms, 5), "tflops": round(tf, 1),
+                        "peak_tflops": peak, "mfma_frac": round(tf / peak, 4)}
+        del t, out, step, table
+        torch.cuda.empty_cache()
+    return {"workload": "prefill_shapes", "heads": [32, 8], "head_dim": 128, "block_size": wl.BLOCK_SIZE,
+            "steps": args.steps, "shapes": shapes}
+
+
 def config_in_child(args, workload: str) -> dict:
     """One `configs` line, measured by this script in a process of its own.
 
@@ -774,8 +816,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3_8b_gqa_decode",
                     choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step", "fp32_mha_decode",
-                             "kv_write_pack"])
+                             "kv_write_pack", "prefill_shapes"])
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--shape", default=None, help="prefill_shapes: measure only this shape")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="only the headline line, without `configs`")
     ap.add_argument("--config-line", action="store_true",
@@ -808,6 +851,9 @@ def main() -> int:
                           "mfma_tflops_with_fp32_fmas_per_mfma": mixed}), flush=True)
         return 0
 
+    if args.workload == "prefill_shapes":
+        print(json.dumps(prefill_shapes_line(args, device)), flush=True)
+        return 0
     w = wl.WORKLOADS[args.workload](seed=args.seed)
     if args.workload == "kv_write_pack":
         print(json.dumps(kv_write_pack_line(args, w, device)), flush=True)

@@ -17,6 +17,9 @@ as a seeded permutation of the pool's block ids.  Shapes and distributions:
   mixed_step            4 prefill chunks x 512 tokens at starts
                         {0, 512, 1024, 1536} + 128 decode seqs with ctx ~
                         U{512..32768}, 32/8 heads, D=128, bf16
+  PREFILL_SHAPES        prefill-only steps of four 512-token chunks (at
+                        {0, 512, 1024, 1536} or all at 4096), 32/8 heads,
+                        D=128, bf16 and fp32
 
 Lengths and block tables come from numpy's PCG64 generator; tensor values
 are drawn with torch (on the target device for the large pools).
@@ -146,6 +149,27 @@ def mixed_step(seed: int = 0) -> StepWorkload:
     ctx = [s + c for s, c in zip(starts, counts)]
     lists, total = _block_tables(rng, ctx, BLOCK_SIZE)
     return StepWorkload("mixed_step", 32, 8, 128, BLOCK_SIZE, torch.bfloat16, 1.0, starts, counts, lists, total)
+
+
+def prefill_chunks(name: str, starts: List[int], counts: List[int], dtype: torch.dtype, num_query_heads: int = 32,
+                   num_kv_heads: int = 8, head_dim: int = 128, seed: int = 0) -> StepWorkload:
+    """A prefill-only step: one chunk of ``counts[i]`` tokens at ``starts[i]``
+    per sequence, over a pool of exactly the blocks the contexts need."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    ctx = [s + c for s, c in zip(starts, counts)]
+    lists, total = _block_tables(rng, ctx, BLOCK_SIZE)
+    return StepWorkload(name, num_query_heads, num_kv_heads, head_dim, BLOCK_SIZE, dtype, 1.0, list(starts),
+                        list(counts), lists, total)
+
+
+# Prefill kernel shapes (32/8 heads, D=128, 512-token chunks): the mixed
+# step's four chunks and four chunks deep in their contexts, in both dtypes.
+PREFILL_SHAPES = {
+    "chunks_0_512_1024_1536_bf16": ([0, 512, 1024, 1536], [512] * 4, torch.bfloat16),
+    "chunks_at_4096_bf16": ([4096] * 4, [512] * 4, torch.bfloat16),
+    "chunks_0_512_1024_1536_fp32": ([0, 512, 1024, 1536], [512] * 4, torch.float32),
+    "chunks_at_4096_fp32": ([4096] * 4, [512] * 4, torch.float32),
+}
 
 
 WORKLOADS = {
