@@ -43,7 +43,8 @@ Also on the line:
 
 --workload prefill_shapes prints one line of the prefill kernel alone on
 prefill-only steps of four 512-token chunks (32/8 heads, D=128, bf16 and
-fp32), each against its dtype's dense MFMA peak (--shape NAME: one of them).
+fp32), each against its dtype's dense MFMA peak, and the same launch writing
+the chunks' new K/V rows (--shape NAME: one of them).
 
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
@@ -689,9 +690,10 @@ def decode_config_line(args, w, t, device):
 
 def mixed_line(args, w, t, device):
     """The mixed step: four 512-token prefill chunks + 128 long-context decodes in one
-    flattened step: the attention step (prefill + split-K decode), the whole
-    step with packing and the K/V write, the decode kernel's GB/s, and the
-    prefill kernel's TFLOP/s against the bf16 MFMA peak."""
+    flattened step: the attention step (prefill + split-K decode), the same
+    step writing the new K/V rows inside its launches, the whole step with
+    packing, the decode kernel's GB/s, and the prefill kernel's TFLOP/s
+    against the bf16 MFMA peak."""
     import torch
 
     ops = pkg("paged_ops")
@@ -723,12 +725,34 @@ def mixed_line(args, w, t, device):
                       new_value=t.new_values)
 
     full_ms = timed_ms(whole, max(5, args.steps // 2), 2, stream)
+    # The attention step writing the new K/V rows inside its launches
+    # (pa_prefill_append + pa_decode_append), on the packed step.
+    write_ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
+                                              new_key=t.new_keys, new_value=t.new_values),
+                        args.steps, args.warmup, stream)
+    if step.__dict__.get("_no_append"):
+        raise RuntimeError("the mixed step did not take the fused K/V writes")
+    # What the K/V write and the packing add to the attention step, each
+    # timed in alternation with it (the decode kernel's time drifts by about
+    # 1 % between loops run seconds apart, more than the differences).
+    def attention_only():
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+
+    def with_write():
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, new_key=t.new_keys,
+                      new_value=t.new_values)
+
+    pair_steps = max(5, args.steps // 2)
+    att1, wr1 = paired_ms(attention_only, with_write, pair_steps, stream)
+    att2, full2 = paired_ms(attention_only, whole, pair_steps, stream)
     sustained = sustained_mfma_tflops(device)
     kv_bytes = wl.decode_bytes(w)
     pf = wl.prefill_flops(w)
     line = {
         "value": round(w.num_query_tokens / (ms * 1e-3), 1), "unit": "tokens/s",
-        "ms_per_step": round(ms, 5), "full_step_ms": round(full_ms, 5),
+        "ms_per_step": round(ms, 5), "with_kv_write_ms": round(write_ms, 5), "full_step_ms": round(full_ms, 5),
+        "paired": {"kv_write_us": round((wr1 - att1) * 1e3, 2), "pack_and_kv_write_us": round((full2 - att2) * 1e3, 2),
+                   "attention_ms": round(att1, 5), "with_kv_write_ms": round(wr1, 5), "full_step_ms": round(full2, 5)},
         "full_step_tokens_per_s": round(w.num_query_tokens / (full_ms * 1e-3), 1), "dtype": "bf16",
         "partition": step.partition_size, "config": workload_config(w),
         "decode": {"kernel": "decode_partition_kernel", "kernel_ms": round(decode_kernel_ms, 5),
@@ -777,12 +801,20 @@ def prefill_shapes_line(args, device):
         ms = events_ms(lambda: None,
                        lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                        args.steps, 20, stream)
+        # The same launch writing the chunks' new K/V rows (pa_prefill_append).
+        app_ms = events_ms(lambda: None,
+                           lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
+                                                 new_key=t.new_keys, new_value=t.new_values),
+                           args.steps, 20, stream)
+        if step.__dict__.get("_no_append"):
+            raise RuntimeError(f"{name}: the prefill did not take the fused write")
         pf = wl.prefill_flops(w)
         peak = MFMA_F32_PEAK_TFLOPS if dtype == torch.float32 else MFMA_BF16_PEAK_TFLOPS
         tf = pf / (ms * 1e-3) / 1e12
         shapes[name] = {"starts": list(starts), "counts": list(counts), "dtype": str(dtype).replace("torch.", ""),
                         "gflop": round(pf / 1e9, 2), "kernel_ms": round(ms, 5), "tflops": round(tf, 1),
-                        "peak_tflops": peak, "mfma_frac": round(tf / peak, 4)}
+                        "peak_tflops": peak, "mfma_frac": round(tf / peak, 4),
+                        "append_kernel_ms": round(app_ms, 5)}
         del t, out, step, table
         torch.cuda.empty_cache()
     return {"workload": "prefill_shapes", "heads": [32, 8], "head_dim": 128, "block_size": wl.BLOCK_SIZE,

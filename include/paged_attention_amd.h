@@ -440,7 +440,7 @@ typedef struct {
 } PaNewRows;
 
 /*
- * Replaces, for a step whose every sequence has one new token (or none):
+ * Replaces, for the single-token sequences of a step:
  * scatter_layer_kv (app/memory/manager.py:150-168, called at
  * app/model/paged_attention.py:152-154) followed by the decode attention
  * (attention_backends.py:88-117) -- pa_reshape_and_cache + pa_decode in the
@@ -449,8 +449,9 @@ typedef struct {
  * table gives position context_len - 1 (bit-exact, as pa_reshape_and_cache
  * writes them; an out-of-pool block id writes nothing), then attend; no
  * other workgroup reads that position.  Rows of sequences with more than
- * one new token are NOT written: use pa_reshape_and_cache for a step with
- * prefill tokens.  Arguments as pa_decode, with writable caches.
+ * one new token are NOT written: for a step with prefill tokens,
+ * pa_prefill_append writes those (or pa_reshape_and_cache writes every
+ * row first).  Arguments as pa_decode, with writable caches.
  * PA_ERR_UNSUPPORTED (nothing launched) for a shape or alignment the fused
  * path does not take (16-byte aligned rows and strides, the tuned decode's
  * shapes): the caller then writes with pa_reshape_and_cache and calls
@@ -519,6 +520,36 @@ int pa_prefill(const void *query, const void *key_cache,
                const int64_t *cu_seqlens, const int32_t *prefill_items,
                int64_t num_prefill_items, int32_t prefill_tile, float scaling,
                void *output, void *stream);
+
+/*
+ * Replaces, for the multi-token sequences of a step: scatter_layer_kv
+ * (app/memory/manager.py:150-168, called at app/model/paged_attention.py:
+ * 152-154) followed by the prefill attention (paged_attention.py:165-180)
+ * -- pa_reshape_and_cache of those sequences' rows + pa_prefill in one
+ * launch.  Each (item, KV head) unit of query-head sub-group 0 writes the
+ * rows of its own tile's tokens for its KV head into the cache at the slots
+ * their block table gives (bit-exact, as pa_reshape_and_cache writes them;
+ * a position without a table column or in a block outside the pool writes
+ * nothing), and every unit reads the positions at or after its sequence's
+ * chunk start (context_len - count) from new_rows rather than the cache,
+ * so no unit reads a row that another one writes.  The rows of the other
+ * sequences of the step (single-token ones: pa_decode_append writes those)
+ * are NOT written, nor those of tokens whose tiles are not in
+ * prefill_items.  A slot is assumed to be written by at most one position
+ * of the step and read by no other sequence of it (the allocator's
+ * copy-on-write keeps shared blocks full and read-only).  Arguments as
+ * pa_prefill, with writable caches.  PA_ERR_UNSUPPORTED (nothing launched)
+ * for a shape the fused path does not take (heads of 256, the generic
+ * kernel's shapes, rows or strides that are not 16-byte multiples, token
+ * strides of 16 MiB or more): the caller then writes with
+ * pa_reshape_and_cache and calls pa_prefill.
+ */
+int pa_prefill_append(const void *query, void *key_cache, void *value_cache,
+                      int32_t layer_idx, PaStepDims dims, PaNewRows new_rows,
+                      const int32_t *block_tables, const int32_t *context_lens,
+                      const int64_t *cu_seqlens, const int32_t *prefill_items,
+                      int64_t num_prefill_items, int32_t prefill_tile,
+                      float scaling, void *output, void *stream);
 
 /* ---- utilities ------------------------------------------------------------ */
 

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode_no_alloc",
     "pa_decode_append",
     "pa_prefill",
+    "pa_prefill_append",
     "pa_map_host_memory",
     "pa_calibrate_mfma",
     "pa_calibrate_mfma_flops",
@@ -209,6 +210,10 @@ _SIGNATURES = {
     "pa_prefill": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i32, PaStepDims, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
+    ),
+    "pa_prefill_append": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i32, PaStepDims, PaNewRows, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
     ),
     "pa_map_host_memory": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "pa_error_string": (ctypes.c_char_p, [ctypes.c_int]),

@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 11; }
+int pa_abi_version(void) { return 12; }
 
 const char* pa_error_string(int code) {
   switch (code) {
@@ -687,25 +687,30 @@ int pa_decode_no_alloc(const void* query, const void* key_cache, const void* val
                        output, nullptr, 0, stream);
 }
 
-int pa_prefill(const void* query, const void* key_cache, const void* value_cache,
-               int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
-               const int32_t* context_lens, const int64_t* cu_seqlens,
-               const int32_t* prefill_items, int64_t num_prefill_items, int32_t prefill_tile,
-               float scaling, void* output, void* stream) {
-  int rc = check_step(dims, "pa_prefill");
+}  // extern "C"
+
+namespace {
+
+// pa_prefill, and with new_rows pa_prefill_append (the fast path only).
+int prefill_impl(const char* who, const void* query, const void* key_cache, const void* value_cache,
+                 int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
+                 const int32_t* context_lens, const int64_t* cu_seqlens, const int32_t* prefill_items,
+                 int64_t num_prefill_items, int32_t prefill_tile, float scaling, void* output,
+                 void* stream, const PaNewRows* new_rows) {
+  int rc = check_step(dims, who);
   if (rc != PA_OK) return rc;
   if (layer_idx < 0 || layer_idx >= dims.num_layers)
     return fail(PA_ERR_INVALID_ARGUMENT, "Layer index %d out of range (num_layers=%d)", layer_idx,
                 dims.num_layers);
   if (num_prefill_items <= 0 || dims.num_seqs == 0) return PA_OK;
-  rc = require("pa_prefill", {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
-                               {output, "output"}, {block_tables, "block_tables"},
-                               {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
-                               {prefill_items, "prefill_items"}});
+  rc = require(who, {{query, "query"}, {key_cache, "key_cache"}, {value_cache, "value_cache"},
+                     {output, "output"}, {block_tables, "block_tables"},
+                     {context_lens, "context_lens"}, {cu_seqlens, "cu_seqlens"},
+                     {prefill_items, "prefill_items"}});
   if (rc != PA_OK) return rc;
   if (num_prefill_items * static_cast<int64_t>(dims.num_kv_heads) *
           pa::decode_sub_groups(dims.num_query_heads / dims.num_kv_heads) > 0x7fffffffLL)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: too many work items");
+    return fail(PA_ERR_UNSUPPORTED, "%s: too many work items", who);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = dims.num_query_heads / dims.num_kv_heads;
   const int eb = elem_bytes(dims.dtype);
@@ -716,6 +721,20 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
       aligned16(query) && aligned16(key_cache) &&
       aligned16(value_cache) && aligned16(output) && (dims.q_token_stride * eb) % 16 == 0 &&
       (dims.q_head_stride * eb) % 16 == 0;
+  if (new_rows != nullptr) {
+    // The kernels copy and store 16-byte pieces of whole heads; a copy's rows
+    // sit at 32-bit offsets of at most 16 token strides from its base.
+    const auto stride_ok = [&](int64_t st) { return st >= 0 && (st * eb) % 16 == 0; };
+    const bool fused = fast && pa::prefill_append_supported(dims.dtype, dims.head_dim) &&
+                       aligned16(new_rows->key) && aligned16(new_rows->value) &&
+                       stride_ok(new_rows->key_token_stride) && stride_ok(new_rows->key_head_stride) &&
+                       stride_ok(new_rows->value_token_stride) && stride_ok(new_rows->value_head_stride) &&
+                       new_rows->key_token_stride * eb < (int64_t{1} << 24) &&
+                       new_rows->value_token_stride * eb < (int64_t{1} << 24);
+    if (!fused)
+      return fail(PA_ERR_UNSUPPORTED, "%s: shape or alignment not taken by the fused write "
+                  "(write the rows with pa_reshape_and_cache, then call pa_prefill)", who);
+  }
   if (fast) {
     pa::PrefillArgs a{};
     a.query = query;
@@ -737,9 +756,15 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
     a.scale_log2e = scaling * pa::kLog2e;
     a.group = group;
     a.sub_groups = pa::decode_sub_groups(group);
-    return from_hip(
-        pa::launch_prefill(a, dims.dtype, dims.head_dim, group, num_prefill_items, s),
-        "pa_prefill");
+    if (new_rows != nullptr) {
+      a.new_key = new_rows->key;
+      a.new_value = new_rows->value;
+      a.new_key_token_stride = new_rows->key_token_stride;
+      a.new_key_head_stride = new_rows->key_head_stride;
+      a.new_value_token_stride = new_rows->value_token_stride;
+      a.new_value_head_stride = new_rows->value_head_stride;
+    }
+    return from_hip(pa::launch_prefill(a, dims.dtype, dims.head_dim, group, num_prefill_items, s), who);
   }
   if (!pa::generic_supported(dims.dtype, dims.head_dim))
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill: head_dim %d / dtype %d not supported",
@@ -766,7 +791,33 @@ int pa_prefill(const void* query, const void* key_cache, const void* value_cache
   a.num_kv_heads = dims.num_kv_heads;
   a.head_dim = dims.head_dim;
   a.scale_log2e = scaling * pa::kLog2e;
-  return from_hip(pa::launch_generic(a, dims.dtype, false, s), "pa_prefill");
+  return from_hip(pa::launch_generic(a, dims.dtype, false, s), who);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_prefill(const void* query, const void* key_cache, const void* value_cache,
+               int32_t layer_idx, PaStepDims dims, const int32_t* block_tables,
+               const int32_t* context_lens, const int64_t* cu_seqlens,
+               const int32_t* prefill_items, int64_t num_prefill_items, int32_t prefill_tile,
+               float scaling, void* output, void* stream) {
+  return prefill_impl("pa_prefill", query, key_cache, value_cache, layer_idx, dims, block_tables,
+                      context_lens, cu_seqlens, prefill_items, num_prefill_items, prefill_tile, scaling,
+                      output, stream, nullptr);
+}
+
+int pa_prefill_append(const void* query, void* key_cache, void* value_cache, int32_t layer_idx,
+                      PaStepDims dims, PaNewRows new_rows, const int32_t* block_tables,
+                      const int32_t* context_lens, const int64_t* cu_seqlens,
+                      const int32_t* prefill_items, int64_t num_prefill_items, int32_t prefill_tile,
+                      float scaling, void* output, void* stream) {
+  int rc = require("pa_prefill_append", {{new_rows.key, "new_rows.key"}, {new_rows.value, "new_rows.value"}});
+  if (rc != PA_OK) return rc;
+  return prefill_impl("pa_prefill_append", query, key_cache, value_cache, layer_idx, dims, block_tables,
+                      context_lens, cu_seqlens, prefill_items, num_prefill_items, prefill_tile, scaling,
+                      output, stream, &new_rows);
 }
 
 }  // extern "C"

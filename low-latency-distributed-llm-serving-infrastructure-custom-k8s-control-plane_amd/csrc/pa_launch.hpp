@@ -193,6 +193,16 @@ struct PrefillArgs {
   // Work units of the launch (items x KV heads x sub-groups): the MFMA
   // prefill runs fewer workgroups than units, each looping over its share.
   int64_t num_units;
+  // pa_prefill_append (null otherwise): the step's new K and V rows
+  // ([T, H_kv, D], element strides).  Context positions at or after a
+  // sequence's chunk start are read from them, and sub-group 0 of each
+  // unit writes its own tile's rows into the (writable) caches.
+  const void* new_key;
+  const void* new_value;
+  int64_t new_key_token_stride;
+  int64_t new_key_head_stride;
+  int64_t new_value_token_stride;
+  int64_t new_value_head_stride;
 };
 
 bool decode_fast_path_supported(int dtype, int head_dim, int group, int block_size,
@@ -228,6 +238,8 @@ hipError_t launch_cache_write(const CacheWriteArgs& a, int dtype, hipStream_t st
 hipError_t launch_copy_blocks(const CopyBlocksArgs& a, bool vec16, hipStream_t stream);
 
 bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_size);
+// Whether the fast path of this shape also takes new rows (PrefillArgs::new_key).
+bool prefill_append_supported(int dtype, int head_dim);
 // Compute units of the current device (cached per device; 0 if unknown): the
 // width of the persistent prefill launches.
 int device_compute_units();

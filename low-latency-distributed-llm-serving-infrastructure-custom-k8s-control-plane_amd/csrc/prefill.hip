@@ -93,7 +93,13 @@ constexpr int kIdAhead = 8;      // stages between an id slot's copy and the sta
 // D: the head dim of the LDS rows and MFMA tiles; DM: the head dim in
 // memory (80 and 96 run on rows of 128 whose pieces past DM are zero: the
 // copies skip them, the query's are zero and the output's are not stored).
-template <typename T, int D, int DM, bool LANE_IDS>
+// APPEND (pa_prefill_append): context positions at or after the chunk's
+// start are copied from the step's new rows instead of the cache, and after
+// its last stage each unit of sub-group 0 stores its own tile's rows from
+// the rings into the cache (the rings then hold the last four stages, which
+// cover the tile's at most 128 tokens), so no unit reads a row another one
+// writes.
+template <typename T, int D, int DM, bool LANE_IDS, bool APPEND>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a) {
   static_assert(Elem<T>::kBytes == 2, "16-bit caches (bf16 or fp16)");
   static_assert(DM <= D && DM % 16 == 0, "memory head dim: a multiple of 16 up to D");
@@ -300,6 +306,20 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       const int bt_stride = row_ok ? a.block_table_stride : 1;
       const char* kbase = reinterpret_cast<const char*>(a.key_cache) + kvh * MEM_ROW;
       const char* vbase = reinterpret_cast<const char*>(a.value_cache) + kvh * MEM_ROW;
+      // APPEND: this KV head's new rows, the row of position p (at or after
+      // start) at nkbase + p * nkstride bytes (the host keeps strides below
+      // 2^24).
+      const char* nkbase = nullptr;
+      const char* nvbase = nullptr;
+      uint32_t nkstride = 0, nvstride = 0;
+      if constexpr (APPEND) {
+        nkstride = static_cast<uint32_t>(a.new_key_token_stride * 2);
+        nvstride = static_cast<uint32_t>(a.new_value_token_stride * 2);
+        nkbase = reinterpret_cast<const char*>(a.new_key) + kvh * a.new_key_head_stride * 2 +
+                 static_cast<int64_t>(first - start) * nkstride;
+        nvbase = reinterpret_cast<const char*>(a.new_value) + kvh * a.new_value_head_stride * 2 +
+                 static_cast<int64_t>(first - start) * nvstride;
+      }
 
       // Rows past G * MTOK (when G does not divide 128) belong to no head.
       const bool row_live = tok < ntok && g < G;
@@ -353,10 +373,16 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         return *reinterpret_cast<const int*>(s_lds + kIdBase + (x & (kIdSlots - 1)) * kIdSlotBytes + idx * 4);
       };
       const int id_last = btc[min(kv_last >> log2_bs, last_col)];  // block of the last readable row
+      // APPEND: the new row of position pos (at or after the chunk's start),
+      // piece chunk_off[j].
+      auto new_row = [&](const char* nbase, uint32_t nstride, int pos, int j) {
+        return nbase + (static_cast<uint64_t>(static_cast<uint32_t>(pos)) * nstride + chunk_off[j]);
+      };
       // Copies of this wave's rows of tensor stage x into LDS region `region`,
       // one per kRowsPerDma rows, with get_id(j, p): the block id of position p
-      // (readable) of copy j.
-      auto copy_each = [&](int x, uint32_t region, const char* base, auto get_id) {
+      // (readable) of copy j.  (nbase, nstride): the tensor's new rows.
+      auto copy_each = [&](int x, uint32_t region, const char* base, const char* nbase, uint32_t nstride,
+                           auto get_id) {
         const int p0 = x * kStage + cw * kCopyRows;
         const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
         if constexpr (!LANE_IDS) {
@@ -372,49 +398,80 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
             const uint32_t voff =
                 __umul24(min(static_cast<uint32_t>(delta), static_cast<uint32_t>(kv_last - pc)), row_bytes) +
                 chunk_off[j];
-            if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+            if (APPEND && p + kRowsPerDma - 1 >= start) {
+              // Some of the copy's rows are new rows: per-lane addresses,
+              // from a lane row made opaque here (hoisted out of the unit
+              // loop, the per-copy terms spilled, and each reload's wait
+              // drained the copies in flight).
+              int dl = delta;
+              asm volatile("" : "+v"(dl));
+              const int pos = min(p + dl, kv_last);
+              const char* lsrc = pos >= start ? new_row(nbase, nstride, pos, j) : src + voff;
+              if (!MASKD || chunk_in[j]) dma16(dst0 + j * kRowsPerDma * ROW_BYTES, lsrc);
+            } else {
+              if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+            }
           }
         } else {
           // Blocks smaller than a copying wave's rows: each lane's row has its own
           // block, read from the ring for every copy of the tensor first (one
           // wait for all of them, not one per copy).
           int pos[kDmaPerWave], b[kDmaPerWave];
+          int dl = delta;
+          if constexpr (APPEND) asm volatile("" : "+v"(dl));  // (as in the path above)
 #pragma unroll
           for (int j = 0; j < kDmaPerWave; ++j) {
-            pos[j] = min(p0 + j * kRowsPerDma + delta, kv_last);
+            pos[j] = min(p0 + j * kRowsPerDma + dl, kv_last);
             b[j] = pos[j] >= x * kStage ? ring_id(x, pos[j]) : id_last;
           }
 #pragma unroll
           for (int j = 0; j < kDmaPerWave; ++j)
-            if (!MASKD || chunk_in[j])
-              dma16(dst0 + j * kRowsPerDma * ROW_BYTES,
-                    base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
-                            (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j])));
+            if (!MASKD || chunk_in[j]) {
+              const char* src = base + (static_cast<uint64_t>(valid_block(b[j])) * block_bytes +
+                                        (static_cast<uint32_t>(pos[j] & bs_mask) * row_bytes + chunk_off[j]));
+              if (APPEND && pos[j] >= start) src = new_row(nbase, nstride, pos[j], j);
+              dma16(dst0 + j * kRowsPerDma * ROW_BYTES, src);
+            }
         }
       };
 
-      // A loop step's copies: one scalar base for the wave's 16 rows when they
-      // share a block and are readable (id_fast: their block id, read from the
-      // ring a step ahead), else one copy at a time with ids from the ring.
-      auto copy_step = [&](int x, uint32_t region, const char* base, int id_fast) {
+      // A step's copies: one scalar base for the wave's 16 rows when they
+      // share a block and are readable (id_fast: their block id) or are all
+      // new rows, else one copy at a time with get_id (in the loop: ids from
+      // the ring, read a step ahead).
+      auto copy_step = [&](int x, uint32_t region, const char* base, const char* nbase, uint32_t nstride,
+                           int id_fast, auto get_id) {
         const int p0 = x * kStage + cw * kCopyRows;
-        if (!LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last) {
+        // The wave's 16 rows: all new rows (APPEND), or all in one block of
+        // the cache -- one scalar base either way, chosen by a select.
+        const bool all_new = APPEND && p0 >= start && p0 + kCopyRows - 1 <= kv_last;
+        const bool all_cache = !LANE_IDS && one_block && p0 + kCopyRows - 1 <= kv_last &&
+                               (!APPEND || p0 + kCopyRows - 1 < start);
+        if (all_new || all_cache) {
           const uint32_t bb = valid_block(__builtin_amdgcn_readfirstlane(id_fast));
           const char* src = base + (static_cast<uint64_t>(bb) * block_bytes +
                                     static_cast<uint32_t>(p0 & bs_mask) * row_bytes);
+          if (APPEND && all_new) src = nbase + static_cast<uint64_t>(static_cast<uint32_t>(p0)) * nstride;
           const uint32_t dst0 = lds0 + region + cw * kCopyRows * ROW_BYTES;
 #pragma unroll
-          for (int j = 0; j < kDmaPerWave; ++j)
-            if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, row_off[j], src);
+          for (int j = 0; j < kDmaPerWave; ++j) {
+            uint32_t voff = row_off[j];
+            if (APPEND && all_new) voff = __umul24(static_cast<uint32_t>(j * kRowsPerDma + delta), nstride) + chunk_off[j];
+            if (!MASKD || chunk_in[j]) dma16_s(dst0 + j * kRowsPerDma * ROW_BYTES, voff, src);
+          }
         } else {
-          copy_each(x, region, base, [&](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); });
+          copy_each(x, region, base, nbase, nstride, get_id);
         }
+      };
+      auto ring_ids = [&](int x) {
+        return [&, x](int, int p) { return __builtin_amdgcn_readfirstlane(ring_id(x, p)); };
       };
       // The first stages' copies, with `id` the block of the wave's rows in
       // stage x (blocks of 16 or more: one block per copying wave and stage;
       // smaller blocks read their ids from the ring).
-      auto copy_first = [&](int x, uint32_t region, const char* base, int id) {
-        copy_each(x, region, base, [&](int, int) { return id; });
+      auto copy_first = [&](int x, uint32_t region, const char* base, const char* nbase, uint32_t nstride,
+                            int id) {
+        copy_step(x, region, base, nbase, nstride, id, [&](int, int) { return id; });
       };
 
       // Scores of tile t (positions [32 t, 32 t + 32)) masked for this lane's row:
@@ -520,10 +577,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
           int pid[4];
 #pragma unroll
           for (int x = 0; x < 4; ++x) pid[x] = btc[min(x * kStage + cw * kCopyRows, kv_last) >> log2_bs];
-          copy_first(0, 0, kbase, pid[0]);
-          if (nstages > 1) copy_first(1, kRegion, kbase, pid[1]);
-          if (nstages > 2) copy_first(2, 2 * kRegion, kbase, pid[2]);
-          copy_first(0, kVBase, vbase, pid[0]);
+          copy_first(0, 0, kbase, nkbase, nkstride, pid[0]);
+          if (nstages > 1) copy_first(1, kRegion, kbase, nkbase, nkstride, pid[1]);
+          if (nstages > 2) copy_first(2, 2 * kRegion, kbase, nkbase, nkstride, pid[2]);
+          copy_first(0, kVBase, vbase, nvbase, nvstride, pid[0]);
           // everything but K 1-2 and V 0 (issued last)
           wait_vmcnt_at_most<3 * kDmaPerWave>(kDmaPerWave * (1 + (nstages > 1 ? 1 : 0) + (nstages > 2 ? 1 : 0)));
         } else {
@@ -551,8 +608,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       // Tiles below this index need no mask for any row of the unit.
       const int first_masked = bad_ids ? 0 : min(start + tok0 + 1, kv_read) / kKvTile;
       if (wave < kCopyWaves) {
-        if (nstages > 3) copy_step(3, 3 * kRegion, kbase, ring_fast(3));
-        if (nstages > 1) copy_step(1, kVBase + kRegion, vbase, ring_fast(1));
+        if (nstages > 3) copy_step(3, 3 * kRegion, kbase, nkbase, nkstride, ring_fast(3), ring_ids(3));
+        if (nstages > 1) copy_step(1, kVBase + kRegion, vbase, nvbase, nvstride, ring_fast(1), ring_ids(1));
       }
       // Ids of step 0's copies (K of stage 4, V of stage 2), from the ring.
       int idk = 0, idv = 0;
@@ -578,7 +635,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         // Copies of this step: K of stage st+4, V of stage st+2 and (wave 0)
         // the id slot of stage st+8, each only if that stage exists.
         const bool cpk = st + 4 < nstages, cpv = st + 2 < nstages, cpi = st + kIdAhead < nstages;
-        if (wave < kCopyWaves && cpk) copy_step(st + 4, slot * kRegion, kbase, idk);
+        if (wave < kCopyWaves && cpk)
+          copy_step(st + 4, slot * kRegion, kbase, nkbase, nkstride, idk, ring_ids(st + 4));
         const int idv_cur = idv;  // (the prefetch below replaces idv)
         if (bad_ids) mask_bad(2 * st + kh, s_cur);
 
@@ -636,7 +694,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
         // The V copies and the id slot go out after the math, so that a copying
         // wave issues its copies in two short runs rather than one long one.
         if (wave < kCopyWaves && cpv)
-          copy_step(st + 2, kVBase + ((slot + 2) & (kKBufs - 1)) * kRegion, vbase, idv_cur);
+          copy_step(st + 2, kVBase + ((slot + 2) & (kKBufs - 1)) * kRegion, vbase, nvbase, nvstride, idv_cur,
+                    ring_ids(st + 2));
         if (wave == 0 && cpi) dma_ids(st + kIdAhead);
         // K of stage st+3, V of stage st+1 and (wave 0) the id slot of stage
         // st+7, copied last step, must have landed before the barrier
@@ -679,6 +738,41 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
       }
       // (the last step waited for every copy; no stage past the last is copied)
       l += __shfl_xor(l, 32, kWave);
+
+      if constexpr (APPEND) {
+        // The unit's share of the step's cache write (sub-group 0 of the KV
+        // head): its tile's tokens, positions [start + tok0, + ntok), stored
+        // from the rings as copied from the new rows -- stage x in slot x % 4
+        // of each ring, which after the last step holds stages nstages - 4 ..
+        // nstages - 1 (the tile's tokens lie in the last three), and its
+        // table entries in id slot x % 8.  Positions without a table column
+        // or in a block outside the pool are not written.
+        if (unit - kvh * a.sub_groups == 0 && row_ok) {
+          constexpr int MCH = DM / 8;  // 16-byte pieces of a head's row in memory
+          const int p_beg = start + tok0;
+          const int np = max(0, min(start + tok0 + ntok, kv_read) - p_beg);
+          char* kdst = const_cast<char*>(kbase);
+          char* vdst = const_cast<char*>(vbase);
+          for (int i = tid; i < 2 * np * MCH; i += kPrefillThreads) {
+            const bool is_v = i >= np * MCH;
+            const int k = is_v ? i - np * MCH : i;
+            const int p = p_beg + k / MCH;
+            const int c = k - (k / MCH) * MCH;
+            const int x = p / kStage;
+            const int r = p - x * kStage;
+            const int b = ring_id(x, p);
+            if (static_cast<uint32_t>(b) < static_cast<uint32_t>(a.total_blocks)) {
+              const uint4 v = *reinterpret_cast<const uint4*>(
+                  s_lds + (is_v ? kVBase : 0) + (x & (kKBufs - 1)) * kRegion + r * ROW_BYTES +
+                  ((c ^ chunk_swizzle<CHUNKS>(r)) * 16));
+              st16((is_v ? vdst : kdst) + (static_cast<uint64_t>(b) * block_bytes +
+                                           static_cast<uint32_t>(p & bs_mask) * row_bytes + c * 16),
+                   v);
+            }
+          }
+          __syncthreads();  // (the merge below writes over the rings)
+        }
+      }
 
       // ---- merge the two context halves of every row group -----------------
       // (after the last step's barrier no wave reads the rings any more)
@@ -790,6 +884,13 @@ bool prefill_fast_path_supported(int dtype, int head_dim, int group, int block_s
   return true;
 }
 
+bool prefill_append_supported(int dtype, int head_dim) {
+  // Every fast-path kernel but the one for heads of 256.
+  if (dtype == PA_DTYPE_F32) return head_dim == 64 || head_dim == 128;
+  return (dtype == PA_DTYPE_BF16 || dtype == PA_DTYPE_F16) &&
+         (head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128);
+}
+
 // Query tokens per work item: 128 rows over the heads of one workgroup (a
 // sub-group of at most 8 when the group is larger).
 int prefill_tile_for(int group) {
@@ -810,7 +911,7 @@ int device_compute_units() {
   return n;
 }
 
-template <typename T, int D, int DM>
+template <typename T, int D, int DM, bool APPEND>
 static hipError_t launch_prefill_d(const PrefillArgs& args, int group, int64_t num_items, hipStream_t s) {
   const int g = group / args.sub_groups;
   if (g < 1 || g > 8) return hipErrorNotSupported;
@@ -828,27 +929,34 @@ static hipError_t launch_prefill_d(const PrefillArgs& args, int group, int64_t n
   // from the ring), which beat one scalar base per copy with its id read
   // just before it.
   if ((1 << a.log2_block_size) >= kCopyRows)
-    hipLaunchKernelGGL((prefill_kernel<T, D, DM, false>), grid, dim3(kPrefillThreads), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D, DM, false, APPEND>), grid, dim3(kPrefillThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((prefill_kernel<T, D, DM, true>), grid, dim3(kPrefillThreads), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D, DM, true, APPEND>), grid, dim3(kPrefillThreads), 0, s, a);
   return hipGetLastError();
+}
+
+template <typename T, int D, int DM>
+static hipError_t launch_prefill_t(const PrefillArgs& a, int group, int64_t num_items, hipStream_t s) {
+  return a.new_key != nullptr ? launch_prefill_d<T, D, DM, true>(a, group, num_items, s)
+                              : launch_prefill_d<T, D, DM, false>(a, group, num_items, s);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, int dtype, int head_dim, int group,
                           int64_t num_items, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   if (dtype == PA_DTYPE_F32) return launch_prefill_f32(a, head_dim, group, num_items, stream);
-  if (head_dim == 256) return launch_prefill256(a, dtype, group, num_items, stream);
+  if (head_dim == 256)
+    return a.new_key != nullptr ? hipErrorNotSupported : launch_prefill256(a, dtype, group, num_items, stream);
   if (dtype == PA_DTYPE_BF16) {
-    if (head_dim == 128) return launch_prefill_d<bf16_t, 128, 128>(a, group, num_items, stream);
-    if (head_dim == 96) return launch_prefill_d<bf16_t, 128, 96>(a, group, num_items, stream);
-    if (head_dim == 80) return launch_prefill_d<bf16_t, 128, 80>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_prefill_d<bf16_t, 64, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_prefill_t<bf16_t, 128, 128>(a, group, num_items, stream);
+    if (head_dim == 96) return launch_prefill_t<bf16_t, 128, 96>(a, group, num_items, stream);
+    if (head_dim == 80) return launch_prefill_t<bf16_t, 128, 80>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_t<bf16_t, 64, 64>(a, group, num_items, stream);
   } else if (dtype == PA_DTYPE_F16) {
-    if (head_dim == 128) return launch_prefill_d<f16_t, 128, 128>(a, group, num_items, stream);
-    if (head_dim == 96) return launch_prefill_d<f16_t, 128, 96>(a, group, num_items, stream);
-    if (head_dim == 80) return launch_prefill_d<f16_t, 128, 80>(a, group, num_items, stream);
-    if (head_dim == 64) return launch_prefill_d<f16_t, 64, 64>(a, group, num_items, stream);
+    if (head_dim == 128) return launch_prefill_t<f16_t, 128, 128>(a, group, num_items, stream);
+    if (head_dim == 96) return launch_prefill_t<f16_t, 128, 96>(a, group, num_items, stream);
+    if (head_dim == 80) return launch_prefill_t<f16_t, 128, 80>(a, group, num_items, stream);
+    if (head_dim == 64) return launch_prefill_t<f16_t, 64, 64>(a, group, num_items, stream);
   }
   return hipErrorNotSupported;
 }

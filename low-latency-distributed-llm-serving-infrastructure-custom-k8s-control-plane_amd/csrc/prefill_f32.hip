@@ -49,7 +49,12 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <int D>
+// APPEND (pa_prefill_append): context positions at or after the chunk's
+// start are copied from the step's new rows, and each unit of sub-group 0
+// stores its own tile's rows from the stage buffers into the cache while
+// each stage is in LDS (their block ids staged in LDS once per unit), so no
+// unit reads a row another one writes.
+template <int D, bool APPEND>
 __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArgs a) {
   constexpr int ROWB = D * 4;                  // bytes of a K or V row
   constexpr int CH = D / 4;                    // 16-byte chunks of a row
@@ -64,6 +69,10 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
   static_assert(4 * kWave * kMerge * 4 <= 2 * kBufBytes, "the merge fits the stage buffers");
 
   __shared__ __attribute__((aligned(16))) char s_lds[2 * kBufBytes];
+  // Block id of every row of each stage buffer (-1 without a table row),
+  // stored by the lanes that copy the row: the masks and the fused write read
+  // them here instead of the table.
+  __shared__ int32_t s_sid[2][kFmStage];
 
   const int G = a.group / a.sub_groups;
   const int MTOK = kFmRows / G;
@@ -116,6 +125,19 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
     const int bt_stride = row_ok ? a.block_table_stride : 1;
     const char* kbase = reinterpret_cast<const char*>(a.key_cache) + static_cast<int64_t>(kvh) * ROWB;
     const char* vbase = reinterpret_cast<const char*>(a.value_cache) + static_cast<int64_t>(kvh) * ROWB;
+    // APPEND: this KV head's new rows, the row of position p (at or after
+    // start) at nk0 + p * nkstride bytes (the host keeps strides below 2^24).
+    const char* nk0 = nullptr;
+    const char* nv0 = nullptr;
+    uint32_t nkstride = 0, nvstride = 0;
+    if constexpr (APPEND) {
+      nkstride = static_cast<uint32_t>(a.new_key_token_stride * 4);
+      nvstride = static_cast<uint32_t>(a.new_value_token_stride * 4);
+      nk0 = reinterpret_cast<const char*>(a.new_key) + kvh * a.new_key_head_stride * 4 +
+            (first - start) * static_cast<int64_t>(nkstride);
+      nv0 = reinterpret_cast<const char*>(a.new_value) + kvh * a.new_value_head_stride * 4 +
+            (first - start) * static_cast<int64_t>(nvstride);
+    }
     const int kv_end = min(ctx, start + tok0 + ntok);  // exclusive
     // Positions that have a block-table column (the rest are never read).
     const int kv_read = static_cast<int>(
@@ -137,19 +159,48 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
     };
     // Copies of stage x into buffer b.  Rows past the readable context
     // re-read its last row and an out-of-pool block reads block 0 (finite
-    // values; their scores are masked).
-    auto issue = [&](int x, int b) {
+    // values; their scores are masked).  APPEND: rows at or after the
+    // chunk's start come from the new rows -- one path per stage (all rows
+    // before the chunk, all in it, or the stage that holds its start), as
+    // per-lane address selects in every stage spilled registers in the
+    // stage loop.
+    auto issue_rows = [&](int x, int b, auto src_of) {
+      // (the lane's row and chunk are made opaque here, so that the copies'
+      // per-lane terms are formed in each stage instead of being hoisted out
+      // of the stage loop into registers)
+      int cr = crow, cp = cpos;
+      asm volatile("" : "+v"(cr), "+v"(cp));
 #pragma unroll
       for (int c = 0; c < kCopies; ++c) {
-        const int R = 8 * wave + c * RPC + crow;
-        const int p = x * kFmStage + R;
-        const int blk = static_cast<uint32_t>(ids[c]) < static_cast<uint32_t>(a.total_blocks) ? ids[c] : 0;
-        const int pc = min(p, kv_last);
-        const int64_t off = ((static_cast<int64_t>(blk) << log2_bs) + (pc & bs_mask)) * row_bytes +
-                            ((cpos ^ chunk_swizzle<CH>(R)) * 16);
+        const int R = 8 * wave + c * RPC + cr;
+        const int pc = min(x * kFmStage + R, kv_last);
+        const int piece = (cp ^ chunk_swizzle<CH>(R)) * 16;
         const uint32_t dst = lds0 + b * kBufBytes + (8 * wave + c * RPC) * ROWB;
-        dma16(dst, kbase + off);
-        dma16(dst + TBYTES, vbase + off);
+        src_of(c, pc, piece, dst);
+        if (cp == 0) s_sid[b][R] = ids[c];
+      }
+    };
+    auto from_cache = [&](int c, int pc, int piece, uint32_t dst) {
+      const int blk = static_cast<uint32_t>(ids[c]) < static_cast<uint32_t>(a.total_blocks) ? ids[c] : 0;
+      const int64_t off = ((static_cast<int64_t>(blk) << log2_bs) + (pc & bs_mask)) * row_bytes + piece;
+      dma16(dst, kbase + off);
+      dma16(dst + TBYTES, vbase + off);
+    };
+    auto from_new = [&](int, int pc, int piece, uint32_t dst) {
+      const uint64_t p = static_cast<uint32_t>(pc);
+      dma16(dst, nk0 + (p * nkstride + piece));
+      dma16(dst + TBYTES, nv0 + (p * nvstride + piece));
+    };
+    auto issue = [&](int x, int b) {
+      if (!APPEND || x * kFmStage + kFmStage - 1 < start || kv_last < start) {
+        issue_rows(x, b, from_cache);
+      } else if (x * kFmStage >= start) {
+        issue_rows(x, b, from_new);
+      } else {
+        issue_rows(x, b, [&](int c, int pc, int piece, uint32_t dst) {
+          if (pc < start) from_cache(c, pc, piece, dst);
+          else from_new(c, pc, piece, dst);
+        });
       }
     };
 
@@ -166,6 +217,12 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
       for (int j = 0; j < CH; ++j)
         q[j] = live ? *reinterpret_cast<const float2*>(qrow + 4 * j) : make_float2(0.f, 0.f);
     }
+    // APPEND: the unit writes positions [p_beg, p_end) of its tile (sub-group
+    // 0 of the KV head, a table row inside the table; positions without a
+    // table column are not written).
+    const bool writer = APPEND && unit - kvh * a.sub_groups == 0 && row_ok;
+    const int p_beg = start + tok0;
+    const int p_end = max(p_beg, kv_read);
     // Positions whose block id lies outside the pool are skipped (as in
     // decode): every wave passes over the row's columns (cached reads) and
     // ballots whether there are any; such units take the masked path in
@@ -228,19 +285,25 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
           __builtin_amdgcn_sched_barrier(0);
         }
         // Masks: past the row's causal limit or the readable context, or in
-        // a block outside the pool (the table entry is checked in every
+        // a block outside the pool (the stage's block id is checked in every
         // tile that takes masks: the diagonal and end tiles, and every tile
-        // of a unit with such blocks).  The table test stays unconditional
+        // of a unit with such blocks).  The id test stays unconditional
         // here: gated as `p > lim || (bad_ids && ...)`, this ROCm's hipcc
         // emitted the -INF write on the `p > lim` path only, and positions in
         // out-of-pool blocks kept their scores.
         if (bad_ids || p0 + kFmTile - 1 > min(start + tok0, kv_last)) {
+          // (every id read first, then one select per score)
+          const int32_t* sid = s_sid[b] + kh * kFmTile + 4 * h;
+          int4 idq[4];
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) idq[q4] = *reinterpret_cast<const int4*>(sid + 8 * q4);
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int tt = 8 * (i >> 2) + 4 * h + (i & 3);
-            const int p = p0 + tt;
-            if (p > lim || !row_ok || static_cast<uint32_t>(bt[p >> log2_bs]) >= static_cast<uint32_t>(a.total_blocks))
-              s[i] = -INFINITY;
+            const int4 q = idq[i >> 2];
+            const int id = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+            const bool off = (p0 + tt > lim) | (static_cast<uint32_t>(id) >= static_cast<uint32_t>(a.total_blocks));
+            s[i] = off ? -INFINITY : s[i];
           }
         }
         float tmax = s[0];
@@ -287,6 +350,27 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
 #pragma unroll
           for (int db = 0; db < DB; ++db) vc[db] = vn[db];
           __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (writer && (st + 1) * kFmStage > p_beg && st * kFmStage < p_end) {
+        // This stage's rows of the tile, stored from buffer b (stable until
+        // the barrier that ends the stage).  Out-of-pool blocks are skipped.
+        const int r0 = max(p_beg - st * kFmStage, 0);
+        const int n = (min(p_end - st * kFmStage, kFmStage) - r0) * CH;  // pieces per tensor
+        for (int i = tid; i < 2 * n; i += kFmThreads) {
+          const bool is_v = i >= n;
+          const int k = is_v ? i - n : i;
+          const int r = r0 + k / CH;
+          const int c = k % CH;
+          const int p = st * kFmStage + r;
+          const int blk = s_sid[b][r];
+          if (static_cast<uint32_t>(blk) < static_cast<uint32_t>(a.total_blocks)) {
+            const uint4 v = *reinterpret_cast<const uint4*>(s_lds + b * kBufBytes + (is_v ? TBYTES : 0) + r * ROWB +
+                                                            ((c ^ chunk_swizzle<CH>(r)) * 16));
+            char* dst = const_cast<char*>(is_v ? vbase : kbase) +
+                        ((static_cast<int64_t>(blk) << log2_bs) + (p & bs_mask)) * row_bytes + c * 16;
+            st16(dst, v);
+          }
         }
       }
       // The next stage's copies have landed and every wave is done with
@@ -337,7 +421,7 @@ __global__ __launch_bounds__(kFmThreads) void prefill_f32_mfma_kernel(PrefillArg
   }
 }
 
-template <int D>
+template <int D, bool APPEND>
 static hipError_t launch_prefill_f32_mfma(const PrefillArgs& args, int group, int64_t num_items,
                                           hipStream_t s) {
   const int g = group / args.sub_groups;
@@ -350,15 +434,21 @@ static hipError_t launch_prefill_f32_mfma(const PrefillArgs& args, int group, in
   // over its share of the units; fewer units than CUs run one each.
   const int cus = device_compute_units();
   const int64_t wgs = cus > 0 ? std::min<int64_t>(a.num_units, cus) : a.num_units;
-  hipLaunchKernelGGL((prefill_f32_mfma_kernel<D>), dim3(static_cast<uint32_t>(wgs)), dim3(kFmThreads), 0, s, a);
+  hipLaunchKernelGGL((prefill_f32_mfma_kernel<D, APPEND>), dim3(static_cast<uint32_t>(wgs)), dim3(kFmThreads), 0, s,
+                     a);
   return hipGetLastError();
 }
 
 hipError_t launch_prefill_f32(const PrefillArgs& a, int head_dim, int group, int64_t num_items,
                               hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
-  if (head_dim == 128) return launch_prefill_f32_mfma<128>(a, group, num_items, stream);
-  if (head_dim == 64) return launch_prefill_f32_mfma<64>(a, group, num_items, stream);
+  const bool append = a.new_key != nullptr;
+  if (head_dim == 128)
+    return append ? launch_prefill_f32_mfma<128, true>(a, group, num_items, stream)
+                  : launch_prefill_f32_mfma<128, false>(a, group, num_items, stream);
+  if (head_dim == 64)
+    return append ? launch_prefill_f32_mfma<64, true>(a, group, num_items, stream)
+                  : launch_prefill_f32_mfma<64, false>(a, group, num_items, stream);
   return hipErrorNotSupported;
 }
 

@@ -1043,6 +1043,38 @@ def _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, o
     )
 
 
+def _launch_prefill_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v) -> int:
+    """pa_prefill_append; returns its status (PA_ERR_UNSUPPORTED: not fused)."""
+    rows = _native.PaNewRows(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1))
+    lib = _native.load_library()
+    return lib.pa_prefill_append(
+        q.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        int(layer_idx),
+        dims,
+        rows,
+        step.ptr("block_tables"),
+        step.ptr("context_lens"),
+        step.ptr("cu_seqlens"),
+        step.ptr("prefill_items"),
+        step.num_prefill_items,
+        step.prefill_tile,
+        float(scaling),
+        out.data_ptr(),
+        _stream(q.device),
+    )
+
+
+def _fused(status: int, who: str) -> bool:
+    """True if a fused-write launch ran, False if it declined the shape."""
+    if status == _native.PA_OK:
+        return True
+    if status != _native.PA_ERR_UNSUPPORTED:
+        _native.check(status, who)
+    return False
+
+
 def attention(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -1057,29 +1089,39 @@ def attention(
     """Attention of a whole flattened step (decode + prefill sequences) -> [T, H_q, D].
 
     With ``new_key`` / ``new_value`` ([T, H_kv, D], the step's new rows) the
-    rows are first written into the caches at the step's scatter slots, as
-    :func:`reshape_and_cache` does: for a step of single-token sequences
-    inside the decode launches themselves (pa_decode_append), otherwise (or
-    for a shape the fused write does not take) by the cache-write kernel.
+    rows are also written into the caches at the step's scatter slots, as
+    :func:`reshape_and_cache` does: inside the prefill launch for the
+    multi-token sequences (pa_prefill_append) and inside the decode launches
+    for the single-token ones (pa_decode_append).  When either declines the
+    shape, the cache-write kernel writes every row first (rows a fused
+    launch already wrote get the same bytes again) and the plain launches
+    follow.
     """
     q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
     if (new_key is None) != (new_value is None):
         raise ValueError("new_key and new_value are given together")
+    need_prefill = step.num_prefill_items > 0
+    need_decode = step.num_decode_items > 0
     if new_key is not None:
         k, v = _new_rows(new_key, new_value, key_cache, step)
-        if step.num_prefill_seqs == 0 and step.num_decode_items > 0 and not step.__dict__.get("_no_append"):
-            status = _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v)
-            if status == _native.PA_OK:
-                return out
-            if status != _native.PA_ERR_UNSUPPORTED:
-                _native.check(status, "pa_decode_append")
-            step.__dict__["_no_append"] = True
-        if step.num_query_tokens > 0:
+        fused = False  # a fused launch wrote rows
+        if not step.__dict__.get("_no_append"):
+            if need_prefill and _fused(
+                    _launch_prefill_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v),
+                    "pa_prefill_append"):
+                need_prefill, fused = False, True
+            if need_decode and not need_prefill and _fused(
+                    _launch_decode_append(q, key_cache, value_cache, layer_idx, step, scaling, out, dims, k, v),
+                    "pa_decode_append"):
+                need_decode, fused = False, True
+            if need_prefill or need_decode:
+                step.__dict__["_no_append"] = True
+        if (need_prefill or need_decode or not fused) and step.num_query_tokens > 0:
             reshape_and_cache(k, v, key_cache, value_cache, step.scatter_slots, layer_idx)
-    if step.num_prefill_items > 0:
+    if need_prefill:
         _launch_prefill(q, key_cache, value_cache, layer_idx, step, scaling, out, dims)
-    if step.num_decode_items > 0:
+    if need_decode:
         _launch_decode(q, key_cache, value_cache, layer_idx, step, scaling, out, dims,
                        _native.PA_DECODE_PHASE_PARTITIONS | _native.PA_DECODE_PHASE_MERGE)
     if step.num_query_tokens > 0 and step.num_decode_items == 0 and step.num_prefill_items == 0:

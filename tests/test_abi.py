@@ -116,6 +116,10 @@ def test_invalid_arguments_rejected_before_launch():
     rc = lib.pa_decode_append(*([None] * 3), 0, native.PaStepDims(), rows, *([None] * 4), 1, None, 0, 1.0,
                               None, None, 0, None)
     assert rc == native.PA_ERR_INVALID_ARGUMENT and b"new_rows.key" in lib.pa_last_error_message()
+    rows = native.PaNewRows(0x1000, None, 128, 1024, 128, 1024)
+    rc = lib.pa_prefill_append(*([None] * 3), 0, native.PaStepDims(), rows, *([None] * 4), 1, 32, 1.0,
+                               None, None)
+    assert rc == native.PA_ERR_INVALID_ARGUMENT and b"new_rows.value" in lib.pa_last_error_message()
     assert lib.pa_calibrate_mfma(None, 1, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
     assert lib.pa_calibrate_mfma(0x1000, 0, 1, 0, None) == native.PA_ERR_INVALID_ARGUMENT
     assert lib.pa_calibrate_mfma(0x1000, 1, 1, 3, None) == native.PA_ERR_INVALID_ARGUMENT

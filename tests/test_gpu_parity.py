@@ -769,9 +769,9 @@ def test_decode_append_equals_write_then_decode(device, hq, hkv, d, dtype):
 
 
 def test_attention_with_new_rows_on_a_mixed_step(device):
-    """A step with prefill tokens given its new rows writes them with the
-    cache-write kernel first (the fused write covers single-token sequences
-    only): the same cache bytes and output bits as writing them beforehand."""
+    """The mixed step (four 512-token chunks + 128 long decodes) given its new
+    rows writes them inside its prefill and decode launches: the same cache
+    bytes and output bits as writing them beforehand."""
     w = wl.WORKLOADS["mixed_step"](seed=2)
     t = wl.make_tensors(w, device, seed=2)
     step = pack_workload(w, device)
@@ -780,6 +780,58 @@ def test_attention_with_new_rows_on_a_mixed_step(device):
     want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values)
     torch.cuda.synchronize()
+    assert not step.__dict__.get("_no_append"), "a fused write was not taken"
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,bs,fused", [
+    (32, 8, 128, torch.bfloat16, 16, True), (16, 16, 128, torch.float16, 32, True),
+    (64, 4, 128, torch.bfloat16, 16, True), (16, 2, 96, torch.bfloat16, 16, True),
+    (16, 4, 80, torch.float16, 8, True), (8, 8, 64, torch.bfloat16, 1, True),
+    (32, 8, 128, torch.float32, 16, True), (8, 8, 64, torch.float32, 4, True),
+    (16, 1, 64, torch.float32, 16, True), (16, 4, 256, torch.bfloat16, 16, False)])
+def test_prefill_append_equals_write_then_prefill(device, hq, hkv, d, dtype, bs, fused):
+    """A step with prefill chunks given its new K/V rows (written inside the
+    prefill launch, pa_prefill_append, and the decode launches) leaves the
+    same cache bytes and returns the same output bits as pa_reshape_and_cache
+    followed by pa_prefill and pa_decode: chunks at 0 and mid-context, one
+    ragged and one of two tokens, a one-token sequence beside them, groups
+    of 1-16 (sub-groups), heads of 64-128 in every dtype, block sizes 1-32,
+    head-major new rows (the model's projections), and chunk positions in a
+    block outside the pool and in a column without a block (written by
+    neither, masked by both).  Heads of 256 decline the fused write and take
+    the cache-write kernel."""
+    rng = np.random.Generator(np.random.PCG64(hq * 31 + d + bs))
+    starts = [0, 0, 37, 512, 100, 5, 3000, 250]
+    counts = [1, 200, 64, 300, 7, 129, 2, 131]
+    ctx = [s_ + c for s_, c in zip(starts, counts)]
+    need = [-(-c // bs) for c in ctx]
+    total = sum(need) + 4
+    perm = rng.permutation(total)
+    lists, off = [], 0
+    for n_ in need:
+        lists.append([int(x) for x in perm[off : off + n_]])
+        off += n_
+    w = wl.StepWorkload("prefill_append", hq, hkv, d, bs, dtype, 1.0, starts, counts, lists, total)
+    t = wl.make_tensors(w, device, seed=5)
+    table_np = w.block_table_array()
+    table_np[3, need[3] - 2] = total + 3  # a chunk block of sequence 3 outside the pool
+    table_np[7, need[7] - 1] = -1  # the last column of sequence 7 without a block
+    table = torch.from_numpy(table_np).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, bs,
+                         prefill_tile=ops.prefill_tile_for(hq, hkv), num_kv_heads=hkv, num_query_heads=hq,
+                         head_dim=d, dtype=dtype)
+    # head-major projections: token stride D, head stride T * D
+    nk = t.new_keys.transpose(0, 1).contiguous().transpose(0, 1)
+    nv = t.new_values.transpose(0, 1).contiguous().transpose(0, 1)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv)
+    torch.cuda.synchronize()
+    log(f"prefill append {dtype} {hq}/{hkv}/{d} bs {bs}: prefill items {step.num_prefill_items}")
+    assert bool(step.__dict__.get("_no_append")) != fused
     assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
     assert torch.equal(_bits(got), _bits(want))
 
