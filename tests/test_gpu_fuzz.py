@@ -9,7 +9,7 @@ batch of decodes (contexts 1-700) and prefill chunks (2-90 tokens at starts
 seed (seed % 4 == 1) is a decode-only batch.  The step is packed, its new
 K/V rows are written into a random non-contiguous pool -- by the cache-write
 kernel for even seeds, handed to the attention for odd ones (written inside
-the decode launches for a decode-only batch) -- decode and prefill run, and
+the prefill and decode launches) -- decode and prefill run, and
 every output row is compared with the oracle run on the cache the GPU read
 (fp32 to 1e-4 absolute, bf16 and fp16 to the relative bound of the parity
 tests).  This covers the combinations the
@@ -126,3 +126,46 @@ def test_random_wide_steps_match_oracle(device, seed):
     out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     torch.cuda.synchronize()
     check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=False)
+
+
+def _bits(x):
+    return x.view({torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}[x.dtype])
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_steps_fused_write_is_bit_exact(device, seed):
+    """The new K/V rows written inside the attention launches (pa_prefill_append
+    and pa_decode_append) leave the same cache bytes and give the same output
+    bits as writing them with the cache-write kernel first, on the random
+    steps above (seeds below 28) and the wide ones (28 on), with token-major
+    or head-major new rows, and with a random table entry of a multi-token
+    sequence set outside the pool or to -1."""
+    rng = np.random.Generator(np.random.PCG64(9000 + seed))
+    if seed < 28:
+        w, partition = random_case(3 * seed + 2)
+    else:
+        w, partition = random_wide_case(seed - 28), None
+    t = wl.make_tensors(w, device, seed=200 + seed)
+    table_np = w.block_table_array()
+    multi = [i for i, c in enumerate(w.new_token_counts) if c > 1]
+    if multi and rng.random() < 0.5:
+        i = int(rng.choice(multi))
+        col = int(rng.integers(0, len(w.block_lists[i])))
+        table_np[i, col] = w.total_blocks + 2 if rng.random() < 0.5 else -1
+    table = torch.from_numpy(table_np).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         partition_size=partition, num_kv_heads=w.num_kv_heads,
+                         num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
+    nk, nv = t.new_keys, t.new_values
+    if seed % 2:  # head-major rows: token stride D, head stride T * D
+        nk = nk.transpose(0, 1).contiguous().transpose(0, 1)
+        nv = nv.transpose(0, 1).contiguous().transpose(0, 1)
+    log(f"fused-write seed={seed}: H_q={w.num_query_heads} H_kv={w.num_kv_heads} D={w.head_dim} {w.dtype} "
+        f"bs={w.block_size} B={w.num_seqs} prefill items={step.num_prefill_items}")
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
