@@ -43,8 +43,10 @@ Also on the line:
 
 --workload prefill_shapes prints one line of the prefill kernel alone on
 prefill-only steps of four 512-token chunks (32/8 heads, D=128, bf16 and
-fp32), each against its dtype's dense MFMA peak, and the same launch writing
-the chunks' new K/V rows (--shape NAME: one of them).
+fp32, and two small prompt steps), each against its dtype's dense MFMA peak,
+the same launch writing the chunks' new K/V rows, and the whole step with
+its write from HIP graphs, the cache-write kernel then the prefill against
+the fused launch (--shape NAME: one of them).
 
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
@@ -804,17 +806,36 @@ def prefill_shapes_line(args, device):
         # The same launch writing the chunks' new K/V rows (pa_prefill_append).
         app_ms = events_ms(lambda: None,
                            lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
-                                                 new_key=t.new_keys, new_value=t.new_values),
+                                                 new_key=t.new_keys, new_value=t.new_values,
+                                                 fused_prefill_write=True),
                            args.steps, 20, stream)
         if step.__dict__.get("_no_append"):
             raise RuntimeError(f"{name}: the prefill did not take the fused write")
+
+        # The whole step with its K/V write from HIP graphs (no launch
+        # gaps): the cache-write kernel then the prefill, against the fused
+        # launch, alternated three times each.
+        def separate(i=0):
+            ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+            ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out)
+
+        def fused(i=0):
+            ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
+                          new_key=t.new_keys, new_value=t.new_values, fused_prefill_write=True)
+
+        sep_g, fus_g = [], []
+        for _ in range(3):
+            sep_g.append(graph_ms(separate, 40, 3, stream))
+            fus_g.append(graph_ms(fused, 40, 3, stream))
         pf = wl.prefill_flops(w)
         peak = MFMA_F32_PEAK_TFLOPS if dtype == torch.float32 else MFMA_BF16_PEAK_TFLOPS
         tf = pf / (ms * 1e-3) / 1e12
         shapes[name] = {"starts": list(starts), "counts": list(counts), "dtype": str(dtype).replace("torch.", ""),
                         "gflop": round(pf / 1e9, 2), "kernel_ms": round(ms, 5), "tflops": round(tf, 1),
                         "peak_tflops": peak, "mfma_frac": round(tf / peak, 4),
-                        "append_kernel_ms": round(app_ms, 5)}
+                        "append_kernel_ms": round(app_ms, 5),
+                        "graph_step_us": {"write_then_prefill": round(median(sep_g) * 1e3, 2),
+                                          "fused_write": round(median(fus_g) * 1e3, 2)}}
         del t, out, step, table
         torch.cuda.empty_cache()
     return {"workload": "prefill_shapes", "heads": [32, 8], "head_dim": 128, "block_size": wl.BLOCK_SIZE,

@@ -19,7 +19,8 @@ as a seeded permutation of the pool's block ids.  Shapes and distributions:
                         U{512..32768}, 32/8 heads, D=128, bf16
   PREFILL_SHAPES        prefill-only steps of four 512-token chunks (at
                         {0, 512, 1024, 1536} or all at 4096), 32/8 heads,
-                        D=128, bf16 and fp32
+                        D=128, bf16 and fp32; one 128-token prompt and
+                        eight 64-token prompts, bf16
 
 Lengths and block tables come from numpy's PCG64 generator; tensor values
 are drawn with torch (on the target device for the large pools).
@@ -162,13 +163,16 @@ def prefill_chunks(name: str, starts: List[int], counts: List[int], dtype: torch
                         list(counts), lists, total)
 
 
-# Prefill kernel shapes (32/8 heads, D=128, 512-token chunks): the mixed
-# step's four chunks and four chunks deep in their contexts, in both dtypes.
+# Prefill kernel shapes (32/8 heads, D=128): the mixed step's four 512-token
+# chunks and four chunks deep in their contexts, in both dtypes, and two
+# small prompt steps (one prompt of 128 tokens, eight of 64).
 PREFILL_SHAPES = {
     "chunks_0_512_1024_1536_bf16": ([0, 512, 1024, 1536], [512] * 4, torch.bfloat16),
     "chunks_at_4096_bf16": ([4096] * 4, [512] * 4, torch.bfloat16),
     "chunks_0_512_1024_1536_fp32": ([0, 512, 1024, 1536], [512] * 4, torch.float32),
     "chunks_at_4096_fp32": ([4096] * 4, [512] * 4, torch.float32),
+    "one_prompt_128_bf16": ([0], [128], torch.bfloat16),
+    "prompts_8x64_bf16": ([0] * 8, [64] * 8, torch.bfloat16),
 }
 
 

@@ -165,7 +165,7 @@ def test_random_steps_fused_write_is_bit_exact(device, seed):
     kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
     ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
     want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
-    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv, fused_prefill_write=True)
     torch.cuda.synchronize()
     assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
     assert torch.equal(_bits(got), _bits(want))

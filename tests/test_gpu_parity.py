@@ -828,10 +828,27 @@ def test_prefill_append_equals_write_then_prefill(device, hq, hkv, d, dtype, bs,
     kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
     ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
     want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
-    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv, fused_prefill_write=True)
     torch.cuda.synchronize()
     log(f"prefill append {dtype} {hq}/{hkv}/{d} bs {bs}: prefill items {step.num_prefill_items}")
     assert bool(step.__dict__.get("_no_append")) != fused
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
+def test_fp32_steps_write_prefill_rows_with_the_cache_write_kernel(device):
+    """By default an fp32 step with prefill tokens writes its rows with the
+    cache-write kernel and runs the plain launches (its fused prefill write
+    measured slower), with the same cache bytes and output bits."""
+    w = wl.prefill_chunks("fp32_policy", [0, 40], [70, 1], torch.float32, 16, 4, 64)
+    t = wl.make_tensors(w, device, seed=4)
+    step = pack_workload(w, device)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values)
+    torch.cuda.synchronize()
+    assert not step.__dict__.get("_no_append")
     assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
     assert torch.equal(_bits(got), _bits(want))
 
