@@ -49,6 +49,7 @@ its write from HIP graphs, the cache-write kernel then the prefill against
 the fused launch (--shape NAME: one of them).
 
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
+                [--calibrate-read]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
                             prefill_shapes]
 """
@@ -395,6 +396,44 @@ def sustained_mfma_tflops(device, iters: int = 4096, reps: int = 9, warmup: int 
     return flops / (median(times) * 1e-3) / 1e12
 
 
+def sustained_read_gbs(device, nbytes: int, reps: int = 9, warmup: int = 5) -> float:
+    """The read rate the device sustains for `nbytes` (pa_calibrate_read: one
+    pass of 16-byte non-temporal loads over a fresh buffer of that size, 64
+    workgroups of 256 threads per CU), median of `reps` launches timed with
+    HIP events after `warmup` untimed ones: the ceiling an HBM-bound kernel's
+    GB/s is read against beside the nominal peak.  Measured after the
+    workload's own timings, so its pool stays the first large allocation of
+    the process."""
+    import torch
+
+    native = pkg("_native")
+    lib = native.load_library()
+    nb = (int(nbytes) + 15) // 16 * 16
+    buf = torch.empty(nb, dtype=torch.uint8, device=device)
+    buf.fill_(1)
+    out = torch.zeros(16, dtype=torch.uint8, device=device)
+    wgs = 64 * torch.cuda.get_device_properties(device).multi_processor_count
+    stream = torch.cuda.current_stream(device)
+
+    def launch():
+        native.check(lib.pa_calibrate_read(buf.data_ptr(), nb, out.data_ptr(), wgs, stream.cuda_stream),
+                     "pa_calibrate_read")
+
+    for _ in range(warmup):
+        launch()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        launch()
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    del buf
+    torch.cuda.empty_cache()
+    return nb / (median(times) * 1e-3) / 1e9
+
+
 # ---------------------------------------------------------------------------
 # the product path's step: an HBM store, its row pool and the step context
 
@@ -499,6 +538,7 @@ def decode_main(args, w, t, device):
     kv_bytes = wl.decode_bytes(w)
     gbs = kv_bytes / (ms * 1e-3) / 1e9
     kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
+    read_gbs = sustained_read_gbs(device, kv_bytes)
     return {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -536,6 +576,8 @@ def decode_main(args, w, t, device):
             "traffic": measured_traffic(w.name),
             "kernel_ms": round(kernel_ms, 5),
             "algorithmic_bytes": kv_bytes,
+            "sustained_read_gbs": round(read_gbs, 1),
+            "frac_of_sustained": round(kernel_gbs / read_gbs, 4),
         },
     }
 
@@ -675,15 +717,18 @@ def decode_config_line(args, w, t, device):
                   args.steps, args.warmup, stream)
     kv_bytes = wl.decode_bytes(w)
     gbs = kv_bytes / (ms * 1e-3) / 1e9
+    kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
+    read_gbs = sustained_read_gbs(device, kv_bytes)
     line = {
         "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "ms_per_step": round(ms, 5), "tokens_per_s": round(w.num_query_tokens / (ms * 1e-3), 1), "dtype": "bf16",
         "partition": step.partition_size, "config": workload_config(w),
         "roofline": {"bound": "hbm", "kernel": "decode_partition_kernel",
-                     "achieved": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kv_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(w.name),
-                     "kernel_ms": round(kernel_ms, 5), "algorithmic_bytes": kv_bytes},
+                     "kernel_ms": round(kernel_ms, 5), "algorithmic_bytes": kv_bytes,
+                     "sustained_read_gbs": round(read_gbs, 1), "frac_of_sustained": round(kernel_gbs / read_gbs, 4)},
     }
     if not args.no_cpu_baseline:
         defer_cpu(lambda: cpu_baseline_per_sequence(w, t, args.cpu_budget / 2), line, "cpu_baseline")
@@ -749,6 +794,7 @@ def mixed_line(args, w, t, device):
     att2, full2 = paired_ms(attention_only, whole, pair_steps, stream)
     sustained = sustained_mfma_tflops(device)
     kv_bytes = wl.decode_bytes(w)
+    read_gbs = sustained_read_gbs(device, kv_bytes)
     pf = wl.prefill_flops(w)
     line = {
         "value": round(w.num_query_tokens / (ms * 1e-3), 1), "unit": "tokens/s",
@@ -760,7 +806,9 @@ def mixed_line(args, w, t, device):
         "decode": {"kernel": "decode_partition_kernel", "kernel_ms": round(decode_kernel_ms, 5),
                    "gbs": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9, 2),
                    "hbm_frac": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                   "traffic": measured_traffic(w.name), "algorithmic_bytes": kv_bytes},
+                   "traffic": measured_traffic(w.name), "algorithmic_bytes": kv_bytes,
+                   "sustained_read_gbs": round(read_gbs, 1),
+                   "frac_of_sustained": round(kv_bytes / (decode_kernel_ms * 1e-3) / 1e9 / read_gbs, 4)},
         "prefill": {"kernel": "prefill_kernel", "gflop": round(pf / 1e9, 2), "kernel_ms": round(prefill_ms, 5),
                     "tflops": round(pf / (prefill_ms * 1e-3) / 1e12, 1),
                     "mfma_frac": round(pf / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -881,6 +929,8 @@ def main() -> int:
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
     ap.add_argument("--calibrate-mfma", action="store_true",
                     help="only measure the sustained bf16 MFMA rate (pa_calibrate_mfma)")
+    ap.add_argument("--calibrate-read", action="store_true",
+                    help="only measure the sustained read rate for 1-8 GiB (pa_calibrate_read)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU sharding "
@@ -895,6 +945,10 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.calibrate_copy:
         calibrate_copy(device)
+        return 0
+    if args.calibrate_read:
+        rates = {f"{gib}GiB": round(sustained_read_gbs(device, gib << 30), 1) for gib in (1, 2, 4, 8)}
+        print(json.dumps({"read_gbs_sustained": rates, "nominal_gbs": HBM_PEAK_GBS}), flush=True)
         return 0
     if args.calibrate_mfma:
         tf = sustained_mfma_tflops(device)

@@ -570,6 +570,14 @@ int pa_calibrate_mfma(float *out, int32_t workgroups, int32_t iters, int32_t val
                       void *stream);
 int64_t pa_calibrate_mfma_flops(int32_t workgroups, int32_t iters);
 
+/* Measurement aid, no counterpart in the reference: `workgroups` x 256
+ * threads read `bytes` (a multiple of 16) of device memory at `data` once,
+ * with 16-byte non-temporal loads.  `out` (16 bytes, device) is written only
+ * when the XOR of everything read equals 0x9e3779b9.  Timing the launch
+ * gives the read rate the device sustains, against which an HBM-bound
+ * kernel's rate can be read besides the nominal peak. */
+int pa_calibrate_read(const void *data, int64_t bytes, void *out, int32_t workgroups, void *stream);
+
 const char *pa_error_string(int code);
 const char *pa_last_error_message(void);
 /* ABI version: bumped whenever a signature or a struct above changes. */

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpaged_attention_amd.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "pa_map_host_memory",
     "pa_calibrate_mfma",
     "pa_calibrate_mfma_flops",
+    "pa_calibrate_read",
     "pa_error_string",
     "pa_last_error_message",
     "pa_abi_version",
@@ -179,6 +180,7 @@ _SIGNATURES = {
     "pa_plan_step": (ctypes.c_int, [_vp, _vp, _vp, _i32, PaPlanParams, ctypes.POINTER(PaStepPlan)]),
     "pa_calibrate_mfma": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp]),
     "pa_calibrate_mfma_flops": (ctypes.c_int64, [_i32, _i32]),
+    "pa_calibrate_read": (ctypes.c_int, [_vp, _i64, _vp, _i32, _vp]),
     "pa_reshape_and_cache": (
         ctypes.c_int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],

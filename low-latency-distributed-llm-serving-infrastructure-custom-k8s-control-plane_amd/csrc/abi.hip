@@ -141,7 +141,7 @@ int scratch_address(void** out, const char* who) {
 
 extern "C" {
 
-int pa_abi_version(void) { return 12; }
+int pa_abi_version(void) { return 13; }
 
 const char* pa_error_string(int code) {
   switch (code) {

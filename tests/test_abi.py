@@ -126,6 +126,10 @@ def test_invalid_arguments_rejected_before_launch():
     assert b"valu_per_mfma" in lib.pa_last_error_message()
     assert lib.pa_calibrate_mfma_flops(512, 4096) == 512 * 8 * 4096 * 2 * 32768
     assert lib.pa_calibrate_mfma_flops(0, 4096) == 0
+    for data, nbytes, out, wgs in ((None, 64, 0x1000, 4), (0x1000, 24, 0x1000, 4), (0x1008, 64, 0x1000, 4),
+                                   (0x1000, 64, None, 4), (0x1000, 64, 0x1000, 0)):
+        assert lib.pa_calibrate_read(data, nbytes, out, wgs, None) == native.PA_ERR_INVALID_ARGUMENT
+    assert b"pa_calibrate_read" in lib.pa_last_error_message()
     for direction in (-1, 2):
         rc = lib.pa_swap_blocks(None, None, None, 1, 1, 1, 1, 16, direction, None)
         assert rc == native.PA_ERR_INVALID_ARGUMENT and b"direction" in lib.pa_last_error_message()
