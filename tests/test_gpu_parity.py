@@ -836,6 +836,27 @@ def test_prefill_append_equals_write_then_prefill(device, hq, hkv, d, dtype, bs,
     assert torch.equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_writes_on_the_second_layer(device, dtype):
+    """The fused writes (prefill and decode) address the layer they are given:
+    on a two-layer cache, writing layer 1 leaves layer 0 untouched and gives
+    the same layer-1 bytes and output bits as the cache-write kernel."""
+    base = wl.prefill_chunks("two_layers", [0, 300, 57], [90, 40, 1], dtype, 16, 4, 128)
+    w = wl.StepWorkload("two_layers", 16, 4, 128, 16, dtype, 1.0, base.start_positions, base.new_token_counts,
+                        base.block_lists, base.total_blocks, num_layers=2)
+    t = wl.make_tensors(w, device, seed=6)
+    step = pack_workload(w, device)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 1)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 1, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 1, step, w.scaling, new_key=t.new_keys, new_value=t.new_values,
+                        fused_prefill_write=True)
+    torch.cuda.synchronize()
+    assert not step.__dict__.get("_no_append")
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
 def test_fp32_steps_write_prefill_rows_with_the_cache_write_kernel(device):
     """By default an fp32 step with prefill tokens writes its rows with the
     cache-write kernel and runs the plain launches (its fused prefill write
