@@ -122,8 +122,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   constexpr int kQRowsPerWave = kPrefillRows / kPrefillWaves;
   constexpr int kQDmaPerWave = kQRowsPerWave / kRowsPerDma;
   static_assert(kQRowsPerWave % kRowsPerDma == 0 && kPrefillRows * ROW_BYTES <= 2 * kRegion, "query tile");
-  constexpr int kMergeChunks = 4 * DB + 1;  // 16-byte pieces of a lane's acc + (m, l)
-  constexpr int kOutBase = 4 * kMergeChunks * kWave * 16;  // finished rows, after the merge regions
+  static_assert(DB % 2 == 0, "the two halves finish half of the d blocks each");
+  constexpr int kHalfDB = DB / 2;                      // d blocks each half of a row group finishes
+  constexpr int kMergeChunks = 4 * kHalfDB + 1;        // 16-byte pieces a lane hands over: acc + (m, l)
+  constexpr int kOutBase = 8 * kMergeChunks * kWave * 16;  // finished rows, after the 8 merge regions
   static_assert(kOutBase + kPrefillRows * ROW_BYTES <= kIdBase, "merge scratch and finished rows must fit");
   static_assert(kVReads % KS == 0, "V^T reads spread over the QK k-steps");
 
@@ -203,14 +205,19 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
   // k_off plus a wave-uniform row shift.
   const int q_shift = kQBase + (rg - kh) * 32 * ROW_BYTES;
   const int li = lane & 15;
-  int v_off[2][DB];  // [8-row half][d block]; +16 rows per k-step is added below
+  // The waves of context half 1 keep their d blocks rotated by DB / 2:
+  // register block b holds d block (b + kh DB / 2) mod DB, so that at the
+  // merge blocks 0 .. DB / 2 - 1 are the ones a wave finishes itself, in
+  // both halves, with indices fixed at compile time.
+  int v_off[2][DB];  // [8-row half][register block]; +16 rows per k-step is added below
 #pragma unroll
   for (int hi = 0; hi < 2; ++hi) {
     const int r = kh * kKvTile + 4 * half + (li >> 2) + 8 * hi;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int b = 0; b < DB; ++b) {
+      const int db = (b + kh * (DB / 2)) % DB;
       const int col = 16 * ((lane >> 4) & 1) + 4 * (li & 3) + 32 * db;  // element
-      v_off[hi][db] = kVBase + r * ROW_BYTES + (((col >> 3) ^ chunk_swizzle<CHUNKS>(r)) * 16) + (col & 7) * 2;
+      v_off[hi][b] = kVBase + r * ROW_BYTES + (((col >> 3) ^ chunk_swizzle<CHUNKS>(r)) * 16) + (col & 7) * 2;
     }
   }
   auto read_k = [&](int slot, uint4* ka) {
@@ -776,81 +783,89 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillArgs a)
 
       // ---- merge the two context halves of every row group -----------------
       // (after the last step's barrier no wave reads the rings any more)
-      // Wave (rg, 1) hands its accumulator and (m, l) to wave (rg, 0) in
-      // 16-byte pieces (piece c of lane i at (c * 64 + i) * 16 of the row
-      // group's region), which reads them back a d block (four pieces) at a
-      // time.
+      // Half kh of a row group finishes d blocks [kh DB/2, (kh + 1) DB/2) of
+      // its rows: each wave hands the other half of its row group the blocks
+      // that half finishes, and its (m, l), in 16-byte pieces (piece c of lane
+      // i at (c * 64 + i) * 16 of its own region), reads the other's back a d
+      // block (four pieces) at a time, and stores its half of every row.
+      // With the rotated d blocks, register blocks 0 .. DB / 2 - 1 are the
+      // ones a wave finishes and the rest are handed over, in both halves.
       {
-        char* region = s_lds + rg * kMergeChunks * kWave * 16 + lane * 16;
-        if (kh == 1) {
+        char* mine = s_lds + (rg * 2 + kh) * kMergeChunks * kWave * 16 + lane * 16;
+        const char* other = s_lds + (rg * 2 + (kh ^ 1)) * kMergeChunks * kWave * 16 + lane * 16;
 #pragma unroll
-          for (int db = 0; db < DB; ++db)
+        for (int b = 0; b < kHalfDB; ++b) {
+          const f32x16& x = acc[kHalfDB + b];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              st16(region + (db * 4 + q) * kWave * 16,
-                   make_uint4(__float_as_uint(acc[db][4 * q + 0]), __float_as_uint(acc[db][4 * q + 1]),
-                              __float_as_uint(acc[db][4 * q + 2]), __float_as_uint(acc[db][4 * q + 3])));
-          st16(region + (4 * DB) * kWave * 16, make_uint4(__float_as_uint(m), __float_as_uint(l), 0u, 0u));
+          for (int q = 0; q < 4; ++q) {
+            st16(mine + (b * 4 + q) * kWave * 16,
+                 make_uint4(__float_as_uint(x[4 * q + 0]), __float_as_uint(x[4 * q + 1]),
+                            __float_as_uint(x[4 * q + 2]), __float_as_uint(x[4 * q + 3])));
+          }
         }
+        st16(mine + (4 * kHalfDB) * kWave * 16, make_uint4(__float_as_uint(m), __float_as_uint(l), 0u, 0u));
         __syncthreads();
-        if (kh == 0) {
-          const uint4 ml = ld16(region + (4 * DB) * kWave * 16);
-          const float m2 = __uint_as_float(ml.x);
-          const float l2 = __uint_as_float(ml.y);
-          const float mm = fmaxf(m, m2);
-          const float a1 = fast_exp2((m - mm) * scale);
-          const float a2 = fast_exp2((m2 - mm) * scale);
-          const float lt = l * a1 + l2 * a2;
-          const float inv = lt > 0.f ? 1.f / lt : 0.f;
-          // The finished rows go through LDS (swizzled like the K rows) so that
-          // each store writes whole rows: lane i stores 16 bytes of row
-          // k kRowsPerStore + i / CHUNKS of the row group.
-          char* stage_rows = s_lds + kOutBase + rg * 32 * ROW_BYTES;
-          int r_lane = lane;  // (kept inside the unit loop, as the copies' rows above)
-          asm volatile("" : "+v"(r_lane));
-          const int r32w = r_lane & 31;
-          const int sw_w = chunk_swizzle<CHUNKS>(r32w);
+        const uint4 ml = ld16(other + (4 * kHalfDB) * kWave * 16);
+        const float m2 = __uint_as_float(ml.x);
+        const float l2 = __uint_as_float(ml.y);
+        const float mm = fmaxf(m, m2);
+        const float a1 = fast_exp2((m - mm) * scale);
+        const float a2 = fast_exp2((m2 - mm) * scale);
+        // (the same sum, in the same order, in both halves)
+        const float lt = kh == 0 ? l * a1 + l2 * a2 : l2 * a2 + l * a1;
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        // The finished rows go through LDS (swizzled like the K rows) so that
+        // each store writes whole 16-byte pieces of a row: lane i of half kh
+        // stores piece kh CHUNKS/2 + i % (CHUNKS/2) of row k kRowsPerStore +
+        // i / (CHUNKS/2) of the row group.
+        char* stage_rows = s_lds + kOutBase + rg * 32 * ROW_BYTES;
+        int r_lane = lane;  // (kept inside the unit loop, as the copies' rows above)
+        asm volatile("" : "+v"(r_lane));
+        const int r32w = r_lane & 31;
+        const int sw_w = chunk_swizzle<CHUNKS>(r32w);
 #pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            uint4 pv[4];
+        for (int b = 0; b < kHalfDB; ++b) {
+          const int db = kh * kHalfDB + b;
+          const f32x16& x = acc[b];
+          uint4 pv[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) pv[q] = ld16(region + (db * 4 + q) * kWave * 16);
+          for (int q = 0; q < 4; ++q) pv[q] = ld16(other + (b * 4 + q) * kWave * 16);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              uint2 w;
-              w.x = pack_half2<T>((acc[db][4 * q + 0] * a1 + __uint_as_float(pv[q].x) * a2) * inv,
-                                  (acc[db][4 * q + 1] * a1 + __uint_as_float(pv[q].y) * a2) * inv);
-              w.y = pack_half2<T>((acc[db][4 * q + 2] * a1 + __uint_as_float(pv[q].z) * a2) * inv,
-                                  (acc[db][4 * q + 3] * a1 + __uint_as_float(pv[q].w) * a2) * inv);
-              *reinterpret_cast<uint2*>(stage_rows + r32w * ROW_BYTES + (((db * 4 + q) ^ sw_w) * 16) + half * 8) = w;
-            }
+          for (int q = 0; q < 4; ++q) {
+            uint2 w;
+            w.x = pack_half2<T>((x[4 * q + 0] * a1 + __uint_as_float(pv[q].x) * a2) * inv,
+                                (x[4 * q + 1] * a1 + __uint_as_float(pv[q].y) * a2) * inv);
+            w.y = pack_half2<T>((x[4 * q + 2] * a1 + __uint_as_float(pv[q].z) * a2) * inv,
+                                (x[4 * q + 3] * a1 + __uint_as_float(pv[q].w) * a2) * inv);
+            *reinterpret_cast<uint2*>(stage_rows + r32w * ROW_BYTES + (((db * 4 + q) ^ sw_w) * 16) + half * 8) = w;
           }
-          constexpr int kRowsPerStore = kWave / CHUNKS;
-          const int c = r_lane % CHUNKS;
-          int r32 = r_lane / CHUNKS;  // row of the row group this lane stores
-          int og = (rg * 32 + r32) / MTOK;
-          int otok = rg * 32 + r32 - og * MTOK;
-          // All of the lane's pieces are read before the first store (one LDS
-          // round trip, not one per store).
-          uint4 piece[32 / kRowsPerStore];
+        }
+        constexpr int kHalfChunks = CHUNKS / 2;
+        constexpr int kRowsPerStore = kWave / kHalfChunks;
+        const int c = kh * kHalfChunks + r_lane % kHalfChunks;
+        int r32 = r_lane / kHalfChunks;  // row of the row group this lane stores
+        int og = (rg * 32 + r32) / MTOK;
+        int otok = rg * 32 + r32 - og * MTOK;
+        // All of the lane's pieces are read before the first store (one LDS
+        // round trip, not one per store); they are this wave's own writes.
+        uint4 piece[32 / kRowsPerStore];
 #pragma unroll
-          for (int k = 0; k < 32 / kRowsPerStore; ++k) {
-            const int rk = r32 + k * kRowsPerStore;
-            piece[k] = *reinterpret_cast<const uint4*>(stage_rows + rk * ROW_BYTES + ((c ^ chunk_swizzle<CHUNKS>(rk)) * 16));
-          }
+        for (int k = 0; k < 32 / kRowsPerStore; ++k) {
+          const int rk = r32 + k * kRowsPerStore;
+          piece[k] = *reinterpret_cast<const uint4*>(stage_rows + rk * ROW_BYTES + ((c ^ chunk_swizzle<CHUNKS>(rk)) * 16));
+        }
 #pragma unroll
-          for (int k = 0; k < 32 / kRowsPerStore; ++k) {
-            const uint4 v = piece[k];
-            if (otok < ntok && og < G && (!MASKD || c * 8 < DM)) {
-              uint16_t* dst = reinterpret_cast<uint16_t*>(a.output) +
-                              (static_cast<int64_t>(first + tok0 + otok) * (hkv * a.group) + h0 + og) *
-                                  static_cast<int64_t>(DM) +
-                              c * 8;
-              st16(dst, v);
-            }
-            otok += kRowsPerStore;
-            if (otok >= MTOK) { otok -= MTOK; ++og; }
+        for (int k = 0; k < 32 / kRowsPerStore; ++k) {
+          const uint4 v = piece[k];
+          if (otok < ntok && og < G && (!MASKD || c * 8 < DM)) {
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.output) +
+                            (static_cast<int64_t>(first + tok0 + otok) * (hkv * a.group) + h0 + og) *
+                                static_cast<int64_t>(DM) +
+                            c * 8;
+            st16(dst, v);
           }
+          otok += kRowsPerStore;
+          if (otok >= MTOK) { otok -= MTOK; ++og; }
         }
       }
       // The next unit's copies overwrite the merge scratch.
