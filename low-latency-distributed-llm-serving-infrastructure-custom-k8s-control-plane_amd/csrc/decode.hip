@@ -379,12 +379,28 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   const int part = a.items[2 * item + 1];
   const int64_t trow = a.rows != nullptr ? a.rows[seq] : seq;
   const bool row_ok = trow >= 0 && trow < a.num_table_rows;
-  const int ctx = a.context_lens[seq];
+  int ctx = a.context_lens[seq];
+  int64_t qtok = a.cu_seqlens[seq];
   const int p0 = part * a.partition;
-  const int n = max(0, min(a.partition, ctx - p0));
-  const int64_t qtok = a.cu_seqlens[seq];
   const int log2_bs = a.log2_block_size;
   const int bs_mask = (1 << log2_bs) - 1;
+
+  // Block ids covering this partition -> LDS (invalid ids become -1).  The
+  // whole partition's span is read, whatever the context length, so that
+  // the reads do not wait for it (entries past the context are never used);
+  // each thread's first entry is loaded here, beside the context length and
+  // the query token, and stored with the first query piece below.
+  const int first_blk = p0 >> log2_bs;
+  const int nblk = ((p0 + a.partition - 1) >> log2_bs) - first_blk + 1;
+  auto table_entry = [&](int i) {
+    const int col = first_blk + i;
+    return row_ok && col < a.block_table_stride ? a.block_tables[trow * a.block_table_stride + col] : -1;
+  };
+  auto valid_block = [&](int b) { return b < 0 || b >= a.total_blocks ? -1 : b; };
+  const int b0 = tid < nblk ? table_entry(tid) : -1;
+  // (both scalar loads issued before either is waited for: one round trip)
+  asm volatile("" : "+s"(ctx), "+s"(qtok));
+  const int n = max(0, min(a.partition, ctx - p0));
   const int64_t row_stride = static_cast<int64_t>(hkv) * DM;
   const T* kbase = reinterpret_cast<const T*>(a.key_cache) + kvh * DM;
   const T* vbase = reinterpret_cast<const T*>(a.value_cache) + kvh * DM;
@@ -421,53 +437,51 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
     }
   }
 
-  // Block ids covering this partition -> LDS (invalid ids become -1).
-  const int first_blk = p0 >> log2_bs;
-  const int nblk = n > 0 ? ((p0 + n - 1) >> log2_bs) - first_blk + 1 : 0;
-  for (int i = tid; i < nblk; i += kDecodeThreads) {
-    const int col = first_blk + i;
-    int b = -1;
-    if (row_ok && col < a.block_table_stride) {
-      b = a.block_tables[trow * a.block_table_stride + col];
-      if (b < 0 || b >= a.total_blocks) b = -1;
-    }
-    s_blk[i] = b;
-  }
-
   // The G query rows of this KV head -> LDS (read back per tile, one head
   // at a time, so they do not occupy registers across the loop).
   const int lig = lane % L;  // lane within its row group
   const int gi = lane / L;   // row group within the wave
   constexpr int QCHUNKS = G * D / CE;  // 16-byte pieces of the G query rows
   constexpr int HC = D / CE / 2;  // 16-byte pieces of a real head when paired
-  if constexpr (RS) {
-    // Per (position p, lane l) of a row group, the two pieces (l and l + L)
-    // lane l dots at position p: those of query head p ^ (l * HPL), zero past
-    // G.  A lane's reads for p = 0 .. NP-1 are then one base address plus
-    // constants.
-    for (int i = tid; i < 2 * L * NP; i += kDecodeThreads) {
+  constexpr int QN = RS ? 2 * L * NP : QCHUNKS;  // 16-byte pieces staged
+  auto query_piece = [&](int i) -> uint4 {
+    if constexpr (RS) {
+      // Per (position p, lane l) of a row group, the two pieces (l and l + L)
+      // lane l dots at position p: those of query head p ^ (l * HPL), zero
+      // past G.  A lane's reads for p = 0 .. NP-1 are then one base address
+      // plus constants.
       const int piece = i & 1;
       const int ln = (i >> 1) % L;
       const int g = ((i >> 1) / L) ^ (ln * HPL);
       const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
                       static_cast<int64_t>(h0 + min(g, G - 1)) * a.q_head_stride;
-      s_q[i] = (g < G && (!MASKD || ln + piece * L < KPM)) ? ld16(qrow + (ln + piece * L) * CE)
-                                                          : make_uint4(0, 0, 0, 0);
-    }
-  }
-  for (int i = tid; i < (RS ? 0 : QCHUNKS); i += kDecodeThreads) {
-    const int g = i / (D / CE);
-    const int c = i - g * (D / CE);
-    const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
-                    static_cast<int64_t>(h0 + g) * a.q_head_stride;
-    if constexpr (PAIR) {
-      // Query head g belongs to real KV head g / GA of the pair: its D/2
-      // elements go into that half of the row (the other half is never read).
-      s_q[i] = (c / HC) == (g / GA) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
+      return (g < G && (!MASKD || ln + piece * L < KPM)) ? ld16(qrow + (ln + piece * L) * CE)
+                                                        : make_uint4(0, 0, 0, 0);
     } else {
-      s_q[i] = (!MASKD || c < KPM) ? ld16(qrow + c * CE) : make_uint4(0, 0, 0, 0);
+      const int g = i / (D / CE);
+      const int c = i - g * (D / CE);
+      const T* qrow = reinterpret_cast<const T*>(a.query) + qtok * a.q_token_stride +
+                      static_cast<int64_t>(h0 + g) * a.q_head_stride;
+      if constexpr (PAIR) {
+        // Query head g belongs to real KV head g / GA of the pair: its D/2
+        // elements go into that half of the row (the other half is never read).
+        return (c / HC) == (g / GA) ? ld16(qrow + (c % HC) * CE) : make_uint4(0, 0, 0, 0);
+      } else {
+        return (!MASKD || c < KPM) ? ld16(qrow + c * CE) : make_uint4(0, 0, 0, 0);
+      }
     }
+  };
+  // Each thread's first table entry and first query piece are both loaded
+  // before either is stored, so that the two round trips overlap; the rest
+  // (partitions of more than kDecodeThreads blocks, more query pieces than
+  // threads) follow.
+  {
+    const uint4 q0 = tid < QN ? query_piece(tid) : make_uint4(0, 0, 0, 0);
+    if (tid < nblk) s_blk[tid] = valid_block(b0);
+    if (tid < QN) s_q[tid] = q0;
   }
+  for (int i = tid + kDecodeThreads; i < nblk; i += kDecodeThreads) s_blk[i] = valid_block(table_entry(i));
+  for (int i = tid + kDecodeThreads; i < QN; i += kDecodeThreads) s_q[i] = query_piece(i);
   if (append_dst != nullptr) st16(append_dst, append_piece);
   if (append) __threadfence_block();
   __syncthreads();
