@@ -738,9 +738,10 @@ def decode_config_line(args, w, t, device):
 def mixed_line(args, w, t, device):
     """The mixed step: four 512-token prefill chunks + 128 long-context decodes in one
     flattened step: the attention step (prefill + split-K decode), the same
-    step writing the new K/V rows inside its launches, the whole step with
-    packing, the decode kernel's GB/s, and the prefill kernel's TFLOP/s
-    against the bf16 MFMA peak."""
+    step writing its new K/V rows (the product's default: the cache-write
+    kernel ahead of the plain launches; and, paired, inside its launches),
+    the whole step with packing, the decode kernel's GB/s, and the prefill
+    kernel's TFLOP/s against the bf16 MFMA peak."""
     import torch
 
     ops = pkg("paged_ops")
@@ -772,13 +773,12 @@ def mixed_line(args, w, t, device):
                       new_value=t.new_values)
 
     full_ms = timed_ms(whole, max(5, args.steps // 2), 2, stream)
-    # The attention step writing the new K/V rows inside its launches
-    # (pa_prefill_append + pa_decode_append), on the packed step.
+    # The attention step writing the new K/V rows, on the packed step: as the
+    # product does by default for a step with decodes (the cache-write
+    # kernel, then the plain launches).
     write_ms = timed_ms(lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
                                               new_key=t.new_keys, new_value=t.new_values),
                         args.steps, args.warmup, stream)
-    if step.__dict__.get("_no_append"):
-        raise RuntimeError("the mixed step did not take the fused K/V writes")
     # What the K/V write and the packing add to the attention step, each
     # timed in alternation with it (the decode kernel's time drifts by about
     # 1 % between loops run seconds apart, more than the differences).
@@ -789,8 +789,17 @@ def mixed_line(args, w, t, device):
         ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, new_key=t.new_keys,
                       new_value=t.new_values)
 
+    # The rows written inside the launches instead (pa_prefill_append +
+    # pa_decode_append).
+    def with_fused_write():
+        ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, new_key=t.new_keys,
+                      new_value=t.new_values, fused_prefill_write=True)
+
     pair_steps = max(5, args.steps // 2)
     att1, wr1 = paired_ms(attention_only, with_write, pair_steps, stream)
+    att3, fw3 = paired_ms(attention_only, with_fused_write, pair_steps, stream)
+    if step.__dict__.get("_no_append"):
+        raise RuntimeError("the mixed step did not take the fused K/V writes")
     att2, full2 = paired_ms(attention_only, whole, pair_steps, stream)
     sustained = sustained_mfma_tflops(device)
     kv_bytes = wl.decode_bytes(w)
@@ -799,7 +808,9 @@ def mixed_line(args, w, t, device):
     line = {
         "value": round(w.num_query_tokens / (ms * 1e-3), 1), "unit": "tokens/s",
         "ms_per_step": round(ms, 5), "with_kv_write_ms": round(write_ms, 5), "full_step_ms": round(full_ms, 5),
-        "paired": {"kv_write_us": round((wr1 - att1) * 1e3, 2), "pack_and_kv_write_us": round((full2 - att2) * 1e3, 2),
+        "paired": {"kv_write_us": round((wr1 - att1) * 1e3, 2),
+                   "fused_kv_write_us": round((fw3 - att3) * 1e3, 2),
+                   "pack_and_kv_write_us": round((full2 - att2) * 1e3, 2),
                    "attention_ms": round(att1, 5), "with_kv_write_ms": round(wr1, 5), "full_step_ms": round(full2, 5)},
         "full_step_tokens_per_s": round(w.num_query_tokens / (full_ms * 1e-3), 1), "dtype": "bf16",
         "partition": step.partition_size, "config": workload_config(w),

@@ -1093,13 +1093,19 @@ def attention(
     rows are also written into the caches at the step's scatter slots, as
     :func:`reshape_and_cache` does: inside the prefill launch for the
     multi-token sequences (pa_prefill_append) and inside the decode launches
-    for the single-token ones (pa_decode_append).  When either declines the
+    for the single-token ones (pa_decode_append), or by the cache-write
+    kernel ahead of the plain launches.  When a fused launch declines the
     shape, the cache-write kernel writes every row first (rows a fused
     launch already wrote get the same bytes again) and the plain launches
     follow.  ``fused_prefill_write``: whether to write the multi-token rows
-    inside the prefill launch; by default for 16-bit caches only (fp32
-    prefills measured 2-4 % slower with the write inside than after the
-    cache-write kernel).
+    inside the prefill launch.  By default: on a step of prefill chunks
+    alone, for 16-bit caches (fp32 prefills measured 2-4 % slower with the
+    write inside than after the cache-write kernel); on a step with decodes
+    too, never -- there the prefill that follows the long decode launch
+    read its chunks' new rows 5-6 us slower than the same rows from the
+    cache, and the cache-write kernel and plain launches measured 4-5 us
+    cheaper per step than the fused writes.  A decode-only step writes its
+    rows inside the decode launches.
     """
     q, dims = _checked(query, key_cache, value_cache, step)
     out = _output_for(q, key_cache, out)
@@ -1110,7 +1116,7 @@ def attention(
     if new_key is not None:
         k, v = _new_rows(new_key, new_value, key_cache, step)
         if fused_prefill_write is None:
-            fused_prefill_write = key_cache.dtype != torch.float32
+            fused_prefill_write = key_cache.dtype != torch.float32 and not need_decode
         fused = False  # a fused launch wrote rows
         if not step.__dict__.get("_no_append"):
             declined = False

@@ -135,11 +135,13 @@ def _bits(x):
 @pytest.mark.parametrize("seed", range(40))
 def test_random_steps_fused_write_is_bit_exact(device, seed):
     """The new K/V rows written inside the attention launches (pa_prefill_append
-    and pa_decode_append) leave the same cache bytes and give the same output
-    bits as writing them with the cache-write kernel first, on the random
-    steps above (seeds below 28) and the wide ones (28 on), with token-major
-    or head-major new rows, and with a random table entry of a multi-token
-    sequence set outside the pool or to -1."""
+    and pa_decode_append), and by the default policy (which takes the
+    cache-write kernel on a step with both kinds of sequences), leave the
+    same cache bytes and give the same output bits as writing them with the
+    cache-write kernel first, on the random steps above (seeds below 28) and
+    the wide ones (28 on), with token-major or head-major new rows, and with
+    a random table entry of a multi-token sequence set outside the pool or
+    to -1."""
     rng = np.random.Generator(np.random.PCG64(9000 + seed))
     if seed < 28:
         w, partition = random_case(3 * seed + 2)
@@ -163,9 +165,14 @@ def test_random_steps_fused_write_is_bit_exact(device, seed):
     log(f"fused-write seed={seed}: H_q={w.num_query_heads} H_kv={w.num_kv_heads} D={w.head_dim} {w.dtype} "
         f"bs={w.block_size} B={w.num_seqs} prefill items={step.num_prefill_items}")
     kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    kc3, vc3 = t.key_cache.clone(), t.value_cache.clone()
     ops.reshape_and_cache(nk, nv, t.key_cache, t.value_cache, step.scatter_slots, 0)
     want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
     got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=nk, new_value=nv, fused_prefill_write=True)
+    step.__dict__.pop("_no_append", None)  # (a decline above must not steer the default call)
+    got_default = ops.attention(t.query, kc3, vc3, 0, step, w.scaling, new_key=nk, new_value=nv)
     torch.cuda.synchronize()
     assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
     assert torch.equal(_bits(got), _bits(want))
+    assert torch.equal(_bits(kc3), _bits(t.key_cache)) and torch.equal(_bits(vc3), _bits(t.value_cache))
+    assert torch.equal(_bits(got_default), _bits(want))

@@ -768,9 +768,11 @@ def test_decode_append_equals_write_then_decode(device, hq, hkv, d, dtype):
     assert torch.equal(_bits(got), _bits(want))
 
 
-def test_attention_with_new_rows_on_a_mixed_step(device):
+@pytest.mark.parametrize("fused_prefill_write", [True, None])
+def test_attention_with_new_rows_on_a_mixed_step(device, fused_prefill_write):
     """The mixed step (four 512-token chunks + 128 long decodes) given its new
-    rows writes them inside its prefill and decode launches: the same cache
+    rows writes them inside its prefill and decode launches (or, by default,
+    with the cache-write kernel ahead of the plain launches): the same cache
     bytes and output bits as writing them beforehand."""
     w = wl.WORKLOADS["mixed_step"](seed=2)
     t = wl.make_tensors(w, device, seed=2)
@@ -778,9 +780,10 @@ def test_attention_with_new_rows_on_a_mixed_step(device):
     kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
     ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
     want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
-    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values,
+                        fused_prefill_write=fused_prefill_write)
     torch.cuda.synchronize()
-    assert not step.__dict__.get("_no_append"), "a fused write was not taken"
+    assert not step.__dict__.get("_no_append"), "a fused write was declined"
     assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
     assert torch.equal(_bits(got), _bits(want))
 
