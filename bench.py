@@ -308,6 +308,17 @@ def timed_ms(fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+def gpu_spacer():
+    """A spin of about 80 us on the current stream, issued after a timed
+    launch: the host prepares the next launch meanwhile, so that the next
+    start event does not fire on an idle GPU before its launch is queued
+    (for launches of tens of microseconds the host's own preparation would
+    otherwise be counted in them)."""
+    import torch
+
+    torch.cuda._sleep(200_000)
+
+
 def events_ms(launch, timed, steps, warmup, stream):
     """Average duration of the launches `timed()` issues, bracketed by HIP
     events on the launch stream, with `launch()` issued around them."""
@@ -772,7 +783,7 @@ def mixed_line(args, w, t, device):
         lambda: None,
         lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out, phases=1),
         args.steps, 120, stream)
-    prefill_ms = events_ms(lambda: None,
+    prefill_ms = events_ms(gpu_spacer,
                            lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                            args.steps, 20, stream)
 
@@ -870,11 +881,11 @@ def prefill_shapes_line(args, device):
                              num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads,
                              head_dim=w.head_dim, dtype=w.dtype)
         out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
-        ms = events_ms(lambda: None,
+        ms = events_ms(gpu_spacer,
                        lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                        args.steps, 20, stream)
         # The same launch writing the chunks' new K/V rows (pa_prefill_append).
-        app_ms = events_ms(lambda: None,
+        app_ms = events_ms(gpu_spacer,
                            lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
                                                  new_key=t.new_keys, new_value=t.new_values,
                                                  fused_prefill_write=True),
