@@ -49,8 +49,12 @@ the same launch writing the chunks' new K/V rows, and the whole step with
 its write from HIP graphs, the cache-write kernel then the prefill against
 the fused launch (--shape NAME: one of them).
 
+--ab-library PATH [--ab-rounds N] times the workload's kernels and step in
+alternation with another build of the library (csrc/build.py --rev REV
+--out PATH builds one from a git revision) and prints one comparison line.
+
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
-                [--calibrate-read]
+                [--calibrate-read] [--ab-library PATH [--ab-rounds N]]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
                             prefill_shapes]
 """
@@ -58,6 +62,7 @@ python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--c
 from __future__ import annotations
 
 import argparse
+import contextlib
 import importlib
 import json
 import os
@@ -943,6 +948,81 @@ def config_in_child(args, workload: str) -> dict:
     return json.loads([ln for ln in proc.stdout.splitlines() if ln.startswith("{")][-1])
 
 
+def ab_line(args, device):
+    """The workload's kernel and step times under the in-tree library ("a") and
+    under another build of it ("b", --ab-library), in args.ab_rounds
+    alternating rounds on the same tensors and packed step (each round:
+    every measure under a, then under b).  Decode workloads: the partition
+    kernel (HIP events) and the decode step; fp32_mha_decode: the step from
+    a HIP graph over rotated pool copies; mixed_step: the attention step and
+    its decode and prefill kernels; prefill_shapes (--shape, or all): the
+    prefill kernel of each shape."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    native = pkg("_native")
+    stream = torch.cuda.current_stream(device)
+    measures = {}  # name -> () -> ms
+
+    def packed(w, **kw):
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        return ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                             prefill_tile=ops.prefill_tile_for(w.num_query_heads, w.num_kv_heads),
+                             num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                             dtype=w.dtype, **kw)
+
+    keep = []
+    if args.workload == "prefill_shapes":
+        for name, (starts, counts, dtype) in wl.PREFILL_SHAPES.items():
+            if args.shape is not None and name != args.shape:
+                continue
+            w = wl.prefill_chunks(name, starts, counts, dtype, seed=args.seed)
+            t = wl.make_tensors(w, device, seed=args.seed)
+            step = packed(w)
+            out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+            keep.append((t, step, out))
+            measures[f"{name}.prefill_kernel_ms"] = (
+                lambda t=t, step=step, out=out, w=w: events_ms(
+                    gpu_spacer, lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                    args.steps, 20, stream))
+    elif args.workload == "fp32_mha_decode":
+        w = wl.WORKLOADS[args.workload](seed=args.seed)
+        args.no_cpu_baseline = True
+        measures["step_ms"] = lambda: decode_rotated(args, w, device)["ms_per_step"]
+    elif args.workload in ("llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step"):
+        w = wl.WORKLOADS[args.workload](seed=args.seed)
+        t = wl.make_tensors(w, device, seed=args.seed)
+        step = packed(w)
+        out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+        keep.append((t, step, out))
+        measures["decode_kernel_ms"] = lambda: events_ms(
+            lambda: None, lambda: ops.decode(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
+                                             phases=1), args.steps, 100, stream)
+        measures["step_ms"] = lambda: timed_ms(
+            lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+            args.steps, args.warmup, stream)
+        if args.workload == "mixed_step":
+            measures["prefill_kernel_ms"] = lambda: events_ms(
+                gpu_spacer, lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+                args.steps, 20, stream)
+    else:
+        raise SystemExit(f"--ab-library does not cover {args.workload}")
+
+    other = str(Path(args.ab_library).resolve())
+    got = {name: {"a": [], "b": []} for name in measures}
+    for _ in range(args.ab_rounds):
+        for side in ("a", "b"):
+            ctx = native.use_library(other) if side == "b" else contextlib.nullcontext()
+            with ctx:
+                for name, fn in measures.items():
+                    got[name][side].append(round(fn(), 5))
+    summary = {name: {"a_median": median(v["a"]), "b_median": median(v["b"]), "a": v["a"], "b": v["b"]}
+               for name, v in got.items()}
+    return {"ab": {"workload": args.workload, "a": str(native.LIBRARY_PATH), "b": other, "rounds": args.ab_rounds,
+                   "steps": args.steps, "metrics": summary}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -964,6 +1044,10 @@ def main() -> int:
                     help="only measure the sustained bf16 MFMA rate (pa_calibrate_mfma)")
     ap.add_argument("--calibrate-read", action="store_true",
                     help="only measure the sustained read rate for 1-8 GiB (pa_calibrate_read)")
+    ap.add_argument("--ab-library", default=None,
+                    help="time the workload's kernels in alternation with this other build of the library "
+                         "(csrc/build.py --rev REV --out PATH) and print one comparison line")
+    ap.add_argument("--ab-rounds", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU sharding "
@@ -991,6 +1075,9 @@ def main() -> int:
                           "mfma_tflops_with_fp32_fmas_per_mfma": mixed}), flush=True)
         return 0
 
+    if args.ab_library is not None:
+        print(json.dumps(ab_line(args, device)), flush=True)
+        return 0
     if args.workload == "prefill_shapes":
         print(json.dumps(prefill_shapes_line(args, device)), flush=True)
         return 0

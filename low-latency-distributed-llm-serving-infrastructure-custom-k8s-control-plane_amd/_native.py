@@ -9,6 +9,7 @@ GPU operation of the package raises with it.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from pathlib import Path
@@ -225,6 +226,7 @@ _SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
+_others: dict = {}  # other builds opened by use_library, by path
 
 
 def library_built() -> bool:
@@ -242,16 +244,43 @@ def load_library():
                 f"HIP extension {LIBRARY_PATH.name} is not built; run __graft_entry__.build() "
                 "(or csrc/build.py) before using the GPU paged-attention path"
             )
-        lib = ctypes.CDLL(str(LIBRARY_PATH))
-        for name, (restype, argtypes) in _SIGNATURES.items():
-            fn = getattr(lib, name)
-            fn.restype = restype
-            fn.argtypes = argtypes
-        version = lib.pa_abi_version()
-        if version != ABI_VERSION:
-            raise RuntimeError(f"{LIBRARY_PATH.name} has ABI version {version}, expected {ABI_VERSION}")
-        _lib = lib
-        return lib
+        _lib = _open(LIBRARY_PATH)
+        return _lib
+
+
+def _open(path: Path):
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.pa_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    return lib
+
+
+@contextlib.contextmanager
+def use_library(path):
+    """A measurement aid: inside the block, :func:`load_library` returns the
+    build of the library at ``path`` (same ABI version) instead of the
+    in-tree one, so that two builds (``csrc/build.py --rev``) can be timed
+    in alternation in one process (``bench.py --ab-library``).  Values the
+    package caches from the library (launch-shape queries) stay those of the
+    in-tree build, so both builds run the same launch shapes."""
+    global _lib
+    key = str(Path(path).resolve())
+    load_library()
+    with _lock:
+        other = _others.get(key)
+        if other is None:
+            other = _others[key] = _open(Path(key))
+        saved, _lib = _lib, other
+    try:
+        yield other
+    finally:
+        with _lock:
+            _lib = saved
 
 
 def check(status: int, what: str) -> None:

@@ -8,11 +8,13 @@ what ``_native.load_library`` opens.  ``python csrc/build.py`` or
 
 from __future__ import annotations
 
+import argparse
 import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 CSRC = Path(__file__).resolve().parent
@@ -87,6 +89,33 @@ def build(verbose: bool = False) -> Path:
     return LIBRARY_PATH
 
 
+def build_revision(rev: str, out: Path) -> Path:
+    """Build the library from the sources of git revision ``rev`` into
+    ``out`` (a measurement aid: ``bench.py --ab-library out`` times it in
+    alternation with the in-tree build).  The revision's own build script
+    compiles its own tree, extracted with ``git archive`` into a temporary
+    directory."""
+    out = Path(out).resolve()
+    with tempfile.TemporaryDirectory() as tmp:
+        archive = subprocess.run(["git", "-C", str(REPO_ROOT), "archive", rev], capture_output=True, check=True)
+        subprocess.run(["tar", "-x", "-C", tmp], input=archive.stdout, check=True)
+        script = Path(tmp) / PACKAGE_DIR.name / "csrc" / "build.py"
+        proc = subprocess.run([sys.executable, str(script)], capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"building {rev} failed:\n{proc.stdout}\n{proc.stderr}")
+        shutil.copy2(Path(tmp) / PACKAGE_DIR.name / LIBRARY_NAME, out)
+    return out
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--rev", help="build this git revision's sources instead of the tree's")
+    ap.add_argument("--out", help="with --rev: where to put the library")
+    args = ap.parse_args()
+    if args.rev:
+        if not args.out:
+            ap.error("--rev needs --out")
+        print(f"built {build_revision(args.rev, Path(args.out))}")
+    else:
+        build(verbose=True)
     sys.exit(0)

@@ -5,6 +5,7 @@ version and argument checks that return before any HIP call."""
 
 import ctypes
 import re
+import shutil
 import subprocess
 from pathlib import Path
 
@@ -34,6 +35,21 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(raw, name), name
     assert lib.pa_abi_version() == native.ABI_VERSION
+
+
+def test_use_library_swaps_and_restores(tmp_path):
+    """The A/B measurement aid: inside use_library(path), load_library()
+    returns the build at path (here a copy of the in-tree one), typed and
+    version-checked; outside, the in-tree library again."""
+    native = pkg("_native")
+    lib = native.load_library()
+    other_path = tmp_path / "libpaged_attention_amd_copy.so"
+    shutil.copy2(native.LIBRARY_PATH, other_path)
+    with native.use_library(other_path) as other:
+        assert native.load_library() is other and other is not lib
+        assert other.pa_abi_version() == native.ABI_VERSION
+        assert other.pa_decode_workspace_size.argtypes == lib.pa_decode_workspace_size.argtypes
+    assert native.load_library() is lib
 
 
 def test_struct_layouts(tmp_path):
