@@ -953,7 +953,8 @@ def ab_line(args, device):
     under another build of it ("b", --ab-library), in args.ab_rounds
     alternating rounds on the same tensors and packed step (each round:
     every measure under a, then under b).  Decode workloads: the partition
-    kernel (HIP events) and the decode step; fp32_mha_decode: the step from
+    kernel (HIP events), the decode step, and the step writing its new K/V
+    rows; fp32_mha_decode: the step from
     a HIP graph over rotated pool copies; mixed_step: the attention step and
     its decode and prefill kernels; prefill_shapes (--shape, or all): the
     prefill kernel of each shape."""
@@ -1001,6 +1002,11 @@ def ab_line(args, device):
                                              phases=1), args.steps, 100, stream)
         measures["step_ms"] = lambda: timed_ms(
             lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
+            args.steps, args.warmup, stream)
+        # The same step writing its new K/V rows (the product's default way).
+        measures["step_with_kv_write_ms"] = lambda: timed_ms(
+            lambda: ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out,
+                                  new_key=t.new_keys, new_value=t.new_values),
             args.steps, args.warmup, stream)
         if args.workload == "mixed_step":
             measures["prefill_kernel_ms"] = lambda: events_ms(

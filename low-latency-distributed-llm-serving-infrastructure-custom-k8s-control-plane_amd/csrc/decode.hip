@@ -340,7 +340,12 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   constexpr int NP = !RS ? 1 : (G <= L ? L : 8);
   constexpr int HPL = RS ? NP / L : 1;
 
-  __shared__ int s_blk[kMaxPartition + 2];
+  // Block ids of the partition; its tail from kParkStart holds the new
+  // token's pieces and their destinations from the staging to the last tile
+  // (pa_decode_append): a 16-byte piece and an 8-byte address per lane.
+  constexpr int kBlkInts = kMaxPartition + 2;
+  constexpr int kParkStart = (kBlkInts - kWave * 6) & ~3;  // 16-byte aligned
+  __shared__ __align__(16) int s_blk[kBlkInts];
   __shared__ uint4 s_q[(RS ? NP : G) * D * S::kE / 16];
   __shared__ uint32_t s_p[kDecodeWaves][PWORDS];
   __shared__ float s_m[kDecodeWaves][G];
@@ -408,31 +413,46 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // pa_decode_append: the workgroups of the partition holding the new token
   // (position ctx - 1) write its K and V rows of this unit (one KV head, or
   // the pair's two) into the cache, as pa_reshape_and_cache would; sibling
-  // sub-groups write the same bytes.  A thread per 16-byte piece loads it
-  // here, so the load overlaps the staging below, and stores it before the
-  // barrier that ends the staging, which orders the stores before this
-  // workgroup's own reads of that position; no other workgroup of the
-  // launch reads it.
+  // sub-groups write the same bytes.  The wave that attends the partition's
+  // last tile (the one holding that position) does it, a lane per 16-byte
+  // piece: it loads the piece here, so the load overlaps the staging below,
+  // parks it in the tail of s_blk (past the partition's block ids) and
+  // stores it in the tile loop just before that tile's loads, with a
+  // barrier of the wave between them, which orders the stores before its
+  // own reads of that position; no other wave or workgroup of the launch
+  // reads it.  (Stored at the top of the launch, the rows were counted by
+  // every later wait of the wave's loads.)  When the block ids leave no
+  // room (one-token blocks and a partition above kMaxPartition - 256), the
+  // pieces are stored before the staging barrier instead, which orders
+  // them before the whole workgroup's reads.
   constexpr int kPieceElems = 16 / static_cast<int>(sizeof(T));
   constexpr int kAppendPieces = DM / kPieceElems;  // 16-byte pieces of the unit's row
-  static_assert(2 * kAppendPieces <= kDecodeThreads, "one piece of K or V per thread");
+  static_assert(2 * kAppendPieces <= kWave, "one piece of K or V per lane of a wave");
   const bool append = a.new_key != nullptr && n > 0 && p0 + n == ctx;
+  const int last_tile = (n + S::kTile - 1) / S::kTile - 1;
+  const int append_wave = append ? last_tile % kDecodeWaves : -1;
+  // Lane l's piece: l < kAppendPieces of K, the rest of V; its element in
+  // the token's row, and where it goes given the block b holding ctx - 1.
+  auto append_elem = [&](int l) { return kvh * DM + (l >= kAppendPieces ? l - kAppendPieces : l) * kPieceElems; };
+  auto append_target = [&](int b, int l) {
+    const int64_t slot = (static_cast<int64_t>(b) << log2_bs) + ((ctx - 1) & bs_mask);
+    return const_cast<T*>(reinterpret_cast<const T*>(l >= kAppendPieces ? a.value_cache : a.key_cache)) +
+           slot * row_stride + append_elem(l);
+  };
   T* append_dst = nullptr;
   uint4 append_piece = make_uint4(0, 0, 0, 0);
-  if (append && tid < 2 * kAppendPieces) {
+  if (wave == append_wave && lane < 2 * kAppendPieces) {
     const int col = (ctx - 1) >> log2_bs;
     const int b = row_ok && col < a.block_table_stride ? a.block_tables[trow * a.block_table_stride + col] : -1;
     if (b >= 0 && b < a.total_blocks) {
-      const bool is_v = tid >= kAppendPieces;
-      const int g = kvh * DM + (is_v ? tid - kAppendPieces : tid) * kPieceElems;  // element in the token's row
+      const bool is_v = lane >= kAppendPieces;
+      const int g = append_elem(lane);  // element in the token's row
       const int h = g / a.head_dim;
       const T* src = reinterpret_cast<const T*>(is_v ? a.new_value : a.new_key) +
                      qtok * (is_v ? a.new_value_token_stride : a.new_key_token_stride) +
                      static_cast<int64_t>(h) * (is_v ? a.new_value_head_stride : a.new_key_head_stride) +
                      (g - h * a.head_dim);
-      const int64_t slot = (static_cast<int64_t>(b) << log2_bs) + ((ctx - 1) & bs_mask);
-      append_dst = const_cast<T*>(reinterpret_cast<const T*>(is_v ? a.value_cache : a.key_cache)) +
-                   slot * row_stride + g;
+      append_dst = append_target(b, lane);
       append_piece = ld16(src);
     }
   }
@@ -482,8 +502,23 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   }
   for (int i = tid + kDecodeThreads; i < nblk; i += kDecodeThreads) s_blk[i] = valid_block(table_entry(i));
   for (int i = tid + kDecodeThreads; i < QN; i += kDecodeThreads) s_q[i] = query_piece(i);
-  if (append_dst != nullptr) st16(append_dst, append_piece);
-  if (append) __threadfence_block();
+  // The new token's pieces: parked past the block ids with their
+  // destinations (null: none), or (no room there) stored now, before the
+  // barrier.
+  uint4* const park_piece = reinterpret_cast<uint4*>(s_blk + kParkStart);
+  T** const park_dst = reinterpret_cast<T**>(s_blk + kParkStart + kWave * 4);
+  const bool park = nblk <= kParkStart;
+  // Whether the last tile's wave stores parked pieces (the array's last
+  // word, past every block id).
+  if (tid == 0) s_blk[kBlkInts - 1] = append && park ? 1 : 0;
+  if (wave == append_wave && lane < 2 * kAppendPieces) {
+    if (park) {
+      park_piece[lane] = append_piece;
+      park_dst[lane] = append_dst;
+    } else if (append_dst != nullptr) {
+      st16(append_dst, append_piece);
+    }
+  }
   __syncthreads();
 
   const float scale = a.scale_log2e;
@@ -908,6 +943,23 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // register budget).
   const int ntiles = (n + kTile - 1) / kTile;
   for (int tile = wave; tile < ntiles; tile += kDecodeWaves) {
+    if (tile == ntiles - 1) {
+      // The new token's parked pieces, stored by the wave that attends the
+      // last tile just before its loads.  (The flag and the pieces are read
+      // here, with the index made opaque, so that nothing of them is held
+      // in registers across the loop.)
+      int l = lane, flag = kBlkInts - 1;
+      asm volatile("" : "+v"(l), "+v"(flag));
+      if (s_blk[flag] != 0) {
+        if (l < 2 * kAppendPieces) {
+          T* const dst = park_dst[l];
+          if (dst != nullptr) st16(dst, park_piece[l]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      }
+    }
     const int blk_lane = tile_blocks(tile);
     // Tile fully inside the partition with every block valid: no masking.
     const bool full = (tile + 1) * kTile <= n && __ballot(lane < kTile && blk_lane < 0) == 0;
