@@ -422,9 +422,9 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
   // own reads of that position; no other wave or workgroup of the launch
   // reads it.  (Stored at the top of the launch, the rows were counted by
   // every later wait of the wave's loads.)  When the block ids leave no
-  // room (one-token blocks and a partition above kMaxPartition - 256), the
-  // pieces are stored before the staging barrier instead, which orders
-  // them before the whole workgroup's reads.
+  // room (more than kParkStart of them: one-token blocks and a partition
+  // above 3712 tokens), the pieces are stored before the staging barrier
+  // instead, which orders them before the whole workgroup's reads.
   constexpr int kPieceElems = 16 / static_cast<int>(sizeof(T));
   constexpr int kAppendPieces = DM / kPieceElems;  // 16-byte pieces of the unit's row
   static_assert(2 * kAppendPieces <= kWave, "one piece of K or V per lane of a wave");

@@ -768,6 +768,41 @@ def test_decode_append_equals_write_then_decode(device, hq, hkv, d, dtype):
     assert torch.equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("bs,partition", [(1, 4096), (1, 2048), (2, 4096)])
+def test_decode_append_with_small_blocks_and_long_partitions(device, bs, partition):
+    """The decode launch's fused write where the partition's block ids fill
+    the LDS that otherwise parks the new rows (one-token blocks, partition
+    4096: the rows are stored before the staging barrier) and where they
+    leave room (the rows parked and stored by the last tile's wave): the
+    same cache bytes and output bits as pa_reshape_and_cache + pa_decode."""
+    rng = np.random.Generator(np.random.PCG64(bs * 7 + partition))
+    hq, hkv, d, dtype = 16, 4, 128, torch.bfloat16
+    ctx = [int(c) for c in rng.integers(1, 9000, size=6)] + [4096, 4097, 1]
+    need = [-(-c // bs) for c in ctx]
+    total = sum(need) + 4
+    perm = rng.permutation(total)
+    lists, off = [], 0
+    for n_ in need:
+        lists.append([int(x) for x in perm[off : off + n_]])
+        off += n_
+    w = wl.StepWorkload("decode_append_small_blocks", hq, hkv, d, bs, dtype, 1.0, [c - 1 for c in ctx],
+                        [1] * len(ctx), lists, total)
+    t = wl.make_tensors(w, device, seed=8)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, bs, partition_size=partition,
+                         num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+    kc2, vc2 = t.key_cache.clone(), t.value_cache.clone()
+    ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+    want = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    got = ops.attention(t.query, kc2, vc2, 0, step, w.scaling, new_key=t.new_keys, new_value=t.new_values)
+    torch.cuda.synchronize()
+    log(f"decode append bs {bs} partition {step.partition_size}: items {step.num_decode_items}")
+    assert step.partition_size == partition
+    assert not step.__dict__.get("_no_append"), "the fused write was not taken"
+    assert torch.equal(_bits(kc2), _bits(t.key_cache)) and torch.equal(_bits(vc2), _bits(t.value_cache))
+    assert torch.equal(_bits(got), _bits(want))
+
+
 @pytest.mark.parametrize("fused_prefill_write", [True, None])
 def test_attention_with_new_rows_on_a_mixed_step(device, fused_prefill_write):
     """The mixed step (four 512-token chunks + 128 long decodes) given its new
