@@ -15,7 +15,9 @@ every output row is compared with the oracle run on the cache the GPU read
 tests).  This covers the combinations the
 fixed-shape tests do not name: paired and unpaired heads of 64 and 128,
 groups that do not divide 128, groups above 8, tiny blocks with short
-partitions, and prefill chunks beside split-K decodes.
+partitions, and prefill chunks beside split-K decodes.  The long cases add
+contexts up to 3000, partitions up to 4096, fp32 heads of 80 and 96 and all
+three ways of writing the new rows, and compare the whole pools bit-exactly.
 """
 
 import numpy as np
@@ -23,6 +25,7 @@ import pytest
 import torch
 
 from helpers import pkg
+from oracle import packing as op
 from test_gpu_parity import check_rows, log, oracle_rows
 
 pytestmark = pytest.mark.gpu
@@ -176,3 +179,78 @@ def test_random_steps_fused_write_is_bit_exact(device, seed):
     assert torch.equal(_bits(got), _bits(want))
     assert torch.equal(_bits(kc3), _bits(t.key_cache)) and torch.equal(_bits(vc3), _bits(t.value_cache))
     assert torch.equal(_bits(got_default), _bits(want))
+
+
+def random_long_case(seed):
+    """Any head dim (64, 80, 96, 128, 256) and dtype (fp32 but for heads of
+    256), a group of 1-16, a block size of 1-64, up to 12 sequences: decodes
+    of contexts up to 3000 and prefill chunks of 2-300 tokens at starts up to
+    1500 (capped so the oracle stays fast), as a mixed, decode-only or
+    prefill-only batch; a split-K partition of automatic or 32-4096 tokens and
+    a K/V write mode: the cache-write kernel first (0), the default policy
+    (1) or the prefill's fused write (2)."""
+    rng = np.random.Generator(np.random.PCG64(77000 + seed))
+    hkv = int(rng.choice([1, 2, 3, 4, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 16]))
+    d = int(rng.choice([64, 128, 128, 256, 80, 96]))
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    if d == 256 and dtype == torch.float32:
+        dtype = torch.bfloat16
+    bs = int(rng.choice([1, 2, 4, 8, 16, 16, 32, 64]))
+    budget = 4e8 / (hkv * group * d)  # sum of n * (start + n) over the batch
+    kind = int(rng.integers(0, 3))  # 0 mixed, 1 decodes only, 2 prefill chunks only
+    starts, counts, cost = [], [], 0
+    for _ in range(int(rng.integers(1, 13))):
+        if kind == 1 or (kind == 0 and rng.random() < 0.6):
+            c = int(rng.integers(1, 3000))
+            s, n = c - 1, 1
+        else:
+            s, n = int(rng.integers(0, 1500)), int(rng.integers(2, 300))
+        if starts and cost + n * (s + n) > budget:
+            break
+        starts.append(s)
+        counts.append(n)
+        cost += n * (s + n)
+    ctx = [s + c for s, c in zip(starts, counts)]
+    need = [-(-c // bs) for c in ctx]
+    pool = sum(need) + int(rng.integers(1, 40))
+    perm = rng.permutation(pool)
+    lists, off = [], 0
+    for n in need:
+        lists.append([int(x) for x in perm[off : off + n]])
+        off += n
+    partition = [None, 32, 64, 128, 256, 512, 1024, 2048, 4096][int(rng.integers(0, 9))]
+    mode = int(rng.integers(0, 3))
+    w = wl.StepWorkload(f"long{seed}", hkv * group, hkv, d, bs, dtype, 1.0, starts, counts, lists, pool)
+    return w, partition, mode
+
+
+@pytest.mark.parametrize("seed", range(200))
+def test_random_long_steps_match_oracle(device, seed):
+    """Every output row against the oracle, and the whole K and V pools
+    against the pools before the step with the new rows placed at the oracle's
+    slots (bit-exact)."""
+    w, partition, mode = random_long_case(seed)
+    log(f"long seed={seed}: H_q={w.num_query_heads} H_kv={w.num_kv_heads} D={w.head_dim} {w.dtype} "
+        f"bs={w.block_size} counts={w.new_token_counts} starts={w.start_positions} partition={partition} "
+        f"mode={mode}")
+    t = wl.make_tensors(w, device, seed=seed)
+    table = torch.from_numpy(w.block_table_array()).to(device)
+    step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                         partition_size=partition, num_kv_heads=w.num_kv_heads,
+                         num_query_heads=w.num_query_heads, head_dim=w.head_dim, dtype=w.dtype)
+    want_k, want_v = t.key_cache.clone(), t.value_cache.clone()
+    if mode == 0:
+        ops.reshape_and_cache(t.new_keys, t.new_values, t.key_cache, t.value_cache, step.scatter_slots, 0)
+        out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling)
+    else:
+        out = ops.attention(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, new_key=t.new_keys,
+                            new_value=t.new_values, fused_prefill_write=True if mode == 2 else None)
+    torch.cuda.synchronize()
+    slots = op.build_slot_mapping(w.block_lists, w.context_lens, w.block_size, w.start_positions,
+                                  w.new_token_counts)
+    idx = torch.as_tensor(slots, dtype=torch.long, device=device)
+    want_k.view(-1, w.num_kv_heads, w.head_dim)[idx] = t.new_keys
+    want_v.view(-1, w.num_kv_heads, w.head_dim)[idx] = t.new_values
+    assert torch.equal(_bits(want_k), _bits(t.key_cache)) and torch.equal(_bits(want_v), _bits(t.value_cache))
+    check_rows(w, out, oracle_rows(w, t, range(w.num_seqs)), fp32=w.dtype == torch.float32)
