@@ -49,6 +49,11 @@ the same launch writing the chunks' new K/V rows, and the whole step with
 its write from HIP graphs, the cache-write kernel then the prefill against
 the fused launch (--shape NAME: one of them).
 
+--workload decode_layers prints, per layer, a model's 32-layer loop over one
+bf16 decode step (16, 64 and 256 sequences; each layer writing its rows
+inside the decode launch) from eager launches and from one HIP graph of the
+32 layers, timed in alternation.
+
 --ab-library PATH [--ab-rounds N] times the workload's kernels and step in
 alternation with another build of the library (csrc/build.py --rev REV
 --out PATH builds one from a git revision) and prints one comparison line.
@@ -56,7 +61,7 @@ alternation with another build of the library (csrc/build.py --rev REV
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
                 [--calibrate-read] [--ab-library PATH [--ab-rounds N]]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
-                            prefill_shapes]
+                            prefill_shapes|decode_layers]
 """
 
 from __future__ import annotations
@@ -928,6 +933,41 @@ def prefill_shapes_line(args, device):
             "steps": args.steps, "shapes": shapes}
 
 
+def decode_layers_line(args, device):
+    """A model's layer loop over one decode step: 32 layers, each writing its
+    new K/V rows inside the decode launch (pa_decode_append) and attending,
+    from eager launches and from one HIP graph of the 32 layers replayed, in
+    alternation (bf16 32/8 heads of 128, contexts of 256-1024 tokens, 16, 64
+    and 256 sequences).  Per-layer microseconds."""
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    stream = torch.cuda.current_stream(device)
+    lines = {}
+    for n in (16, 64, 256):
+        w = wl.decode_layers(n, seed=args.seed)
+        t = wl.make_tensors(w, device, seed=args.seed)
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size,
+                             num_kv_heads=w.num_kv_heads, num_query_heads=w.num_query_heads, head_dim=w.head_dim,
+                             dtype=w.dtype)
+        out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+
+        def layers(_i, t=t, step=step, out=out, w=w):
+            for layer in range(w.num_layers):
+                ops.attention(t.query, t.key_cache, t.value_cache, layer, step, w.scaling, out=out,
+                              new_key=t.new_keys, new_value=t.new_values)
+
+        eager, graph = graph_vs_eager_ms(layers, 20, stream, rounds=5)
+        lines[str(n)] = {"eager_us_per_layer": round(eager * 1e3 / w.num_layers, 2),
+                         "graph_us_per_layer": round(graph * 1e3 / w.num_layers, 2),
+                         "partition": step.partition_size, "context_tokens": w.num_context_tokens}
+        del t, step, out, table
+        torch.cuda.empty_cache()
+    return {"decode_layers": lines, "layers": 32, "unit": "us per layer", "data": "synthetic"}
+
+
 def config_in_child(args, workload: str) -> dict:
     """One `configs` line, measured by this script in a process of its own.
 
@@ -1036,7 +1076,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3_8b_gqa_decode",
                     choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step", "fp32_mha_decode",
-                             "kv_write_pack", "prefill_shapes"])
+                             "kv_write_pack", "prefill_shapes", "decode_layers"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--shape", default=None, help="prefill_shapes: measure only this shape")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1086,6 +1126,9 @@ def main() -> int:
         return 0
     if args.workload == "prefill_shapes":
         print(json.dumps(prefill_shapes_line(args, device)), flush=True)
+        return 0
+    if args.workload == "decode_layers":
+        print(json.dumps(decode_layers_line(args, device)), flush=True)
         return 0
     w = wl.WORKLOADS[args.workload](seed=args.seed)
     if args.workload == "kv_write_pack":

@@ -163,6 +163,17 @@ def prefill_chunks(name: str, starts: List[int], counts: List[int], dtype: torch
                         list(counts), lists, total)
 
 
+def decode_layers(num_seqs: int, num_layers: int = 32, seed: int = 0) -> StepWorkload:
+    """A bf16 decode step of ``num_seqs`` sequences with contexts of 256-1024
+    tokens (uniform) over 32/8 heads of 128, with ``num_layers`` layers of
+    cache: the step a model's layer loop runs once per layer."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    ctx = [int(c) for c in rng.integers(256, 1024, size=num_seqs, endpoint=True)]
+    lists, total = _block_tables(rng, ctx, BLOCK_SIZE)
+    return StepWorkload(f"decode_layers_{num_seqs}", 32, 8, 128, BLOCK_SIZE, torch.bfloat16, 1.0,
+                        [c - 1 for c in ctx], [1] * num_seqs, lists, total, num_layers)
+
+
 # Prefill kernel shapes (32/8 heads, D=128): the mixed step's four 512-token
 # chunks and four chunks deep in their contexts, in both dtypes, and two
 # small prompt steps (one prompt of 128 tokens, eight of 64).
