@@ -54,6 +54,10 @@ bf16 decode step (16, 64 and 256 sequences; each layer writing its rows
 inside the decode launch) from eager launches and from one HIP graph of the
 32 layers, timed in alternation.
 
+--workload decode_partitions prints, for latency-bound decode steps in a
+32-layer loop, the per-layer time of every split-K partition from 64 to 4096
+and the partition pa_plan_step picks.
+
 --ab-library PATH [--ab-rounds N] times the workload's kernels and step in
 alternation with another build of the library (csrc/build.py --rev REV
 --out PATH builds one from a git revision) and prints one comparison line.
@@ -61,7 +65,7 @@ alternation with another build of the library (csrc/build.py --rev REV
 python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--config-line] [--calibrate-mfma]
                 [--calibrate-read] [--ab-library PATH [--ab-rounds N]]
                 [--workload llama3_8b_gqa_decode|llama7b_mha_decode|mixed_step|fp32_mha_decode|kv_write_pack|
-                            prefill_shapes|decode_layers]
+                            prefill_shapes|decode_layers|decode_partitions]
 """
 
 from __future__ import annotations
@@ -968,6 +972,97 @@ def decode_layers_line(args, device):
     return {"decode_layers": lines, "layers": 32, "unit": "us per layer", "data": "synthetic"}
 
 
+def decode_partition_shapes(seed: int = 0):
+    """Latency-bound decode steps (too small to fill the chip): (name, contexts,
+    H_q, H_kv, D, dtype).  bf16 32/8 heads of 128 unless named otherwise."""
+    import numpy as np
+    import torch
+
+    rng = np.random.Generator(np.random.PCG64(3 + seed))
+
+    def draw(lo, hi, n):
+        return [int(c) for c in rng.integers(lo, hi, size=n, endpoint=True)]
+
+    bf = (32, 8, 128, torch.bfloat16)
+    return [
+        ("1x1024", [1024], *bf), ("4x1024", [1024] * 4, *bf), ("16x1024", [1024] * 16, *bf),
+        ("24x1024", [1024] * 24, *bf), ("8x512", [512] * 8, *bf), ("2x2048", [2048] * 2, *bf),
+        ("8x2048", [2048] * 8, *bf), ("64x2048", [2048] * 64, *bf), ("1x4096", [4096], *bf),
+        ("4x4096", [4096] * 4, *bf), ("16x4096", [4096] * 16, *bf), ("2x8192", [8192] * 2, *bf),
+        ("1x16384", [16384], *bf), ("4x16384", [16384] * 4, *bf),
+        ("16x256-1024", draw(256, 1024, 16), *bf), ("64x256-1024", draw(256, 1024, 64), *bf),
+        ("32x300-700", draw(300, 700, 32), *bf), ("32x512-4096", draw(512, 4096, 32), *bf),
+        ("8x1000-8000", draw(1000, 8000, 8), *bf),
+        ("8x16-512 fp32 8/8/64", draw(16, 512, 8), 8, 8, 64, torch.float32),
+        ("4x2048 fp32 32/8/128", [2048] * 4, 32, 8, 128, torch.float32),
+        ("8x1024 bf16 64/8/128", [1024] * 8, 64, 8, 128, torch.bfloat16),
+    ]
+
+
+def decode_partitions_line(args, device):
+    """Latency-bound decode steps in a model's 32-layer loop (every layer's
+    cache read cold, each layer writing its new rows inside the decode
+    launch): per-layer time of each split-K partition from 64 to 4096 from
+    one HIP graph of 10 passes, 7 alternated rounds, medians; beside it the
+    partition pa_plan_step picks and how far it is from the fastest."""
+    import numpy as np
+    import torch
+
+    ops = pkg("paged_ops")
+    wl = pkg("workloads")
+    stream = torch.cuda.current_stream(device)
+    lines = {}
+    for name, ctx, hq, hkv, d, dtype in decode_partition_shapes(args.seed):
+        rng = np.random.Generator(np.random.PCG64(7))
+        lists, total = wl._block_tables(rng, ctx, wl.BLOCK_SIZE)
+        w = wl.StepWorkload(name, hq, hkv, d, wl.BLOCK_SIZE, dtype, 1.0, [c - 1 for c in ctx], [1] * len(ctx),
+                            lists, total, 32)
+        t = wl.make_tensors(w, device, seed=args.seed)
+        table = torch.from_numpy(w.block_table_array()).to(device)
+        out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+        graphs = {}  # partition -> (graph, step): the graph reads the step's buffers, so the step lives as long
+        picked = None
+        for part in [None, 64, 128, 256, 512, 1024, 2048, 4096]:
+            if part is not None and (part > 2 * max(ctx) or part in graphs):
+                continue
+            step = ops.pack_step(table, w.start_positions, w.new_token_counts, w.block_size, partition_size=part,
+                                 num_kv_heads=hkv, num_query_heads=hq, head_dim=d, dtype=dtype)
+            if part is None:
+                picked = step.partition_size
+
+            def layers(step=step):
+                for layer in range(w.num_layers):
+                    ops.attention(t.query, t.key_cache, t.value_cache, layer, step, w.scaling, out=out,
+                                  new_key=t.new_keys, new_value=t.new_values)
+
+            layers()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(10):
+                    layers()
+            g.replay()
+            torch.cuda.synchronize()
+            graphs[step.partition_size] = (g, step)
+        times = {p: [] for p in graphs}
+        for _ in range(7):
+            for p, (g, _step) in graphs.items():
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                g.replay()
+                b.record(stream)
+                torch.cuda.synchronize()
+                times[p].append(a.elapsed_time(b) * 1e3 / (10 * w.num_layers))
+        us = {p: round(median(v), 2) for p, v in sorted(times.items())}
+        fastest = min(us, key=us.get)
+        lines[name] = {"us_per_layer": {str(p): v for p, v in us.items()}, "picked": picked, "fastest": fastest,
+                       "picked_over_fastest": round(us[picked] / us[fastest], 4)}
+        print(f"{name}: picked {picked} ({us[picked]} us), fastest {fastest} ({us[fastest]} us)", flush=True)
+        del graphs, t, out, table
+        torch.cuda.empty_cache()
+    return {"decode_partitions": lines, "layers": 32, "unit": "us per layer", "data": "synthetic"}
+
+
 def config_in_child(args, workload: str) -> dict:
     """One `configs` line, measured by this script in a process of its own.
 
@@ -1076,7 +1171,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3_8b_gqa_decode",
                     choices=["llama3_8b_gqa_decode", "llama7b_mha_decode", "mixed_step", "fp32_mha_decode",
-                             "kv_write_pack", "prefill_shapes", "decode_layers"])
+                             "kv_write_pack", "prefill_shapes", "decode_layers", "decode_partitions"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--shape", default=None, help="prefill_shapes: measure only this shape")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1129,6 +1224,9 @@ def main() -> int:
         return 0
     if args.workload == "decode_layers":
         print(json.dumps(decode_layers_line(args, device)), flush=True)
+        return 0
+    if args.workload == "decode_partitions":
+        print(json.dumps(decode_partitions_line(args, device)), flush=True)
         return 0
     w = wl.WORKLOADS[args.workload](seed=args.seed)
     if args.workload == "kv_write_pack":

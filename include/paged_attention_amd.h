@@ -245,10 +245,12 @@ typedef struct {
  * decode split-K partition when params.partition_size is 0: the largest of
  * 4096 ... 256 tokens whose decode launch (items x workgroups_per_item)
  * gives every resident workgroup slot (compute_units x workgroups_per_cu)
- * one and a half workgroups; failing that (a latency-bound step) the
- * largest partition still giving two thirds of the slots a workgroup with
- * at most 64 partials per sequence, else the smallest of 64, 128, ... that
- * keeps every sequence to 64 partials.
+ * one and a half workgroups; failing that (a latency-bound step) the one of
+ * 64 ... 4096 with the least modelled time: the longest workgroup's read at
+ * 0.049 us per token, slowed by its share of HBM when more than 310
+ * workgroups run at once and multiplied by the waves of workgroups, plus
+ * 3.5 us per batch of 8 split-K partials of the longest sequence (ties to
+ * the shorter partition; 64 for a step without decodes).
  * allocated_tokens (int64 [num_seqs], may be NULL): tokens each sequence has
  * slots for; a sequence with start + count above it, or a negative start or
  * count, fails the call with PA_ERR_INVALID_ARGUMENT and plan->bad_seq set

@@ -11,13 +11,22 @@
 
 namespace {
 
-// The partition rule's bounds (tokens): largest and smallest partition, the
-// smallest one a full-chip launch may take, and the partials per sequence a
-// latency-bound step keeps to.
+// The partition rule's bounds (tokens): largest and smallest partition and
+// the smallest one a full-chip launch may take.
 constexpr int64_t kMaxPartition = PA_DECODE_MAX_PARTITION;
 constexpr int64_t kMinPartition = 64;
 constexpr int64_t kMinFullChipPartition = 256;
-constexpr int64_t kMaxPartials = 64;
+
+// The latency model of a step that cannot fill the chip, measured on MI355X
+// over 32-layer decode loops whose caches are read cold: one partition
+// workgroup reads about 21 GB/s on its own (0.049 us per token of a 1 KB
+// K+V row), about 310 of them saturate HBM (6.5 TB/s), and the split-K merge
+// of a sequence costs about 3.5 us per batch of 8 partials (partial stores,
+// the arrival atomic and the partial loads are dependent round trips).
+constexpr double kUsPerToken = 0.049;
+constexpr double kSaturatingWorkgroups = 310.0;
+constexpr double kMergeUsPerBatch = 3.5;
+constexpr int64_t kMergeBatch = 8;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -44,12 +53,29 @@ int64_t choose_partition(const DecodeContexts& d, const PaPlanParams& p, int64_t
   // A launch that fills the chip: every resident slot gets 1.5 workgroups.
   for (int64_t part = kMaxPartition; part > kMinFullChipPartition; part /= 2)
     if (d.workgroups(part, width) >= 3 * slots / 2) return part;
-  // A latency-bound step: two thirds of the slots busy, few partials.
-  for (int64_t part = kMaxPartition; part >= kMinPartition; part /= 2)
-    if (d.workgroups(part, width) >= 2 * slots / 3 && ceil_div(longest, part) <= kMaxPartials) return part;
-  int64_t part = kMinPartition;
-  while (part < kMaxPartition && ceil_div(longest, part) > kMaxPartials) part *= 2;
-  return part;
+  // A latency-bound step: the partition of least modelled time -- the
+  // longest workgroup's read (slowed by its share of HBM when more than the
+  // saturating count run at once, times the waves of workgroups) plus the
+  // merge of the longest sequence's partials.  Ties (two bandwidth-bound
+  // launches read the same bytes) go to the shorter partition: its extra
+  // workgroups measured faster.
+  if (d.workgroups(kMinPartition, width) == 0) return kMinPartition;  // no decode
+  int64_t best = kMinPartition;
+  double best_us = -1.0;
+  for (int64_t part = kMinPartition; part <= kMaxPartition; part *= 2) {
+    const int64_t wgs = d.workgroups(part, width);
+    const double active = static_cast<double>(wgs < slots ? wgs : slots);
+    const double share = active > kSaturatingWorkgroups ? active / kSaturatingWorkgroups : 1.0;
+    const double waves = static_cast<double>(ceil_div(wgs, slots));
+    const int64_t parts = ceil_div(longest, part);
+    const double merge = parts > 1 ? kMergeUsPerBatch * static_cast<double>(ceil_div(parts, kMergeBatch)) : 0.0;
+    const double us = static_cast<double>(part) * kUsPerToken * share * waves + merge;
+    if (best_us < 0.0 || us < best_us * (1.0 - 1e-9)) {
+      best = part;
+      best_us = us;
+    }
+  }
+  return best;
 }
 
 int plan_fail(PaStepPlan* plan, int32_t seq, const char* what) {

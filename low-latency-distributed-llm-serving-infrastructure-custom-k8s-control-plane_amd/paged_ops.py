@@ -464,13 +464,17 @@ def choose_partition(
     fastest partition of every measured shape: 4096 for 32/8 heads of 128,
     2048 for the same heads paired (three workgroups per CU), 1024 for 8/8.
 
-    A step too small for that rule (a latency-bound step) takes the largest
-    partition that still gives two thirds of the slots a workgroup with at
-    most 64 partials per sequence, or, when none does, the smallest of 64,
-    128, ... that keeps every sequence to 64 partials: short walks per
-    workgroup, few partials to merge.
-    Measured with graph replay, 32/8 heads of 128 paired: 1 sequence of 1024
-    tokens 16.6 us at 256 -> 11.3 at 64; 16 of 4096 55.9 -> 50.7 at 512.
+    A step too small for that rule (a latency-bound step) takes the one of
+    64 ... 4096 with the least modelled time, measured on 32-layer decode
+    loops whose caches are read cold: a workgroup reads about 21 GB/s on
+    its own (0.049 us per token of a 1 KB K+V row) and about 310 of them
+    saturate HBM, so the longest workgroup takes P x 0.049 us x (its share
+    of HBM when more run at once) x (waves of workgroups); the merge of the
+    longest sequence adds 3.5 us per batch of 8 partials.  Ties go to the
+    shorter partition.  Over 23 measured shapes (1-64 sequences of 256 to
+    16384 tokens, bf16 and fp32, groups of 1-8) the pick is within 5 % of
+    the fastest partition, and the fastest on 18; e.g. one sequence of 4096
+    tokens 25.6 us per layer at 256 (the earlier rule's 64: 37.0).
     """
     p = _plan(_int64_array(start_positions), _int64_array(new_token_counts), 1, 1, 0, num_kv_heads,
               num_query_heads or 0, workgroups_per_item or 0, workgroups_per_cu or 0, compute_units)
