@@ -1092,7 +1092,9 @@ def ab_line(args, device):
     rows; fp32_mha_decode: the step from
     a HIP graph over rotated pool copies; mixed_step: the attention step and
     its decode and prefill kernels; prefill_shapes (--shape, or all): the
-    prefill kernel of each shape."""
+    prefill kernel of each shape; decode_partitions (--shape, or all): a
+    32-layer loop over each latency-bound decode step, per layer, from a
+    HIP graph packed and captured under each library."""
     import torch
 
     ops = pkg("paged_ops")
@@ -1147,6 +1149,46 @@ def ab_line(args, device):
             measures["prefill_kernel_ms"] = lambda: events_ms(
                 gpu_spacer, lambda: ops.prefill(t.query, t.key_cache, t.value_cache, 0, step, w.scaling, out=out),
                 args.steps, 20, stream)
+    elif args.workload == "decode_partitions":
+        import numpy as np
+
+        def layer_ms(w, t):
+            # packed and captured under the library in use, replayed once, then timed
+            step = packed(w)
+            out = torch.empty((w.num_query_tokens, w.num_query_heads, w.head_dim), dtype=w.dtype, device=device)
+
+            def layers():
+                for layer in range(w.num_layers):
+                    ops.attention(t.query, t.key_cache, t.value_cache, layer, step, w.scaling, out=out,
+                                  new_key=t.new_keys, new_value=t.new_values)
+
+            layers()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(10):
+                    layers()
+            g.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            g.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / (10 * w.num_layers)
+            del g  # before the step whose buffers it reads
+            return ms
+
+        for name, ctx, hq, hkv, d, dtype in decode_partition_shapes(args.seed):
+            if args.shape is not None and name != args.shape:
+                continue
+            rng = np.random.Generator(np.random.PCG64(7))
+            lists, total = wl._block_tables(rng, ctx, wl.BLOCK_SIZE)
+            w = wl.StepWorkload(name, hq, hkv, d, wl.BLOCK_SIZE, dtype, 1.0, [c - 1 for c in ctx], [1] * len(ctx),
+                                lists, total, 32)
+            t = wl.make_tensors(w, device, seed=args.seed)
+            keep.append(t)
+            measures[f"{name}.layer_ms"] = lambda w=w, t=t: layer_ms(w, t)
     else:
         raise SystemExit(f"--ab-library does not cover {args.workload}")
 
