@@ -249,7 +249,7 @@ typedef struct {
  * 64 ... 4096 with the least modelled time: the longest workgroup's read at
  * 0.049 us per token, slowed by its share of HBM when more than 310
  * workgroups run at once and multiplied by the waves of workgroups, plus
- * 3.5 us per batch of 8 split-K partials of the longest sequence (ties to
+ * 2 us per batch of 8 split-K partials of the longest sequence (ties to
  * the shorter partition; 64 for a step without decodes).
  * allocated_tokens (int64 [num_seqs], may be NULL): tokens each sequence has
  * slots for; a sequence with start + count above it, or a negative start or

@@ -21,11 +21,11 @@ constexpr int64_t kMinFullChipPartition = 256;
 // over 32-layer decode loops whose caches are read cold: one partition
 // workgroup reads about 21 GB/s on its own (0.049 us per token of a 1 KB
 // K+V row), about 310 of them saturate HBM (6.5 TB/s), and the split-K merge
-// of a sequence costs about 3.5 us per batch of 8 partials (partial stores,
+// of a sequence costs about 2 us per batch of 8 partials (partial stores,
 // the arrival atomic and the partial loads are dependent round trips).
 constexpr double kUsPerToken = 0.049;
 constexpr double kSaturatingWorkgroups = 310.0;
-constexpr double kMergeUsPerBatch = 3.5;
+constexpr double kMergeUsPerBatch = 2.0;
 constexpr int64_t kMergeBatch = 8;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

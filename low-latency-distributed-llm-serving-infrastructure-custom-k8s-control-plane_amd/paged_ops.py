@@ -470,11 +470,11 @@ def choose_partition(
     its own (0.049 us per token of a 1 KB K+V row) and about 310 of them
     saturate HBM, so the longest workgroup takes P x 0.049 us x (its share
     of HBM when more run at once) x (waves of workgroups); the merge of the
-    longest sequence adds 3.5 us per batch of 8 partials.  Ties go to the
-    shorter partition.  Over 23 measured shapes (1-64 sequences of 256 to
-    16384 tokens, bf16 and fp32, groups of 1-8) the pick is within 5 % of
-    the fastest partition, and the fastest on 18; e.g. one sequence of 4096
-    tokens 25.6 us per layer at 256 (the earlier rule's 64: 37.0).
+    longest sequence adds 2 us per batch of 8 partials.  Ties go to the
+    shorter partition.  Over 22 measured steps (1-64 sequences of 256 to
+    16384 tokens, bf16 and fp32, groups of 4 and 8) the pick is the fastest
+    partition on 17 and within 3.4 % on the rest; e.g. two sequences of 8192
+    tokens 32.6 us per layer at 256 (the earlier rule's 128: 43.7).
     """
     p = _plan(_int64_array(start_positions), _int64_array(new_token_counts), 1, 1, 0, num_kv_heads,
               num_query_heads or 0, workgroups_per_item or 0, workgroups_per_cu or 0, compute_units)

@@ -304,21 +304,21 @@ def test_choose_partition_fills_the_chip():
     assert ops.choose_partition([4095] * 32, [1] * 32, 8, 32) == 512
     # A latency-bound step takes the partition of least modelled time:
     # P x 0.049 us x (active workgroups / 310 when above 310) x waves, plus
-    # 3.5 us per batch of 8 partials of the longest sequence.  4 x 3001
-    # tokens, width 8, 1024 slots: 128 -> 768 workgroups, 15.5 + 3 x 3.5 =
-    # 26.0 us; 256 -> 384, 15.5 + 2 x 3.5 = 22.5; 512 -> 192, 25.1 + 3.5 = 28.6.
+    # 2 us per batch of 8 partials of the longest sequence.  4 x 3001
+    # tokens, width 8, 1024 slots: 128 -> 768 workgroups, 15.5 + 3 x 2 =
+    # 21.5 us; 256 -> 384, 15.5 + 2 x 2 = 19.5; 512 -> 192, 25.1 + 2 = 27.1.
     assert ops.choose_partition([3000] * 4, [1] * 4, 8, 32) == 256
     assert ops.choose_partition([16383] * 4, [1] * 4, 8, 32) == 1024
-    # one sequence of 3001: 64 -> 3.8 + 6 x 3.5 = 24.8; 128 -> 6.3 + 3 x 3.5
-    # = 16.8; 256 -> 12.5 + 2 x 3.5 = 19.5
+    # one sequence of 3001: 64 -> 3.8 + 6 x 2 = 15.8; 128 -> 6.3 + 3 x 2 =
+    # 12.3; 256 -> 12.5 + 2 x 2 = 16.5
     assert ops.choose_partition([3000], [1], 8, 32) == 128
     assert ops.choose_partition([16383], [1], 8, 32) == 512
-    # short contexts (16, 301, 512): 64 -> 3.1 + 3.5 = 6.6; 128 -> 6.3 + 3.5
+    # short contexts (16, 301, 512): 64 -> 3.1 + 2 = 5.1; 128 -> 6.3 + 2
     assert ops.choose_partition([15, 300, 511], [1, 1, 1], 8, 8) == 64
     # a bandwidth-bound tie (the same bytes over more or fewer workgroups,
     # the same merge batches) goes to the shorter partition: 24 x 1024
     # tokens over 768 slots, 128 -> 768 workgroups and 256 -> 384 both
-    # model 15.5 + 3.5 us
+    # model 15.5 + 2 us
     assert ops.choose_partition([1023] * 24, [1] * 24, 8, 32, workgroups_per_item=4, workgroups_per_cu=3) == 128
     # prefill rows do not count as decode work
     assert ops.choose_partition([0, 3000], [500, 1], 8, 32) == 128
