@@ -227,7 +227,8 @@ __device__ __forceinline__ float across_groups_max(float x) {
 // merge paths (the merge kernel, K = 1, and the in-launch merge of the
 // partition kernel) run this, so they give the same bits.
 constexpr int kMergeBatch = 8;
-constexpr int kMergeOutputs = 2;  // elements a thread of the in-launch merge merges at once
+constexpr int kMergeOutputs = 2;        // elements a thread of the in-launch merge merges at once
+constexpr int kMergeOutputsPaired = 4;  // the same for paired KV heads (their occupancy allows it)
 
 // Partials read by the in-launch merge are written by workgroups on other
 // XCDs in the same launch: they are stored and loaded as device-scope
@@ -1119,7 +1120,8 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
         // (more at once cost some instances a wave of occupancy; fp32 heads
         // of 80 and 96 take one at a time, which keeps theirs).
         constexpr int KO = (G * ODM + kDecodeThreads - 1) / kDecodeThreads;
-        constexpr int KC = KO < kMergeOutputs ? KO : (MASKD && sizeof(T) == 4 ? 1 : kMergeOutputs);
+        constexpr int KM = PAIR ? kMergeOutputsPaired : kMergeOutputs;
+        constexpr int KC = KO < KM ? KO : (MASKD && sizeof(T) == 4 ? 1 : KM);
         if constexpr (KC == 1) {
           for (int i = tid; i < G * ODM; i += kDecodeThreads) {
             const float* const mlk[1] = {a.part_ml + 2 * (h0 + i / ODM)};
