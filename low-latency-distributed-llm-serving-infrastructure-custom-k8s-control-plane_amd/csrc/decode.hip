@@ -213,22 +213,22 @@ __device__ __forceinline__ float across_groups_max(float x) {
   return max_halves(x);
 }
 
-// Output elements of a multi-partition sequence from its split-K partials,
-// K elements per thread at once (element k: ml[k] / acc[k] address its
-// (max, sum) pair and accumulator in item 0, out[k] its output; only the
-// first `live` are real).  Partitions 0 .. nfull-1 are items first .. first +
-// nfull - 1, partition nfull (when nparts > nfull) is item rem; ml_stride /
-// stride step one item.  kMergeBatch partitions per round trip, with a
-// running maximum (the stored maxima are already in the exp2 domain); slots
-// past the last partition read the first one again and get no weight.  The
-// K elements' loads of a batch are issued together, so a thread's elements
-// share one round trip per batch (one after the other, eight heads of 128
-// took four).  Each element's arithmetic is the same whatever K, and both
-// merge paths (the merge kernel, K = 1, and the in-launch merge of the
-// partition kernel) run this, so they give the same bits.
+// K output elements of one head of a multi-partition sequence from its
+// split-K partials: ml addresses the head's (max, sum) pair in item 0, acc
+// the first element's accumulator and out its output; element k sits
+// k * estride elements further.  Partitions 0 .. nfull-1 are items first ..
+// first + nfull - 1, partition nfull (when nparts > nfull) is item rem;
+// ml_stride / stride step one item.  kMergeBatch partitions per round trip,
+// with a running maximum (the stored maxima are already in the exp2
+// domain); slots past the last partition read the first one again and get
+// no weight.  The elements share each partial's (max, sum), loaded once for
+// all of them, and their loads go out together: one round trip per batch
+// for the K elements (one after the other, eight heads of 128 took four).
+// Each element's arithmetic is the same whatever K, and both merge paths
+// (the merge kernel, K = 1, and the in-launch merge of the partition
+// kernel) run this, so they give the same bits.
 constexpr int kMergeBatch = 8;
-constexpr int kMergeOutputs = 2;        // elements a thread of the in-launch merge merges at once
-constexpr int kMergeOutputsPaired = 4;  // the same for paired KV heads (their occupancy allows it)
+constexpr int kMergeOutputs = 4;  // elements a thread of the in-launch merge merges at once
 
 // Partials read by the in-launch merge are written by workgroups on other
 // XCDs in the same launch: they are stored and loaded as device-scope
@@ -242,66 +242,50 @@ __device__ __forceinline__ float load_device(const float* p) {
 }
 
 template <typename T, int K, bool DEVICE_LOADS = false>
-__device__ __forceinline__ void merge_partials(const float* const (&ml)[K], const float* const (&acc)[K], int live,
-                                               int64_t ml_stride, int64_t stride, int64_t first, int nfull,
-                                               int64_t rem, int nparts, T* const (&out)[K]) {
+__device__ __forceinline__ void merge_partials(const float* ml, const float* acc, int estride, int64_t ml_stride,
+                                               int64_t stride, int64_t first, int nfull, int64_t rem, int nparts,
+                                               T* out) {
   auto item_of = [&](int p) -> int64_t { return p < nfull ? first + p : rem; };
-  float mx[K], sum[K], o[K];
+  auto ld = [&](const float* q) { return DEVICE_LOADS ? load_device(q) : *q; };
+  float mx = kScoreFloor, sum = 0.f, o[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    mx[k] = kScoreFloor;
-    sum[k] = 0.f;
-    o[k] = 0.f;
-  }
+  for (int k = 0; k < K; ++k) o[k] = 0.f;
   for (int p = 0; p < nparts; p += kMergeBatch) {
-    float mp[K][kMergeBatch], lp[K][kMergeBatch], xp[K][kMergeBatch];
+    float mp[kMergeBatch], lp[kMergeBatch], xp[kMergeBatch][K];
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
       const int64_t it = item_of(p + u < nparts ? p + u : 0);
+      mp[u] = ld(ml + it * ml_stride);
+      lp[u] = ld(ml + it * ml_stride + 1);
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        if (k >= live) {
-          mp[k][u] = kScoreFloor;
-          lp[k][u] = 0.f;
-          xp[k][u] = 0.f;
-        } else if constexpr (DEVICE_LOADS) {
-          mp[k][u] = load_device(ml[k] + it * ml_stride);
-          lp[k][u] = load_device(ml[k] + it * ml_stride + 1);
-          xp[k][u] = load_device(acc[k] + it * stride);
-        } else {
-          mp[k][u] = ml[k][it * ml_stride];
-          lp[k][u] = ml[k][it * ml_stride + 1];
-          xp[k][u] = acc[k][it * stride];
-        }
-      }
+      for (int k = 0; k < K; ++k) xp[u][k] = ld(acc + it * stride + k * estride);
     }
+    float mn = mx;
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      float mn = mx[k];
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (u > 0 && p + u >= nparts) {
+        mp[u] = kScoreFloor;
+        lp[u] = 0.f;
 #pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        if (u > 0 && p + u >= nparts) {
-          mp[k][u] = kScoreFloor;
-          lp[k][u] = 0.f;
-          xp[k][u] = 0.f;
-        }
-        mn = fmaxf(mn, mp[k][u]);
+        for (int k = 0; k < K; ++k) xp[u][k] = 0.f;
       }
-      const float r = fast_exp2(mx[k] - mn);
-      sum[k] *= r;
-      o[k] *= r;
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        const float w = fast_exp2(mp[k][u] - mn);
-        sum[k] = fmaf(lp[k][u], w, sum[k]);
-        o[k] = fmaf(xp[k][u], w, o[k]);
-      }
-      mx[k] = mn;
+      mn = fmaxf(mn, mp[u]);
     }
+    const float r = fast_exp2(mx - mn);
+    sum *= r;
+#pragma unroll
+    for (int k = 0; k < K; ++k) o[k] *= r;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float w = fast_exp2(mp[u] - mn);
+      sum = fmaf(lp[u], w, sum);
+#pragma unroll
+      for (int k = 0; k < K; ++k) o[k] = fmaf(xp[u][k], w, o[k]);
+    }
+    mx = mn;
   }
 #pragma unroll
-  for (int k = 0; k < K; ++k)
-    if (k < live) store_scalar<T>(out[k], sum[k] > 0.f ? o[k] / sum[k] : 0.f);
+  for (int k = 0; k < K; ++k) store_scalar<T>(out + k * estride, sum > 0.f ? o[k] / sum : 0.f);
 }
 
 // PAIR: two adjacent real KV heads of D/2 run as one head of D with the G
@@ -1116,40 +1100,23 @@ __global__ __launch_bounds__(kDecodeThreads) PA_DECODE_OCCUPANCY(T, D, (PAIR ? G
       const int64_t rem = has_rem ? s_merge[2] : -1;
       const bool ok = first >= 0 && first + nfull <= a.num_items && (!has_rem || (rem >= 0 && rem < a.num_items));
       if (ok) {
-        // Elements tid, tid + 256, ... of the G * ODM outputs, KC at a time
-        // (more at once cost some instances a wave of occupancy; fp32 heads
-        // of 80 and 96 take one at a time, which keeps theirs).
+        // KC elements of one head per thread, ODM / KC apart, so that the
+        // lanes of a wave read consecutive floats of each partial; the
+        // thread's group r = tid, tid + 256, ... covers elements j + k *
+        // ODM / KC (k < KC) of head r / (ODM / KC), j = r % (ODM / KC).
+        // (fp32 heads of 80 and 96 take one at a time, which keeps their
+        // occupancy.)
         constexpr int KO = (G * ODM + kDecodeThreads - 1) / kDecodeThreads;
-        constexpr int KM = PAIR ? kMergeOutputsPaired : kMergeOutputs;
-        constexpr int KC = KO < KM ? KO : (MASKD && sizeof(T) == 4 ? 1 : KM);
-        if constexpr (KC == 1) {
-          for (int i = tid; i < G * ODM; i += kDecodeThreads) {
-            const float* const mlk[1] = {a.part_ml + 2 * (h0 + i / ODM)};
-            const float* const acck[1] = {a.part_acc + static_cast<int64_t>(h0) * ODM + i};
-            T* const outk[1] = {out + i};
-            merge_partials<T, 1, true>(mlk, acck, 1, 2 * static_cast<int64_t>(hq), static_cast<int64_t>(hq) * ODM,
-                                       first, nfull, rem, nparts, outk);
-          }
-        } else {
-#pragma unroll
-          for (int k0 = 0; k0 < KO; k0 += KC) {
-            const float* mlk[KC];
-            const float* acck[KC];
-            T* outk[KC];
-            int live = 0;  // elements k < live exist (i grows with k)
-#pragma unroll
-            for (int k = 0; k < KC; ++k) {
-              const int i = tid + (k0 + k) * kDecodeThreads;
-              const int ii = i < G * ODM ? i : 0;
-              mlk[k] = a.part_ml + 2 * (h0 + ii / ODM);
-              acck[k] = a.part_acc + static_cast<int64_t>(h0) * ODM + ii;
-              outk[k] = out + ii;
-              if (i < G * ODM) live = k + 1;
-            }
-            if (live > 0)
-              merge_partials<T, KC, true>(mlk, acck, live, 2 * static_cast<int64_t>(hq),
-                                          static_cast<int64_t>(hq) * ODM, first, nfull, rem, nparts, outk);
-          }
+        constexpr int KM = MASKD && sizeof(T) == 4 ? 1 : kMergeOutputs;
+        constexpr int KC = KO >= 4 && KM >= 4 ? 4 : KO >= 2 && KM >= 2 ? 2 : 1;
+        constexpr int RUN = ODM / KC;  // groups per head
+        static_assert(ODM % KC == 0, "a group's elements stay inside one head");
+        for (int r = tid; r < G * RUN; r += kDecodeThreads) {
+          const int g = r / RUN;
+          const int e = g * ODM + (r - g * RUN);
+          merge_partials<T, KC, true>(a.part_ml + 2 * (h0 + g), a.part_acc + static_cast<int64_t>(h0) * ODM + e,
+                                      RUN, 2 * static_cast<int64_t>(hq), static_cast<int64_t>(hq) * ODM, first,
+                                      nfull, rem, nparts, out + e);
         }
       }
     }
@@ -1183,11 +1150,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_merge_kernel(DecodeArgs
   const int i = static_cast<int>(blockIdx.y) * kDecodeThreads + static_cast<int>(threadIdx.x);
   if (i >= G * D) return;
   const int h = kvh * G + i / D;
-  const float* const ml[1] = {a.part_ml + 2 * h};
-  const float* const acc[1] = {a.part_acc + static_cast<int64_t>(kvh) * G * D + i};
-  T* const outp[1] = {out + i};
-  merge_partials<T, 1>(ml, acc, 1, 2 * static_cast<int64_t>(hq), static_cast<int64_t>(hq) * D, first, nfull,
-                       has_rem ? e.w : -1, nparts, outp);
+  merge_partials<T, 1>(a.part_ml + 2 * h, a.part_acc + static_cast<int64_t>(kvh) * G * D + i, 0,
+                       2 * static_cast<int64_t>(hq), static_cast<int64_t>(hq) * D, first, nfull, has_rem ? e.w : -1,
+                       nparts, out + i);
 }
 
 // ---- host-side dispatch ------------------------------------------------
