@@ -473,8 +473,8 @@ def choose_partition(
     longest sequence adds 2 us per batch of 8 partials.  Ties go to the
     shorter partition.  Over 22 measured steps (1-64 sequences of 256 to
     16384 tokens, bf16 and fp32, groups of 4 and 8) the pick is the fastest
-    partition on 17 and within 3.5 % on the rest; e.g. two sequences of 8192
-    tokens 30.7 us per layer at 256 (the earlier rule's 128: 40.0).
+    partition on 17 and within 9.2 % on the rest; e.g. two sequences of 8192
+    tokens 26.7 us per layer at 256 (the earlier rule's 128: 29.7).
     """
     p = _plan(_int64_array(start_positions), _int64_array(new_token_counts), 1, 1, 0, num_kv_heads,
               num_query_heads or 0, workgroups_per_item or 0, workgroups_per_cu or 0, compute_units)
